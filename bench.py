@@ -1,0 +1,220 @@
+"""Benchmark: the non-GEMM ops of one Qwen3-4B prefill layer on one MI355X.
+
+Workload (one step = one layer's hot path over one batch): 4 x 2048 = 8192 tokens, fp16 activations
+~N(0,1): input RMSNorm [8192, 2560] -> q/k head RMSNorm + NeoX RoPE (32 q + 8 kv heads of 128,
+theta 1e6, positions 0..2047 per sequence) -> post-attention RMSNorm [8192, 2560] -> SwiGLU on
+gate/up [8192, 9728]. Inputs are resident in HBM before timing.
+
+Each op is timed with HIP events on the stream it runs on, after a 512 MiB streaming write that
+evicts L2 and the 256 MB Infinity Cache, so every op reads its operands from HBM (the flush is
+outside the event pair). value = algorithmic bytes of the four ops / sum of their median times.
+ms_per_step is that per-layer kernel time; wall_ms_per_step (the barrier-to-barrier clock of the K
+timed steps, divided by K) also contains the flushes.
+
+cpu_baseline: the reference's portable C++ ops (oracle/_ref, compiled from its sources) -- or the
+oracle's C restatement where that is absent -- on one pinned core, over a bounded row sample of the
+same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = ("achieved HBM GB/s (% of 8 TB/s) per fused op; µs/layer non-GEMM ops, Qwen3-4B")
+HBM_PEAK_GBS = 8000.0
+OPS = ("rmsnorm_in", "qk_norm_rope", "rmsnorm_post", "swiglu")
+DOMINANT = "swiglu"
+KERNEL_NAMES = {"swiglu": "swiglu_kernel", "rmsnorm_in": "norm_rows_kernel", "qk_norm_rope": "qk_rope_kernel"}
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--no-flush", action="store_true", help="skip the cache flush (cache-warm figures)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--only", default=None, help="time a single op (for profiling runs)")
+    return p.parse_args()
+
+
+def gpu_bench(args):
+    import torch
+
+    from nekochat_amd import ops
+    from nekochat_amd import workloads as wl
+
+    dev = torch.device("cuda:0")
+    cfg = wl.QWEN3_PREFILL
+    inp = wl.qwen3_prefill_inputs(cfg, dev)
+    xn = torch.empty_like(inp["x"])
+    g = torch.empty((cfg.T, cfg.I), dtype=torch.float16, device=dev)
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    op_bytes = cfg.op_bytes()
+
+    calls = {
+        "rmsnorm_in": lambda: ops.rms_norm(inp["x"], inp["w_in"], cfg.eps, out=xn),
+        "qk_norm_rope": lambda: ops.qk_norm_rope(inp["qkv"], cfg.n_q, cfg.n_kv, cfg.hd, inp["cs"], cfg.eps,
+                                                 wqk=inp["wqk"], positions=inp["positions"]),
+        "rmsnorm_post": lambda: ops.rms_norm(inp["x"], inp["w_post"], cfg.eps, out=xn),
+        "swiglu": lambda: ops.silu_mul(inp["h"], out=g),
+    }
+    names = [args.only] if args.only else list(OPS)
+
+    def step(record):
+        for name in names:
+            if not args.no_flush:
+                flush.zero_()
+            if record is None:
+                calls[name]()
+            else:
+                s, e = record[name]
+                s.record()
+                calls[name]()
+                e.record()
+
+    for _ in range(args.warmup):
+        step(None)
+    events = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for n in names}
+              for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(events[k])
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps * 1e3
+
+    per_op = {}
+    for n in names:
+        times_ms = [events[k][n][0].elapsed_time(events[k][n][1]) for k in range(args.steps)]
+        med = statistics.median(times_ms)
+        gbs = op_bytes[n] / (med * 1e-3) / 1e9
+        per_op[n] = {"us": round(med * 1e3, 3), "mean_us": round(statistics.fmean(times_ms) * 1e3, 3),
+                     "bytes": op_bytes[n], "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return cfg, per_op, wall
+
+
+def cpu_baseline(cfg, rows=256, reps=5):
+    """The reference CPU ops on one core over `rows` tokens of the same workload, scaled to GB/s."""
+    import ctypes
+
+    import numpy as np
+
+    from nekochat_amd import workloads as wl
+    from oracle import oracle as O
+
+    try:
+        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    except (AttributeError, OSError):
+        pass
+    x = wl.normal_f16((rows, cfg.C), 0.0, 1.0, 1, "cpu").numpy().view(np.uint16)
+    w = wl.weight_f32(cfg.C, 1.0, 0.05, 2, "cpu").numpy()
+    qkv = wl.normal_f16((rows, cfg.qkv_stride), 0.0, 1.0, 4, "cpu").numpy().view(np.uint16).copy()
+    wqk = wl.weight_f32(2 * cfg.hd, 1.0, 0.05, 5, "cpu").numpy()
+    pos = (np.arange(rows) % cfg.seq).astype(np.int32)
+    cs = O.rope_table(cfg.theta, cfg.hd, cfg.seq)
+    h = wl.normal_f16((rows, 2 * cfg.I), 0.0, 1.0, 6, "cpu").numpy().view(np.uint16)
+    y = np.empty_like(x)
+    g = np.empty((rows, cfg.I), np.uint16)
+    P = O._ptr
+    if O.ref_available():
+        R = O.ref()
+        kind = "reference"
+        run = {
+            "rmsnorm": lambda: R.ref_rmsnorm_f16(P(x), P(y), P(w), rows, cfg.C, ctypes.c_float(cfg.eps)),
+            "qk_norm_rope": lambda: R.ref_qk_norm_rope_f16(P(qkv), cfg.qkv_stride, rows, cfg.n_q, cfg.n_kv, cfg.hd,
+                                                           P(pos), P(wqk[:cfg.hd].copy()), P(wqk[cfg.hd:].copy()),
+                                                           P(cs), ctypes.c_float(cfg.eps)),
+            "swiglu": lambda: R.ref_silu_mul_f16(P(h), P(g), rows, cfg.I),
+        }
+    else:
+        kind = "port"
+        run = {
+            "rmsnorm": lambda: O.lib().oracle_rmsnorm_f16(P(x), cfg.C, P(y), cfg.C, P(w), rows, cfg.C, cfg.eps),
+            "qk_norm_rope": lambda: O.lib().oracle_qk_norm_rope_f16(P(qkv), cfg.qkv_stride, rows, cfg.n_q, cfg.n_kv,
+                                                                    cfg.hd, 0, P(pos), P(wqk), P(cs), cfg.seq, cfg.eps),
+            "swiglu": lambda: O.lib().oracle_swiglu_f16(P(h), 2 * cfg.I, P(g), cfg.I, rows, cfg.I),
+        }
+    t = {}
+    for name, fn in run.items():
+        fn()
+        samples = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            samples.append(time.perf_counter() - t0)
+        t[name] = statistics.median(samples) * cfg.T / rows  # seconds for the full 8192 rows
+    layer_s = 2 * t["rmsnorm"] + t["qk_norm_rope"] + t["swiglu"]
+    total_bytes = sum(cfg.op_bytes().values())
+    return {
+        "value": round(total_bytes / layer_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+        "us_per_layer": round(layer_s * 1e6, 1),
+        "per_op_us": {k: round(v * 1e6, 1) for k, v in t.items()},
+        "sample": f"{rows} of {cfg.T} tokens per op (median of {reps}), scaled to the full layer; "
+                  f"1 pinned core of {os.cpu_count()}; g++ -O3 portable x86-64 build",
+    }
+
+
+def traffic_from_profiles():
+    """Per-launch HBM bytes of the dominant kernel measured by rocprofv3 --pmc (profiles/), if recorded."""
+    path = os.path.join(ROOT, "profiles", "swiglu_qwen3_4b_prefill_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the ops are per-row and shard by tokens with no "
+              "communication, so N > 1 is not run here.", file=sys.stderr)
+        sys.exit(2)
+    cfg, per_op, wall = gpu_bench(args)
+    total_us = sum(v["us"] for v in per_op.values())
+    total_bytes = sum(v["bytes"] for v in per_op.values())
+    value = total_bytes / (total_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_us / 1e3, 5),
+        "wall_ms_per_step": round(wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Qwen3-4B prefill layer, non-GEMM ops: 2x RMSNorm [8192,2560] + q/k RMSNorm+NeoX RoPE "
+                        "(32q+8kv x 128) + SwiGLU [8192,9728]; fp16 I/O, f32 math, f64 norm sums",
+            "tokens": cfg.T, "hidden": cfg.C, "heads": [cfg.n_q, cfg.n_kv], "head_dim": cfg.hd,
+            "intermediate": cfg.I, "io_dtype": "f16", "cache_flush": not args.no_flush,
+        },
+        "us_per_layer": round(total_us, 3),
+        "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "ops": per_op,
+    }
+    if not args.only or args.only == DOMINANT:
+        d = per_op[DOMINANT]
+        achieved = d["bytes"] / (d["mean_us"] * 1e-6) / 1e9
+        line["roofline"] = {"bound": "hbm", "kernel": DOMINANT, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                            "traffic": traffic_from_profiles()}
+    if not args.no_cpu and not args.only:
+        line["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,162 @@
+/*
+ * neko_hip: MI355X (gfx950) kernels for NekoChat's per-row transformer layer ops, behind a C ABI.
+ *
+ * Reference interfaces replaced (paths relative to the reference's app/architecture/shared/cpp/):
+ *   - the GPU backend contract neko::gpu::ComputeBackend (gpu/compute.h:24-45): buffers, upload /
+ *     download, ordered dispatch, submitAndWait -- the HIP adapter (nekochat_amd/csrc/hip_backend.cpp)
+ *     implements it over the functions below;
+ *   - its per-kernel dispatches Embed / LayerNorm / Rope / SiluMul (gpu/compute.h:17, shaders
+ *     embed.comp, layernorm.comp, rope.comp, silu_mul.comp), plus the CPU-only Granite gated norm
+ *     (granite/cpp/granite_model.cpp:278-287) and standalone GELU (cpu_ops.cpp:20-23);
+ *   - the host codecs quantRowBytes / quantizeMatrix (quant.h:32,57) and Qwen3Model::ropeTable
+ *     (qwen3/cpp/qwen3_model.cpp:102-114).
+ *
+ * Conventions
+ *   - Every function returns an int status: NEKO_OK (0) or a negative NEKO_ERR_*; nothing throws.
+ *     The message of the last failure on a context is neko_hip_last_error(ctx).
+ *   - One context per host thread. A context owns one in-order HIP stream, so every op is ordered
+ *     after the previous one on that context (the reference's "each dispatch is ordered after the
+ *     previous", gpu/compute.h:38) without barriers. Ops only enqueue work; neko_hip_download and
+ *     neko_hip_synchronize wait.
+ *   - Device pointers are plain addresses from neko_hip_alloc (or any HIP allocation on the
+ *     context's device). Sizes and strides are int64 element counts unless the name says bytes.
+ *   - dtype selects the activation type: NEKO_DT_F16 (IEEE half, fp32 arithmetic inside, one RNE
+ *     rounding per output) or NEKO_DT_F32 (the reference's own activation type). Norm and gate
+ *     weights (gamma, beta, w, wqk) are f32 arrays, as the reference keeps them.
+ *   - Arithmetic follows the reference's CPU ops (cpu_ops.cpp:20-23,483-533): norms accumulate in
+ *     double and round the scale to float; products are evaluated in the same order, unfused.
+ */
+#ifndef NEKO_HIP_H
+#define NEKO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NEKO_OK 0
+#define NEKO_ERR_INVALID (-1)     /* bad argument: null pointer, size, stride, alignment or format */
+#define NEKO_ERR_HIP (-2)         /* a HIP runtime call or kernel launch failed */
+#define NEKO_ERR_NO_DEVICE (-3)   /* no usable gfx950 device */
+#define NEKO_ERR_UNSUPPORTED (-4) /* valid request this build does not implement */
+
+typedef enum { NEKO_DT_F32 = 0, NEKO_DT_F16 = 1 } neko_dtype;
+
+/* Weight row formats, numbered as the reference's WeightFormat (quant.h:19). */
+typedef enum { NEKO_FMT_F16 = 0, NEKO_FMT_FP8 = 1, NEKO_FMT_FP4 = 2 } neko_weight_format;
+
+typedef struct neko_hip_ctx neko_hip_ctx;
+
+/* ---------------------------------------------------------------- context and memory
+ * Replace the ComputeBackend factory / create / upload / download / submitAndWait
+ * (gpu/compute.h:28-44, vk_compute.cpp:459-466). */
+
+/* Opens device `device` and creates the context's stream. *out is NULL on failure; the message of
+ * a failed create is available as neko_hip_last_error(NULL). */
+int neko_hip_create(int device, neko_hip_ctx** out);
+/* Waits for outstanding work, releases the stream and any memory still allocated through the ctx. */
+int neko_hip_destroy(neko_hip_ctx* ctx);
+/* Last error message on ctx (or of the last failed neko_hip_create when ctx is NULL). Never NULL. */
+const char* neko_hip_last_error(const neko_hip_ctx* ctx);
+/* Device name and the largest single allocation (ComputeBackend::deviceName / maxBufferBytes). */
+int neko_hip_device_name(neko_hip_ctx* ctx, char* buf, size_t buf_bytes);
+size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx);
+/* Routes subsequent work to an external hipStream_t on the same device (e.g. a framework's
+ * current stream); NULL restores the context's own stream, a blocking stream that is ordered with
+ * the device's null stream. The caller keeps ownership of an external stream. */
+int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream);
+void* neko_hip_get_stream(const neko_hip_ctx* ctx);
+
+int neko_hip_alloc(neko_hip_ctx* ctx, size_t bytes, void** dev_ptr);
+int neko_hip_free(neko_hip_ctx* ctx, void* dev_ptr);
+/* Ordered on the context's stream; upload returns once src may be reused. */
+int neko_hip_upload(neko_hip_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+/* Waits for all work queued before it, then copies. */
+int neko_hip_download(neko_hip_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+int neko_hip_memset(neko_hip_ctx* ctx, void* dst_dev, int value, size_t bytes);
+int neko_hip_synchronize(neko_hip_ctx* ctx);
+
+/* ---------------------------------------------------------------- row norms */
+
+/* LayerNorm over rows of C: y = (x - mean) * rstd * gamma + beta, two-pass mean / variance in
+ * double (cpu_ops.cpp:483-500; GPU form layernorm.comp flags = 0). x and y may alias. */
+int neko_hip_layernorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y, int64_t y_stride,
+                       const float* gamma, const float* beta, int64_t rows, int64_t C, float eps, int dtype);
+
+/* RMSNorm over rows of C: y = x * float(1/sqrt(sum(x^2)/C + eps)) * w; x and y may alias
+ * (cpu_ops.cpp:502-511, cpu_ops.h:27; GPU form layernorm.comp flags = 1). Also the Qwen3 q/k head
+ * norm when called on heads as rows (qwen3_model.cpp:250-251). */
+int neko_hip_rmsnorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y, int64_t y_stride, const float* w,
+                     int64_t rows, int64_t C, float eps, int dtype);
+
+/* Granite-4.0-H Mamba2 output gate + group RMSNorm: g = y * silu(z), then RMSNorm of each group of
+ * D/groups channels with its slice of w, written to out (granite_model.cpp:278-287, which gates and
+ * norms y in place; out may alias y). z rows have stride z_stride (the gate columns of the in_proj
+ * row, granite_model.h:86-88). D % groups == 0. */
+int neko_hip_gated_rmsnorm(neko_hip_ctx* ctx, const void* y, int64_t y_stride, const void* z, int64_t z_stride,
+                           void* out, int64_t out_stride, const float* w, int64_t rows, int64_t D, int groups,
+                           float eps, int dtype);
+
+/* ---------------------------------------------------------------- attention prologue */
+
+/* Qwen3 per-head q/k RMSNorm then NeoX half-split RoPE, in place on the q and k heads of each qkv
+ * row (row = [q n_q*hd | k n_kv*hd | v n_kv*hd], stride row_stride); v is neither read nor written
+ * (rope.comp:1-55, dispatch qwen3_model.cpp:313; CPU qwen3_model.cpp:249-253).
+ *   wqk       f32 [2*hd]: q_norm weights then k_norm weights; NULL = rotation only (rope.comp flags 0).
+ *   cs        f32 [n_pos][hd]: hd/2 (cos, sin) pairs per position (Qwen3Model::ropeTable layout).
+ *   positions int32 [rows] per-row positions, or NULL for pos0 + row (the reference's GPU ABI).
+ * Rows whose position lies outside [0, n_pos) are left untouched. hd even, hd <= 512. */
+int neko_hip_qk_norm_rope(neko_hip_ctx* ctx, void* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd,
+                          int64_t pos0, const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos,
+                          float eps, int dtype);
+
+/* ---------------------------------------------------------------- activations */
+
+/* SwiGLU: out[t][i] = gate / (1 + exp(-gate)) * up with gate = h[t][i], up = h[t][I + i]
+ * (cpu_ops.cpp:526-533, silu_mul.comp). h rows hold gate then up (stride h_stride >= 2*I). */
+int neko_hip_swiglu(neko_hip_ctx* ctx, const void* h, int64_t h_stride, void* out, int64_t out_stride, int64_t rows,
+                    int64_t I, int dtype);
+
+/* GELU, tanh form: y = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))) over n contiguous elements
+ * (cpu_ops.cpp:20-23; the matmul epilogue of matmul.comp:16-19). x and y may alias. */
+int neko_hip_gelu_tanh(neko_hip_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
+
+/* ---------------------------------------------------------------- embedding gather */
+
+/* out[t] = dequant(table[tokens[t] - row_base]) (+ f32(wpe[pos0 + t])) for tokens with
+ * row_base <= tokens[t] < row_base + rows; other tokens leave out[t] untouched, so a table split
+ * into row chunks is gathered with one call per chunk (embed.comp:1-51, quant.cpp:230-253,
+ * gpt2_model.cpp:182-187, qwen3_model.cpp:301-305).
+ *   table     rows of row_bytes bytes in weight format fmt (quant.h:30-36 layout); row_bytes must
+ *             be even and at least neko_quant_row_bytes(fmt, C). FP8/FP4 need C % 32 == 0.
+ *   wpe       f16 [wpe_rows][C] position table added in f32, or NULL. Requires pos0 + T <= wpe_rows.
+ *   out       rows of out_stride elements of out_dtype; f16 output is one RNE rounding of the f32
+ *             result. Dequantisation is exact, so the output is bit-exact with the reference. */
+int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const void* table, int64_t row_bytes, int fmt,
+                   int64_t C, int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t wpe_rows, int64_t pos0,
+                   void* out, int64_t out_stride, int out_dtype);
+
+/* ---------------------------------------------------------------- host-side codecs */
+
+/* Bytes per stored row (quant.cpp:199-208): F16 2*cols; FP8 / FP4 the codes (cols or cols/2
+ * bytes) followed by cols/32 f16 block scales, zero-padded to a multiple of 16 bytes. */
+size_t neko_quant_row_bytes(int fmt, int64_t cols);
+
+/* Encodes rows x cols f32 weights (host memory) into rows of neko_quant_row_bytes(fmt, cols) bytes,
+ * bit-identical to the reference's quantizeMatrix (quant.cpp:255-279, portable branch). cols % 32
+ * != 0 stores F16, like the reference; *fmt_used reports the format written (may be NULL).
+ * threads <= 0 uses every hardware thread. */
+int neko_quantize_rows(int fmt, int64_t rows, int64_t cols, const float* src, uint8_t* dst, int threads,
+                       int* fmt_used);
+
+/* RoPE table (host memory): cs[p][2i] = float(cos(p * theta^(-2i/hd))), cs[p][2i+1] = float(sin(..))
+ * for p < n_pos, i < hd/2, evaluated in double (qwen3_model.cpp:102-114). */
+int neko_rope_table(double theta, int hd, int64_t n_pos, float* cs);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEKO_HIP_H */

@@ -1,0 +1,55 @@
+// Host-side internals shared by the C-ABI translation units: the context, status helpers and the
+// launch-time checks every entry point runs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+#include <unordered_set>
+
+#include "../../include/neko_hip.h"
+#include "device.h"
+
+struct neko_hip_ctx {
+    int device = -1;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;  // own_stream unless the caller routed work elsewhere
+    int cu_count = 0;
+    size_t max_alloc = 0;
+    std::string name;
+    std::string err;
+    std::unordered_set<void*> allocs;
+};
+
+namespace neko_hip {
+
+// Records a formatted message on ctx (or the thread-wide create error when ctx is null) and
+// returns code.
+int fail(neko_hip_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+// NEKO_OK, or NEKO_ERR_HIP with the HIP error string and the failing call named.
+int check(neko_hip_ctx* ctx, hipError_t e, const char* what);
+// Validates ctx and makes its device current for this thread.
+int enter(neko_hip_ctx* ctx);
+// Picks up launch errors of the kernel just enqueued.
+int after_launch(neko_hip_ctx* ctx, const char* what);
+
+FastDiv make_fast_div(uint32_t d);
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline size_t dtype_size(int dtype) { return dtype == NEKO_DT_F16 ? 2 : 4; }
+inline bool valid_dtype(int dtype) { return dtype == NEKO_DT_F16 || dtype == NEKO_DT_F32; }
+
+}  // namespace neko_hip
+
+#define NEKO_ENTER(ctx)                          \
+    do {                                         \
+        const int neko_rc_ = neko_hip::enter(ctx); \
+        if (neko_rc_ != NEKO_OK) return neko_rc_; \
+    } while (0)
+
+#define NEKO_REQUIRE(ctx, cond, ...)                                        \
+    do {                                                                    \
+        if (!(cond)) return neko_hip::fail(ctx, NEKO_ERR_INVALID, __VA_ARGS__); \
+    } while (0)

@@ -1,0 +1,373 @@
+// Row norms for gfx950: LayerNorm (cpu_ops.cpp:483-500), RMSNorm (cpu_ops.cpp:502-511) and the
+// Granite-4.0-H gated group RMSNorm (granite_model.cpp:278-287).
+//
+// Fast path: one 64-wide wavefront per row (four rows per 256-thread workgroup), or one workgroup
+// of four waves per row for rows wider than 4096 halves. Each lane issues all of its 16-byte loads
+// up front and keeps the row in registers, so HBM is read exactly once and written once. Sums are
+// accumulated in double, like the reference, reduced across the wave with DPP and v_readlane (no
+// LDS; LDS only joins the partial sums of multi-wave rows). The norm scale is rounded to float
+// exactly where the reference rounds it, and the output is (x * s) * w unfused, so the result
+// matches the reference's CPU op bit for bit unless a double sum lands within an ulp of a float
+// rounding boundary.
+//
+// Fallback (any width, alignment or stride): one workgroup per row streaming the row from memory
+// once per pass.
+#include <cmath>
+
+#include "internal.h"
+
+namespace neko_hip {
+namespace {
+
+enum class Norm : int { Rms = 0, Layer = 1, Gated = 2 };
+
+struct NormArgs {
+    const void* x;  // input rows (the y operand of the gated norm)
+    int64_t xs;
+    const void* z;  // gate rows (gated norm only)
+    int64_t zs;
+    void* y;  // output rows
+    int64_t ys;
+    const float* w;  // gamma / norm weight [groups * C]
+    const float* b;  // beta (LayerNorm only)
+    int64_t rows;    // logical rows = rows * groups
+    int C;           // channels per normalised group
+    int groups;
+    float eps;
+};
+
+// Mamba2 output gate, granite_model.cpp:21: v / (1 + exp(-v)) in float.
+__device__ __forceinline__ float silu_ref(float v) { return v / (1.0f + expf(-v)); }
+
+template <Norm K, typename T>
+struct RowPtrs {
+    const T* x;
+    const T* z;
+    T* y;
+    const float* w;
+    const float* b;
+};
+
+template <Norm K, typename T>
+__device__ __forceinline__ RowPtrs<K, T> row_ptrs(const NormArgs& a, int64_t r) {
+    const int64_t t = a.groups == 1 ? r : r / a.groups;
+    const int64_t g = r - t * a.groups;
+    const int64_t off = g * a.C;
+    RowPtrs<K, T> p;
+    p.x = static_cast<const T*>(a.x) + t * a.xs + off;
+    p.z = K == Norm::Gated ? static_cast<const T*>(a.z) + t * a.zs + off : nullptr;
+    p.y = static_cast<T*>(a.y) + t * a.ys + off;
+    p.w = a.w + off;
+    p.b = a.b;
+    return p;
+}
+
+// ------------------------------------------------------------------ register-resident rows
+// W waves per row, up to CH 16-byte chunks per lane.
+template <Norm K, typename T, int W, int CH>
+__global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a) {
+    using CT = Chunk16<T>;
+    constexpr int N = CT::N;
+    typedef typename CT::V V;
+    constexpr int RPB = 4 / W;  // rows per workgroup
+    constexpr int NT = kWave * W;  // threads per row
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * RPB + wave / W;
+    const bool live = r < a.rows;
+    if constexpr (W == 1) {
+        if (!live) return;  // wave-uniform; single-wave rows meet no barrier
+    }
+    const RowPtrs<K, T> p = row_ptrs<K, T>(a, live ? r : 0);
+    const int tid = (wave % W) * kWave + lane;
+    const int nch = a.C / N;
+
+    V xv[CH], zv[CH];
+#pragma unroll
+    for (int k = 0; k < CH; k++) {
+        const int j = k * NT + tid;
+        xv[k] = V{};
+        zv[k] = V{};
+        if (j < nch) {
+            xv[k] = load_nt(reinterpret_cast<const V*>(p.x + j * N));
+            if constexpr (K == Norm::Gated) zv[k] = load_nt(reinterpret_cast<const V*>(p.z + j * N));
+        }
+    }
+    // Weights do not depend on the data: fetch them while the row is in flight.
+    float4v wv[CH][N / 4], bv[CH][N / 4];
+#pragma unroll
+    for (int k = 0; k < CH; k++) {
+        const int j = k * NT + tid;
+#pragma unroll
+        for (int q = 0; q < N / 4; q++) {
+            wv[k][q] = float4v{};
+            bv[k][q] = float4v{};
+            if (j < nch) {
+                wv[k][q] = *reinterpret_cast<const float4v*>(p.w + j * N + 4 * q);
+                if constexpr (K == Norm::Layer) bv[k][q] = *reinterpret_cast<const float4v*>(p.b + j * N + 4 * q);
+            }
+        }
+    }
+
+    // Row values in float; lanes past the row end hold zeros, which add nothing to the sums.
+    float f[CH][N];
+#pragma unroll
+    for (int k = 0; k < CH; k++) {
+#pragma unroll
+        for (int e = 0; e < N; e++) {
+            if constexpr (K == Norm::Gated) f[k][e] = to_f32(xv[k][e]) * silu_ref(to_f32(zv[k][e]));
+            else f[k][e] = to_f32(xv[k][e]);
+        }
+    }
+
+    __shared__ double part[2][4];
+    auto row_total = [&](double v, int slot) -> double {
+        v = wave_sum_f64(v);
+        if constexpr (W > 1) {
+            if (lane == 0) part[slot][wave] = v;
+            __syncthreads();
+            const int w0 = (wave / W) * W;
+            double s = part[slot][w0];
+#pragma unroll
+            for (int i = 1; i < W; i++) s += part[slot][w0 + i];
+            v = s;
+        }
+        return v;
+    };
+
+    float scale, mean_f = 0.0f;
+    if constexpr (K == Norm::Layer) {
+        double s1 = 0.0;
+#pragma unroll
+        for (int k = 0; k < CH; k++)
+#pragma unroll
+            for (int e = 0; e < N; e++) s1 += static_cast<double>(f[k][e]);
+        const double mean = row_total(s1, 0) / a.C;
+        double s2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int j = k * NT + tid;
+#pragma unroll
+            for (int e = 0; e < N; e++) {
+                const double d = static_cast<double>(f[k][e]) - mean;
+                if (j < nch) s2 += d * d;
+            }
+        }
+        const double var = row_total(s2, 1) / a.C;
+        scale = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+        mean_f = static_cast<float>(mean);
+    } else {
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < CH; k++)
+#pragma unroll
+            for (int e = 0; e < N; e++) {
+                const double d = static_cast<double>(f[k][e]);
+                ss += d * d;
+            }
+        const double tot = row_total(ss, 0);
+        scale = static_cast<float>(1.0 / sqrt(tot / a.C + static_cast<double>(a.eps)));
+    }
+    if (!live) return;
+
+#pragma unroll
+    for (int k = 0; k < CH; k++) {
+        const int j = k * NT + tid;
+        if (j >= nch) continue;
+        V out;
+#pragma unroll
+        for (int e = 0; e < N; e++) {
+            const float w = wv[k][e / 4][e % 4];
+            float v;
+            if constexpr (K == Norm::Layer) v = (f[k][e] - mean_f) * scale * w + bv[k][e / 4][e % 4];
+            else v = f[k][e] * scale * w;
+            out[e] = from_f32<T>(v);
+        }
+        store_nt(reinterpret_cast<V*>(p.y + j * N), out);
+    }
+}
+
+// ------------------------------------------------------------------ generic rows
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+    v = wave_sum_f64(v);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    const double s = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return s;
+}
+
+template <Norm K, typename T>
+__device__ __forceinline__ float gen_value(const RowPtrs<K, T>& p, int c) {
+    if constexpr (K == Norm::Gated) return to_f32(p.x[c]) * silu_ref(to_f32(p.z[c]));
+    else return to_f32(p.x[c]);
+}
+
+template <Norm K, typename T>
+__global__ __launch_bounds__(256) void norm_rows_generic(NormArgs a) {
+    __shared__ double red[4];
+    for (int64_t r = blockIdx.x; r < a.rows; r += gridDim.x) {
+        const RowPtrs<K, T> p = row_ptrs<K, T>(a, r);
+        float scale, mean_f = 0.0f;
+        if constexpr (K == Norm::Layer) {
+            double s1 = 0.0;
+            for (int c = threadIdx.x; c < a.C; c += 256) s1 += static_cast<double>(gen_value<K, T>(p, c));
+            const double mean = block_sum_f64(s1, red) / a.C;
+            double s2 = 0.0;
+            for (int c = threadIdx.x; c < a.C; c += 256) {
+                const double d = static_cast<double>(gen_value<K, T>(p, c)) - mean;
+                s2 += d * d;
+            }
+            const double var = block_sum_f64(s2, red) / a.C;
+            scale = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+            mean_f = static_cast<float>(mean);
+        } else {
+            double ss = 0.0;
+            for (int c = threadIdx.x; c < a.C; c += 256) {
+                const double d = static_cast<double>(gen_value<K, T>(p, c));
+                ss += d * d;
+            }
+            scale = static_cast<float>(1.0 / sqrt(block_sum_f64(ss, red) / a.C + static_cast<double>(a.eps)));
+        }
+        // Separate loops per pass: the output may alias the input, so every read of this row by
+        // any thread precedes the barrier inside block_sum_f64 above.
+        for (int c = threadIdx.x; c < a.C; c += 256) {
+            const float v = gen_value<K, T>(p, c);
+            float o;
+            if constexpr (K == Norm::Layer) o = (v - mean_f) * scale * p.w[c] + p.b[c];
+            else o = v * scale * p.w[c];
+            p.y[c] = from_f32<T>(o);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ dispatch
+typedef void (*NormKernel)(NormArgs);
+
+template <Norm K, typename T>
+NormKernel pick_rows_kernel(int W, int CH) {
+    if (W == 1) {
+        switch (CH) {
+            case 1: return norm_rows_kernel<K, T, 1, 1>;
+            case 2: return norm_rows_kernel<K, T, 1, 2>;
+            case 3: return norm_rows_kernel<K, T, 1, 3>;
+            case 4: return norm_rows_kernel<K, T, 1, 4>;
+            case 5: return norm_rows_kernel<K, T, 1, 5>;
+            case 6: return norm_rows_kernel<K, T, 1, 6>;
+            case 8: return norm_rows_kernel<K, T, 1, 8>;
+        }
+    } else if (W == 4) {
+        switch (CH) {
+            case 4: return norm_rows_kernel<K, T, 4, 4>;
+            case 8: return norm_rows_kernel<K, T, 4, 8>;
+        }
+    }
+    return nullptr;
+}
+
+template <Norm K>
+NormKernel pick(int dtype, int W, int CH) {
+    if (W == 0) return dtype == NEKO_DT_F16 ? norm_rows_generic<K, half_t> : norm_rows_generic<K, float>;
+    return dtype == NEKO_DT_F16 ? pick_rows_kernel<K, half_t>(W, CH) : pick_rows_kernel<K, float>(W, CH);
+}
+
+int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, const char* what) {
+    const size_t esz = dtype_size(dtype);
+    const int N = static_cast<int>(16 / esz);
+    // The register path loads 16-byte chunks of every operand row and 16-byte weight vectors.
+    bool vec = a.C % N == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.w, 16) &&
+               (a.xs * esz) % 16 == 0 && (a.ys * esz) % 16 == 0;
+    if (kind == Norm::Gated) vec = vec && aligned(a.z, 16) && (a.zs * esz) % 16 == 0;
+    if (kind == Norm::Layer) vec = vec && aligned(a.b, 16);
+    int W = 0, CH = 0;
+    if (vec) {
+        const int nch = a.C / N;
+        if (nch <= kWave * 8) {
+            W = 1;
+            CH = (nch + kWave - 1) / kWave;
+            if (CH == 7) CH = 8;
+        } else if (nch <= 4 * kWave * 8) {
+            W = 4;
+            CH = (nch + 4 * kWave - 1) / (4 * kWave) <= 4 ? 4 : 8;
+        }
+    }
+    NormKernel k = nullptr;
+    switch (kind) {
+        case Norm::Rms: k = pick<Norm::Rms>(dtype, W, CH); break;
+        case Norm::Layer: k = pick<Norm::Layer>(dtype, W, CH); break;
+        case Norm::Gated: k = pick<Norm::Gated>(dtype, W, CH); break;
+    }
+    if (!k) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: no kernel for C=%d", what, a.C);
+    int64_t blocks;
+    if (W == 1) blocks = (a.rows + 3) / 4;
+    else if (W == 4) blocks = a.rows;
+    else blocks = a.rows < 65536 ? a.rows : 65536;
+    if (blocks > 0x7fffffff) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: %lld rows exceed one launch", what, (long long)a.rows);
+    hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a);
+    return after_launch(ctx, what);
+}
+
+int check_rows(neko_hip_ctx* ctx, const char* what, int64_t rows, int64_t C, int64_t stride, const char* name) {
+    NEKO_REQUIRE(ctx, stride >= C, "%s: %s stride %lld < row width %lld", what, name, (long long)stride, (long long)C);
+    (void)rows;
+    return NEKO_OK;
+}
+
+}  // namespace
+}  // namespace neko_hip
+
+using namespace neko_hip;
+
+extern "C" {
+
+int neko_hip_layernorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y, int64_t y_stride, const float* gamma,
+                       const float* beta, int64_t rows, int64_t C, float eps, int dtype) {
+    const char* what = "neko_hip_layernorm";
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, valid_dtype(dtype), "%s: bad dtype %d", what, dtype);
+    NEKO_REQUIRE(ctx, rows >= 0 && C > 0 && C <= 0x7fffffff, "%s: bad shape rows=%lld C=%lld", what, (long long)rows,
+                 (long long)C);
+    if (rows == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, x && y && gamma && beta, "%s: null pointer", what);
+    if (int rc = check_rows(ctx, what, rows, C, x_stride, "x")) return rc;
+    if (int rc = check_rows(ctx, what, rows, C, y_stride, "y")) return rc;
+    NormArgs a{x, x_stride, nullptr, 0, y, y_stride, gamma, beta, rows, static_cast<int>(C), 1, eps};
+    return launch_norm(ctx, Norm::Layer, a, dtype, what);
+}
+
+int neko_hip_rmsnorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y, int64_t y_stride, const float* w,
+                     int64_t rows, int64_t C, float eps, int dtype) {
+    const char* what = "neko_hip_rmsnorm";
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, valid_dtype(dtype), "%s: bad dtype %d", what, dtype);
+    NEKO_REQUIRE(ctx, rows >= 0 && C > 0 && C <= 0x7fffffff, "%s: bad shape rows=%lld C=%lld", what, (long long)rows,
+                 (long long)C);
+    if (rows == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, x && y && w, "%s: null pointer", what);
+    if (int rc = check_rows(ctx, what, rows, C, x_stride, "x")) return rc;
+    if (int rc = check_rows(ctx, what, rows, C, y_stride, "y")) return rc;
+    NormArgs a{x, x_stride, nullptr, 0, y, y_stride, w, nullptr, rows, static_cast<int>(C), 1, eps};
+    return launch_norm(ctx, Norm::Rms, a, dtype, what);
+}
+
+int neko_hip_gated_rmsnorm(neko_hip_ctx* ctx, const void* y, int64_t y_stride, const void* z, int64_t z_stride, void* out,
+                           int64_t out_stride, const float* w, int64_t rows, int64_t D, int groups, float eps, int dtype) {
+    const char* what = "neko_hip_gated_rmsnorm";
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, valid_dtype(dtype), "%s: bad dtype %d", what, dtype);
+    NEKO_REQUIRE(ctx, rows >= 0 && D > 0 && D <= 0x7fffffff && groups > 0 && D % groups == 0,
+                 "%s: bad shape rows=%lld D=%lld groups=%d", what, (long long)rows, (long long)D, groups);
+    if (rows == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, y && z && out && w, "%s: null pointer", what);
+    if (int rc = check_rows(ctx, what, rows, D, y_stride, "y")) return rc;
+    if (int rc = check_rows(ctx, what, rows, D, z_stride, "z")) return rc;
+    if (int rc = check_rows(ctx, what, rows, D, out_stride, "out")) return rc;
+    NEKO_REQUIRE(ctx, rows <= INT64_MAX / groups, "%s: too many rows", what);
+    NormArgs a{y, y_stride, z, z_stride, out, out_stride, w, nullptr, rows * groups, static_cast<int>(D / groups), groups, eps};
+    return launch_norm(ctx, Norm::Gated, a, dtype, what);
+}
+
+}  // extern "C"

@@ -1,0 +1,168 @@
+// C ABI: contexts, streams, memory and error reporting (the ComputeBackend buffer / submission
+// contract, gpu/compute.h:28-44, expressed as plain C over one in-order HIP stream per context).
+#include <cstdio>
+#include <cstring>
+
+#include "internal.h"
+
+namespace {
+thread_local std::string g_create_error = "no error";
+}
+
+namespace neko_hip {
+
+int fail(neko_hip_ctx* ctx, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    else g_create_error = buf;
+    return code;
+}
+
+int check(neko_hip_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return NEKO_OK;
+    return fail(ctx, NEKO_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int enter(neko_hip_ctx* ctx) {
+    if (!ctx) return fail(nullptr, NEKO_ERR_INVALID, "null context");
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess || cur != ctx->device) return check(ctx, hipSetDevice(ctx->device), "hipSetDevice");
+    return NEKO_OK;
+}
+
+int after_launch(neko_hip_ctx* ctx, const char* what) { return check(ctx, hipGetLastError(), what); }
+
+FastDiv make_fast_div(uint32_t d) {
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) s++;
+    const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+    return FastDiv{d, static_cast<uint32_t>(m), s};
+}
+
+}  // namespace neko_hip
+
+using namespace neko_hip;
+
+extern "C" {
+
+int neko_hip_create(int device, neko_hip_ctx** out) {
+    if (!out) return fail(nullptr, NEKO_ERR_INVALID, "neko_hip_create: null output pointer");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return fail(nullptr, NEKO_ERR_NO_DEVICE, "neko_hip_create: no HIP device is visible");
+    }
+    if (device < 0 || device >= n)
+        return fail(nullptr, NEKO_ERR_INVALID, "neko_hip_create: device %d out of range (%d visible)", device, n);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail(nullptr, NEKO_ERR_HIP, "neko_hip_create: hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, NEKO_ERR_NO_DEVICE, "neko_hip_create: device %d is %s; this build targets gfx950", device,
+                    prop.gcnArchName);
+    if (hipSetDevice(device) != hipSuccess) return fail(nullptr, NEKO_ERR_HIP, "neko_hip_create: hipSetDevice failed");
+    auto* ctx = new neko_hip_ctx;
+    ctx->device = device;
+    ctx->cu_count = prop.multiProcessorCount;
+    ctx->max_alloc = prop.totalGlobalMem;
+    ctx->name = prop.name;
+    // A blocking stream: ordered with the device's null stream, so work a caller queued there (e.g. a
+    // framework's default stream) is never overtaken.
+    if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamDefault) != hipSuccess) {
+        delete ctx;
+        return fail(nullptr, NEKO_ERR_HIP, "neko_hip_create: hipStreamCreate failed");
+    }
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return NEKO_OK;
+}
+
+int neko_hip_destroy(neko_hip_ctx* ctx) {
+    if (!ctx) return NEKO_OK;
+    int rc = enter(ctx);
+    if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    for (void* p : ctx->allocs) (void)hipFree(p);
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return rc;
+}
+
+const char* neko_hip_last_error(const neko_hip_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_error.c_str(); }
+
+int neko_hip_device_name(neko_hip_ctx* ctx, char* buf, size_t buf_bytes) {
+    NEKO_REQUIRE(ctx, ctx && buf && buf_bytes > 0, "neko_hip_device_name: null argument");
+    std::snprintf(buf, buf_bytes, "%s", ctx->name.c_str());
+    return NEKO_OK;
+}
+
+size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx) { return ctx ? ctx->max_alloc : 0; }
+
+int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream) {
+    NEKO_ENTER(ctx);
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return NEKO_OK;
+}
+
+void* neko_hip_get_stream(const neko_hip_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+int neko_hip_alloc(neko_hip_ctx* ctx, size_t bytes, void** dev_ptr) {
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, dev_ptr != nullptr, "neko_hip_alloc: null output pointer");
+    *dev_ptr = nullptr;
+    void* p = nullptr;
+    const int rc = check(ctx, hipMalloc(&p, bytes ? bytes : 16), "hipMalloc");
+    if (rc != NEKO_OK) return rc;
+    ctx->allocs.insert(p);
+    *dev_ptr = p;
+    return NEKO_OK;
+}
+
+int neko_hip_free(neko_hip_ctx* ctx, void* dev_ptr) {
+    NEKO_ENTER(ctx);
+    if (!dev_ptr) return NEKO_OK;
+    NEKO_REQUIRE(ctx, ctx->allocs.count(dev_ptr) == 1, "neko_hip_free: %p was not allocated by this context", dev_ptr);
+    // Work queued on the stream may still use the buffer.
+    int rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (rc != NEKO_OK) return rc;
+    ctx->allocs.erase(dev_ptr);
+    return check(ctx, hipFree(dev_ptr), "hipFree");
+}
+
+int neko_hip_upload(neko_hip_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes) {
+    NEKO_ENTER(ctx);
+    if (bytes == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, dst_dev && src_host, "neko_hip_upload: null pointer");
+    int rc = check(ctx, hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync H2D");
+    if (rc != NEKO_OK) return rc;
+    // The source is pageable host memory the caller may reuse as soon as this returns.
+    return check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+int neko_hip_download(neko_hip_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes) {
+    NEKO_ENTER(ctx);
+    if (bytes == 0) return check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    NEKO_REQUIRE(ctx, dst_host && src_dev, "neko_hip_download: null pointer");
+    int rc = check(ctx, hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync D2H");
+    if (rc != NEKO_OK) return rc;
+    return check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+int neko_hip_memset(neko_hip_ctx* ctx, void* dst_dev, int value, size_t bytes) {
+    NEKO_ENTER(ctx);
+    if (bytes == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, dst_dev != nullptr, "neko_hip_memset: null pointer");
+    return check(ctx, hipMemsetAsync(dst_dev, value, bytes, ctx->stream), "hipMemsetAsync");
+}
+
+int neko_hip_synchronize(neko_hip_ctx* ctx) {
+    NEKO_ENTER(ctx);
+    return check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+}  // extern "C"

@@ -1,0 +1,265 @@
+// Port of the reference's GPU backend self-test (gpu/compute.cpp:32-290) for the kernels the HIP
+// backend implements, driven through neko::gpu::ComputeBackend::dispatch with the reference's own
+// parameter blocks. The CPU side is the oracle (oracle/neko_oracle.c), standing where the reference
+// calls its cpu:: ops. Same inputs scheme (std::mt19937(1234), uniform(-1, 1), f16-rounded weights),
+// same shapes and the reference's tolerance test |gpu - cpu| <= tol * (1 + |cpu|); the gather cases
+// additionally require bit equality.
+//
+// Built into tests/cpp/_build/libbackend_selftest.so and called from tests/test_gpu_backend.py.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../nekochat_amd/csrc/compute.h"
+#include "../../oracle/neko_oracle.h"
+
+using namespace neko;
+using namespace neko::gpu;
+
+namespace {
+
+struct Failure {
+    std::string msg;
+};
+
+void closeOrFail(const std::vector<float>& gpu, const std::vector<float>& cpu, float tol, const char* what, bool exact) {
+    for (size_t i = 0; i < gpu.size(); i++) {
+        const float d = std::fabs(gpu[i] - cpu[i]);
+        const bool bitsEqual = std::memcmp(&gpu[i], &cpu[i], 4) == 0;
+        if (!(d <= tol * (1.0f + std::fabs(cpu[i]))) || (exact && !bitsEqual)) {
+            char buf[256];
+            std::snprintf(buf, sizeof buf, "self-test %s mismatch at %zu: gpu %.9g cpu %.9g%s", what, i, gpu[i], cpu[i],
+                          exact ? " (bit-exact required)" : "");
+            throw Failure{buf};
+        }
+    }
+}
+
+struct Harness {
+    ComputeBackend& be;
+    std::mt19937 rng{1234};
+    std::uniform_real_distribution<float> u{-1.0f, 1.0f};
+
+    std::vector<float> rnd(size_t n) {
+        std::vector<float> v(n);
+        for (auto& x : v) x = u(rng);
+        return v;
+    }
+    // Rounds v to f16 in place and returns the bits.
+    static std::vector<uint16_t> halves(std::vector<float>& v) {
+        std::vector<uint16_t> h(v.size());
+        for (size_t i = 0; i < v.size(); i++) {
+            h[i] = oracle_f32_to_f16(v[i]);
+            v[i] = oracle_f16_to_f32(h[i]);
+        }
+        return h;
+    }
+    void run(Kernel k, std::initializer_list<Buffer*> b, std::initializer_list<int32_t> p, uint32_t gx, uint32_t gy) {
+        Buffer* binds[4] = {};
+        int32_t params[8] = {};
+        std::copy(b.begin(), b.end(), binds);
+        std::copy(p.begin(), p.end(), params);
+        be.dispatch(k, binds, params, gx, gy);
+    }
+    std::vector<float> read(Buffer* b, size_t n) {
+        std::vector<float> v(n);
+        be.download(b, 0, v.data(), n * 4);
+        return v;
+    }
+
+    void embed() {  // compute.cpp:106-132
+        const int EV = 10, EC = 64, EP = 4, ET = 3, epos = 1, split = 6;
+        auto wte = rnd(size_t(EV * EC)), wpe = rnd(size_t(EP * EC));
+        auto hte = halves(wte), hpe = halves(wpe);
+        int32_t toks[ET] = {3, 7, 9};
+        std::vector<float> ref(size_t(ET * EC)), refNoPos(size_t(ET * EC));
+        for (int t = 0; t < ET; t++)
+            for (int c = 0; c < EC; c++) {
+                refNoPos[size_t(t * EC + c)] = wte[size_t(toks[t] * EC + c)];
+                ref[size_t(t * EC + c)] = wte[size_t(toks[t] * EC + c)] + wpe[size_t((epos + t) * EC + c)];
+            }
+        Buffer* bt = be.create(sizeof toks, toks);
+        Buffer* out = be.create(ref.size() * 4, nullptr, true);
+        be.begin();
+        run(Kernel::Embed, {bt, be.create(hte.size() * 2, hte.data()), be.create(hpe.size() * 2, hpe.data()), out},
+            {ET, EC, epos, 1, 0, EV}, 1, ET);
+        be.submitAndWait();
+        closeOrFail(read(out, ref.size()), ref, 1e-5f, "embed", true);
+        Buffer* c0 = be.create(size_t(split * EC) * 2, hte.data());
+        Buffer* c1 = be.create(size_t((EV - split) * EC) * 2, hte.data() + split * EC);
+        be.begin();
+        run(Kernel::Embed, {bt, c0, nullptr, out}, {ET, EC, 0, 0, 0, split}, 1, ET);
+        run(Kernel::Embed, {bt, c1, nullptr, out}, {ET, EC, 0, 0, split, EV - split}, 1, ET);
+        be.submitAndWait();
+        closeOrFail(read(out, ref.size()), refNoPos, 1e-5f, "embed-chunked", true);
+    }
+
+    void norms() {  // compute.cpp:134-154
+        const int C = 96, R = 3;
+        auto lx = rnd(size_t(C * R)), g = rnd(size_t(C)), b = rnd(size_t(C));
+        for (auto& v : lx) v *= 20.0f;
+        std::vector<float> lref(lx.size()), rref(lx.size());
+        oracle_layernorm(lx.data(), lref.data(), g.data(), b.data(), R, C, 1e-5f);
+        oracle_rmsnorm(lx.data(), rref.data(), g.data(), R, C, 1e-6f);
+        Buffer* blx = be.create(lx.size() * 4, lx.data());
+        Buffer* bg = be.create(g.size() * 4, g.data());
+        Buffer* bbb = be.create(b.size() * 4, b.data());
+        Buffer* bly = be.create(lx.size() * 4, nullptr, true);
+        be.begin();
+        run(Kernel::LayerNorm, {blx, bly, bg, bbb}, {C, floatBits(1e-5f), 0, 0}, R, 1);
+        be.submitAndWait();
+        closeOrFail(read(bly, lx.size()), lref, 1e-3f, "layernorm", false);
+        be.begin();
+        run(Kernel::LayerNorm, {blx, bly, bg, nullptr}, {C, floatBits(1e-6f), 0, 1}, R, 1);
+        be.submitAndWait();
+        closeOrFail(read(bly, lx.size()), rref, 1e-3f, "rmsnorm", false);
+        // rowOffset: the final-norm form, one row normalised from row R - 1 (gpt2_model.cpp:274).
+        Buffer* one = be.create(size_t(C) * 4, nullptr, true);
+        be.begin();
+        run(Kernel::LayerNorm, {blx, one, bg, bbb}, {C, floatBits(1e-5f), R - 1, 0}, 1, 1);
+        be.submitAndWait();
+        std::vector<float> last(lref.end() - C, lref.end());
+        closeOrFail(read(one, size_t(C)), last, 1e-3f, "layernorm-rowOffset", false);
+        // Chained dispatches in one submission (layernorm -> gelu reading its output, compute.cpp:156-176).
+        Buffer* bgl = be.create(lx.size() * 4, nullptr, true);
+        be.begin();
+        run(Kernel::LayerNorm, {blx, bly, bg, bbb}, {C, floatBits(1e-5f), 0, 0}, R, 1);
+        run(Kernel::Gelu, {bly, bgl}, {C * R}, uint32_t((C * R + 63) / 64), 1);
+        be.submitAndWait();
+        std::vector<float> gref(lref.size());
+        for (size_t i = 0; i < gref.size(); i++) gref[i] = oracle_gelu(lref[i]);
+        closeOrFail(read(bgl, gref.size()), gref, 1e-3f, "chained layernorm->gelu", false);
+    }
+
+    void rope() {  // compute.cpp:178-202
+        const int H = 2, KV = 1, hd = 64, T = 2, pos0 = 3, stride = (H + 2 * KV) * hd;
+        auto qkv = rnd(size_t(T * stride)), wn = rnd(size_t(2 * hd));
+        std::vector<float> cs(size_t((pos0 + T) * hd));
+        for (int p = 0; p < pos0 + T; p++)
+            for (int i = 0; i < hd / 2; i++) {
+                double a = p * std::pow(10000.0, -2.0 * i / hd);
+                cs[size_t(p * hd + 2 * i)] = float(std::cos(a));
+                cs[size_t(p * hd + 2 * i + 1)] = float(std::sin(a));
+            }
+        std::vector<float> ref = qkv;
+        for (int t = 0; t < T; t++) {
+            float* r = ref.data() + t * stride;
+            oracle_rmsnorm(r, r, wn.data(), H, hd, 1e-6f);
+            oracle_rmsnorm(r + H * hd, r + H * hd, wn.data() + hd, KV, hd, 1e-6f);
+            oracle_rope(r, H + KV, hd, cs.data() + (pos0 + t) * hd);
+        }
+        Buffer* bq = be.create(qkv.size() * 4, qkv.data(), true);
+        be.begin();
+        run(Kernel::Rope, {bq, be.create(wn.size() * 4, wn.data()), be.create(cs.size() * 4, cs.data())},
+            {stride, H, hd, pos0, floatBits(1e-6f), 1}, H + KV, T);
+        be.submitAndWait();
+        closeOrFail(read(bq, ref.size()), ref, 1e-3f, "rope", false);
+    }
+
+    void siluMul() {  // compute.cpp:204-216
+        const int T = 2, I = 100;
+        auto h = rnd(size_t(T * 2 * I));
+        for (auto& v : h) v *= 6.0f;
+        std::vector<float> ref(size_t(T * I));
+        oracle_silu_mul(h.data(), ref.data(), T, I);
+        Buffer* bo = be.create(ref.size() * 4, nullptr, true);
+        be.begin();
+        run(Kernel::SiluMul, {be.create(h.size() * 4, h.data()), bo}, {T, I}, uint32_t((I + 63) / 64), T);
+        be.submitAndWait();
+        closeOrFail(read(bo, ref.size()), ref, 1e-4f, "silu_mul", false);
+    }
+
+    void quantEmbed() {  // compute.cpp:245-260
+        for (int fmt : {ORACLE_FMT_FP8, ORACLE_FMT_FP4}) {
+            const int EV = 10, EC = 64, ET = 3;
+            auto table = rnd(size_t(EV * EC));
+            const size_t rb = oracle_quant_row_bytes(fmt, EC);
+            std::vector<uint8_t> q(rb * EV);
+            oracle_quantize_rows(fmt, EV, EC, table.data(), q.data());
+            int32_t toks[ET] = {3, 7, 9};
+            std::vector<float> ref(size_t(ET * EC));
+            for (int t = 0; t < ET; t++) oracle_dequantize_row(fmt, EC, q.data() + rb * size_t(toks[t]), ref.data() + t * EC);
+            Buffer* out = be.create(ref.size() * 4, nullptr, true);
+            be.begin();
+            run(Kernel::Embed, {be.create(sizeof toks, toks), be.create(q.size(), q.data()), nullptr, out},
+                {ET, EC, 0, fmt == ORACLE_FMT_FP8 ? 2 : 4, 0, EV, int(rb / 4)}, 1, ET);
+            be.submitAndWait();
+            closeOrFail(read(out, ref.size()), ref, 1e-5f, fmt == ORACLE_FMT_FP8 ? "embed-FP8" : "embed-FP4", true);
+        }
+    }
+
+    void gatedNorm() {  // granite_model.cpp:278-287 through the GatedRmsNorm extension
+        const int T = 3, D = 128, groups = 2, zStride = 200;
+        auto y = rnd(size_t(T * D)), z = rnd(size_t(T * zStride)), w = rnd(size_t(D));
+        for (auto& v : z) v *= 4.0f;
+        std::vector<float> ref = y;
+        oracle_gated_rmsnorm(ref.data(), z.data(), zStride, w.data(), T, D, groups, 1e-5f);
+        Buffer* by = be.create(y.size() * 4, y.data(), true);
+        be.begin();
+        run(Kernel::GatedRmsNorm, {by, be.create(z.size() * 4, z.data()), be.create(w.size() * 4, w.data())},
+            {D, floatBits(1e-5f), groups, zStride}, T, 1);
+        be.submitAndWait();
+        closeOrFail(read(by, ref.size()), ref, 1e-3f, "gated-rmsnorm", false);
+    }
+
+    void unsupported() {  // dense kernels are outside the HIP backend and must throw, not run
+        Buffer* b = be.create(64);
+        try {
+            run(Kernel::Matmul, {b, b, nullptr, b}, {4, 4, 1, 0}, 4, 1);
+        } catch (const NekoError&) {
+            return;
+        }
+        throw Failure{"Matmul dispatch did not throw"};
+    }
+
+    void outOfRange() {  // a dispatch reading past a buffer throws instead of faulting
+        Buffer* small = be.create(16);
+        Buffer* g = be.create(96 * 4);
+        try {
+            run(Kernel::LayerNorm, {small, small, g, g}, {96, floatBits(1e-5f), 0, 0}, 3, 1);
+        } catch (const NekoError&) {
+            return;
+        }
+        throw Failure{"out-of-range LayerNorm dispatch did not throw"};
+    }
+};
+
+}  // namespace
+
+extern "C" int backend_selftest(char* err, int err_bytes) {
+    std::string error;
+    std::unique_ptr<ComputeBackend> be = createHip(error);
+    if (!be) {
+        std::snprintf(err, size_t(err_bytes), "createHip: %s", error.c_str());
+        return 2;
+    }
+    try {
+        Harness h{*be};
+        h.embed();
+        h.norms();
+        h.rope();
+        h.siluMul();
+        h.quantEmbed();
+        h.gatedNorm();
+        h.unsupported();
+        h.outOfRange();
+        std::snprintf(err, size_t(err_bytes), "ok on %s (%s)", be->deviceName().c_str(), be->name());
+        return 0;
+    } catch (const Failure& f) {
+        std::snprintf(err, size_t(err_bytes), "%s", f.msg.c_str());
+    } catch (const std::exception& e) {
+        std::snprintf(err, size_t(err_bytes), "self-test failed: %s", e.what());
+    }
+    return 1;
+}
+
+// createHip with no usable device returns null and an error string (factory convention) — runs on CPU.
+extern "C" int backend_create_without_device(char* err, int err_bytes) {
+    std::string error;
+    std::unique_ptr<ComputeBackend> be = createHip(error);
+    std::snprintf(err, size_t(err_bytes), "%s", error.c_str());
+    return be ? 1 : 0;
+}

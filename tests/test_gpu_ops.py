@@ -1,0 +1,424 @@
+"""GPU parity of every hot-path op against the oracle, through the C ABI (nekochat_amd.ops).
+
+Bars: embedding gather / dequant bit-exact; norms, activations and RoPE within 2 fp16 ulp of the
+oracle (in practice almost every output is bit-identical: the kernels accumulate in double and round
+where the reference rounds). Configured shapes run at full size; edge cases cover empty inputs, odd
+widths (fallback kernels), strided rows, in-place calls, f32 activations and out-of-range positions.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_f16_close, to_bits
+from nekochat_amd import NekoError, ops
+from nekochat_amd import workloads as wl
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _f16(shape, stream, dev, mean=0.0, std=1.0):
+    return wl.normal_f16(shape, mean, std, stream, dev)
+
+
+def _w(n, stream, dev, mean=1.0, std=0.05):
+    return wl.weight_f32(n, mean, std, stream, dev)
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+@pytest.mark.parametrize("T,C,eps", [
+    (64, 1024, 1e-6),      # Qwen3-0.6B decode
+    (8192, 2560, 1e-6),    # Qwen3-4B prefill
+    (16384, 1536, 1e-5),   # Granite pre-norm
+    (3, 96, 1e-6),         # reference self-test width
+    (5, 4104, 1e-6),       # four waves per row
+    (7, 100, 1e-6),        # width not a multiple of 8: fallback kernel
+    (2, 20000, 1e-6),      # wider than the register path
+    (1, 8, 1e-6),
+])
+def test_rmsnorm_f16(dev, T, C, eps):
+    _case(f"rmsnorm f16 T={T} C={C}")
+    x = _f16((T, C), 1, dev)
+    w = _w(C, 2, dev)
+    y = ops.rms_norm(x, w, eps)
+    want = O.rmsnorm_f16(to_bits(x), w.cpu().numpy(), eps)
+    d = assert_f16_close(to_bits(y), want, what=f"rmsnorm {T}x{C}")
+    assert np.count_nonzero(d) <= max(2, d.size // 10000), "more outputs off the reference than double accumulation allows"
+
+
+def test_rmsnorm_strided_inplace_and_edges(dev):
+    _case("rmsnorm strided / in place / empty / zero rows")
+    T, C, S = 33, 1024, 1536
+    buf = _f16((T, S), 3, dev)
+    buf[5].zero_()  # zero row: scale = 1/sqrt(eps)
+    buf[6].fill_(0.5)  # constant row
+    x = buf[:, :C]
+    w = _w(C, 4, dev)
+    want = O.rmsnorm_f16(to_bits(x), w.cpu().numpy(), 1e-6)
+    tail = to_bits(buf[:, C:]).copy()
+    ops.rms_norm(x, w, 1e-6, out=x)  # in place on a strided view
+    assert_f16_close(to_bits(x), want, what="rmsnorm in place strided")
+    assert np.array_equal(to_bits(buf[:, C:]), tail), "columns past C were written"
+    empty = torch.empty((0, C), dtype=torch.float16, device=dev)
+    assert ops.rms_norm(empty, w, 1e-6).shape == (0, C)
+
+
+def test_rmsnorm_f32(dev):
+    _case("rmsnorm f32")
+    T, C = 17, 2560
+    x = _f16((T, C), 5, dev).float() * 20
+    w = _w(C, 6, dev)
+    y = ops.rms_norm(x, w, 1e-6)
+    want = np.empty((T, C), np.float32)
+    O.lib().oracle_rmsnorm(O._ptr(x.cpu().numpy()), O._ptr(want), O._ptr(w.cpu().numpy()), T, C, 1e-6)
+    np.testing.assert_allclose(y.cpu().numpy(), want, rtol=2e-7, atol=0)
+
+
+# ------------------------------------------------------------------ LayerNorm
+
+@pytest.mark.parametrize("T,C,shift", [(128, 768, 0.0), (64, 1024, 100.0), (3, 96, 0.0), (9, 770, 3.0), (4, 2560, 0.0)])
+def test_layernorm_f16(dev, T, C, shift):
+    _case(f"layernorm f16 T={T} C={C} shift={shift}")
+    x = _f16((T, C), 7, dev, mean=shift)
+    g = _w(C, 8, dev, 1.0, 0.02)
+    b = _w(C, 9, dev, 0.0, 0.02)
+    y = ops.layer_norm(x, g, b, 1e-5)
+    want = O.layernorm_f16(to_bits(x), g.cpu().numpy(), b.cpu().numpy(), 1e-5)
+    assert_f16_close(to_bits(y), want, what=f"layernorm {T}x{C}")
+
+
+def test_layernorm_constant_row(dev):
+    _case("layernorm constant rows")
+    x = torch.full((4, 768), 1.5, dtype=torch.float16, device=dev)
+    g = _w(768, 10, dev)
+    b = _w(768, 11, dev, 0.0, 0.02)
+    y = ops.layer_norm(x, g, b, 1e-5)
+    want = O.layernorm_f16(to_bits(x), g.cpu().numpy(), b.cpu().numpy(), 1e-5)
+    assert np.array_equal(to_bits(y), want)
+
+
+def test_layernorm_f32(dev):
+    _case("layernorm f32")
+    T, C = 3, 96
+    x = _f16((T, C), 12, dev).float() * 20
+    g, b = _w(C, 13, dev), _w(C, 14, dev, 0.0, 0.1)
+    y = ops.layer_norm(x, g, b, 1e-5)
+    want = np.empty((T, C), np.float32)
+    O.lib().oracle_layernorm(O._ptr(x.cpu().numpy()), O._ptr(want), O._ptr(g.cpu().numpy()), O._ptr(b.cpu().numpy()),
+                             T, C, 1e-5)
+    np.testing.assert_allclose(y.cpu().numpy(), want, rtol=2e-7, atol=1e-7)
+
+
+# ------------------------------------------------------------------ gated RMSNorm
+
+@pytest.mark.parametrize("T,D,groups,zpad", [(16384, 3072, 1, 0), (64, 3072, 1, 640), (37, 1024, 4, 8), (5, 300, 3, 0)])
+def test_gated_rmsnorm_f16(dev, T, D, groups, zpad):
+    _case(f"gated rmsnorm T={T} D={D} groups={groups} zpad={zpad}")
+    y = _f16((T, D), 15, dev)
+    zfull = _f16((T, D + zpad), 16, dev)
+    z = zfull[:, :D]
+    w = _w(D, 17, dev)
+    out = ops.gated_rms_norm(y, z, w, groups, 1e-5)
+    want = O.gated_rmsnorm_f16(to_bits(y), to_bits(z), w.cpu().numpy(), groups, 1e-5)
+    assert_f16_close(to_bits(out), want, what=f"gated {T}x{D}/{groups}")
+
+
+def test_gated_rmsnorm_inplace(dev):
+    _case("gated rmsnorm in place")
+    y = _f16((100, 3072), 18, dev)
+    z = _f16((100, 3072), 19, dev)
+    w = _w(3072, 20, dev)
+    want = O.gated_rmsnorm_f16(to_bits(y), to_bits(z), w.cpu().numpy(), 1, 1e-5)
+    ops.gated_rms_norm(y, z, w, 1, 1e-5, out=y)
+    assert_f16_close(to_bits(y), want, what="gated in place")
+
+
+# ------------------------------------------------------------------ q/k norm + RoPE
+
+def _qk_case(dev, T, n_q, n_kv, hd, n_pos, positions, norm, theta=1e6, stream=21, dtype=torch.float16):
+    stride = (n_q + 2 * n_kv) * hd
+    qkv = _f16((T, stride), stream, dev)
+    if dtype == torch.float32:
+        qkv = qkv.float()
+    wqk = _w(2 * hd, stream + 1, dev) if norm else None
+    cs = ops.rope_table(theta, hd, n_pos)
+    before = qkv.cpu().numpy().copy()
+    pos_t = None if positions is None else torch.from_numpy(positions).to(dev)
+    ops.qk_norm_rope(qkv, n_q, n_kv, hd, torch.from_numpy(cs).to(dev), 1e-6, wqk=wqk, positions=pos_t)
+    w_np = None if wqk is None else wqk.cpu().numpy()
+    if dtype == torch.float16:
+        want = O.qk_norm_rope_f16(before.view(np.uint16), n_q, n_kv, hd, cs, n_pos, 1e-6, wqk=w_np, positions=positions)
+        got = to_bits(qkv)
+        assert_f16_close(got, want, what=f"qk rope T={T} heads={n_q}+{n_kv} hd={hd}")
+        # V heads are neither read nor written.
+        v0 = (n_q + n_kv) * hd
+        assert np.array_equal(got[:, v0:], before.view(np.uint16)[:, v0:])
+    else:
+        want = O.qk_norm_rope_f32(before, n_q, n_kv, hd, cs, n_pos, 1e-6, wqk=w_np, positions=positions)
+        np.testing.assert_allclose(qkv.cpu().numpy(), want, rtol=1e-6, atol=1e-6)
+
+
+def test_qk_rope_decode(dev):
+    _case("qk rope Qwen3-0.6B decode, random positions")
+    cfg = wl.QWEN3_DECODE
+    pos = wl.uniform_ids(cfg.T, cfg.n_pos, 7)
+    _qk_case(dev, cfg.T, cfg.n_q, cfg.n_kv, cfg.hd, cfg.n_pos, pos, True)
+
+
+def test_qk_rope_prefill(dev):
+    _case("qk rope Qwen3-4B prefill")
+    cfg = wl.QWEN3_PREFILL
+    pos = (np.arange(cfg.T) % cfg.seq).astype(np.int32)
+    _qk_case(dev, cfg.T, cfg.n_q, cfg.n_kv, cfg.hd, cfg.seq, pos, True)
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,norm,dtype", [
+    (16, 8, 128, False, torch.float16),  # rotation only (rope.comp flags 0)
+    (2, 1, 64, True, torch.float16),
+    (3, 1, 96, True, torch.float16),     # hd/2 not a power-of-two lane count: fallback kernel
+    (4, 2, 256, True, torch.float16),
+    (2, 1, 64, True, torch.float32),
+    (8, 2, 128, True, torch.float32),
+])
+def test_qk_rope_shapes(dev, n_q, n_kv, hd, norm, dtype):
+    _case(f"qk rope n_q={n_q} n_kv={n_kv} hd={hd} norm={norm} {dtype}")
+    pos = wl.uniform_ids(37, 512, 22)
+    _qk_case(dev, 37, n_q, n_kv, hd, 512, pos, norm, theta=1e4, dtype=dtype)
+
+
+def test_qk_rope_pos0_and_out_of_range(dev):
+    _case("qk rope pos0 form and out-of-range positions")
+    # pos0 + row (the reference's GPU ABI)
+    T, n_q, n_kv, hd = 6, 4, 2, 128
+    stride = (n_q + 2 * n_kv) * hd
+    qkv = _f16((T, stride), 23, dev)
+    cs = ops.rope_table(1e6, hd, 16)
+    before = to_bits(qkv).copy()
+    ops.qk_norm_rope(qkv, n_q, n_kv, hd, torch.from_numpy(cs).to(dev), 1e-6, pos0=3)
+    want = O.qk_norm_rope_f16(before, n_q, n_kv, hd, cs, 16, 1e-6, pos0=3)
+    assert_f16_close(to_bits(qkv), want, what="qk rope pos0")
+    # rows whose position falls outside the table stay untouched
+    qkv = _f16((T, stride), 24, dev)
+    before = to_bits(qkv).copy()
+    pos = np.array([0, -1, 15, 16, 1 << 30, 2], np.int32)
+    ops.qk_norm_rope(qkv, n_q, n_kv, hd, torch.from_numpy(cs).to(dev), 1e-6, positions=torch.from_numpy(pos).to(dev))
+    got = to_bits(qkv)
+    for r in (1, 3, 4):
+        assert np.array_equal(got[r], before[r])
+    want = O.qk_norm_rope_f16(before, n_q, n_kv, hd, cs, 16, 1e-6, positions=pos)
+    assert_f16_close(got, want, what="qk rope out of range")
+
+
+def test_qk_rope_position_zero_is_norm_only(dev):
+    _case("qk rope position 0 = identity rotation")
+    T, n_q, n_kv, hd = 4, 2, 1, 128
+    qkv = _f16((T, (n_q + 2 * n_kv) * hd), 25, dev)
+    wqk = _w(2 * hd, 26, dev)
+    x = qkv.clone()
+    cs = torch.from_numpy(ops.rope_table(1e6, hd, 8)).to(dev)
+    ops.qk_norm_rope(qkv, n_q, n_kv, hd, cs, 1e-6, wqk=wqk, positions=torch.zeros(T, dtype=torch.int32, device=dev))
+    heads = x[:, :(n_q + n_kv) * hd].reshape(T * (n_q + n_kv), hd)
+    wq = torch.cat([wqk[:hd].repeat(n_q, 1), wqk[hd:].repeat(n_kv, 1)]).repeat(T, 1)
+    normed = torch.empty_like(heads)
+    for i in range(heads.shape[0]):
+        normed[i] = ops.rms_norm(heads[i:i + 1], wq[i].contiguous(), 1e-6)[0]
+    got = to_bits(qkv[:, :(n_q + n_kv) * hd]).reshape(-1, hd)
+    assert np.array_equal(got, to_bits(normed))
+
+
+# ------------------------------------------------------------------ SwiGLU / GELU
+
+@pytest.mark.parametrize("T,I", [(64, 3072), (8192, 9728), (16384, 4096), (2, 100), (3, 7)])
+def test_swiglu_f16(dev, T, I):
+    _case(f"swiglu T={T} I={I}")
+    h = _f16((T, 2 * I), 27, dev)
+    got = ops.silu_mul(h)
+    want = O.swiglu_f16(to_bits(h))
+    d = assert_f16_close(to_bits(got), want, what=f"swiglu {T}x{I}")
+    assert np.count_nonzero(d > 1) == 0
+
+
+def test_swiglu_all_gates(dev):
+    _case("swiglu every fp16 gate value")
+    gates = np.arange(65536, dtype=np.uint16)
+    ups = np.array([0x3C00, 0xBC00, 0x3555, 0x7BFF, 0x0001, 0x4900], np.uint16)  # 1, -1, 1/3, max, min sub, 10
+    h = np.empty((len(ups), 2 * 65536), np.uint16)
+    h[:, :65536] = gates
+    h[:, 65536:] = ups[:, None]
+    ht = torch.from_numpy(h.view(np.float16)).to(dev)
+    got = to_bits(ops.silu_mul(ht))
+    want = O.swiglu_f16(h)
+    assert_f16_close(got, want, max_ulp=1, what="swiglu all gates")
+
+
+def test_swiglu_strided_f32(dev):
+    _case("swiglu strided and f32")
+    T, I = 9, 1000
+    buf = _f16((T, 2 * I + 16), 28, dev)
+    h = buf[:, :2 * I]
+    out = torch.zeros((T, I + 8), dtype=torch.float16, device=dev)
+    ops.silu_mul(h, out=out[:, :I])
+    assert_f16_close(to_bits(out[:, :I]), O.swiglu_f16(to_bits(h)), what="swiglu strided")
+    assert torch.count_nonzero(out[:, I:]) == 0
+    hf = h.float() * 6
+    want = np.empty((T, I), np.float32)
+    O.lib().oracle_silu_mul(O._ptr(hf.cpu().numpy()), O._ptr(want), T, I)
+    np.testing.assert_allclose(ops.silu_mul(hf).cpu().numpy(), want, rtol=4e-7, atol=1e-30)
+
+
+def test_gelu_all_halves(dev):
+    _case("gelu every fp16 value")
+    x = np.arange(65536, dtype=np.uint16)
+    got = to_bits(ops.gelu(torch.from_numpy(x.view(np.float16)).to(dev)))
+    assert_f16_close(got, O.gelu_f16(x), what="gelu all halves")
+
+
+@pytest.mark.parametrize("n", [128 * 3072, 1, 7, 4099])
+def test_gelu_sizes(dev, n):
+    _case(f"gelu n={n}")
+    x = _f16((n,), 29, dev)
+    assert_f16_close(to_bits(ops.gelu(x)), O.gelu_f16(to_bits(x)), what=f"gelu n={n}")
+
+
+def test_gelu_f32_inplace(dev):
+    _case("gelu f32 in place")
+    x = _f16((1000,), 30, dev).float() * 4
+    want = np.array([O.lib().oracle_gelu(float(v)) for v in x.cpu().numpy()], np.float32)
+    ops.gelu(x, out=x)
+    np.testing.assert_allclose(x.cpu().numpy(), want, rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------ embedding gather
+
+def _table(fmt, rows, C, stream):
+    x = wl.normal_f16((rows, C), 0.0, 0.02, stream, "cpu").float().numpy()
+    table, used = ops.quantize_rows(fmt, x)
+    assert used == fmt
+    return table
+
+
+@pytest.mark.parametrize("fmt", [ops.FMT_F16, ops.FMT_FP8, ops.FMT_FP4])
+def test_embed_quant_gather_full(dev, fmt):
+    """Qwen3-1.7B-shaped tied table, 16384 Zipf ids: bit-exact."""
+    cfg = wl.QUANT_GATHER
+    _case(f"embed gather fmt={fmt} {cfg.vocab}x{cfg.C}")
+    x = wl.normal_f16((cfg.vocab, cfg.C), 0.0, 0.02, 31, dev).float().cpu().numpy()
+    table, _ = ops.quantize_rows(fmt, x)
+    ids = wl.zipf_ids(cfg.T, cfg.vocab, cfg.s, 32)
+    got = ops.embed(torch.from_numpy(ids).to(dev), torch.from_numpy(table).to(dev), fmt, cfg.C)
+    want = O.embed(ids, table, fmt, cfg.C)
+    assert np.array_equal(to_bits(got), want)
+
+
+@pytest.mark.parametrize("fmt", [ops.FMT_FP8, ops.FMT_FP4])
+def test_embed_every_code_and_scale(dev, fmt):
+    """Every code under scales spanning f16 subnormals to the maximum, both signs: bit-exact, f16 and f32 out."""
+    _case(f"embed every code fmt={fmt}")
+    C = 256
+    scales = np.array([0x0001, 0x0003, 0x03FF, 0x0400, 0x1400, 0x2E66, 0x3C00, 0x4400, 0x5BFF, 0x7800, 0x7BFF,
+                       0x8001, 0xBC00, 0xFBFF, 0x0000, 0x8000], np.uint16)
+    rb = ops.quant_row_bytes(fmt, C)
+    table = np.zeros((len(scales), rb), np.uint8)
+    for r, s in enumerate(scales):
+        if fmt == ops.FMT_FP8:
+            table[r, :C] = np.arange(256, dtype=np.uint8)
+            table[r, C:C + 16].view(np.uint16)[:] = s
+        else:
+            nib = np.arange(C, dtype=np.uint8) % 16
+            blocks = nib.reshape(C // 32, 32)
+            packed = (blocks[:, :16] | (blocks[:, 16:] << 4)).astype(np.uint8)
+            table[r, :C // 2] = packed.reshape(-1)
+            table[r, C // 2:C // 2 + 16].view(np.uint16)[:] = s
+    ids = np.arange(len(scales), dtype=np.int32)[::-1].copy()
+    tt = torch.from_numpy(table).to(dev)
+    it = torch.from_numpy(ids).to(dev)
+    got16 = ops.embed(it, tt, fmt, C)
+    assert np.array_equal(to_bits(got16), O.embed(ids, table, fmt, C))
+    got32 = ops.embed(it, tt, fmt, C, out_dtype=torch.float32)
+    want32 = O.embed(ids, table, fmt, C, out_f16=False)
+    assert np.array_equal(got32.cpu().numpy().view(np.uint32), want32.view(np.uint32))
+
+
+def test_embed_gpt2_wpe(dev):
+    """GPT-2 wte + wpe (f32 add, then one f16 rounding) at the configured shape: bit-exact."""
+    cfg = wl.GPT2_CHAIN
+    _case("embed gpt2 wte+wpe")
+    wte = wl.normal_f16((cfg.vocab, cfg.C), 0.0, 0.02, 33, "cpu").numpy()
+    wpe = wl.normal_f16((cfg.n_ctx, cfg.C), 0.0, 0.02, 34, "cpu").numpy()
+    ids = wl.uniform_ids(cfg.T, cfg.vocab, 35)
+    table = wte.view(np.uint8).reshape(cfg.vocab, 2 * cfg.C)
+    for pos0 in (0, cfg.n_ctx - cfg.T):
+        got = ops.embed(torch.from_numpy(ids).to(dev), torch.from_numpy(table).to(dev), ops.FMT_F16, cfg.C,
+                        wpe=torch.from_numpy(wpe).to(dev), pos0=pos0)
+        want = O.embed(ids, table, ops.FMT_F16, cfg.C, wpe=wpe.view(np.uint16), pos0=pos0)
+        assert np.array_equal(to_bits(got), want)
+    with pytest.raises(NekoError):
+        ops.embed(torch.from_numpy(ids).to(dev), torch.from_numpy(table).to(dev), ops.FMT_F16, cfg.C,
+                  wpe=torch.from_numpy(wpe).to(dev), pos0=cfg.n_ctx - cfg.T + 1)
+
+
+@pytest.mark.parametrize("fmt", [ops.FMT_F16, ops.FMT_FP8, ops.FMT_FP4])
+def test_embed_chunked_table_and_wpe(dev, fmt):
+    """A table split into row chunks gathered with one call per chunk; quantized rows + wpe; f32 out."""
+    _case(f"embed chunked fmt={fmt}")
+    V, C, T = 1000, 512, 300
+    table = _table(fmt, V, C, 36)
+    ids = wl.uniform_ids(T, V, 37)
+    ids[:3] = [0, V - 1, 417]
+    wpe = wl.normal_f16((T + 5, C), 0.0, 0.02, 38, "cpu").numpy()
+    out = torch.zeros((T, C), dtype=torch.float32, device=dev)
+    it = torch.from_numpy(ids).to(dev)
+    for r0, r1 in ((0, 417), (417, 1000)):
+        chunk = torch.from_numpy(table[r0:r1].copy()).to(dev)
+        ops.embed(it, chunk, fmt, C, row_base=r0, wpe=torch.from_numpy(wpe).to(dev), pos0=5, out=out)
+    want = O.embed(ids, table, fmt, C, wpe=wpe.view(np.uint16), pos0=5, out_f16=False)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_embed_fallback_layouts(dev):
+    """Odd widths and unaligned rows take the per-element kernel: still bit-exact."""
+    _case("embed fallback layouts")
+    V, C, T = 50, 100, 40
+    tab = wl.normal_f16((V, C), 0.0, 0.02, 39, "cpu").numpy().view(np.uint8).reshape(V, 2 * C)
+    ids = wl.uniform_ids(T, V + 10, 40)  # some ids outside the table: rows left as they were
+    out = torch.full((T, C), 7.0, dtype=torch.float16, device=dev)
+    ops.embed(torch.from_numpy(ids).to(dev), torch.from_numpy(tab).to(dev), ops.FMT_F16, C, out=out)
+    want = np.full((T, C), 0x4700, np.uint16)
+    want = O.embed(ids, tab, ops.FMT_F16, C, out=want)
+    assert np.array_equal(to_bits(out), want)
+
+
+def test_embed_empty_and_invalid(dev):
+    _case("embed empty and invalid")
+    tab = torch.zeros((4, 64), dtype=torch.uint8, device=dev)
+    none = torch.zeros(0, dtype=torch.int32, device=dev)
+    assert ops.embed(none, tab, ops.FMT_F16, 32).shape == (0, 32)
+    with pytest.raises(NekoError):
+        ops.embed(torch.zeros(2, dtype=torch.int32, device=dev), tab, ops.FMT_FP8, 48)  # C % 32 != 0
+
+
+# ------------------------------------------------------------------ the GPT-2 op chain
+
+def test_gpt2_chain(dev):
+    """gather wte+wpe -> LayerNorm -> GELU, each stage against the oracle chain on the same data."""
+    cfg = wl.GPT2_CHAIN
+    _case("gpt2 chain")
+    wte = wl.normal_f16((cfg.vocab, cfg.C), 0.0, 0.02, 41, "cpu").numpy()
+    wpe = wl.normal_f16((cfg.n_ctx, cfg.C), 0.0, 0.02, 42, "cpu").numpy()
+    ids = wl.uniform_ids(cfg.T, cfg.vocab, 43)
+    g = _w(cfg.C, 44, dev, 1.0, 0.02)
+    b = _w(cfg.C, 45, dev, 0.0, 0.02)
+    table = wte.view(np.uint8).reshape(cfg.vocab, 2 * cfg.C)
+    x = ops.embed(torch.from_numpy(ids).to(dev), torch.from_numpy(table).to(dev), ops.FMT_F16, cfg.C,
+                  wpe=torch.from_numpy(wpe).to(dev))
+    xw = O.embed(ids, table, ops.FMT_F16, cfg.C, wpe=wpe.view(np.uint16))
+    assert np.array_equal(to_bits(x), xw)
+    y = ops.layer_norm(x, g, b, cfg.eps)
+    assert_f16_close(to_bits(y), O.layernorm_f16(xw, g.cpu().numpy(), b.cpu().numpy(), cfg.eps), what="chain LN")
+    hf = _f16((cfg.T, cfg.F), 46, dev)
+    assert_f16_close(to_bits(ops.gelu(hf)), O.gelu_f16(to_bits(hf)), what="chain GELU")

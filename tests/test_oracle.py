@@ -1,0 +1,324 @@
+"""Pins the CPU oracle (oracle/neko_oracle.c) before anything is checked against it.
+
+1. Golden fixtures written by the reference's own compiled ops (tests/golden/golden.npz): bit-exact.
+2. The compiled reference itself (oracle/_ref), where it was built here: bit-exact on fresh seeded inputs.
+3. What the mathematics fixes, chosen so that a dropped term, wrong sign/index or transposed operand fails:
+   IEEE fp16 conversions exhaustively, closed-form code tables, long-double textbook norms and
+   activations, RoPE identities (position 0, norm preservation, the angle table), encoder invariants.
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+
+from conftest import f32_line
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+P = O._ptr
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+# ------------------------------------------------------------------ 1. golden fixtures
+
+def test_golden_rmsnorm(golden):
+    assert np.array_equal(O.rmsnorm_f16(golden["rms_x"], golden["rms_w"], 1e-6), golden["rms_y"])
+
+
+def test_golden_layernorm(golden):
+    assert np.array_equal(O.layernorm_f16(golden["ln_x"], golden["ln_g"], golden["ln_b"], 1e-5), golden["ln_y"])
+
+
+def test_golden_qk_norm_rope(golden):
+    H, KV, hd = (int(v) for v in golden["qk_shape"])
+    cs, pos = golden["qk_cs"], golden["qk_pos"]
+    got = O.qk_norm_rope_f16(golden["qk_qkv"], H, KV, hd, cs, cs.shape[0], 1e-6, wqk=golden["qk_wqk"], positions=pos)
+    assert np.array_equal(got, golden["qk_out"])
+    got = O.qk_norm_rope_f16(golden["qk_qkv"], H, KV, hd, cs, cs.shape[0], 1e-6, positions=pos)
+    assert np.array_equal(got, golden["qk_out_nonorm"])
+
+
+def test_golden_swiglu_gelu(golden):
+    assert np.array_equal(O.swiglu_f16(golden["swiglu_h"]), golden["swiglu_out"])
+    assert np.array_equal(O.gelu_f16(np.arange(65536, dtype=np.uint16)), golden["gelu_y"])
+
+
+def test_golden_gated(golden):
+    for groups in (1, 4):
+        got = O.gated_rmsnorm_f16(golden["gated_y"], golden["gated_z"], golden["gated_w"], groups, 1e-5)
+        assert np.array_equal(got, golden[f"gated_out_g{groups}"])
+
+
+@pytest.mark.parametrize("fmt,name", [(0, "f16"), (1, "fp8"), (2, "fp4")])
+def test_golden_codecs_and_gather(golden, fmt, name):
+    tab = O.quantize_rows(fmt, golden["quant_src"])
+    assert np.array_equal(tab, golden[f"quant_{name}"])
+    ids = golden["embed_ids"]
+    assert np.array_equal(O.embed(ids, tab, fmt, 256), golden[f"embed_{name}_f16"])
+    o32 = O.embed(ids, tab, fmt, 256, out_f16=False)
+    assert np.array_equal(o32.view(np.uint32), golden[f"embed_{name}_f32"].view(np.uint32))
+
+
+def test_golden_wpe(golden):
+    got = O.embed(golden["embed_ids"], golden["quant_f16"], 0, 256, wpe=golden["embed_wpe"], pos0=3)
+    assert np.array_equal(got, golden["embed_wpe_f16"])
+
+
+def test_golden_decoders(golden):
+    d8 = np.array([O.lib().oracle_decode_fp8(c) for c in range(256)], np.float32)
+    assert np.array_equal(d8.view(np.uint32), golden["fp8_decode"].view(np.uint32))
+    d4 = np.array([O.lib().oracle_decode_fp4(c) for c in range(16)], np.float32)
+    assert np.array_equal(d4.view(np.uint32), golden["fp4_decode"].view(np.uint32))
+
+
+# ------------------------------------------------------------------ 2. the compiled reference
+
+needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no reference checkout here)")
+
+
+@needs_ref
+def test_ref_f16_conversions_exhaustive():
+    R = O.ref()
+    h = np.arange(65536, dtype=np.uint16)
+    a, b = O.f16_to_f32(h), np.empty(65536, np.float32)
+    R.ref_f16_to_f32_n(P(h), P(b), 65536)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    rng = np.random.default_rng(1)
+    f = (rng.standard_normal(300000) * 10.0 ** rng.integers(-9, 6, 300000)).astype(np.float32)
+    f = np.concatenate([f, b[np.isfinite(b)], np.nextafter(b[np.isfinite(b)], np.float32(np.inf))])
+    r = np.empty(f.size, np.uint16)
+    R.ref_f32_to_f16_n(P(f), P(r), f.size)
+    assert np.array_equal(O.f32_to_f16(f), r)
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [2, 3])
+def test_ref_ops_bitexact(seed):
+    R = O.ref()
+    rng = np.random.default_rng(seed)
+    F = ctypes.c_float
+    x = (rng.standard_normal((33, 1536)) * 2).astype(np.float16).view(np.uint16)
+    w = rng.standard_normal(1536).astype(np.float16).astype(np.float32)
+    b = rng.standard_normal(1536).astype(np.float32)
+    y = np.empty_like(x)
+    R.ref_rmsnorm_f16(P(x), P(y), P(w), 33, 1536, F(1e-5))
+    assert np.array_equal(O.rmsnorm_f16(x, w, 1e-5), y)
+    R.ref_layernorm_f16(P(x), P(y), P(w), P(b), 33, 1536, F(1e-5))
+    assert np.array_equal(O.layernorm_f16(x, w, b, 1e-5), y)
+    h = (rng.standard_normal((5, 2000)) * 5).astype(np.float16).view(np.uint16)
+    o = np.empty((5, 1000), np.uint16)
+    R.ref_silu_mul_f16(P(h), P(o), 5, 1000)
+    assert np.array_equal(O.swiglu_f16(h), o)
+    H, KV, hd = 4, 2, 64
+    qkv = rng.standard_normal((9, (H + 2 * KV) * hd)).astype(np.float16).view(np.uint16)
+    cs = O.rope_table(1e4, hd, 100)
+    pos = rng.integers(0, 100, 9).astype(np.int32)
+    wq = rng.standard_normal(2 * hd).astype(np.float32)
+    ref = qkv.copy()
+    R.ref_qk_norm_rope_f16(P(ref), qkv.shape[1], 9, H, KV, hd, P(pos), P(wq[:hd].copy()), P(wq[hd:].copy()), P(cs),
+                           F(1e-6))
+    assert np.array_equal(O.qk_norm_rope_f16(qkv, H, KV, hd, cs, 100, 1e-6, wqk=wq, positions=pos), ref)
+    yy = rng.standard_normal((4, 640)).astype(np.float16).view(np.uint16)
+    zz = (rng.standard_normal((4, 640)) * 3).astype(np.float16).view(np.uint16)
+    wg = rng.standard_normal(640).astype(np.float32)
+    for groups in (1, 5):
+        o = np.empty_like(yy)
+        R.ref_gated_rmsnorm_f16(P(yy), P(zz), P(o), P(wg), 4, 640, groups, F(1e-5))
+        assert np.array_equal(O.gated_rmsnorm_f16(yy, zz, wg, groups, 1e-5), o)
+    xs = rng.standard_normal(4096).astype(np.float32) * 6
+    assert np.array_equal(np.array([O.lib().oracle_gelu(v) for v in xs], np.float32).view(np.uint32),
+                          np.array([R.ref_gelu(v) for v in xs], np.float32).view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+@pytest.mark.parametrize("cols,scale", [(256, 0.02), (1024, 1.0), (96, 1e-4), (100, 0.02), (64, 3e4)])
+def test_ref_quantizer_bitexact(fmt, cols, scale):
+    R = O.ref()
+    rng = np.random.default_rng(cols)
+    x = (rng.standard_normal((40, cols)) * scale).astype(np.float32)
+    x[0, :] = 0
+    x[1, 3] = scale * 50
+    x[2, :] = rng.standard_t(2, cols) * scale
+    got = O.quantize_rows(fmt, x)
+    want = np.zeros_like(got)
+    R.ref_quantize_rows(fmt, 40, cols, P(x), P(want))
+    assert np.array_equal(got, want)
+    used = fmt if cols % 32 == 0 else 0
+    for r in range(0, 40, 7):
+        a, b = np.empty(cols, np.float32), np.empty(cols, np.float32)
+        O.lib().oracle_dequantize_row(used, cols, P(got[r]), P(a))
+        R.ref_dequantize_row(used, cols, P(got[r]), P(b))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------------------ 3. what the mathematics fixes
+
+def test_f16_widen_is_ieee():
+    h = np.arange(65536, dtype=np.uint16)
+    assert np.array_equal(O.f16_to_f32(h).view(np.uint32), h.view(np.float16).astype(np.float32).view(np.uint32))
+
+
+def test_f16_narrow_is_ieee_rne():
+    rng = np.random.default_rng(4)
+    f = (rng.standard_normal(200000) * 10.0 ** rng.integers(-9, 6, 200000)).astype(np.float32)
+    edges = np.array([65504, 65519.996, 65520, 2 ** -24, 2 ** -25, 2 ** -25 * 1.0000001, 2 ** -14, np.inf, -0.0],
+                     np.float32)
+    f = np.concatenate([f, edges, -edges])
+    assert np.array_equal(O.f32_to_f16(f), f.astype(np.float16).view(np.uint16))
+    nan = np.array([np.nan, -np.nan], np.float32)
+    assert list(O.f32_to_f16(nan)) == [0x7E00, 0xFE00]
+
+
+def _e4m3(c):
+    s = -1.0 if c & 0x80 else 1.0
+    e, m = (c >> 3) & 0xF, c & 7
+    return s * (2.0 ** -6 * m / 8 if e == 0 else 2.0 ** (e - 7) * (1 + m / 8))
+
+
+def test_fp8_code_table_closed_form():
+    got = np.array([O.lib().oracle_decode_fp8(c) for c in range(256)])
+    want = np.array([_e4m3(c) for c in range(256)])
+    assert np.array_equal(got, want)  # includes 0x7F -> 480, 0xFF -> -480 (no NaN code)
+    assert math.copysign(1, got[0x80]) == -1 and got[0x80] == 0
+
+
+def test_fp4_code_table_closed_form():
+    mags = [0, 0.5, 1, 1.5, 2, 3, 4, 6]
+    got = [O.lib().oracle_decode_fp4(c) for c in range(16)]
+    assert got == mags + [-m for m in mags]
+    assert math.copysign(1, got[8]) == -1
+
+
+def test_quant_row_bytes_closed_form():
+    for cols in (32, 64, 96, 256, 768, 2048, 4096):
+        nb = cols // 32
+        pad = -(-2 * nb // 16) * 16
+        assert O.quant_row_bytes(0, cols) == 2 * cols
+        assert O.quant_row_bytes(1, cols) == cols + pad
+        assert O.quant_row_bytes(2, cols) == cols // 2 + pad
+    assert O.quant_row_bytes(1, 2048) == 2176 and O.quant_row_bytes(2, 2048) == 1152
+
+
+def test_fp8_encoder_invariants():
+    """Scale = RNE_f16(amax / 448). Each code is x * (1/scale) rounded to fp16 first and then to the
+    nearest E4M3 value, ties to the even code (the reference rounds twice, quant.cpp:43-49); the sign bit
+    is the sign of x."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((50, 64)) * 0.05).astype(np.float32)
+    x[0, :8] = [-0.0, 0.0, -1e-30, 1e-30, 0.05, -0.05, 0.025, -0.0125]
+    tab = O.quantize_rows(1, x)
+    grid = np.array([_e4m3(c) for c in range(0x7F)])
+    for r in range(50):
+        for b in range(2):
+            blk = x[r, 32 * b:32 * b + 32]
+            s_bits = int(tab[r, 64 + 2 * b]) | (int(tab[r, 65 + 2 * b]) << 8)
+            assert s_bits == int(np.float16(np.abs(blk).max() / np.float32(448)).view(np.uint16))
+            inv = np.float32(1) / np.float32(np.uint16(s_bits).view(np.float16))
+            for i, v in enumerate(blk):
+                c = int(tab[r, 32 * b + i])
+                q16 = abs(float(np.float16(np.float32(v) * inv * np.float32(1 / 256)))) * 256
+                d = np.abs(grid - q16)
+                best = np.flatnonzero(d == d.min())
+                assert (c & 0x7F) in best
+                if len(best) == 2:
+                    assert (c & 1) == 0  # tie -> even mantissa
+                assert bool(c & 0x80) == bool(np.signbit(v))
+
+
+def test_fp4_scale_is_best_of_candidates():
+    """The FP4 block scale is amax/6 or a least-squares refit, never worse (squared error) than amax/6."""
+    rng = np.random.default_rng(6)
+    mags = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6])
+    for _ in range(200):
+        blk = (rng.standard_normal(32) * 0.02).astype(np.float32)
+        s = float(np.uint16(O.lib().oracle_fp4_block_scale(P(blk))).view(np.float16))
+        s0 = float(np.float16(np.abs(blk).max() / np.float32(6)))
+
+        def err(sc):
+            q = np.abs(blk) / sc
+            r = mags[np.abs(q[:, None] - mags[None, :]).argmin(1)]
+            return float(((np.abs(blk) - r * sc) ** 2).sum())
+
+        assert err(s) <= err(s0) * (1 + 1e-5) + 1e-18
+
+
+def _ld(a):
+    return np.asarray(a, dtype=np.longdouble)
+
+
+def test_rmsnorm_textbook():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((20, 2560)) * 3).astype(np.float32)
+    x[4] = 0
+    w = (1 + 0.05 * rng.standard_normal(2560)).astype(np.float32)
+    y = np.empty_like(x)
+    O.lib().oracle_rmsnorm(P(x), P(y), P(w), 20, 2560, 1e-6)
+    xl = _ld(x)
+    want = xl / np.sqrt((xl * xl).mean(1, keepdims=True) + _ld(np.float32(1e-6))) * _ld(w)
+    np.testing.assert_allclose(y.astype(np.float64), want.astype(np.float64), rtol=4e-7, atol=0)
+    assert not y[4].any()
+
+
+def test_layernorm_textbook():
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((20, 768)) + 50).astype(np.float32)
+    x[3] = 7.25  # constant row: output = beta
+    g = (1 + 0.02 * rng.standard_normal(768)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(768)).astype(np.float32)
+    y = np.empty_like(x)
+    O.lib().oracle_layernorm(P(x), P(y), P(g), P(b), 20, 768, 1e-5)
+    xl = _ld(x)
+    mu = xl.mean(1, keepdims=True)
+    want = (xl - mu) / np.sqrt(((xl - mu) ** 2).mean(1, keepdims=True) + _ld(np.float32(1e-5))) * _ld(g) + _ld(b)
+    np.testing.assert_allclose(y.astype(np.float64), want.astype(np.float64), rtol=0, atol=3e-6)
+    assert np.array_equal(y[3], b)
+
+
+def test_gelu_silu_textbook():
+    xs = np.linspace(-12, 12, 4001).astype(np.float32)
+    got = np.array([O.lib().oracle_gelu(v) for v in xs])
+    xl = _ld(xs)
+    inner = _ld(np.float32(0.7978845608)) * (xl + _ld(np.float32(0.044715)) * xl ** 3)
+    want = 0.5 * xl * (1 + np.tanh(inner))
+    # 1 + tanh cancels for x << 0: the bound adds a few f32 ulps of 1 scaled by |x|.
+    assert np.all(np.abs(got - want.astype(np.float64)) <= 2e-6 * np.abs(want.astype(np.float64)) + np.abs(xs) * 2.0 ** -23)
+    assert O.lib().oracle_gelu(0.0) == 0.0
+    sil = np.array([O.lib().oracle_silu(v) for v in xs])
+    np.testing.assert_allclose(sil, (xl / (1 + np.exp(-xl))).astype(np.float64), rtol=1e-6, atol=1e-30)
+    assert np.all(got[xs > 6] == xs[xs > 6])  # tanh saturates to 1 in float: gelu(x) = x
+
+
+def test_rope_identities():
+    hd, n_pos = 128, 4096
+    cs = O.rope_table(1e6, hd, n_pos)
+    c, s = cs[:, 0::2].astype(np.float64), cs[:, 1::2].astype(np.float64)
+    assert np.all(np.abs(c * c + s * s - 1) < 2.5e-7)
+    assert np.array_equal(cs[0, 0::2], np.ones(64, np.float32)) and not cs[0, 1::2].any()
+    p = np.arange(n_pos, dtype=np.float64)
+    assert np.all(np.abs(f32_line(cs[:, 0]) - f32_line(np.cos(p).astype(np.float32))) <= 1)  # i = 0: angle p
+    assert np.all(np.abs(f32_line(cs[:, 1]) - f32_line(np.sin(p).astype(np.float32))) <= 1)
+    inv = 1e6 ** (-2.0 * 63 / hd)
+    ang = p * inv
+    assert np.all(np.abs(f32_line(cs[:, 126]) - f32_line(np.cos(ang).astype(np.float32))) <= 1)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((3, hd)).astype(np.float32)
+    v = x.copy()
+    O.lib().oracle_rope(P(v), 3, hd, P(cs[0]))
+    assert np.array_equal(v, x)  # position 0 rotates nothing
+    v = x.copy()
+    O.lib().oracle_rope(P(v), 3, hd, P(cs[1234]))
+    before = x[:, :64] ** 2 + x[:, 64:] ** 2
+    after = v[:, :64].astype(np.float64) ** 2 + v[:, 64:].astype(np.float64) ** 2
+    np.testing.assert_allclose(after, before, rtol=2e-6)
+    # pair i of the first half rotates with pair i of the second half (NeoX split), by angle pos * inv_i
+    a, b = x[0, 5], x[0, 69]
+    cc, ss = cs[1234, 10], cs[1234, 11]
+    assert v[0, 5] == np.float32(a * cc) - np.float32(b * ss)
+    assert v[0, 69] == np.float32(a * ss) + np.float32(b * cc)
