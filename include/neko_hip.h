@@ -14,9 +14,10 @@
  * Conventions
  *   - Every function returns an int status: NEKO_OK (0) or a negative NEKO_ERR_*; nothing throws.
  *     The message of the last failure on a context is neko_hip_last_error(ctx).
- *   - One context per host thread. A context owns one in-order HIP stream, so every op is ordered
- *     after the previous one on that context (the reference's "each dispatch is ordered after the
- *     previous", gpu/compute.h:38) without barriers. Ops only enqueue work; neko_hip_download and
+ *   - One context per host thread. A context issues all work to one in-order HIP stream -- the
+ *     device's null stream unless neko_hip_set_stream routes it elsewhere -- so every op is ordered
+ *     after the previous one (the reference's "each dispatch is ordered after the previous",
+ *     gpu/compute.h:38) without barriers. Ops only enqueue work; neko_hip_download and
  *     neko_hip_synchronize wait.
  *   - Device pointers are plain addresses from neko_hip_alloc (or any HIP allocation on the
  *     context's device). Sizes and strides are int64 element counts unless the name says bytes.
@@ -53,19 +54,18 @@ typedef struct neko_hip_ctx neko_hip_ctx;
  * Replace the ComputeBackend factory / create / upload / download / submitAndWait
  * (gpu/compute.h:28-44, vk_compute.cpp:459-466). */
 
-/* Opens device `device` and creates the context's stream. *out is NULL on failure; the message of
- * a failed create is available as neko_hip_last_error(NULL). */
+/* Opens device `device`. *out is NULL on failure; the message of a failed create is available as
+ * neko_hip_last_error(NULL). */
 int neko_hip_create(int device, neko_hip_ctx** out);
-/* Waits for outstanding work, releases the stream and any memory still allocated through the ctx. */
+/* Waits for outstanding work and releases any memory still allocated through the ctx. */
 int neko_hip_destroy(neko_hip_ctx* ctx);
 /* Last error message on ctx (or of the last failed neko_hip_create when ctx is NULL). Never NULL. */
 const char* neko_hip_last_error(const neko_hip_ctx* ctx);
 /* Device name and the largest single allocation (ComputeBackend::deviceName / maxBufferBytes). */
 int neko_hip_device_name(neko_hip_ctx* ctx, char* buf, size_t buf_bytes);
 size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx);
-/* Routes subsequent work to an external hipStream_t on the same device (e.g. a framework's
- * current stream); NULL restores the context's own stream, a blocking stream that is ordered with
- * the device's null stream. The caller keeps ownership of an external stream. */
+/* Routes subsequent work to a hipStream_t on the same device (e.g. a framework's current stream);
+ * NULL selects the device's null stream, the default. The caller keeps ownership of the stream. */
 int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream);
 void* neko_hip_get_stream(const neko_hip_ctx* ctx);
 

@@ -64,6 +64,13 @@ class NekoError(RuntimeError):
 
 
 def _load() -> ctypes.CDLL:
+    # One HIP runtime per process: torch bundles its own libamdhip64 (same SONAME, different file
+    # name), so it must be loaded first for libneko_hip.so to bind to it. Loaded the other way round,
+    # the process would hold two runtimes and torch's device pointers would be foreign to ours.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "

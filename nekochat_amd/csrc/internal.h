@@ -14,8 +14,7 @@
 
 struct neko_hip_ctx {
     int device = -1;
-    hipStream_t own_stream = nullptr;
-    hipStream_t stream = nullptr;  // own_stream unless the caller routed work elsewhere
+    hipStream_t stream = nullptr;  // null = the device's null stream
     int cu_count = 0;
     size_t max_alloc = 0;
     std::string name;
@@ -36,6 +35,11 @@ int enter(neko_hip_ctx* ctx);
 int after_launch(neko_hip_ctx* ctx, const char* what);
 
 FastDiv make_fast_div(uint32_t d);
+
+// Workgroups of `block` threads of `kernel` that fit on one CU at once (cached per kernel), and the
+// grid of a persistent kernel: that many per CU, or fewer when there is less work.
+int resident_blocks_per_cu(const void* kernel, int block);
+int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline size_t dtype_size(int dtype) { return dtype == NEKO_DT_F16 ? 2 : 4; }

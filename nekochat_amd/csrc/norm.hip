@@ -1,14 +1,15 @@
 // Row norms for gfx950: LayerNorm (cpu_ops.cpp:483-500), RMSNorm (cpu_ops.cpp:502-511) and the
 // Granite-4.0-H gated group RMSNorm (granite_model.cpp:278-287).
 //
-// Fast path: one 64-wide wavefront per row (four rows per 256-thread workgroup), or one workgroup
-// of four waves per row for rows wider than 4096 halves. Each lane issues all of its 16-byte loads
-// up front and keeps the row in registers, so HBM is read exactly once and written once. Sums are
-// accumulated in double, like the reference, reduced across the wave with DPP and v_readlane (no
-// LDS; LDS only joins the partial sums of multi-wave rows). The norm scale is rounded to float
-// exactly where the reference rounds it, and the output is (x * s) * w unfused, so the result
-// matches the reference's CPU op bit for bit unless a double sum lands within an ulp of a float
-// rounding boundary.
+// Fast path: one 64-wide wavefront per row, persistent. A grid of four 256-thread workgroups per CU
+// walks the rows; each wave keeps its norm weights in registers for all of its rows and issues the
+// 16-byte non-temporal loads of its next row before it reduces the current one, so HBM is read
+// once, written once, and always has loads in flight. Rows wider than one wave's registers use four
+// waves per row. Sums are accumulated in double, like the reference, and reduced across the wave
+// with DPP and v_readlane (LDS only joins the partial sums of multi-wave rows). The norm scale is
+// rounded to float exactly where the reference rounds it and the output is (x * s) * w unfused, so
+// results match the reference's CPU op bit for bit unless a double sum lands within an ulp of a
+// float rounding boundary.
 //
 // Fallback (any width, alignment or stride): one workgroup per row streaming the row from memory
 // once per pass.
@@ -63,39 +64,34 @@ __device__ __forceinline__ RowPtrs<K, T> row_ptrs(const NormArgs& a, int64_t r) 
 }
 
 // ------------------------------------------------------------------ register-resident rows
-// W waves per row, up to CH 16-byte chunks per lane.
-template <Norm K, typename T, int W, int CH>
-__global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a) {
-    using CT = Chunk16<T>;
-    constexpr int N = CT::N;
-    typedef typename CT::V V;
-    constexpr int RPB = 4 / W;  // rows per workgroup
-    constexpr int NT = kWave * W;  // threads per row
+// The row (and the gate operand) of one lane: up to CH 16-byte chunks, chunk j = k * NT + tid.
+template <Norm K, typename T, int CH>
+struct RowRegs {
+    typedef typename Chunk16<T>::V V;
+    V x[CH];
+    V z[CH];
+};
 
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * RPB + wave / W;
-    const bool live = r < a.rows;
-    if constexpr (W == 1) {
-        if (!live) return;  // wave-uniform; single-wave rows meet no barrier
-    }
-    const RowPtrs<K, T> p = row_ptrs<K, T>(a, live ? r : 0);
-    const int tid = (wave % W) * kWave + lane;
-    const int nch = a.C / N;
-
-    V xv[CH], zv[CH];
+template <Norm K, typename T, int CH, int NT>
+__device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K, T>& p, int tid, int nch) {
+    typedef typename Chunk16<T>::V V;
+    constexpr int N = Chunk16<T>::N;
 #pragma unroll
     for (int k = 0; k < CH; k++) {
         const int j = k * NT + tid;
-        xv[k] = V{};
-        zv[k] = V{};
+        rr.x[k] = V{};
+        rr.z[k] = V{};
         if (j < nch) {
-            xv[k] = load_nt(reinterpret_cast<const V*>(p.x + j * N));
-            if constexpr (K == Norm::Gated) zv[k] = load_nt(reinterpret_cast<const V*>(p.z + j * N));
+            rr.x[k] = load_nt(reinterpret_cast<const V*>(p.x + j * N));
+            if constexpr (K == Norm::Gated) rr.z[k] = load_nt(reinterpret_cast<const V*>(p.z + j * N));
         }
     }
-    // Weights do not depend on the data: fetch them while the row is in flight.
-    float4v wv[CH][N / 4], bv[CH][N / 4];
+}
+
+template <Norm K, typename T, int CH, int NT>
+__device__ __forceinline__ void load_weights(float4v (&wv)[CH][Chunk16<T>::N / 4], float4v (&bv)[CH][Chunk16<T>::N / 4],
+                                             const float* w, const float* b, int tid, int nch) {
+    constexpr int N = Chunk16<T>::N;
 #pragma unroll
     for (int k = 0; k < CH; k++) {
         const int j = k * NT + tid;
@@ -104,73 +100,84 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a) {
             wv[k][q] = float4v{};
             bv[k][q] = float4v{};
             if (j < nch) {
-                wv[k][q] = *reinterpret_cast<const float4v*>(p.w + j * N + 4 * q);
-                if constexpr (K == Norm::Layer) bv[k][q] = *reinterpret_cast<const float4v*>(p.b + j * N + 4 * q);
+                wv[k][q] = *reinterpret_cast<const float4v*>(w + j * N + 4 * q);
+                if constexpr (K == Norm::Layer) bv[k][q] = *reinterpret_cast<const float4v*>(b + j * N + 4 * q);
             }
         }
     }
+}
 
-    // Row values in float; lanes past the row end hold zeros, which add nothing to the sums.
-    float f[CH][N];
+// The row in float. Plain norms convert from the loaded halves on every use (cheaper than holding a
+// float copy in registers); the gated norm evaluates y * silu(z) once and keeps it. Lanes past the
+// row end hold zeros, which add nothing to the sums.
+template <Norm K, typename T, int CH>
+struct RowVals {
+    static constexpr int N = Chunk16<T>::N;
+    float f[K == Norm::Gated ? CH : 1][K == Norm::Gated ? N : 1];
+    const RowRegs<K, T, CH>* rr;
+
+    __device__ __forceinline__ void init(const RowRegs<K, T, CH>& regs) {
+        rr = &regs;
+        if constexpr (K == Norm::Gated) {
 #pragma unroll
-    for (int k = 0; k < CH; k++) {
+            for (int k = 0; k < CH; k++)
+#pragma unroll
+                for (int e = 0; e < N; e++) f[k][e] = to_f32(regs.x[k][e]) * silu_ref(to_f32(regs.z[k][e]));
+        }
+    }
+    __device__ __forceinline__ float operator()(int k, int e) const {
+        if constexpr (K == Norm::Gated) return f[k][e];
+        else return to_f32(rr->x[k][e]);
+    }
+};
+
+// Squares of f16 values, and of the f32 values the f32 ABI passes, are exact in double, so
+// fma(d, d, s) equals the reference's s += d * d.
+template <int CH, int N, typename F>
+__device__ __forceinline__ double sum_squares(const F& f) {
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < CH; k++)
 #pragma unroll
         for (int e = 0; e < N; e++) {
-            if constexpr (K == Norm::Gated) f[k][e] = to_f32(xv[k][e]) * silu_ref(to_f32(zv[k][e]));
-            else f[k][e] = to_f32(xv[k][e]);
+            const double d = static_cast<double>(f(k, e));
+            ss = __builtin_fma(d, d, ss);
+        }
+    return ss;
+}
+
+template <int CH, int N, typename F>
+__device__ __forceinline__ double sum_values(const F& f) {
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < CH; k++)
+#pragma unroll
+        for (int e = 0; e < N; e++) s += static_cast<double>(f(k, e));
+    return s;
+}
+
+// Sum of (x - mean)^2 over valid chunks; the product is rounded before the add, as in the reference.
+template <int CH, int N, int NT, typename F>
+__device__ __forceinline__ double sum_centered(const F& f, double mean, int tid, int nch) {
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < CH; k++) {
+        const int j = k * NT + tid;
+#pragma unroll
+        for (int e = 0; e < N; e++) {
+            const double d = static_cast<double>(f(k, e)) - mean;
+            if (j < nch) s += d * d;
         }
     }
+    return s;
+}
 
-    __shared__ double part[2][4];
-    auto row_total = [&](double v, int slot) -> double {
-        v = wave_sum_f64(v);
-        if constexpr (W > 1) {
-            if (lane == 0) part[slot][wave] = v;
-            __syncthreads();
-            const int w0 = (wave / W) * W;
-            double s = part[slot][w0];
-#pragma unroll
-            for (int i = 1; i < W; i++) s += part[slot][w0 + i];
-            v = s;
-        }
-        return v;
-    };
-
-    float scale, mean_f = 0.0f;
-    if constexpr (K == Norm::Layer) {
-        double s1 = 0.0;
-#pragma unroll
-        for (int k = 0; k < CH; k++)
-#pragma unroll
-            for (int e = 0; e < N; e++) s1 += static_cast<double>(f[k][e]);
-        const double mean = row_total(s1, 0) / a.C;
-        double s2 = 0.0;
-#pragma unroll
-        for (int k = 0; k < CH; k++) {
-            const int j = k * NT + tid;
-#pragma unroll
-            for (int e = 0; e < N; e++) {
-                const double d = static_cast<double>(f[k][e]) - mean;
-                if (j < nch) s2 += d * d;
-            }
-        }
-        const double var = row_total(s2, 1) / a.C;
-        scale = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
-        mean_f = static_cast<float>(mean);
-    } else {
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < CH; k++)
-#pragma unroll
-            for (int e = 0; e < N; e++) {
-                const double d = static_cast<double>(f[k][e]);
-                ss += d * d;
-            }
-        const double tot = row_total(ss, 0);
-        scale = static_cast<float>(1.0 / sqrt(tot / a.C + static_cast<double>(a.eps)));
-    }
-    if (!live) return;
-
+template <Norm K, typename T, int CH, int NT, typename F>
+__device__ __forceinline__ void store_row(T* y, const F& f, float scale, float mean_f,
+                                          const float4v (&wv)[CH][Chunk16<T>::N / 4],
+                                          const float4v (&bv)[CH][Chunk16<T>::N / 4], int tid, int nch) {
+    typedef typename Chunk16<T>::V V;
+    constexpr int N = Chunk16<T>::N;
 #pragma unroll
     for (int k = 0; k < CH; k++) {
         const int j = k * NT + tid;
@@ -180,12 +187,87 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(NormArgs a) {
         for (int e = 0; e < N; e++) {
             const float w = wv[k][e / 4][e % 4];
             float v;
-            if constexpr (K == Norm::Layer) v = (f[k][e] - mean_f) * scale * w + bv[k][e / 4][e % 4];
-            else v = f[k][e] * scale * w;
+            if constexpr (K == Norm::Layer) v = (f(k, e) - mean_f) * scale * w + bv[k][e / 4][e % 4];
+            else v = f(k, e) * scale * w;
             out[e] = from_f32<T>(v);
         }
-        store_nt(reinterpret_cast<V*>(p.y + j * N), out);
+        store_nt(reinterpret_cast<V*>(y + j * N), out);
     }
+}
+
+// One wavefront per row, persistent: wave w handles rows w, w + nw, ... (nw = waves in the grid),
+// keeps the weights in registers across rows and loads the next row while it normalises this one.
+// Every row of a wave shares one group index (the host makes nw a multiple of groups, or gives
+// each wave at most one row).
+template <Norm K, typename T, int CH>
+__global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
+    constexpr int N = Chunk16<T>::N;
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= a.rows) return;  // wave-uniform
+    const int nch = a.C / N;
+    const RowPtrs<K, T> p0 = row_ptrs<K, T>(a, r);
+    float4v wv[CH][N / 4], bv[CH][N / 4];
+    load_weights<K, T, CH, kWave>(wv, bv, p0.w, p0.b, lane, nch);
+
+    RowRegs<K, T, CH> cur, nxt;
+    load_row<K, T, CH, kWave>(cur, p0, lane, nch);
+    for (; r < a.rows; r += nw) {
+        const bool more = r + nw < a.rows;
+        if (more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
+        RowVals<K, T, CH> f;
+        f.init(cur);
+        float scale, mean_f = 0.0f;
+        if constexpr (K == Norm::Layer) {
+            const double mean = wave_sum_f64(sum_values<CH, N>(f)) / a.C;
+            const double var = wave_sum_f64(sum_centered<CH, N, kWave>(f, mean, lane, nch)) / a.C;
+            scale = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+            mean_f = static_cast<float>(mean);
+        } else {
+            const double ss = wave_sum_f64(sum_squares<CH, N>(f));
+            scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
+        }
+        store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wv, bv, lane, nch);
+        if (more) cur = nxt;
+    }
+}
+
+// Four wavefronts per row for rows wider than one wave's registers; partial sums meet in LDS.
+template <Norm K, typename T, int CH>
+__global__ __launch_bounds__(256) void norm_wide_kernel(NormArgs a) {
+    constexpr int N = Chunk16<T>::N;
+    constexpr int NT = 4 * kWave;
+    const int64_t r = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int nch = a.C / N;
+    const RowPtrs<K, T> p = row_ptrs<K, T>(a, r);
+    RowRegs<K, T, CH> rr;
+    load_row<K, T, CH, NT>(rr, p, tid, nch);
+    float4v wv[CH][N / 4], bv[CH][N / 4];
+    load_weights<K, T, CH, NT>(wv, bv, p.w, p.b, tid, nch);
+    RowVals<K, T, CH> f;
+    f.init(rr);
+
+    __shared__ double part[2][4];
+    auto block_total = [&](double v, int slot) -> double {
+        v = wave_sum_f64(v);
+        if ((tid & 63) == 0) part[slot][wave] = v;
+        __syncthreads();
+        return (part[slot][0] + part[slot][1]) + (part[slot][2] + part[slot][3]);
+    };
+    float scale, mean_f = 0.0f;
+    if constexpr (K == Norm::Layer) {
+        const double mean = block_total(sum_values<CH, N>(f), 0) / a.C;
+        const double var = block_total(sum_centered<CH, N, NT>(f, mean, tid, nch), 1) / a.C;
+        scale = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
+        mean_f = static_cast<float>(mean);
+    } else {
+        const double ss = block_total(sum_squares<CH, N>(f), 0);
+        scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
+    }
+    store_row<K, T, CH, NT>(p.y, f, scale, mean_f, wv, bv, tid, nch);
 }
 
 // ------------------------------------------------------------------ generic rows
@@ -248,38 +330,51 @@ __global__ __launch_bounds__(256) void norm_rows_generic(NormArgs a) {
 typedef void (*NormKernel)(NormArgs);
 
 template <Norm K, typename T>
-NormKernel pick_rows_kernel(int W, int CH) {
-    if (W == 1) {
-        switch (CH) {
-            case 1: return norm_rows_kernel<K, T, 1, 1>;
-            case 2: return norm_rows_kernel<K, T, 1, 2>;
-            case 3: return norm_rows_kernel<K, T, 1, 3>;
-            case 4: return norm_rows_kernel<K, T, 1, 4>;
-            case 5: return norm_rows_kernel<K, T, 1, 5>;
-            case 6: return norm_rows_kernel<K, T, 1, 6>;
-            case 8: return norm_rows_kernel<K, T, 1, 8>;
-        }
-    } else if (W == 4) {
-        switch (CH) {
-            case 4: return norm_rows_kernel<K, T, 4, 4>;
-            case 8: return norm_rows_kernel<K, T, 4, 8>;
-        }
+NormKernel pick_wave(int CH) {
+    switch (CH) {
+        case 1: return norm_wave_kernel<K, T, 1>;
+        case 2: return norm_wave_kernel<K, T, 2>;
+        case 3: return norm_wave_kernel<K, T, 3>;
+        case 4: return norm_wave_kernel<K, T, 4>;
+        case 5: return norm_wave_kernel<K, T, 5>;
+        case 6: return norm_wave_kernel<K, T, 6>;
+        case 8: return norm_wave_kernel<K, T, 8>;
+    }
+    return nullptr;
+}
+
+template <Norm K, typename T>
+NormKernel pick_wide(int CH) {
+    switch (CH) {
+        case 4: return norm_wide_kernel<K, T, 4>;
+        case 8: return norm_wide_kernel<K, T, 8>;
     }
     return nullptr;
 }
 
 template <Norm K>
 NormKernel pick(int dtype, int W, int CH) {
-    if (W == 0) return dtype == NEKO_DT_F16 ? norm_rows_generic<K, half_t> : norm_rows_generic<K, float>;
-    return dtype == NEKO_DT_F16 ? pick_rows_kernel<K, half_t>(W, CH) : pick_rows_kernel<K, float>(W, CH);
+    const bool h = dtype == NEKO_DT_F16;
+    if (W == 0) return h ? norm_rows_generic<K, half_t> : norm_rows_generic<K, float>;
+    if (W == 1) return h ? pick_wave<K, half_t>(CH) : pick_wave<K, float>(CH);
+    return h ? pick_wide<K, half_t>(CH) : pick_wide<K, float>(CH);
+}
+
+int64_t gcd64(int64_t a, int64_t b) {
+    while (b) {
+        const int64_t t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
 }
 
 int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, const char* what) {
     const size_t esz = dtype_size(dtype);
     const int N = static_cast<int>(16 / esz);
-    // The register path loads 16-byte chunks of every operand row and 16-byte weight vectors.
-    bool vec = a.C % N == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.w, 16) &&
-               (a.xs * esz) % 16 == 0 && (a.ys * esz) % 16 == 0;
+    // The register paths load 16-byte chunks of every operand row and 16-byte weight vectors.
+    bool vec = a.C % N == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.w, 16) && (a.xs * esz) % 16 == 0 &&
+               (a.ys * esz) % 16 == 0;
     if (kind == Norm::Gated) vec = vec && aligned(a.z, 16) && (a.zs * esz) % 16 == 0;
     if (kind == Norm::Layer) vec = vec && aligned(a.b, 16);
     int W = 0, CH = 0;
@@ -302,9 +397,21 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
     }
     if (!k) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: no kernel for C=%d", what, a.C);
     int64_t blocks;
-    if (W == 1) blocks = (a.rows + 3) / 4;
-    else if (W == 4) blocks = a.rows;
-    else blocks = a.rows < 65536 ? a.rows : 65536;
+    if (W == 1) {
+        // Persistent waves: as many workgroups as stay resident together. A wave that handles several
+        // rows must see one group index, so the wave count is then a multiple of groups.
+        const int64_t need = (a.rows + 3) / 4;
+        blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        if (blocks < need) {
+            const int64_t m = a.groups / gcd64(a.groups, 4);
+            blocks = blocks / m * m;
+            if (blocks == 0) blocks = m;
+        }
+    } else if (W == 4) {
+        blocks = a.rows;
+    } else {
+        blocks = a.rows < 65536 ? a.rows : 65536;
+    }
     if (blocks > 0x7fffffff) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: %lld rows exceed one launch", what, (long long)a.rows);
     hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a);
     return after_launch(ctx, what);

@@ -2,12 +2,13 @@
 // place on the q and k heads of each qkv row (rope.comp:1-55; CPU qwen3_model.cpp:249-253 =
 // cpu::rmsNorm per head, cpu_ops.cpp:502-511, then cpu::rope, cpu_ops.cpp:513-524).
 //
-// Fast path: one wavefront per token row. A head of hd elements is spread over L lanes; lane l
-// holds the V elements [lV, lV+V) of the first half AND their NeoX partners [hd/2 + lV, ...), so the
-// rotation needs no cross-lane exchange. 64/L heads are processed per wave pass and up to U passes
-// are loaded before any is computed. The head's sum of squares (double, like the reference) is
-// reduced over its L lanes with DPP only. The token's cos/sin row and the two norm weight vectors
-// are loaded once per row and reused by every head. V heads are never touched.
+// Fast path: one wavefront per token row, persistent over tokens. A head of hd elements is spread
+// over L lanes; lane l holds the V elements [lV, lV+V) of the first half AND their NeoX partners
+// [hd/2 + lV, ...), so the rotation needs no cross-lane exchange. 64/L heads are processed per wave
+// pass; all passes of a token are loaded at once, and the next token's heads and cos/sin row are in
+// flight while the current token is normalised and rotated. The head's sum of squares (double, like
+// the reference) is reduced over its L lanes with DPP only. The norm weights stay in registers for
+// all tokens of a wave. V heads are never touched.
 //
 // Fallback: one 64-thread workgroup per (head, row) staging the head in LDS (any even hd <= 512).
 #include <cmath>
@@ -37,30 +38,120 @@ __device__ __forceinline__ bool row_position(const QkArgs& a, int64_t t, int64_t
     return pos >= 0 && pos < a.n_pos;
 }
 
-template <typename T, int L, int V, int U>
-__global__ __launch_bounds__(256) void qk_rope_kernel(QkArgs a) {
-    constexpr int HPW = kWave / L;  // heads per wave pass
+// One token's q/k heads held by one wave: U passes of 64/L heads, each lane V elements of the first
+// half of its head and their V partners in the second half.
+template <typename T, int V, int U>
+struct TokenRegs {
     typedef typename VecOf<T, V>::V VT;
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-    if (t >= a.rows) return;
-    int64_t pos;
-    if (!row_position(a, t, pos)) return;  // wave-uniform
+    VT a[U];
+    VT b[U];
+    float c[V];
+    float s[V];
+};
 
-    const int hl = lane % L;  // lane within its head
-    const int hs = lane / L;  // head slot within the pass
+template <typename T, int L, int V, int U>
+__device__ __forceinline__ void load_token(TokenRegs<T, V, U>& tr, const QkArgs& a, int64_t t, int64_t pos, int p0, int hl,
+                                           int hs) {
+    typedef typename VecOf<T, V>::V VT;
+    constexpr int HPW = kWave / L;
     const int half = a.hd / 2;
-    const int i0 = hl * V;  // first rotation pair of this lane
-
-    float cv[V], sv[V];
+    const int i0 = hl * V;
     const float* csr = a.cs + pos * a.hd + 2 * i0;
 #pragma unroll
     for (int e = 0; e < V; e++) {
         const float2v c = *reinterpret_cast<const float2v*>(csr + 2 * e);
-        cv[e] = c[0];
-        sv[e] = c[1];
+        tr.c[e] = c[0];
+        tr.s[e] = c[1];
     }
+    const T* row = static_cast<const T*>(a.qkv) + t * a.stride;
+    const int nh = a.n_q + a.n_kv;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int head = p0 + u * HPW + hs;
+        tr.a[u] = VT{};
+        tr.b[u] = VT{};
+        if (head < nh) {
+            const T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
+            tr.a[u] = load_nt(reinterpret_cast<const VT*>(hp));
+            tr.b[u] = load_nt(reinterpret_cast<const VT*>(hp + half));
+        }
+    }
+}
+
+template <typename T, int L, int V, int U>
+__device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const QkArgs& a, int64_t t, int p0, int hl,
+                                             int hs, bool norm, const float (&wqa)[V], const float (&wqb)[V],
+                                             const float (&wka)[V], const float (&wkb)[V]) {
+    typedef typename VecOf<T, V>::V VT;
+    constexpr int HPW = kWave / L;
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
+    const int nh = a.n_q + a.n_kv;
+    T* row = static_cast<T*>(a.qkv) + t * a.stride;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int head = p0 + u * HPW + hs;
+        float fa[V], fb[V];
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            if constexpr (V == 1) {
+                fa[e] = to_f32(tr.a[u]);
+                fb[e] = to_f32(tr.b[u]);
+            } else {
+                fa[e] = to_f32(tr.a[u][e]);
+                fb[e] = to_f32(tr.b[u][e]);
+            }
+        }
+        if (norm) {
+            // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
+            double ss = 0.0;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
+                ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
+            }
+            ss = group_sum_f64<L>(ss);
+            const float r = static_cast<float>(1.0 / sqrt(ss / a.hd + static_cast<double>(a.eps)));
+            const bool is_q = head < a.n_q;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                fa[e] = fa[e] * r * (is_q ? wqa[e] : wka[e]);
+                fb[e] = fb[e] * r * (is_q ? wqb[e] : wkb[e]);
+            }
+        }
+        VT oa, ob;
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            const float x0 = fa[e] * tr.c[e] - fb[e] * tr.s[e];
+            const float x1 = fa[e] * tr.s[e] + fb[e] * tr.c[e];
+            if constexpr (V == 1) {
+                oa = from_f32<T>(x0);
+                ob = from_f32<T>(x1);
+            } else {
+                oa[e] = from_f32<T>(x0);
+                ob[e] = from_f32<T>(x1);
+            }
+        }
+        if (head < nh) {
+            T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
+            *reinterpret_cast<VT*>(hp) = oa;
+            *reinterpret_cast<VT*>(hp + half) = ob;
+        }
+    }
+}
+
+// Persistent: wave w handles tokens w, w + nw, ... with the norm weights in registers. When a
+// token's heads fit in U passes (FIT), the next token's heads and cos/sin row are loaded before the
+// current token is rotated; otherwise the token is processed in batches of U passes.
+template <typename T, int L, int V, int U, bool FIT>
+__global__ __launch_bounds__(256) void qk_rope_kernel(QkArgs a) {
+    constexpr int HPW = kWave / L;  // heads per wave pass
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int hl = lane % L;  // lane within its head
+    const int hs = lane / L;  // head slot within the pass
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
     const bool norm = a.wqk != nullptr;
     float wqa[V], wqb[V], wka[V], wkb[V];
 #pragma unroll
@@ -70,71 +161,35 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QkArgs a) {
         wka[e] = norm ? a.wqk[a.hd + i0 + e] : 1.0f;
         wkb[e] = norm ? a.wqk[a.hd + half + i0 + e] : 1.0f;
     }
-
-    T* row = static_cast<T*>(a.qkv) + t * a.stride;
+    // Next token of this wave with a position inside the table (rows outside it stay untouched).
+    auto next_valid = [&](int64_t t, int64_t& pos) -> int64_t {
+        for (; t < a.rows; t += nw)
+            if (row_position(a, t, pos)) return t;
+        return a.rows;
+    };
+    int64_t pos;
+    int64_t t = next_valid(static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6), pos);
+    if (t >= a.rows) return;  // wave-uniform
     const int nh = a.n_q + a.n_kv;
-    for (int p0 = 0; p0 < nh; p0 += HPW * U) {
-        VT va[U], vb[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int head = p0 + u * HPW + hs;
-            va[u] = VT{};
-            vb[u] = VT{};
-            if (head < nh) {
-                const T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
-                va[u] = *reinterpret_cast<const VT*>(hp);
-                vb[u] = *reinterpret_cast<const VT*>(hp + half);
-            }
+    if constexpr (FIT) {
+        TokenRegs<T, V, U> cur, nxt;
+        load_token<T, L, V, U>(cur, a, t, pos, 0, hl, hs);
+        while (t < a.rows) {
+            int64_t npos;
+            const int64_t tn = next_valid(t + nw, npos);
+            if (tn < a.rows) load_token<T, L, V, U>(nxt, a, tn, npos, 0, hl, hs);
+            rotate_token<T, L, V, U>(cur, a, t, 0, hl, hs, norm, wqa, wqb, wka, wkb);
+            t = tn;
+            if (tn < a.rows) cur = nxt;
         }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int head = p0 + u * HPW + hs;
-            float fa[V], fb[V];
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                if constexpr (V == 1) {
-                    fa[e] = to_f32(va[u]);
-                    fb[e] = to_f32(vb[u]);
-                } else {
-                    fa[e] = to_f32(va[u][e]);
-                    fb[e] = to_f32(vb[u][e]);
-                }
+    } else {
+        while (t < a.rows) {
+            for (int p0 = 0; p0 < nh; p0 += HPW * U) {
+                TokenRegs<T, V, U> cur;
+                load_token<T, L, V, U>(cur, a, t, pos, p0, hl, hs);
+                rotate_token<T, L, V, U>(cur, a, t, p0, hl, hs, norm, wqa, wqb, wka, wkb);
             }
-            if (norm) {
-                // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
-                double ss = 0.0;
-#pragma unroll
-                for (int e = 0; e < V; e++) {
-                    ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
-                    ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
-                }
-                ss = group_sum_f64<L>(ss);
-                const float r = static_cast<float>(1.0 / sqrt(ss / a.hd + static_cast<double>(a.eps)));
-                const bool is_q = head < a.n_q;
-#pragma unroll
-                for (int e = 0; e < V; e++) {
-                    fa[e] = fa[e] * r * (is_q ? wqa[e] : wka[e]);
-                    fb[e] = fb[e] * r * (is_q ? wqb[e] : wkb[e]);
-                }
-            }
-            VT oa, ob;
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                const float x0 = fa[e] * cv[e] - fb[e] * sv[e];
-                const float x1 = fa[e] * sv[e] + fb[e] * cv[e];
-                if constexpr (V == 1) {
-                    oa = from_f32<T>(x0);
-                    ob = from_f32<T>(x1);
-                } else {
-                    oa[e] = from_f32<T>(x0);
-                    ob[e] = from_f32<T>(x1);
-                }
-            }
-            if (head < nh) {
-                T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
-                *reinterpret_cast<VT*>(hp) = oa;
-                *reinterpret_cast<VT*>(hp + half) = ob;
-            }
+            t = next_valid(t + nw, pos);
         }
     }
 }
@@ -176,26 +231,48 @@ __global__ __launch_bounds__(64) void qk_rope_generic(QkArgs a) {
 
 typedef void (*QkKernel)(QkArgs);
 
+template <typename T, int L, int V, int U>
+QkKernel pick_fit(bool fit) {
+    return fit ? qk_rope_kernel<T, L, V, U, true> : qk_rope_kernel<T, L, V, U, false>;
+}
+
+// U = passes per token when they fit in 8, else batches of 8 passes.
+template <typename T, int L, int V>
+QkKernel pick_u(int passes) {
+    switch (passes) {
+        case 1: return pick_fit<T, L, V, 1>(true);
+        case 2: return pick_fit<T, L, V, 2>(true);
+        case 3: return pick_fit<T, L, V, 3>(true);
+        case 4: return pick_fit<T, L, V, 4>(true);
+        case 5: return pick_fit<T, L, V, 5>(true);
+        case 6: return pick_fit<T, L, V, 6>(true);
+        case 7: return pick_fit<T, L, V, 7>(true);
+        case 8: return pick_fit<T, L, V, 8>(true);
+    }
+    return pick_fit<T, L, V, 8>(false);
+}
+
 template <typename T, int V>
-QkKernel pick_l(int L) {
+QkKernel pick_l(int L, int nh) {
+    const int passes = (nh + kWave / L - 1) / (kWave / L);
     switch (L) {
-        case 2: return qk_rope_kernel<T, 2, V, 8>;
-        case 4: return qk_rope_kernel<T, 4, V, 8>;
-        case 8: return qk_rope_kernel<T, 8, V, 8>;
-        case 16: return qk_rope_kernel<T, 16, V, 4>;
-        case 32: return qk_rope_kernel<T, 32, V, 4>;
-        case 64: return qk_rope_kernel<T, 64, V, 4>;
+        case 2: return pick_u<T, 2, V>(passes);
+        case 4: return pick_u<T, 4, V>(passes);
+        case 8: return pick_u<T, 8, V>(passes);
+        case 16: return pick_u<T, 16, V>(passes);
+        case 32: return pick_u<T, 32, V>(passes);
+        case 64: return pick_u<T, 64, V>(passes);
     }
     return nullptr;
 }
 
 template <typename T>
-QkKernel pick_lv(int L, int V) {
+QkKernel pick_lv(int L, int V, int nh) {
     switch (V) {
-        case 1: return pick_l<T, 1>(L);
-        case 2: return pick_l<T, 2>(L);
-        case 4: return pick_l<T, 4>(L);
-        case 8: return pick_l<T, 8>(L);
+        case 1: return pick_l<T, 1>(L, nh);
+        case 2: return pick_l<T, 2>(L, nh);
+        case 4: return pick_l<T, 4>(L, nh);
+        case 8: return pick_l<T, 8>(L, nh);
     }
     return nullptr;
 }
@@ -233,10 +310,12 @@ extern "C" int neko_hip_qk_norm_rope(neko_hip_ctx* ctx, void* qkv, int64_t row_s
         const size_t vb = V * esz;
         if (!aligned(qkv, vb) || (row_stride * esz) % vb || (half * esz) % vb) continue;
         if (!aligned(cs, 8)) break;
-        k = dtype == NEKO_DT_F16 ? pick_lv<half_t>(L, V) : pick_lv<float>(L, V);
+        k = dtype == NEKO_DT_F16 ? pick_lv<half_t>(L, V, nh) : pick_lv<float>(L, V, nh);
     }
     if (k) {
-        hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>((rows + 3) / 4)), dim3(256), 0, ctx->stream,
+        // Persistent waves: as many workgroups as stay resident together.
+        const int64_t blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, (rows + 3) / 4);
+        hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream,
                            QkArgs{qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps});
         return after_launch(ctx, what);
     }

@@ -2,6 +2,8 @@
 // contract, gpu/compute.h:28-44, expressed as plain C over one in-order HIP stream per context).
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <unordered_map>
 
 #include "internal.h"
 
@@ -44,6 +46,26 @@ FastDiv make_fast_div(uint32_t d) {
     return FastDiv{d, static_cast<uint32_t>(m), s};
 }
 
+int resident_blocks_per_cu(const void* kernel, int block) {
+    static std::mutex mu;
+    static std::unordered_map<const void*, int> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(kernel);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        n = 1;
+    }
+    cache.emplace(kernel, n);
+    return n;
+}
+
+int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks) {
+    const int64_t cap = static_cast<int64_t>(ctx->cu_count > 0 ? ctx->cu_count : 256) * resident_blocks_per_cu(kernel, block);
+    return work_blocks < cap ? work_blocks : cap;
+}
+
 }  // namespace neko_hip
 
 using namespace neko_hip;
@@ -72,13 +94,7 @@ int neko_hip_create(int device, neko_hip_ctx** out) {
     ctx->cu_count = prop.multiProcessorCount;
     ctx->max_alloc = prop.totalGlobalMem;
     ctx->name = prop.name;
-    // A blocking stream: ordered with the device's null stream, so work a caller queued there (e.g. a
-    // framework's default stream) is never overtaken.
-    if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamDefault) != hipSuccess) {
-        delete ctx;
-        return fail(nullptr, NEKO_ERR_HIP, "neko_hip_create: hipStreamCreate failed");
-    }
-    ctx->stream = ctx->own_stream;
+    ctx->stream = nullptr;  // the device's null stream until the caller routes work elsewhere
     *out = ctx;
     return NEKO_OK;
 }
@@ -88,7 +104,6 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     int rc = enter(ctx);
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (void* p : ctx->allocs) (void)hipFree(p);
-    (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return rc;
 }
@@ -105,7 +120,7 @@ size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx) { return ctx ? ctx->ma
 
 int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream) {
     NEKO_ENTER(ctx);
-    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
     return NEKO_OK;
 }
 

@@ -20,7 +20,7 @@ from ._lib import DT_F16, DT_F32, FMT_F16, FMT_FP4, FMT_FP8, NEKO_OK, NekoError,
 
 __all__ = [
     "Context", "context", "layer_norm", "rms_norm", "qk_norm_rope", "silu_mul", "gelu", "gated_rms_norm", "embed",
-    "quant_row_bytes", "quantize_rows", "rope_table", "FMT_F16", "FMT_FP8", "FMT_FP4", "NekoError",
+    "prepare", "quant_row_bytes", "quantize_rows", "rope_table", "FMT_F16", "FMT_FP8", "FMT_FP4", "NekoError",
 ]
 
 
@@ -34,6 +34,7 @@ class Context:
             raise NekoError(lib.neko_hip_last_error(None).decode(), rc)
         self.handle = h.value
         self.device = int(device)
+        self._bound = -1  # stream handle last routed to the C context
 
     def check(self, rc: int) -> None:
         if rc != NEKO_OK:
@@ -42,7 +43,9 @@ class Context:
     def bind_torch_stream(self) -> None:
         """Orders the next ops after work already queued on torch's current stream."""
         s = torch.cuda.current_stream(self.device).cuda_stream
-        self.check(lib.neko_hip_set_stream(self.handle, s or None))
+        if s != self._bound:  # 0 is the null stream, which the C context uses for NULL too
+            self.check(lib.neko_hip_set_stream(self.handle, s or None))
+            self._bound = s
 
     def synchronize(self) -> None:
         self.check(lib.neko_hip_synchronize(self.handle))
@@ -111,6 +114,39 @@ def _ctx_for(t: torch.Tensor) -> Context:
     return ctx
 
 
+_recording = threading.local()
+
+
+def _issue(ctx: Context, fn, *args):
+    rec = getattr(_recording, "rec", None)
+    if rec is not None:  # being prepared: remember the call instead of issuing it
+        rec.append((fn, args))
+        return
+    ctx.check(fn(*args))
+
+
+def prepare(op, *args, **kwargs):
+    """Validates op(*args, **kwargs) once and returns (run, result): run() re-issues the same C call
+    on the same buffers with no Python-side checks -- for tight loops that replay one op. The stream
+    is the torch stream current at preparation time."""
+    _recording.rec = rec = []
+    try:
+        result = op(*args, **kwargs)
+    finally:
+        _recording.rec = None
+    if len(rec) != 1:
+        raise NekoError(f"prepare: {getattr(op, '__name__', op)} issued {len(rec)} calls; expected one")
+    fn, cargs = rec[0]
+    handle = cargs[0]
+
+    def run():
+        rc = fn(*cargs)
+        if rc != NEKO_OK:
+            raise NekoError(lib.neko_hip_last_error(handle).decode(), rc)
+
+    return run, result
+
+
 def _out_like(x: torch.Tensor, rows: int, cols: int, out: torch.Tensor | None, name: str) -> torch.Tensor:
     if out is None:
         return torch.empty((rows, cols), dtype=x.dtype, device=x.device)
@@ -126,9 +162,9 @@ def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: fl
     rows, C, xs = _rows(x, "x")
     out = _out_like(x, rows, C, out, "out")
     ctx = _ctx_for(x)
-    ctx.check(lib.neko_hip_layernorm(ctx.handle, x.data_ptr(), xs, out.data_ptr(), out.stride(0),
+    _issue(ctx, lib.neko_hip_layernorm, ctx.handle, x.data_ptr(), xs, out.data_ptr(), out.stride(0),
                                      _vec(gamma, C, "gamma", x.device), _vec(beta, C, "beta", x.device), rows, C,
-                                     float(eps), _dtype_code(x)))
+                                     float(eps), _dtype_code(x))
     return out
 
 
@@ -137,8 +173,8 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | N
     rows, C, xs = _rows(x, "x")
     out = _out_like(x, rows, C, out, "out")
     ctx = _ctx_for(x)
-    ctx.check(lib.neko_hip_rmsnorm(ctx.handle, x.data_ptr(), xs, out.data_ptr(), out.stride(0),
-                                   _vec(w, C, "w", x.device), rows, C, float(eps), _dtype_code(x)))
+    _issue(ctx, lib.neko_hip_rmsnorm, ctx.handle, x.data_ptr(), xs, out.data_ptr(), out.stride(0),
+                                   _vec(w, C, "w", x.device), rows, C, float(eps), _dtype_code(x))
     return out
 
 
@@ -152,8 +188,8 @@ def gated_rms_norm(y: torch.Tensor, z: torch.Tensor, w: torch.Tensor, groups: in
         raise NekoError(f"z must be {y.dtype} with {rows} rows of at least {D} columns")
     out = _out_like(y, rows, D, out, "out")
     ctx = _ctx_for(y)
-    ctx.check(lib.neko_hip_gated_rmsnorm(ctx.handle, y.data_ptr(), ys, z.data_ptr(), zs, out.data_ptr(), out.stride(0),
-                                         _vec(w, D, "w", y.device), rows, D, int(groups), float(eps), _dtype_code(y)))
+    _issue(ctx, lib.neko_hip_gated_rmsnorm, ctx.handle, y.data_ptr(), ys, z.data_ptr(), zs, out.data_ptr(), out.stride(0),
+                                         _vec(w, D, "w", y.device), rows, D, int(groups), float(eps), _dtype_code(y))
     return out
 
 
@@ -172,9 +208,9 @@ def qk_norm_rope(qkv: torch.Tensor, n_q: int, n_kv: int, hd: int, cs: torch.Tens
             raise NekoError("positions must be a contiguous int32 vector with one entry per row")
         pos_ptr = positions.data_ptr()
     ctx = _ctx_for(qkv)
-    ctx.check(lib.neko_hip_qk_norm_rope(ctx.handle, qkv.data_ptr(), stride, rows, int(n_q), int(n_kv), int(hd),
+    _issue(ctx, lib.neko_hip_qk_norm_rope, ctx.handle, qkv.data_ptr(), stride, rows, int(n_q), int(n_kv), int(hd),
                                         int(pos0), pos_ptr, _vec(wqk, 2 * hd, "wqk", qkv.device), cs.data_ptr(),
-                                        cs.shape[0], float(eps), _dtype_code(qkv)))
+                                        cs.shape[0], float(eps), _dtype_code(qkv))
     return qkv
 
 
@@ -186,7 +222,7 @@ def silu_mul(h: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     I = two_i // 2
     out = _out_like(h, rows, I, out, "out")
     ctx = _ctx_for(h)
-    ctx.check(lib.neko_hip_swiglu(ctx.handle, h.data_ptr(), hs, out.data_ptr(), out.stride(0), rows, I, _dtype_code(h)))
+    _issue(ctx, lib.neko_hip_swiglu, ctx.handle, h.data_ptr(), hs, out.data_ptr(), out.stride(0), rows, I, _dtype_code(h))
     return out
 
 
@@ -199,7 +235,7 @@ def gelu(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
         raise NekoError("out must match x")
     ctx = _ctx_for(x)
-    ctx.check(lib.neko_hip_gelu_tanh(ctx.handle, x.data_ptr(), out.data_ptr(), x.numel(), _dtype_code(x)))
+    _issue(ctx, lib.neko_hip_gelu_tanh, ctx.handle, x.data_ptr(), out.data_ptr(), x.numel(), _dtype_code(x))
     return out
 
 
@@ -228,9 +264,9 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base:
             raise NekoError("wpe must be a contiguous float16 [P, C] table")
         wpe_ptr, wpe_rows = wpe.data_ptr(), wpe.shape[0]
     ctx = _ctx_for(tokens)
-    ctx.check(lib.neko_hip_embed(ctx.handle, tokens.data_ptr(), T, table.data_ptr(), table.shape[1], int(fmt), int(C),
+    _issue(ctx, lib.neko_hip_embed, ctx.handle, tokens.data_ptr(), T, table.data_ptr(), table.shape[1], int(fmt), int(C),
                                  int(row_base), n_rows, wpe_ptr, wpe_rows, int(pos0), out.data_ptr(), os_,
-                                 _dtype_code(out)))
+                                 _dtype_code(out))
     return out
 
 
