@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--no-flush", action="store_true", help="skip the cache flush (cache-warm figures)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--only", default=None, help="time a single op (for profiling runs)")
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
 
 
@@ -84,6 +86,13 @@ def gpu_bench(args):
                 calls[name]()
                 e.record()
 
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        flush.sum()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         step(None)
     events = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for n in names}

@@ -17,6 +17,15 @@
 
 #include "internal.h"
 
+// Build-time tuning knobs (measured defaults): whether a persistent wave prefetches its next row, and
+// whether the grid is capped at the resident workgroup count (persistent) or covers every row.
+#ifndef NEKO_TUNE_NORM_PF
+#define NEKO_TUNE_NORM_PF 1
+#endif
+#ifndef NEKO_TUNE_NORM_FULLGRID
+#define NEKO_TUNE_NORM_FULLGRID 0
+#endif
+
 namespace neko_hip {
 namespace {
 
@@ -199,12 +208,13 @@ __device__ __forceinline__ void store_row(T* y, const F& f, float scale, float m
 // keeps the weights in registers across rows and loads the next row while it normalises this one.
 // Every row of a wave shares one group index (the host makes nw a multiple of groups, or gives
 // each wave at most one row).
-template <Norm K, typename T, int CH>
+template <Norm K, typename T, int CH, bool PF = NEKO_TUNE_NORM_PF>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     constexpr int N = Chunk16<T>::N;
     const int lane = threadIdx.x & 63;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
-    int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    // readfirstlane tells the compiler the row index is wave-uniform, so row pointers stay in SGPRs.
+    int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (r >= a.rows) return;  // wave-uniform
     const int nch = a.C / N;
     const RowPtrs<K, T> p0 = row_ptrs<K, T>(a, r);
@@ -215,7 +225,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     load_row<K, T, CH, kWave>(cur, p0, lane, nch);
     for (; r < a.rows; r += nw) {
         const bool more = r + nw < a.rows;
-        if (more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
+        if (PF && more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
         RowVals<K, T, CH> f;
         f.init(cur);
         float scale, mean_f = 0.0f;
@@ -229,7 +239,8 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
             scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
         }
         store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wv, bv, lane, nch);
-        if (more) cur = nxt;
+        if (PF && more) cur = nxt;
+        else if (more) load_row<K, T, CH, kWave>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
     }
 }
 
@@ -401,7 +412,7 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         // Persistent waves: as many workgroups as stay resident together. A wave that handles several
         // rows must see one group index, so the wave count is then a multiple of groups.
         const int64_t need = (a.rows + 3) / 4;
-        blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        blocks = NEKO_TUNE_NORM_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
         if (blocks < need) {
             const int64_t m = a.groups / gcd64(a.groups, 4);
             blocks = blocks / m * m;

@@ -15,6 +15,19 @@
 
 #include "internal.h"
 
+// Build-time tuning knobs (measured defaults): persistent grid vs one token per wave, and the widest
+// per-lane vector (elements) a head half is split into.
+#ifndef NEKO_TUNE_QK_FULLGRID
+#define NEKO_TUNE_QK_FULLGRID 0
+#endif
+#ifndef NEKO_TUNE_QK_MAXV
+#define NEKO_TUNE_QK_MAXV 8
+#endif
+// Minimum waves per SIMD the rolling kernel is compiled for (caps its VGPRs at 512 / waves).
+#ifndef NEKO_TUNE_QK_WAVES
+#define NEKO_TUNE_QK_WAVES 3
+#endif
+
 namespace neko_hip {
 namespace {
 
@@ -140,16 +153,157 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
     }
 }
 
-// Persistent: wave w handles tokens w, w + nw, ... with the norm weights in registers. When a
-// token's heads fit in U passes (FIT), the next token's heads and cos/sin row are loaded before the
-// current token is rotated; otherwise the token is processed in batches of U passes.
-template <typename T, int L, int V, int U, bool FIT>
-__global__ __launch_bounds__(256) void qk_rope_kernel(QkArgs a) {
+// Rolling pipeline for tokens whose heads fit in U passes: a wave holds one token's q/k heads in
+// registers; as each pass of token t is normalised, rotated and stored, the same registers receive
+// that pass of the wave's next token. A whole token of loads is therefore always in flight behind
+// the token being computed, with one token's worth of data registers, and because every load is
+// issued after the stores it follows, waiting for it never waits on later stores. The norm weights
+// are staged in LDS once per workgroup and read per pass; the cos/sin row of the next token is
+// loaded one token ahead.
+template <typename T, int L, int V, int U>
+__global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(QkArgs a) {
+    constexpr int HPW = kWave / L;  // heads per wave pass
+    typedef typename VecOf<T, V>::V VT;
+    __shared__ float wsh[2 * 512];
+    const bool norm = a.wqk != nullptr;
+    if (norm)
+        for (int i = threadIdx.x; i < 2 * a.hd; i += 256) wsh[i] = a.wqk[i];
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, kept in SGPRs
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int hl = lane % L;
+    const int hs = lane / L;
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
+    const int nh = a.n_q + a.n_kv;
+    auto next_valid = [&](int64_t t, int64_t& pos) -> int64_t {
+        for (; t < a.rows; t += nw)
+            if (row_position(a, t, pos)) return t;
+        return a.rows;
+    };
+    auto load_cs = [&](int64_t pos, float (&c)[V], float (&s)[V]) {
+        const float* csr = a.cs + pos * a.hd + 2 * i0;
+#pragma unroll
+        for (int e = 0; e < V; e += 2) {
+            if constexpr (V == 1) {
+                const float2v v = *reinterpret_cast<const float2v*>(csr);
+                c[0] = v[0];
+                s[0] = v[1];
+            } else {
+                const float4v v = *reinterpret_cast<const float4v*>(csr + 2 * e);
+                c[e] = v[0];
+                s[e] = v[1];
+                c[e + 1] = v[2];
+                s[e + 1] = v[3];
+            }
+        }
+    };
+
+    int64_t pos;
+    int64_t t = next_valid(static_cast<int64_t>(blockIdx.x) * 4 + wave, pos);
+    if (t >= a.rows) return;
+
+    VT A[U], B[U];
+    float cc[V], sn[V];
+    load_cs(pos, cc, sn);
+    {
+        const T* row = static_cast<const T*>(a.qkv) + t * a.stride;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int head = u * HPW + hs;
+            A[u] = VT{};
+            B[u] = VT{};
+            if (head < nh) {
+                A[u] = load_nt(reinterpret_cast<const VT*>(row + head * a.hd + i0));
+                B[u] = load_nt(reinterpret_cast<const VT*>(row + head * a.hd + half + i0));
+            }
+        }
+    }
+    while (t < a.rows) {
+        int64_t npos;
+        const int64_t tn = next_valid(t + nw, npos);
+        const bool more = tn < a.rows;
+        float ncc[V], nsn[V];
+        if (more) load_cs(npos, ncc, nsn);
+        T* row = static_cast<T*>(a.qkv) + t * a.stride;
+        const T* nrow = static_cast<const T*>(a.qkv) + (more ? tn : t) * a.stride;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int head = u * HPW + hs;
+            float fa[V], fb[V];
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                if constexpr (V == 1) {
+                    fa[e] = to_f32(A[u]);
+                    fb[e] = to_f32(B[u]);
+                } else {
+                    fa[e] = to_f32(A[u][e]);
+                    fb[e] = to_f32(B[u][e]);
+                }
+            }
+            if (norm) {
+                // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
+                double ss = 0.0;
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
+                    ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
+                }
+                ss = group_sum_f64<L>(ss);
+                const float r = static_cast<float>(1.0 / sqrt(ss / a.hd + static_cast<double>(a.eps)));
+                const float* w = wsh + (head < a.n_q ? 0 : a.hd) + i0;
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    fa[e] = fa[e] * r * w[e];
+                    fb[e] = fb[e] * r * w[half + e];
+                }
+            }
+            VT oa, ob;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                const float x0 = fa[e] * cc[e] - fb[e] * sn[e];
+                const float x1 = fa[e] * sn[e] + fb[e] * cc[e];
+                if constexpr (V == 1) {
+                    oa = from_f32<T>(x0);
+                    ob = from_f32<T>(x1);
+                } else {
+                    oa[e] = from_f32<T>(x0);
+                    ob[e] = from_f32<T>(x1);
+                }
+            }
+            if (head < nh) {
+                T* hp = row + head * a.hd + i0;
+                *reinterpret_cast<VT*>(hp) = oa;
+                *reinterpret_cast<VT*>(hp + half) = ob;
+                if (more) {
+                    A[u] = load_nt(reinterpret_cast<const VT*>(nrow + head * a.hd + i0));
+                    B[u] = load_nt(reinterpret_cast<const VT*>(nrow + head * a.hd + half + i0));
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                cc[e] = ncc[e];
+                sn[e] = nsn[e];
+            }
+        }
+        t = tn;
+    }
+}
+
+// Tokens with more heads than U passes: persistent waves, each token in batches of U passes, the norm
+// weights in registers.
+template <typename T, int L, int V, int U>
+__global__ __launch_bounds__(256) void qk_rope_batch_kernel(QkArgs a) {
     constexpr int HPW = kWave / L;  // heads per wave pass
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
-    const int hl = lane % L;  // lane within its head
-    const int hs = lane / L;  // head slot within the pass
+    const int hl = lane % L;
+    const int hs = lane / L;
     const int half = a.hd / 2;
     const int i0 = hl * V;
     const bool norm = a.wqk != nullptr;
@@ -161,35 +315,14 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(QkArgs a) {
         wka[e] = norm ? a.wqk[a.hd + i0 + e] : 1.0f;
         wkb[e] = norm ? a.wqk[a.hd + half + i0 + e] : 1.0f;
     }
-    // Next token of this wave with a position inside the table (rows outside it stay untouched).
-    auto next_valid = [&](int64_t t, int64_t& pos) -> int64_t {
-        for (; t < a.rows; t += nw)
-            if (row_position(a, t, pos)) return t;
-        return a.rows;
-    };
-    int64_t pos;
-    int64_t t = next_valid(static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6), pos);
-    if (t >= a.rows) return;  // wave-uniform
     const int nh = a.n_q + a.n_kv;
-    if constexpr (FIT) {
-        TokenRegs<T, V, U> cur, nxt;
-        load_token<T, L, V, U>(cur, a, t, pos, 0, hl, hs);
-        while (t < a.rows) {
-            int64_t npos;
-            const int64_t tn = next_valid(t + nw, npos);
-            if (tn < a.rows) load_token<T, L, V, U>(nxt, a, tn, npos, 0, hl, hs);
-            rotate_token<T, L, V, U>(cur, a, t, 0, hl, hs, norm, wqa, wqb, wka, wkb);
-            t = tn;
-            if (tn < a.rows) cur = nxt;
-        }
-    } else {
-        while (t < a.rows) {
-            for (int p0 = 0; p0 < nh; p0 += HPW * U) {
-                TokenRegs<T, V, U> cur;
-                load_token<T, L, V, U>(cur, a, t, pos, p0, hl, hs);
-                rotate_token<T, L, V, U>(cur, a, t, p0, hl, hs, norm, wqa, wqb, wka, wkb);
-            }
-            t = next_valid(t + nw, pos);
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave; t < a.rows; t += nw) {
+        int64_t pos;
+        if (!row_position(a, t, pos)) continue;  // rows outside the table stay untouched
+        for (int p0 = 0; p0 < nh; p0 += HPW * U) {
+            TokenRegs<T, V, U> cur;
+            load_token<T, L, V, U>(cur, a, t, pos, p0, hl, hs);
+            rotate_token<T, L, V, U>(cur, a, t, p0, hl, hs, norm, wqa, wqb, wka, wkb);
         }
     }
 }
@@ -233,7 +366,7 @@ typedef void (*QkKernel)(QkArgs);
 
 template <typename T, int L, int V, int U>
 QkKernel pick_fit(bool fit) {
-    return fit ? qk_rope_kernel<T, L, V, U, true> : qk_rope_kernel<T, L, V, U, false>;
+    return fit ? qk_rope_roll_kernel<T, L, V, U> : qk_rope_batch_kernel<T, L, V, U>;
 }
 
 // U = passes per token when they fit in 8, else batches of 8 passes.
@@ -303,7 +436,8 @@ extern "C" int neko_hip_qk_norm_rope(neko_hip_ctx* ctx, void* qkv, int64_t row_s
     const int half = hd / 2;
     QkKernel k = nullptr;
     // Widest per-lane vector whose lane count per head is a power of two and whose loads stay aligned.
-    for (int V = static_cast<int>(16 / esz); V >= 1 && !k; V /= 2) {
+    const int vmax = static_cast<int>(16 / esz) < NEKO_TUNE_QK_MAXV ? static_cast<int>(16 / esz) : NEKO_TUNE_QK_MAXV;
+    for (int V = vmax; V >= 1 && !k; V /= 2) {
         if (half % V) continue;
         const int L = half / V;
         if (L < 2 || L > 64 || (L & (L - 1))) continue;
@@ -314,7 +448,8 @@ extern "C" int neko_hip_qk_norm_rope(neko_hip_ctx* ctx, void* qkv, int64_t row_s
     }
     if (k) {
         // Persistent waves: as many workgroups as stay resident together.
-        const int64_t blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, (rows + 3) / 4);
+        const int64_t need = (rows + 3) / 4;
+        const int64_t blocks = NEKO_TUNE_QK_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
         hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream,
                            QkArgs{qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps});
         return after_launch(ctx, what);
