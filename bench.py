@@ -5,7 +5,9 @@ Workload (one step = one layer's hot path over one batch): 4 x 2048 = 8192 token
 theta 1e6, positions 0..2047 per sequence) -> post-attention RMSNorm [8192, 2560] -> SwiGLU on
 gate/up [8192, 9728]. Inputs are resident in HBM before timing.
 
-Each op is timed with HIP events on the stream it runs on, after a 1 GiB streaming read that
+Each op is timed with HIP events (created with hipEventDisableSystemFence, so recording them does not
+write back and invalidate the caches; their intervals then match rocprofv3's kernel durations) on
+the stream it runs on, after a 1 GiB streaming read that
 evicts L2 and the 256 MB Infinity Cache, so every op reads its operands from HBM (the flush is
 outside the event pair). The sweep reads, so it leaves no dirty lines whose write-back the timed op
 would pay for. value = algorithmic bytes of the four ops / sum of their median times.
@@ -48,6 +50,49 @@ def parse():
     return p.parse_args()
 
 
+class HipTimer:
+    """Start/stop HIP event pairs on one stream, created with hipEventDisableSystemFence."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self, stream: int):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch already loaded
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.stream = ctypes.c_void_p(stream or None)
+        self.events = []
+
+    def pair(self):
+        ev = []
+        for _ in range(2):
+            e = self.ct.c_void_p()
+            if self.hip.hipEventCreateWithFlags(self.ct.byref(e), self.DISABLE_SYSTEM_FENCE) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            ev.append(e)
+        self.events += ev
+        return ev
+
+    def record(self, e):
+        if self.hip.hipEventRecord(e, self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, s, e) -> float:
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), s, e) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def close(self):
+        for e in self.events:
+            self.hip.hipEventDestroy(e)
+        self.events = []
+
+
 def gpu_bench(args):
     import torch
 
@@ -74,6 +119,8 @@ def gpu_bench(args):
     }
     names = [args.only] if args.only else list(OPS)
 
+    timer = HipTimer(torch.cuda.current_stream().cuda_stream)
+
     def step(record):
         for name in names:
             if not args.no_flush:
@@ -82,9 +129,9 @@ def gpu_bench(args):
                 calls[name]()
             else:
                 s, e = record[name]
-                s.record()
+                timer.record(s)
                 calls[name]()
-                e.record()
+                timer.record(e)
 
     if args.copy_mib:
         src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
@@ -95,8 +142,7 @@ def gpu_bench(args):
         del src, dst
     for _ in range(args.warmup):
         step(None)
-    events = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for n in names}
-              for _ in range(args.steps)]
+    events = [{n: timer.pair() for n in names} for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
@@ -106,11 +152,12 @@ def gpu_bench(args):
 
     per_op = {}
     for n in names:
-        times_ms = [events[k][n][0].elapsed_time(events[k][n][1]) for k in range(args.steps)]
+        times_ms = [timer.elapsed_ms(*events[k][n]) for k in range(args.steps)]
         med = statistics.median(times_ms)
         gbs = op_bytes[n] / (med * 1e-3) / 1e9
         per_op[n] = {"us": round(med * 1e3, 3), "mean_us": round(statistics.fmean(times_ms) * 1e3, 3),
                      "bytes": op_bytes[n], "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    timer.close()
     return cfg, per_op, wall
 
 

@@ -17,7 +17,9 @@
 
 #include "internal.h"
 
-// Build-time tuning knobs (measured defaults): whether a persistent wave prefetches its next row, and
+// Build-time tuning knobs (measured defaults): how a persistent wave overlaps its next row's loads
+// (0: not at all, 1: a second row buffer loaded before the current row is reduced, 2: rolling -- each
+// output chunk's registers are refilled with the next row's chunk right after its store), and
 // whether the grid is capped at the resident workgroup count (persistent) or covers every row.
 #ifndef NEKO_TUNE_NORM_PF
 #define NEKO_TUNE_NORM_PF 1
@@ -208,7 +210,7 @@ __device__ __forceinline__ void store_row(T* y, const F& f, float scale, float m
 // keeps the weights in registers across rows and loads the next row while it normalises this one.
 // Every row of a wave shares one group index (the host makes nw a multiple of groups, or gives
 // each wave at most one row).
-template <Norm K, typename T, int CH, bool PF = NEKO_TUNE_NORM_PF>
+template <Norm K, typename T, int CH, int PF = NEKO_TUNE_NORM_PF>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     constexpr int N = Chunk16<T>::N;
     const int lane = threadIdx.x & 63;
@@ -225,7 +227,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     load_row<K, T, CH, kWave>(cur, p0, lane, nch);
     for (; r < a.rows; r += nw) {
         const bool more = r + nw < a.rows;
-        if (PF && more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
+        if (PF == 1 && more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
         RowVals<K, T, CH> f;
         f.init(cur);
         float scale, mean_f = 0.0f;
@@ -238,9 +240,35 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
             const double ss = wave_sum_f64(sum_squares<CH, N>(f));
             scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
         }
-        store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wv, bv, lane, nch);
-        if (PF && more) cur = nxt;
-        else if (more) load_row<K, T, CH, kWave>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
+        if constexpr (PF == 2) {
+            // Rolling: store chunk k, then load chunk k of the next row into the registers it used.
+            typedef typename Chunk16<T>::V V;
+            T* y = row_ptrs<K, T>(a, r).y;
+            const RowPtrs<K, T> pn = row_ptrs<K, T>(a, more ? r + nw : r);
+#pragma unroll
+            for (int k = 0; k < CH; k++) {
+                const int j = k * kWave + lane;
+                if (j >= nch) continue;
+                V out;
+#pragma unroll
+                for (int e = 0; e < N; e++) {
+                    const float w = wv[k][e / 4][e % 4];
+                    float v;
+                    if constexpr (K == Norm::Layer) v = (f(k, e) - mean_f) * scale * w + bv[k][e / 4][e % 4];
+                    else v = f(k, e) * scale * w;
+                    out[e] = from_f32<T>(v);
+                }
+                store_nt(reinterpret_cast<V*>(y + j * N), out);
+                if (more) {
+                    cur.x[k] = load_nt(reinterpret_cast<const V*>(pn.x + j * N));
+                    if constexpr (K == Norm::Gated) cur.z[k] = load_nt(reinterpret_cast<const V*>(pn.z + j * N));
+                }
+            }
+        } else {
+            store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wv, bv, lane, nch);
+            if (PF == 1 && more) cur = nxt;
+            else if (more) load_row<K, T, CH, kWave>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
+        }
     }
 }
 
