@@ -1,13 +1,14 @@
 // Embedding gather with fused row dequantisation for gfx950 (embed.comp:1-51,
 // QMatrix::dequantizeRow quant.cpp:230-253, GPT-2 wte + wpe gpt2_model.cpp:182-187).
 //
-// One wavefront per token. Each lane takes one 16-byte chunk of the stored row per step:
-//   F16: 8 halves;  FP8: 16 codes sharing one block scale;  FP4: one whole 32-weight block
-//   (weight j in the low nibble of byte j, weight 16 + j in the high nibble).
+// Each wavefront gathers a few consecutive tokens with all their rows' loads in flight at once; each
+// lane produces one 16-byte chunk of an output row per step (see embed_kernel), so every store
+// instruction writes whole cache lines.
 // Codes are decoded with the reference's bit trick (the code's bits placed into an f16 pattern that
 // equals value / 256 for E4M3 or value / 16384 for E2M1, subnormals included), then multiplied in
 // f32 by scale * 256 (or * 16384). Every such product has at most 15 significant bits, so it is
-// exact and identical to the reference's f32 value; f16 output is one RNE rounding of it. This
+// exact and identical to the reference's f32 value; f16 output is one RNE rounding of it (or, for
+// f16 output without wpe, the same rounding done by a packed f16 multiply, see fp8_pair_bits). This
 // keeps the reference's 0x7F / 0xFF = +-480 (not NaN) and -0 codes. With wpe the position row is
 // added in f32 first, then rounded once, as the reference does.
 #include "internal.h"
@@ -43,137 +44,187 @@ __device__ __forceinline__ void fp8_pair(uint32_t w, float& f0, float& f1) {
 // E2M1 code in bits [3:0] of n -> its f16 pattern (value / 16384) as f32.
 __device__ __forceinline__ float fp4_code(uint32_t n) { return half_bits_to_f32(((n & 8u) << 12) | ((n & 7u) << 9)); }
 
-template <typename TO, int M>
-__device__ __forceinline__ void store_out(TO* dst, const float (&v)[M]) {
-    // M f32 results -> M outputs, written as 16-byte vectors.
-    constexpr int PER = 16 / sizeof(TO);
-#pragma unroll
-    for (int q = 0; q < M / PER; q++) {
-        typedef typename VecOf<TO, PER>::V VO;
-        VO o;
-#pragma unroll
-        for (int e = 0; e < PER; e++) o[e] = from_f32<TO>(v[q * PER + e]);
-        store_nt(reinterpret_cast<VO*>(dst) + q, o);
-    }
+// Packed-f16 decoding, for f16 output without a position table: two codes (in the low bits of the
+// two 16-bit halves of p) become the f16 patterns above, which one v_pk_mul_f16 by 2^8 (FP8) or
+// 2^14 (FP4) turns exactly into the code values and a second multiplies by the f16 block scale. The
+// product of two f16 values is exact in f32, so the single RNE rounding of the f16 multiply equals
+// the reference's f32 product rounded to f16 (f16 subnormals are kept, as the hardware does by
+// default for f16).
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t fp8_pair_bits(uint32_t p) { return (p + (p & 0x00800080u)) << 7; }
+__device__ __forceinline__ uint32_t fp4_pair_bits(uint32_t p) {
+    const uint32_t m = p & 0x000F000Fu;
+    return (m + 7u * (m & 0x00080008u)) << 9;  // sign bit 3 -> bit 6 before the shift -> bit 15
 }
 
-template <int M>
-__device__ __forceinline__ void add_wpe(float (&v)[M], const half_t* pe) {
-    // M consecutive position values (M multiple of 8), 16-byte loads.
-#pragma unroll
-    for (int q = 0; q < M / 8; q++) {
-        const half8 h = *reinterpret_cast<const half8*>(pe + 8 * q);
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[8 * q + e] = v[8 * q + e] + static_cast<float>(h[e]);
-    }
+// 32-bit word w of a loaded chunk (a scalar when the chunk is one word).
+template <typename R>
+__device__ __forceinline__ uint32_t word_of(const R& r, int w) {
+    if constexpr (sizeof(R) == 4) return static_cast<uint32_t>(r);
+    else return static_cast<uint32_t>(r[w]);
 }
 
-// Vector path. FMT: 0 F16, 1 FP8, 2 FP4. Requires C % 32 == 0 for FP8/FP4, C % 8 == 0 for F16, and
-// 16-byte aligned rows everywhere.
+// Launch-shape knobs (compile-time; defaults are the fastest measured on MI355X for a 16384-token
+// gather of 2048-wide rows). NT_STORE 1 writes the output with non-temporal stores (no faster).
+#ifndef NEKO_TUNE_EMBED_NT_STORE
+#define NEKO_TUNE_EMBED_NT_STORE 0
+#endif
+
+// Tokens per wavefront, per table format (F16, FP8, FP4): more tokens put more rows' loads in
+// flight per wave, at the cost of registers (occupancy) for the decoding formats.
+#ifndef NEKO_TUNE_EMBED_TPW_F16
+#define NEKO_TUNE_EMBED_TPW_F16 4
+#endif
+#ifndef NEKO_TUNE_EMBED_TPW_FP8
+#define NEKO_TUNE_EMBED_TPW_FP8 2
+#endif
+#ifndef NEKO_TUNE_EMBED_TPW_FP4
+#define NEKO_TUNE_EMBED_TPW_FP4 2
+#endif
+// PACKED 1 decodes FP8/FP4 in packed f16 when the output is f16 and no position table is added.
+#ifndef NEKO_TUNE_EMBED_PACKED
+#define NEKO_TUNE_EMBED_PACKED 1
+#endif
+// 16-byte output chunks per lane per token in flight, per format.
+#ifndef NEKO_TUNE_EMBED_B_F16
+#define NEKO_TUNE_EMBED_B_F16 4
+#endif
+#ifndef NEKO_TUNE_EMBED_B_FP8
+#define NEKO_TUNE_EMBED_B_FP8 4
+#endif
+#ifndef NEKO_TUNE_EMBED_B_FP4
+#define NEKO_TUNE_EMBED_B_FP4 4
+#endif
+__host__ __device__ constexpr int chunks_in_flight(int fmt) {
+    return fmt == 0 ? NEKO_TUNE_EMBED_B_F16 : fmt == 1 ? NEKO_TUNE_EMBED_B_FP8 : NEKO_TUNE_EMBED_B_FP4;
+}
+__host__ __device__ constexpr int tokens_per_wave(int fmt) {
+    return fmt == 0 ? NEKO_TUNE_EMBED_TPW_F16 : fmt == 1 ? NEKO_TUNE_EMBED_TPW_FP8 : NEKO_TUNE_EMBED_TPW_FP4;
+}
+
+// Vector path. FMT: 0 F16, 1 FP8, 2 FP4. The output row is cut into chunks of EPC = 16 bytes of
+// output elements (8 halves or 4 floats); lane l takes chunks l, l + 64, ..., so every store
+// instruction writes 1 KB of contiguous output (whole cache lines). Each chunk loads exactly the
+// stored bytes it decodes: EPC halves (F16), EPC code bytes (FP8), or the EPC bytes of its 32-weight
+// block that hold its elements (FP4: elements j < 16 sit in the low nibbles of bytes j, elements
+// 16 + j in the high nibbles). Requires C % 32 == 0 for FP8/FP4, C % EPC == 0 for F16, and
+// 16-byte aligned output rows (plus 2 * EPC-byte aligned table rows and wpe rows).
+// Each wave owns tokens_per_wave(FMT) consecutive tokens: their ids come in one load, then every
+// row's chunk loads are issued before any is decoded.
 template <int FMT, typename TO, bool WPE>
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
-    const int wave = threadIdx.x >> 6;
+    constexpr int EPC = 16 / sizeof(TO);  // output elements per chunk
+    constexpr int TPW = tokens_per_wave(FMT);  // tokens per wave, all in flight together
+    constexpr int B = chunks_in_flight(FMT);   // chunks per lane per token in flight
+    typedef typename VecOf<TO, EPC>::V VO;
+    typedef typename VecOf<half_t, EPC>::V VH;
+    constexpr bool kPacked = FMT != 0 && EPC == 8 && !WPE && NEKO_TUNE_EMBED_PACKED;
+    // Raw chunk bytes: F16 2*EPC bytes, FP8/FP4 EPC bytes.
+    typedef typename VecOf<uint32_t, (FMT == 0 ? 2 * EPC : EPC) / 4>::V Raw;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-    if (t >= a.T) return;
-    const int64_t r = static_cast<int64_t>(a.tokens[t]) - a.row_base;
-    if (r < 0 || r >= a.rows) return;  // another chunk of the table owns this token
-    const uint8_t* row = a.table + r * a.row_bytes;
-    TO* out = static_cast<TO*>(a.out) + t * a.out_stride;
-    const half_t* pe = WPE ? a.wpe + (a.pos0 + t) * a.C : nullptr;
+    const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * TPW;
+    if (t0 >= a.T) return;
+    // The wave's token ids in one load (lane i holds token t0 + i), then broadcast as scalars.
+    const int32_t my_id = lane < TPW && t0 + lane < a.T ? a.tokens[t0 + lane] : 0;
+    const uint8_t* rowp[TPW];
+    bool live[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; k++) {
+        const int64_t r = static_cast<int64_t>(__builtin_amdgcn_readlane(my_id, k)) - a.row_base;
+        live[k] = t0 + k < a.T && r >= 0 && r < a.rows;  // other tokens belong to another table chunk
+        rowp[k] = a.table + (live[k] ? r : 0) * a.row_bytes;
+    }
+    const int nch = a.C / EPC;
+    const int64_t soff = FMT == 1 ? a.C : a.C / 2;  // scales follow the codes
 
-    if constexpr (FMT == 0) {
-        const int nch = a.C / 8;
-        constexpr int B = 4;  // chunks in flight per lane
-        for (int j0 = 0; j0 < nch; j0 += B * kWave) {
-            half8 h[B];
+    for (int c0 = 0; c0 < nch; c0 += B * kWave) {
+        Raw raw[TPW][B];
+        half_t sc[TPW][B];
+        VH pw[TPW][B];
+#pragma unroll
+        for (int k = 0; k < TPW; k++) {
+            if (!live[k]) continue;
+            const uint8_t* row = rowp[k];
 #pragma unroll
             for (int b = 0; b < B; b++) {
-                const int j = j0 + b * kWave + lane;
-                if (j < nch) h[b] = *reinterpret_cast<const half8*>(row + 16 * j);
-            }
-#pragma unroll
-            for (int b = 0; b < B; b++) {
-                const int j = j0 + b * kWave + lane;
-                if (j >= nch) continue;
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = static_cast<float>(h[b][e]);
-                if constexpr (WPE) add_wpe<8>(v, pe + 8 * j);
-                store_out<TO, 8>(out + 8 * j, v);
+                const int c = c0 + b * kWave + lane;
+                if (c >= nch) continue;
+                const int e0 = c * EPC;
+                if constexpr (FMT == 0) {
+                    raw[k][b] = *reinterpret_cast<const Raw*>(row + 2 * e0);
+                } else if constexpr (FMT == 1) {
+                    raw[k][b] = *reinterpret_cast<const Raw*>(row + e0);
+                    sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * (e0 >> 5));
+                } else {
+                    const int blk = e0 >> 5, j0 = e0 & 15;
+                    raw[k][b] = *reinterpret_cast<const Raw*>(row + 16 * blk + j0);
+                    sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * blk);
+                }
+                if constexpr (WPE) pw[k][b] = *reinterpret_cast<const VH*>(a.wpe + (a.pos0 + t0 + k) * a.C + e0);
             }
         }
-    } else if constexpr (FMT == 1) {
-        const int nch = a.C / 16;  // 16 codes per chunk, two chunks per block scale
-        const uint8_t* scales = row + a.C;
-        constexpr int B = 2;
-        for (int j0 = 0; j0 < nch; j0 += B * kWave) {
-            uint4v q[B];
-            float s[B];
+#pragma unroll
+        for (int k = 0; k < TPW; k++) {
+            if (!live[k]) continue;
+            TO* out = static_cast<TO*>(a.out) + (t0 + k) * a.out_stride;
 #pragma unroll
             for (int b = 0; b < B; b++) {
-                const int j = j0 + b * kWave + lane;
-                if (j < nch) {
-                    q[b] = *reinterpret_cast<const uint4v*>(row + 16 * j);
-                    const half_t sh = *reinterpret_cast<const half_t*>(scales + 2 * (j >> 1));
-                    s[b] = static_cast<float>(sh) * 256.0f;
-                }
-            }
+                const int c = c0 + b * kWave + lane;
+                if (c >= nch) continue;
+                VO o;
+                if constexpr (kPacked) {
+                    const half2v s2 = {sc[k][b], sc[k][b]};
+                    const half2v k2 = FMT == 1 ? half2v{256.0f16, 256.0f16} : half2v{16384.0f16, 16384.0f16};
+                    const int shift = FMT == 2 && ((c * EPC) & 16) ? 4 : 0;
+                    uint4v ob;
 #pragma unroll
-            for (int b = 0; b < B; b++) {
-                const int j = j0 + b * kWave + lane;
-                if (j >= nch) continue;
-                float v[16];
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    float f0, f1, f2, f3;
-                    fp8_pair(q[b][w], f0, f1);
-                    fp8_pair(q[b][w] >> 16, f2, f3);
-                    v[4 * w + 0] = f0 * s[b];
-                    v[4 * w + 1] = f1 * s[b];
-                    v[4 * w + 2] = f2 * s[b];
-                    v[4 * w + 3] = f3 * s[b];
-                }
-                if constexpr (WPE) add_wpe<16>(v, pe + 16 * j);
-                store_out<TO, 16>(out + 16 * j, v);
-            }
-        }
-    } else {
-        const int nb = a.C / 32;  // one 16-byte block per chunk
-        const uint8_t* scales = row + a.C / 2;
-        constexpr int B = 2;
-        for (int j0 = 0; j0 < nb; j0 += B * kWave) {
-            uint4v q[B];
-            float s[B];
-#pragma unroll
-            for (int b = 0; b < B; b++) {
-                const int j = j0 + b * kWave + lane;
-                if (j < nb) {
-                    q[b] = *reinterpret_cast<const uint4v*>(row + 16 * j);
-                    const half_t sh = *reinterpret_cast<const half_t*>(scales + 2 * j);
-                    s[b] = static_cast<float>(sh) * 16384.0f;
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < B; b++) {
-                const int j = j0 + b * kWave + lane;
-                if (j >= nb) continue;
-                float lo[16], hi[16];
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const uint32_t byte = (q[b][w] >> (8 * k)) & 0xffu;
-                        lo[4 * w + k] = fp4_code(byte) * s[b];
-                        hi[4 * w + k] = fp4_code(byte >> 4) * s[b];
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t word = word_of(raw[k][b], i >> 1) >> shift;
+                        const uint32_t p = __builtin_amdgcn_perm(0u, word, (i & 1) ? 0x0C030C02u : 0x0C010C00u);
+                        const uint32_t bits = FMT == 1 ? fp8_pair_bits(p) : fp4_pair_bits(p);
+                        ob[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, bits) * k2 * s2);
                     }
+                    o = __builtin_bit_cast(VO, ob);
+                } else {
+                    float v[EPC];
+                    if constexpr (FMT == 0) {
+                        const VH h = __builtin_bit_cast(VH, raw[k][b]);
+#pragma unroll
+                        for (int e = 0; e < EPC; e++) v[e] = static_cast<float>(h[e]);
+                    } else if constexpr (FMT == 1) {
+                        const float sf = static_cast<float>(sc[k][b]) * 256.0f;
+#pragma unroll
+                        for (int w = 0; w < EPC / 4; w++) {
+                            const uint32_t word = word_of(raw[k][b], w);
+                            float f0, f1, f2, f3;
+                            fp8_pair(word, f0, f1);
+                            fp8_pair(word >> 16, f2, f3);
+                            v[4 * w + 0] = f0 * sf;
+                            v[4 * w + 1] = f1 * sf;
+                            v[4 * w + 2] = f2 * sf;
+                            v[4 * w + 3] = f3 * sf;
+                        }
+                    } else {
+                        const int shift = ((c * EPC) & 16) ? 4 : 0;  // high nibbles for elements 16..31 of the block
+                        const float sf = static_cast<float>(sc[k][b]) * 16384.0f;
+#pragma unroll
+                        for (int w = 0; w < EPC / 4; w++) {
+                            const uint32_t word = word_of(raw[k][b], w) >> shift;
+#pragma unroll
+                            for (int q = 0; q < 4; q++) v[4 * w + q] = fp4_code(word >> (8 * q)) * sf;
+                        }
+                    }
+                    if constexpr (WPE) {
+#pragma unroll
+                        for (int e = 0; e < EPC; e++) v[e] = v[e] + static_cast<float>(pw[k][b][e]);
+                    }
+#pragma unroll
+                    for (int e = 0; e < EPC; e++) o[e] = from_f32<TO>(v[e]);
                 }
-                if constexpr (WPE) {
-                    add_wpe<16>(lo, pe + 32 * j);
-                    add_wpe<16>(hi, pe + 32 * j + 16);
-                }
-                store_out<TO, 16>(out + 32 * j, lo);
-                store_out<TO, 16>(out + 32 * j + 16, hi);
+                VO* dst = reinterpret_cast<VO*>(out + c * EPC);
+                if (NEKO_TUNE_EMBED_NT_STORE) store_nt(dst, o);
+                else *dst = o;
             }
         }
     }
@@ -252,12 +303,17 @@ extern "C" int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t 
     const size_t osz = dtype_size(out_dtype);
     EmbedArgs a{tokens, T, static_cast<const uint8_t*>(table), row_bytes, static_cast<int>(C), row_base, rows,
                 reinterpret_cast<const half_t*>(wpe), pos0, out, out_stride};
-    const bool vec = (fmt != NEKO_FMT_F16 || C % 8 == 0) && aligned(table, 16) && row_bytes % 16 == 0 &&
-                     aligned(out, 16) && (out_stride * osz) % 16 == 0 && (!wpe || (aligned(wpe, 16) && C % 8 == 0));
+    // Chunks of 16 output bytes: EPC elements; loads of 2*EPC (F16) or EPC (FP8/FP4) table bytes.
+    const int64_t epc = static_cast<int64_t>(16 / osz);
+    const int64_t chunk_in = fmt == NEKO_FMT_F16 ? 2 * epc : epc;
+    const bool vec = C % epc == 0 && aligned(table, static_cast<size_t>(chunk_in)) && row_bytes % chunk_in == 0 &&
+                     aligned(out, 16) && (out_stride * osz) % 16 == 0 &&
+                     (!wpe || (aligned(wpe, static_cast<size_t>(2 * epc)) && (C * 2) % (2 * epc) == 0));
     if (vec) {
-        NEKO_REQUIRE(ctx, T <= 0x7fffffffLL * 4, "%s: too many tokens", what);
+        const int64_t per_block = 4 * tokens_per_wave(fmt);
+        NEKO_REQUIRE(ctx, T <= 0x7fffffffLL * per_block, "%s: too many tokens", what);
         EmbedKernel k = out_dtype == NEKO_DT_F16 ? pick_fmt<half_t>(fmt, wpe != nullptr) : pick_fmt<float>(fmt, wpe != nullptr);
-        hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>((T + 3) / 4)), dim3(256), 0, ctx->stream, a);
+        hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>((T + per_block - 1) / per_block)), dim3(256), 0, ctx->stream, a);
         return after_launch(ctx, what);
     }
     const uint32_t gx = static_cast<uint32_t>((C + 255) / 256);
