@@ -54,6 +54,40 @@ __device__ __forceinline__ void store_nt(V* p, V v) {
     __builtin_nontemporal_store(v, p);
 }
 
+// silu(g) = g / (1 + exp(-g)) in float, the reference's formula (cpu_ops.cpp:526-533,
+// granite_model.cpp:21), with a cheaper evaluation than libm expf + IEEE division (those cost ~33
+// VALU ops per element and left streaming kernels VALU-bound on MI355X; this form takes ~17):
+//   exp(-g) = 2^(h + l) with h = -g*log2(e) rounded and l its exact rounding error (fma) plus the
+//   low part of log2(e), evaluated as v_exp_f32(h) * (1 + l*ln2);
+//   q = g / d by v_rcp_f32 and one Newton correction of the quotient, fma(fma(-q, d, g), r, q).
+// The exponent argument is clamped at 126 so d stays finite (no 0 * inf in the correction); gates
+// below about -87.3 then give a value of magnitude < 2^-119 instead of the reference's (also tiny
+// or -0) quotient, which rounds to the same signed zero once multiplied by an fp16 operand. A +inf
+// gate passes through as +inf and -inf / NaN give NaN, as in the reference. Measured against the
+// oracle over every fp16 gate value: SwiGLU outputs within 1 fp16 ulp.
+__device__ __forceinline__ float silu_fast(float gate) {
+    const float kLog2e = 1.44269504088896341f, kLog2eLo = 1.925963033500011e-08f, kLn2 = 0.69314718055994531f;
+    const float h = gate * -kLog2e;
+    const float l = __builtin_fmaf(gate, -kLog2e, -h) - gate * kLog2eLo;
+    const float e = __builtin_amdgcn_exp2f(fminf(h, 126.0f)) * __builtin_fmaf(l, kLn2, 1.0f);
+    const float d = 1.0f + e;
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float q0 = gate * r;
+    float q = __builtin_fmaf(__builtin_fmaf(-q0, d, gate), r, q0);
+    if (gate == __builtin_inff()) q = gate;
+    return q;
+}
+
+// silu(g) = g * rcp(1 + 2^(-g*log2(e))): five VALU ops. Relative error vs the exact quotient is
+// below |g| * 2^-24 * ln 2 (the rounding of the exponent argument) plus ~2 ulp (v_exp_f32, v_rcp_f32,
+// the product): under 1.3e-6 for |g| <= 20, and for g < -20 the value is below 5e-8 * |g|. Special
+// values need no guards: g = +inf gives +inf, -inf and NaN give NaN, and very negative g gives -0
+// (exp overflows to inf, rcp(inf) = 0), as the reference's quotient does.
+__device__ __forceinline__ float silu_lite(float g) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 template <typename T>
 __device__ __forceinline__ float to_f32(T v) {
     return static_cast<float>(v);

@@ -38,8 +38,8 @@ FastDiv make_fast_div(uint32_t d);
 
 // Workgroups of `block` threads of `kernel` that fit on one CU at once (cached per kernel), and the
 // grid of a persistent kernel: that many per CU, or fewer when there is less work.
-int resident_blocks_per_cu(const void* kernel, int block);
-int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks);
+int resident_blocks_per_cu(const void* kernel, int block, size_t lds_bytes = 0);
+int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks, size_t lds_bytes = 0);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline size_t dtype_size(int dtype) { return dtype == NEKO_DT_F16 ? 2 : 4; }

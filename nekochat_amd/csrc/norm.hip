@@ -27,6 +27,26 @@
 #ifndef NEKO_TUNE_NORM_FULLGRID
 #define NEKO_TUNE_NORM_FULLGRID 0
 #endif
+// Where the one-wave-per-row kernel keeps the norm weights: 0 in every lane's registers, 1 in one
+// LDS copy per workgroup (frees CH * 8 VGPRs per lane for occupancy). Per norm kind.
+#ifndef NEKO_TUNE_NORM_WLDS_RMS
+#define NEKO_TUNE_NORM_WLDS_RMS 0
+#endif
+#ifndef NEKO_TUNE_NORM_WLDS_LAYER
+#define NEKO_TUNE_NORM_WLDS_LAYER 0
+#endif
+#ifndef NEKO_TUNE_NORM_WLDS_GATED
+#define NEKO_TUNE_NORM_WLDS_GATED 1
+#endif
+// Gated norm: 1 keeps y * silu(z) in float registers between the sum and the store, 0 evaluates it
+// again at the store (fewer registers, twice the silu work); and its prefetch mode (as NORM_PF: the
+// gated rows already hold two operands, and more resident waves beat a second row buffer).
+#ifndef NEKO_TUNE_GATED_KEEP
+#define NEKO_TUNE_GATED_KEEP 1
+#endif
+#ifndef NEKO_TUNE_GATED_PF
+#define NEKO_TUNE_GATED_PF 0
+#endif
 
 namespace neko_hip {
 namespace {
@@ -48,8 +68,36 @@ struct NormArgs {
     float eps;
 };
 
-// Mamba2 output gate, granite_model.cpp:21: v / (1 + exp(-v)) in float.
-__device__ __forceinline__ float silu_ref(float v) { return v / (1.0f + expf(-v)); }
+// Mamba2 output gate, granite_model.cpp:21: v / (1 + exp(-v)) in float. Evaluation (knob): 0 libm
+// expf and IEEE division, 1 silu_fast, 2 silu_lite (device.h). The gated norm streams two operands
+// per output and is VALU-limited on MI355X with the longer forms; silu_lite's relative error (< 1.3e-6
+// for |v| <= 20) stays far below the fp16 output's half ulp (4.9e-4).
+#ifndef NEKO_TUNE_GATED_SILU
+#define NEKO_TUNE_GATED_SILU 2
+#endif
+__device__ __forceinline__ float silu_ref(float v) {
+    if constexpr (NEKO_TUNE_GATED_SILU == 0) return v / (1.0f + expf(-v));
+    else if constexpr (NEKO_TUNE_GATED_SILU == 1) return silu_fast(v);
+    else return silu_lite(v);
+}
+
+constexpr bool weights_in_lds(Norm k) {
+    return k == Norm::Rms ? NEKO_TUNE_NORM_WLDS_RMS : k == Norm::Layer ? NEKO_TUNE_NORM_WLDS_LAYER : NEKO_TUNE_NORM_WLDS_GATED;
+}
+constexpr int prefetch_mode(Norm k) { return k == Norm::Gated ? NEKO_TUNE_GATED_PF : NEKO_TUNE_NORM_PF; }
+
+// Output stores: non-temporal (1) or plain (0), for the plain norms and for the gated norm.
+#ifndef NEKO_TUNE_NORM_NT_STORE
+#define NEKO_TUNE_NORM_NT_STORE 1
+#endif
+#ifndef NEKO_TUNE_GATED_NT_STORE
+#define NEKO_TUNE_GATED_NT_STORE 0
+#endif
+template <Norm K, typename V>
+__device__ __forceinline__ void store_out(V* p, V v) {
+    if constexpr (K == Norm::Gated ? NEKO_TUNE_GATED_NT_STORE : NEKO_TUNE_NORM_NT_STORE) store_nt(p, v);
+    else *p = v;
+}
 
 template <Norm K, typename T>
 struct RowPtrs {
@@ -99,24 +147,49 @@ __device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K,
     }
 }
 
-template <Norm K, typename T, int CH, int NT>
-__device__ __forceinline__ void load_weights(float4v (&wv)[CH][Chunk16<T>::N / 4], float4v (&bv)[CH][Chunk16<T>::N / 4],
-                                             const float* w, const float* b, int tid, int nch) {
-    constexpr int N = Chunk16<T>::N;
+// The norm weights (and LayerNorm's beta) of one lane's chunks, as float4 quads: held in registers
+// (WL = false), or read at the store from the workgroup's LDS copy of the weight vector (WL = true).
+template <Norm K, typename T, int CH, int NT, bool WL>
+struct Weights {
+    static constexpr int N = Chunk16<T>::N;
+    float4v w[CH][N / 4], b[CH][N / 4];
+
+    __device__ __forceinline__ void init(const float* wp, const float* bp, int tid, int nch) {
 #pragma unroll
-    for (int k = 0; k < CH; k++) {
-        const int j = k * NT + tid;
+        for (int k = 0; k < CH; k++) {
+            const int j = k * NT + tid;
 #pragma unroll
-        for (int q = 0; q < N / 4; q++) {
-            wv[k][q] = float4v{};
-            bv[k][q] = float4v{};
-            if (j < nch) {
-                wv[k][q] = *reinterpret_cast<const float4v*>(w + j * N + 4 * q);
-                if constexpr (K == Norm::Layer) bv[k][q] = *reinterpret_cast<const float4v*>(b + j * N + 4 * q);
+            for (int q = 0; q < N / 4; q++) {
+                w[k][q] = float4v{};
+                b[k][q] = float4v{};
+                if (j < nch) {
+                    w[k][q] = *reinterpret_cast<const float4v*>(wp + j * N + 4 * q);
+                    if constexpr (K == Norm::Layer) b[k][q] = *reinterpret_cast<const float4v*>(bp + j * N + 4 * q);
+                }
             }
         }
     }
-}
+    __device__ __forceinline__ float4v wq(int k, int q) const { return w[k][q]; }
+    __device__ __forceinline__ float4v bq(int k, int q) const { return b[k][q]; }
+};
+
+template <Norm K, typename T, int CH, int NT>
+struct Weights<K, T, CH, NT, true> {
+    static constexpr int N = Chunk16<T>::N;
+    const float* w;  // LDS: this row group's weights, at this lane's first chunk
+    const float* b;
+
+    __device__ __forceinline__ void init(const float* wl, const float* bl, int tid, int) {
+        w = wl + tid * N;
+        b = bl + tid * N;
+    }
+    __device__ __forceinline__ float4v wq(int k, int q) const {
+        return *reinterpret_cast<const float4v*>(w + k * NT * N + 4 * q);
+    }
+    __device__ __forceinline__ float4v bq(int k, int q) const {
+        return *reinterpret_cast<const float4v*>(b + k * NT * N + 4 * q);
+    }
+};
 
 // The row in float. Plain norms convert from the loaded halves on every use (cheaper than holding a
 // float copy in registers); the gated norm evaluates y * silu(z) once and keeps it. Lanes past the
@@ -124,12 +197,13 @@ __device__ __forceinline__ void load_weights(float4v (&wv)[CH][Chunk16<T>::N / 4
 template <Norm K, typename T, int CH>
 struct RowVals {
     static constexpr int N = Chunk16<T>::N;
-    float f[K == Norm::Gated ? CH : 1][K == Norm::Gated ? N : 1];
+    static constexpr bool kKeep = K == Norm::Gated && NEKO_TUNE_GATED_KEEP;
+    float f[kKeep ? CH : 1][kKeep ? N : 1];
     const RowRegs<K, T, CH>* rr;
 
     __device__ __forceinline__ void init(const RowRegs<K, T, CH>& regs) {
         rr = &regs;
-        if constexpr (K == Norm::Gated) {
+        if constexpr (kKeep) {
 #pragma unroll
             for (int k = 0; k < CH; k++)
 #pragma unroll
@@ -137,7 +211,8 @@ struct RowVals {
         }
     }
     __device__ __forceinline__ float operator()(int k, int e) const {
-        if constexpr (K == Norm::Gated) return f[k][e];
+        if constexpr (kKeep) return f[k][e];
+        else if constexpr (K == Norm::Gated) return to_f32(rr->x[k][e]) * silu_ref(to_f32(rr->z[k][e]));
         else return to_f32(rr->x[k][e]);
     }
 };
@@ -183,45 +258,72 @@ __device__ __forceinline__ double sum_centered(const F& f, double mean, int tid,
     return s;
 }
 
-template <Norm K, typename T, int CH, int NT, typename F>
-__device__ __forceinline__ void store_row(T* y, const F& f, float scale, float mean_f,
-                                          const float4v (&wv)[CH][Chunk16<T>::N / 4],
-                                          const float4v (&bv)[CH][Chunk16<T>::N / 4], int tid, int nch) {
+// Output chunk k: (x - mean) * scale * gamma + beta, or x * scale * w, rounded once.
+template <Norm K, typename T, int CH, typename F, typename W>
+__device__ __forceinline__ typename Chunk16<T>::V out_chunk(const F& f, int k, float scale, float mean_f, const W& wt) {
+    constexpr int N = Chunk16<T>::N;
+    typename Chunk16<T>::V out;
+#pragma unroll
+    for (int q = 0; q < N / 4; q++) {
+        const float4v w = wt.wq(k, q);
+        float4v b{};
+        if constexpr (K == Norm::Layer) b = wt.bq(k, q);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = 4 * q + i;
+            float v;
+            if constexpr (K == Norm::Layer) v = (f(k, e) - mean_f) * scale * w[i] + b[i];
+            else v = f(k, e) * scale * w[i];
+            out[e] = from_f32<T>(v);
+        }
+    }
+    return out;
+}
+
+template <Norm K, typename T, int CH, int NT, typename F, typename W>
+__device__ __forceinline__ void store_row(T* y, const F& f, float scale, float mean_f, const W& wt, int tid, int nch) {
     typedef typename Chunk16<T>::V V;
     constexpr int N = Chunk16<T>::N;
 #pragma unroll
     for (int k = 0; k < CH; k++) {
         const int j = k * NT + tid;
         if (j >= nch) continue;
-        V out;
-#pragma unroll
-        for (int e = 0; e < N; e++) {
-            const float w = wv[k][e / 4][e % 4];
-            float v;
-            if constexpr (K == Norm::Layer) v = (f(k, e) - mean_f) * scale * w + bv[k][e / 4][e % 4];
-            else v = f(k, e) * scale * w;
-            out[e] = from_f32<T>(v);
-        }
-        store_nt(reinterpret_cast<V*>(y + j * N), out);
+        store_out<K>(reinterpret_cast<V*>(y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
     }
 }
 
 // One wavefront per row, persistent: wave w handles rows w, w + nw, ... (nw = waves in the grid),
-// keeps the weights in registers across rows and loads the next row while it normalises this one.
-// Every row of a wave shares one group index (the host makes nw a multiple of groups, or gives
-// each wave at most one row).
-template <Norm K, typename T, int CH, int PF = NEKO_TUNE_NORM_PF>
+// keeps the weights in registers (or its workgroup's LDS copy) across rows and loads the next row
+// while it normalises this one. Every row of a wave shares one group index (the host makes nw a
+// multiple of groups, or gives each wave at most one row). With WL the dynamic LDS holds the
+// groups * C weights (then C betas for LayerNorm).
+template <Norm K, typename T, int CH, bool WL, int PF = prefetch_mode(K)>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     constexpr int N = Chunk16<T>::N;
     const int lane = threadIdx.x & 63;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    extern __shared__ float4v wlds[];
+    if constexpr (WL) {
+        // Every wave reaches this barrier before any may leave.
+        const int nq = a.groups * a.C / 4;
+        float4v* wl = wlds;
+        for (int i = threadIdx.x; i < nq; i += 256) wl[i] = reinterpret_cast<const float4v*>(a.w)[i];
+        if constexpr (K == Norm::Layer)
+            for (int i = threadIdx.x; i < a.C / 4; i += 256) wl[nq + i] = reinterpret_cast<const float4v*>(a.b)[i];
+        __syncthreads();
+    }
     // readfirstlane tells the compiler the row index is wave-uniform, so row pointers stay in SGPRs.
     int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (r >= a.rows) return;  // wave-uniform
     const int nch = a.C / N;
     const RowPtrs<K, T> p0 = row_ptrs<K, T>(a, r);
-    float4v wv[CH][N / 4], bv[CH][N / 4];
-    load_weights<K, T, CH, kWave>(wv, bv, p0.w, p0.b, lane, nch);
+    Weights<K, T, CH, kWave, WL> wt;
+    if constexpr (WL) {
+        const float* wl = reinterpret_cast<const float*>(wlds);
+        wt.init(wl + (p0.w - a.w), wl + a.groups * a.C, lane, nch);
+    } else {
+        wt.init(p0.w, p0.b, lane, nch);
+    }
 
     RowRegs<K, T, CH> cur, nxt;
     load_row<K, T, CH, kWave>(cur, p0, lane, nch);
@@ -249,23 +351,14 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
             for (int k = 0; k < CH; k++) {
                 const int j = k * kWave + lane;
                 if (j >= nch) continue;
-                V out;
-#pragma unroll
-                for (int e = 0; e < N; e++) {
-                    const float w = wv[k][e / 4][e % 4];
-                    float v;
-                    if constexpr (K == Norm::Layer) v = (f(k, e) - mean_f) * scale * w + bv[k][e / 4][e % 4];
-                    else v = f(k, e) * scale * w;
-                    out[e] = from_f32<T>(v);
-                }
-                store_nt(reinterpret_cast<V*>(y + j * N), out);
+                store_out<K>(reinterpret_cast<V*>(y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
                 if (more) {
                     cur.x[k] = load_nt(reinterpret_cast<const V*>(pn.x + j * N));
                     if constexpr (K == Norm::Gated) cur.z[k] = load_nt(reinterpret_cast<const V*>(pn.z + j * N));
                 }
             }
         } else {
-            store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wv, bv, lane, nch);
+            store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wt, lane, nch);
             if (PF == 1 && more) cur = nxt;
             else if (more) load_row<K, T, CH, kWave>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
         }
@@ -284,8 +377,8 @@ __global__ __launch_bounds__(256) void norm_wide_kernel(NormArgs a) {
     const RowPtrs<K, T> p = row_ptrs<K, T>(a, r);
     RowRegs<K, T, CH> rr;
     load_row<K, T, CH, NT>(rr, p, tid, nch);
-    float4v wv[CH][N / 4], bv[CH][N / 4];
-    load_weights<K, T, CH, NT>(wv, bv, p.w, p.b, tid, nch);
+    Weights<K, T, CH, NT, false> wt;
+    wt.init(p.w, p.b, tid, nch);
     RowVals<K, T, CH> f;
     f.init(rr);
 
@@ -306,7 +399,7 @@ __global__ __launch_bounds__(256) void norm_wide_kernel(NormArgs a) {
         const double ss = block_total(sum_squares<CH, N>(f), 0);
         scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
     }
-    store_row<K, T, CH, NT>(p.y, f, scale, mean_f, wv, bv, tid, nch);
+    store_row<K, T, CH, NT>(p.y, f, scale, mean_f, wt, tid, nch);
 }
 
 // ------------------------------------------------------------------ generic rows
@@ -368,16 +461,16 @@ __global__ __launch_bounds__(256) void norm_rows_generic(NormArgs a) {
 // ------------------------------------------------------------------ dispatch
 typedef void (*NormKernel)(NormArgs);
 
-template <Norm K, typename T>
+template <Norm K, typename T, bool WL>
 NormKernel pick_wave(int CH) {
     switch (CH) {
-        case 1: return norm_wave_kernel<K, T, 1>;
-        case 2: return norm_wave_kernel<K, T, 2>;
-        case 3: return norm_wave_kernel<K, T, 3>;
-        case 4: return norm_wave_kernel<K, T, 4>;
-        case 5: return norm_wave_kernel<K, T, 5>;
-        case 6: return norm_wave_kernel<K, T, 6>;
-        case 8: return norm_wave_kernel<K, T, 8>;
+        case 1: return norm_wave_kernel<K, T, 1, WL>;
+        case 2: return norm_wave_kernel<K, T, 2, WL>;
+        case 3: return norm_wave_kernel<K, T, 3, WL>;
+        case 4: return norm_wave_kernel<K, T, 4, WL>;
+        case 5: return norm_wave_kernel<K, T, 5, WL>;
+        case 6: return norm_wave_kernel<K, T, 6, WL>;
+        case 8: return norm_wave_kernel<K, T, 8, WL>;
     }
     return nullptr;
 }
@@ -392,12 +485,17 @@ NormKernel pick_wide(int CH) {
 }
 
 template <Norm K>
-NormKernel pick(int dtype, int W, int CH) {
+NormKernel pick(int dtype, int W, int CH, bool wl) {
     const bool h = dtype == NEKO_DT_F16;
     if (W == 0) return h ? norm_rows_generic<K, half_t> : norm_rows_generic<K, float>;
-    if (W == 1) return h ? pick_wave<K, half_t>(CH) : pick_wave<K, float>(CH);
+    if (W == 1) {
+        if (wl) return h ? pick_wave<K, half_t, true>(CH) : pick_wave<K, float, true>(CH);
+        return h ? pick_wave<K, half_t, false>(CH) : pick_wave<K, float, false>(CH);
+    }
     return h ? pick_wide<K, half_t>(CH) : pick_wide<K, float>(CH);
 }
+
+constexpr size_t kMaxWeightLds = 32768;  // bytes of weights one workgroup may stage in LDS
 
 int64_t gcd64(int64_t a, int64_t b) {
     while (b) {
@@ -428,11 +526,14 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
             CH = (nch + 4 * kWave - 1) / (4 * kWave) <= 4 ? 4 : 8;
         }
     }
+    // Weights staged in LDS: groups * C floats (+ C betas), when they fit and the kind asks for it.
+    const size_t lds = (static_cast<size_t>(a.groups) * a.C + (kind == Norm::Layer ? a.C : 0)) * sizeof(float);
+    const bool wl = W == 1 && weights_in_lds(kind) && lds <= kMaxWeightLds && (kind != Norm::Layer || aligned(a.b, 16));
     NormKernel k = nullptr;
     switch (kind) {
-        case Norm::Rms: k = pick<Norm::Rms>(dtype, W, CH); break;
-        case Norm::Layer: k = pick<Norm::Layer>(dtype, W, CH); break;
-        case Norm::Gated: k = pick<Norm::Gated>(dtype, W, CH); break;
+        case Norm::Rms: k = pick<Norm::Rms>(dtype, W, CH, wl); break;
+        case Norm::Layer: k = pick<Norm::Layer>(dtype, W, CH, wl); break;
+        case Norm::Gated: k = pick<Norm::Gated>(dtype, W, CH, wl); break;
     }
     if (!k) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: no kernel for C=%d", what, a.C);
     int64_t blocks;
@@ -440,7 +541,7 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         // Persistent waves: as many workgroups as stay resident together. A wave that handles several
         // rows must see one group index, so the wave count is then a multiple of groups.
         const int64_t need = (a.rows + 3) / 4;
-        blocks = NEKO_TUNE_NORM_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        blocks = NEKO_TUNE_NORM_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need, wl ? lds : 0);
         if (blocks < need) {
             const int64_t m = a.groups / gcd64(a.groups, 4);
             blocks = blocks / m * m;
@@ -452,7 +553,7 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         blocks = a.rows < 65536 ? a.rows : 65536;
     }
     if (blocks > 0x7fffffff) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: %lld rows exceed one launch", what, (long long)a.rows);
-    hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), wl ? lds : 0, ctx->stream, a);
     return after_launch(ctx, what);
 }
 

@@ -2,6 +2,7 @@
 // contract, gpu/compute.h:28-44, expressed as plain C over one in-order HIP stream per context).
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <unordered_map>
 
@@ -46,23 +47,25 @@ FastDiv make_fast_div(uint32_t d) {
     return FastDiv{d, static_cast<uint32_t>(m), s};
 }
 
-int resident_blocks_per_cu(const void* kernel, int block) {
+int resident_blocks_per_cu(const void* kernel, int block, size_t lds_bytes) {
     static std::mutex mu;
-    static std::unordered_map<const void*, int> cache;
+    static std::map<std::pair<const void*, size_t>, int> cache;
     std::lock_guard<std::mutex> lk(mu);
-    auto it = cache.find(kernel);
+    const auto key = std::make_pair(kernel, lds_bytes);
+    auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, 0) != hipSuccess || n < 1) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, block, lds_bytes) != hipSuccess || n < 1) {
         (void)hipGetLastError();
         n = 1;
     }
-    cache.emplace(kernel, n);
+    cache.emplace(key, n);
     return n;
 }
 
-int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks) {
-    const int64_t cap = static_cast<int64_t>(ctx->cu_count > 0 ? ctx->cu_count : 256) * resident_blocks_per_cu(kernel, block);
+int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks, size_t lds_bytes) {
+    const int64_t cap =
+        static_cast<int64_t>(ctx->cu_count > 0 ? ctx->cu_count : 256) * resident_blocks_per_cu(kernel, block, lds_bytes);
     return work_blocks < cap ? work_blocks : cap;
 }
 

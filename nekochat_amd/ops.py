@@ -163,8 +163,8 @@ def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: fl
     out = _out_like(x, rows, C, out, "out")
     ctx = _ctx_for(x)
     _issue(ctx, lib.neko_hip_layernorm, ctx.handle, x.data_ptr(), xs, out.data_ptr(), out.stride(0),
-                                     _vec(gamma, C, "gamma", x.device), _vec(beta, C, "beta", x.device), rows, C,
-                                     float(eps), _dtype_code(x))
+           _vec(gamma, C, "gamma", x.device), _vec(beta, C, "beta", x.device), rows, C,
+           float(eps), _dtype_code(x))
     return out
 
 
@@ -174,7 +174,7 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | N
     out = _out_like(x, rows, C, out, "out")
     ctx = _ctx_for(x)
     _issue(ctx, lib.neko_hip_rmsnorm, ctx.handle, x.data_ptr(), xs, out.data_ptr(), out.stride(0),
-                                   _vec(w, C, "w", x.device), rows, C, float(eps), _dtype_code(x))
+           _vec(w, C, "w", x.device), rows, C, float(eps), _dtype_code(x))
     return out
 
 
@@ -189,7 +189,7 @@ def gated_rms_norm(y: torch.Tensor, z: torch.Tensor, w: torch.Tensor, groups: in
     out = _out_like(y, rows, D, out, "out")
     ctx = _ctx_for(y)
     _issue(ctx, lib.neko_hip_gated_rmsnorm, ctx.handle, y.data_ptr(), ys, z.data_ptr(), zs, out.data_ptr(), out.stride(0),
-                                         _vec(w, D, "w", y.device), rows, D, int(groups), float(eps), _dtype_code(y))
+           _vec(w, D, "w", y.device), rows, D, int(groups), float(eps), _dtype_code(y))
     return out
 
 
@@ -209,8 +209,8 @@ def qk_norm_rope(qkv: torch.Tensor, n_q: int, n_kv: int, hd: int, cs: torch.Tens
         pos_ptr = positions.data_ptr()
     ctx = _ctx_for(qkv)
     _issue(ctx, lib.neko_hip_qk_norm_rope, ctx.handle, qkv.data_ptr(), stride, rows, int(n_q), int(n_kv), int(hd),
-                                        int(pos0), pos_ptr, _vec(wqk, 2 * hd, "wqk", qkv.device), cs.data_ptr(),
-                                        cs.shape[0], float(eps), _dtype_code(qkv))
+           int(pos0), pos_ptr, _vec(wqk, 2 * hd, "wqk", qkv.device), cs.data_ptr(),
+           cs.shape[0], float(eps), _dtype_code(qkv))
     return qkv
 
 
@@ -265,8 +265,8 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base:
         wpe_ptr, wpe_rows = wpe.data_ptr(), wpe.shape[0]
     ctx = _ctx_for(tokens)
     _issue(ctx, lib.neko_hip_embed, ctx.handle, tokens.data_ptr(), T, table.data_ptr(), table.shape[1], int(fmt), int(C),
-                                 int(row_base), n_rows, wpe_ptr, wpe_rows, int(pos0), out.data_ptr(), os_,
-                                 _dtype_code(out))
+           int(row_base), n_rows, wpe_ptr, wpe_rows, int(pos0), out.data_ptr(), os_,
+           _dtype_code(out))
     return out
 
 

@@ -138,6 +138,33 @@ def test_gated_rmsnorm_inplace(dev):
     assert_f16_close(to_bits(y), want, what="gated in place")
 
 
+def test_gated_rmsnorm_every_gate(dev):
+    """Every f16 gate value, one per element (subnormals, +-65504, +-inf and NaNs, which fill rows 31
+    and 63), under random y: within 2 ulp of the oracle, NaN exactly where the oracle has NaN."""
+    _case("gated rmsnorm every gate value")
+    D = 1024
+    z = torch.from_numpy(np.arange(65536, dtype=np.uint16).view(np.float16).reshape(64, D).copy()).to(dev)
+    y = _f16((64, D), 57, dev)
+    w = _w(D, 58, dev)
+    out = ops.gated_rms_norm(y, z, w, 1, 1e-5)
+    want = O.gated_rmsnorm_f16(to_bits(y), to_bits(z), w.cpu().numpy(), 1, 1e-5)
+    assert_f16_close(to_bits(out), want, what="gated every gate")
+
+
+@pytest.mark.parametrize("groups", [1, 2])
+def test_gated_rmsnorm_f32(dev, groups):
+    """f32 I/O (the reference's activation type) at the Granite width, against the oracle's f32 op."""
+    T, D = 64, 3072
+    _case(f"gated rmsnorm f32 groups={groups}")
+    y = _f16((T, D), 59, dev).float()
+    z = (_f16((T, D), 60, dev) * 4).float()
+    w = _w(D, 61, dev)
+    out = ops.gated_rms_norm(y, z, w, groups, 1e-5)
+    want = y.cpu().numpy().copy()
+    O.lib().oracle_gated_rmsnorm(O._ptr(want), O._ptr(z.cpu().numpy()), D, O._ptr(w.cpu().numpy()), T, D, groups, 1e-5)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-30)
+
+
 # ------------------------------------------------------------------ q/k norm + RoPE
 
 def _qk_case(dev, T, n_q, n_kv, hd, n_pos, positions, norm, theta=1e6, stream=21, dtype=torch.float16):
