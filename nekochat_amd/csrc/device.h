@@ -78,6 +78,22 @@ __device__ __forceinline__ float silu_fast(float gate) {
     return q;
 }
 
+// float(1 / sqrt(d)) of a double d, the norm scale the reference computes with a correctly rounded
+// double sqrt and division before rounding to float (cpu_ops.cpp:508). Here: v_rsq_f64 and two
+// Newton steps y *= 1.5 - (d/2) y^2 (about 12 double ops instead of ~40). Each step squares the
+// relative error, so the double result is within a few ulps of 1/sqrt(d), and its rounding to float
+// equals the reference's unless 1/sqrt(d) lies within ~2^-50 (relative) of a float rounding
+// boundary, where the two may differ by one float ulp. d outside [2^-1000, 2^1000] (zero,
+// subnormal, infinite or NaN) takes the exact expression.
+__device__ __forceinline__ float rsqrt_to_float(double d) {
+    if (!(d >= 0x1p-1000 && d <= 0x1p1000)) return static_cast<float>(1.0 / sqrt(d));
+    const double h = 0.5 * d;
+    double y = __builtin_amdgcn_rsq(d);
+    y = y * __builtin_fma(-h * y, y, 1.5);
+    y = y * __builtin_fma(-h * y, y, 1.5);
+    return static_cast<float>(y);
+}
+
 // silu(g) = g * rcp(1 + 2^(-g*log2(e))): five VALU ops. Relative error vs the exact quotient is
 // below |g| * 2^-24 * ln 2 (the rounding of the exponent argument) plus ~2 ulp (v_exp_f32, v_rcp_f32,
 // the product): under 1.3e-6 for |g| <= 20, and for g < -20 the value is below 5e-8 * |g|. Special

@@ -20,6 +20,9 @@
 #ifndef NEKO_TUNE_QK_FULLGRID
 #define NEKO_TUNE_QK_FULLGRID 0
 #endif
+#ifndef NEKO_TUNE_QK_RSQ
+#define NEKO_TUNE_QK_RSQ 1
+#endif
 #ifndef NEKO_TUNE_QK_MAXV
 #define NEKO_TUNE_QK_MAXV 8
 #endif
@@ -45,6 +48,34 @@ struct QkArgs {
     int64_t n_pos;
     float eps;
 };
+
+// The head's norm scale float(1 / sqrt(ss / hd + eps)) (cpu_ops.cpp:508 with C = hd). ss / hd is
+// the exact product with 1/hd when hd is a power of two (every Qwen3 head size); the reciprocal
+// square root comes from rsqrt_to_float (device.h) or, with the knob off, the libm-style expression.
+__device__ __forceinline__ float head_scale(const QkArgs& a, double ss) {
+    const double m = (a.hd & (a.hd - 1)) == 0 ? ss * (1.0 / a.hd) : ss / a.hd;
+    if constexpr (NEKO_TUNE_QK_RSQ) return rsqrt_to_float(m + static_cast<double>(a.eps));
+    else return static_cast<float>(1.0 / sqrt(m + static_cast<double>(a.eps)));
+}
+
+// Head stores: non-temporal (knob 1) or plain (0).
+#ifndef NEKO_TUNE_QK_NT_STORE
+#define NEKO_TUNE_QK_NT_STORE 0
+#endif
+template <typename VT>
+__device__ __forceinline__ void qk_store(VT* p, VT v) {
+    if constexpr (NEKO_TUNE_QK_NT_STORE) store_nt(p, v);
+    else *p = v;
+}
+// Head loads: non-temporal (knob 1) or plain (0).
+#ifndef NEKO_TUNE_QK_NT_LOAD
+#define NEKO_TUNE_QK_NT_LOAD 1
+#endif
+template <typename VT>
+__device__ __forceinline__ VT qk_load(const VT* p) {
+    if constexpr (NEKO_TUNE_QK_NT_LOAD) return load_nt(p);
+    else return *p;
+}
 
 __device__ __forceinline__ bool row_position(const QkArgs& a, int64_t t, int64_t& pos) {
     pos = a.positions ? static_cast<int64_t>(a.positions[t]) : a.pos0 + t;
@@ -85,8 +116,8 @@ __device__ __forceinline__ void load_token(TokenRegs<T, V, U>& tr, const QkArgs&
         tr.b[u] = VT{};
         if (head < nh) {
             const T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
-            tr.a[u] = load_nt(reinterpret_cast<const VT*>(hp));
-            tr.b[u] = load_nt(reinterpret_cast<const VT*>(hp + half));
+            tr.a[u] = qk_load(reinterpret_cast<const VT*>(hp));
+            tr.b[u] = qk_load(reinterpret_cast<const VT*>(hp + half));
         }
     }
 }
@@ -124,7 +155,7 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
                 ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
             }
             ss = group_sum_f64<L>(ss);
-            const float r = static_cast<float>(1.0 / sqrt(ss / a.hd + static_cast<double>(a.eps)));
+            const float r = head_scale(a, ss);
             const bool is_q = head < a.n_q;
 #pragma unroll
             for (int e = 0; e < V; e++) {
@@ -147,8 +178,8 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
         }
         if (head < nh) {
             T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
-            *reinterpret_cast<VT*>(hp) = oa;
-            *reinterpret_cast<VT*>(hp + half) = ob;
+            qk_store(reinterpret_cast<VT*>(hp), oa);
+            qk_store(reinterpret_cast<VT*>(hp + half), ob);
         }
     }
 }
@@ -216,8 +247,8 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
             A[u] = VT{};
             B[u] = VT{};
             if (head < nh) {
-                A[u] = load_nt(reinterpret_cast<const VT*>(row + head * a.hd + i0));
-                B[u] = load_nt(reinterpret_cast<const VT*>(row + head * a.hd + half + i0));
+                A[u] = qk_load(reinterpret_cast<const VT*>(row + head * a.hd + i0));
+                B[u] = qk_load(reinterpret_cast<const VT*>(row + head * a.hd + half + i0));
             }
         }
     }
@@ -252,7 +283,7 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
                     ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
                 }
                 ss = group_sum_f64<L>(ss);
-                const float r = static_cast<float>(1.0 / sqrt(ss / a.hd + static_cast<double>(a.eps)));
+                const float r = head_scale(a, ss);
                 const float* w = wsh + (head < a.n_q ? 0 : a.hd) + i0;
 #pragma unroll
                 for (int e = 0; e < V; e++) {
@@ -275,11 +306,11 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
             }
             if (head < nh) {
                 T* hp = row + head * a.hd + i0;
-                *reinterpret_cast<VT*>(hp) = oa;
-                *reinterpret_cast<VT*>(hp + half) = ob;
+                qk_store(reinterpret_cast<VT*>(hp), oa);
+                qk_store(reinterpret_cast<VT*>(hp + half), ob);
                 if (more) {
-                    A[u] = load_nt(reinterpret_cast<const VT*>(nrow + head * a.hd + i0));
-                    B[u] = load_nt(reinterpret_cast<const VT*>(nrow + head * a.hd + half + i0));
+                    A[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * a.hd + i0));
+                    B[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * a.hd + half + i0));
                 }
             }
         }

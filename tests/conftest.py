@@ -47,12 +47,30 @@ def ulp_diff_f16(got, want):
     return d
 
 
-def assert_f16_close(got, want, max_ulp=2, what=""):
-    """The fp16 parity bar: every output within max_ulp fp16 ulp of the oracle (2 = the stated bound)."""
+PARITY = []  # (what, differing outputs, outputs, worst ulp) of every fp16 comparison this session
+
+
+def assert_f16_close(got, want, max_ulp=2, what="", max_diff_frac=1e-3):
+    """The fp16 parity bar: every output within max_ulp fp16 ulp of the oracle (2 = the stated bound),
+    and at most max_diff_frac of the outputs not bit-identical (the kernels round where the reference
+    rounds, so differences come only from summation order or the fast SiLU forms; measured on MI355X
+    they are below 1e-4 of outputs and 1 ulp). None disables the second check."""
     d = ulp_diff_f16(got, want)
     worst = int(d.max()) if d.size else 0
-    assert worst <= max_ulp, f"{what}: max {worst} fp16 ulp from the oracle ({np.count_nonzero(d)} of {d.size} differ)"
+    n = int(np.count_nonzero(d))
+    PARITY.append((what, n, int(d.size), worst))
+    assert worst <= max_ulp, f"{what}: max {worst} fp16 ulp from the oracle ({n} of {d.size} differ)"
+    if max_diff_frac is not None and d.size:
+        assert n <= max_diff_frac * d.size, f"{what}: {n} of {d.size} outputs differ from the oracle"
     return d
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not PARITY:
+        return
+    terminalreporter.write_sep("-", "fp16 parity against the oracle (outputs not bit-identical / total, worst ulp)")
+    for what, n, size, worst in PARITY:
+        terminalreporter.write_line(f"{what}: {n} / {size} ({n / max(size, 1):.2e}), worst {worst} ulp")
 
 
 def to_bits(t):
