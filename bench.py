@@ -47,6 +47,9 @@ def parse():
     p.add_argument("--only", default=None, help="time a single op (for profiling runs)")
     p.add_argument("--all", action="store_true",
                    help="time every configured workload's ops (one JSON line with all of them) instead")
+    p.add_argument("--workload", default=None,
+                   help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
+                        "quant_gather_qwen3_1.7b, granite_4.0h_norms)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -181,6 +184,13 @@ def all_configs(args):
     flush = torch.ones(256 << 20, dtype=torch.float32, device=dev)
     out = {}
 
+    labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "granite_4.0h_norms")
+    if args.workload is not None and args.workload not in labels:
+        raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
+
+    def want(label):
+        return args.workload is None or args.workload == label
+
     def run(label, calls, op_bytes, workload):
         timer = HipTimer(torch.cuda.current_stream().cuda_stream)
         per_op, _ = time_ops(calls, op_bytes, list(calls), args.steps, args.warmup, flush, timer)
@@ -188,86 +198,91 @@ def all_configs(args):
         torch.cuda.synchronize()
 
     # GPT-2 small chain: wte+wpe gather [128, 768] -> LayerNorm -> GELU [128, 3072]
-    c1 = wl.GPT2_CHAIN
-    wte = wl.normal_f16((c1.vocab, c1.C), 0.0, 0.02, 41, dev)
-    wpe = wl.normal_f16((c1.n_ctx, c1.C), 0.0, 0.02, 42, dev)
-    ids = torch.from_numpy(wl.uniform_ids(c1.T, c1.vocab, 43)).to(dev)
-    table = wte.view(torch.uint8).reshape(c1.vocab, 2 * c1.C)
-    x1 = torch.empty((c1.T, c1.C), dtype=torch.float16, device=dev)
-    g1, b1 = wl.weight_f32(c1.C, 1.0, 0.02, 44, dev), wl.weight_f32(c1.C, 0.0, 0.02, 45, dev)
-    y1 = torch.empty_like(x1)
-    h1 = wl.normal_f16((c1.T, c1.F), 0.0, 1.0, 46, dev)
-    o1 = torch.empty_like(h1)
-    run("gpt2_small_chain", {
-        "gather_wte_wpe": ops.prepare(ops.embed, ids, table, ops.FMT_F16, c1.C, wpe=wpe, out=x1)[0],
-        "layernorm": ops.prepare(ops.layer_norm, x1, g1, b1, c1.eps, out=y1)[0],
-        "gelu": ops.prepare(ops.gelu, h1, out=o1)[0],
-    }, {"gather_wte_wpe": wl.bytes_gather(c1.T, 2 * c1.C, c1.C, wpe=True),
-        "layernorm": wl.bytes_layernorm(c1.T, c1.C), "gelu": wl.bytes_gelu(c1.T * c1.F)},
-        "GPT-2 small: gather wte+wpe [128,768], LayerNorm [128,768], GELU-tanh [128,3072]")
+    if want("gpt2_small_chain"):
+        c1 = wl.GPT2_CHAIN
+        wte = wl.normal_f16((c1.vocab, c1.C), 0.0, 0.02, 41, dev)
+        wpe = wl.normal_f16((c1.n_ctx, c1.C), 0.0, 0.02, 42, dev)
+        ids = torch.from_numpy(wl.uniform_ids(c1.T, c1.vocab, 43)).to(dev)
+        table = wte.view(torch.uint8).reshape(c1.vocab, 2 * c1.C)
+        x1 = torch.empty((c1.T, c1.C), dtype=torch.float16, device=dev)
+        g1, b1 = wl.weight_f32(c1.C, 1.0, 0.02, 44, dev), wl.weight_f32(c1.C, 0.0, 0.02, 45, dev)
+        y1 = torch.empty_like(x1)
+        h1 = wl.normal_f16((c1.T, c1.F), 0.0, 1.0, 46, dev)
+        o1 = torch.empty_like(h1)
+        run("gpt2_small_chain", {
+            "gather_wte_wpe": ops.prepare(ops.embed, ids, table, ops.FMT_F16, c1.C, wpe=wpe, out=x1)[0],
+            "layernorm": ops.prepare(ops.layer_norm, x1, g1, b1, c1.eps, out=y1)[0],
+            "gelu": ops.prepare(ops.gelu, h1, out=o1)[0],
+        }, {"gather_wte_wpe": wl.bytes_gather(c1.T, 2 * c1.C, c1.C, wpe=True),
+            "layernorm": wl.bytes_layernorm(c1.T, c1.C), "gelu": wl.bytes_gelu(c1.T * c1.F)},
+            "GPT-2 small: gather wte+wpe [128,768], LayerNorm [128,768], GELU-tanh [128,3072]")
 
     # Qwen3-0.6B decode batch
-    c2 = wl.QWEN3_DECODE
-    stride2 = (c2.n_q + 2 * c2.n_kv) * c2.hd
-    x2 = wl.normal_f16((c2.T, c2.C), 0.0, 1.0, 1, dev)
-    w2 = wl.weight_f32(c2.C, 1.0, 0.05, 2, dev)
-    y2 = torch.empty_like(x2)
-    qkv2 = wl.normal_f16((c2.T, stride2), 0.0, 1.0, 4, dev)
-    wqk2 = wl.weight_f32(2 * c2.hd, 1.0, 0.05, 5, dev)
-    pos2 = torch.from_numpy(wl.uniform_ids(c2.T, c2.n_pos, 7)).to(dev)
-    cs2 = torch.from_numpy(ops.rope_table(c2.theta, c2.hd, c2.n_pos)).to(dev)
-    h2 = wl.normal_f16((c2.T, 2 * c2.I), 0.0, 1.0, 6, dev)
-    o2 = torch.empty((c2.T, c2.I), dtype=torch.float16, device=dev)
-    run("qwen3_0.6b_decode", {
-        "rmsnorm": ops.prepare(ops.rms_norm, x2, w2, c2.eps, out=y2)[0],
-        "qk_norm_rope": ops.prepare(ops.qk_norm_rope, qkv2, c2.n_q, c2.n_kv, c2.hd, cs2, c2.eps, wqk=wqk2,
-                                    positions=pos2)[0],
-        "swiglu": ops.prepare(ops.silu_mul, h2, out=o2)[0],
-    }, {"rmsnorm": wl.bytes_rmsnorm(c2.T, c2.C), "qk_norm_rope": wl.bytes_qk_rope(c2.T, c2.n_q, c2.n_kv, c2.hd),
-        "swiglu": wl.bytes_swiglu(c2.T, c2.I)},
-        "Qwen3-0.6B decode: 64 rows, RMSNorm 1024, q/k RoPE 16q+8kv x 128 at random positions, SwiGLU I=3072")
+    if want("qwen3_0.6b_decode"):
+        c2 = wl.QWEN3_DECODE
+        stride2 = (c2.n_q + 2 * c2.n_kv) * c2.hd
+        x2 = wl.normal_f16((c2.T, c2.C), 0.0, 1.0, 1, dev)
+        w2 = wl.weight_f32(c2.C, 1.0, 0.05, 2, dev)
+        y2 = torch.empty_like(x2)
+        qkv2 = wl.normal_f16((c2.T, stride2), 0.0, 1.0, 4, dev)
+        wqk2 = wl.weight_f32(2 * c2.hd, 1.0, 0.05, 5, dev)
+        pos2 = torch.from_numpy(wl.uniform_ids(c2.T, c2.n_pos, 7)).to(dev)
+        cs2 = torch.from_numpy(ops.rope_table(c2.theta, c2.hd, c2.n_pos)).to(dev)
+        h2 = wl.normal_f16((c2.T, 2 * c2.I), 0.0, 1.0, 6, dev)
+        o2 = torch.empty((c2.T, c2.I), dtype=torch.float16, device=dev)
+        run("qwen3_0.6b_decode", {
+            "rmsnorm": ops.prepare(ops.rms_norm, x2, w2, c2.eps, out=y2)[0],
+            "qk_norm_rope": ops.prepare(ops.qk_norm_rope, qkv2, c2.n_q, c2.n_kv, c2.hd, cs2, c2.eps, wqk=wqk2,
+                                        positions=pos2)[0],
+            "swiglu": ops.prepare(ops.silu_mul, h2, out=o2)[0],
+        }, {"rmsnorm": wl.bytes_rmsnorm(c2.T, c2.C), "qk_norm_rope": wl.bytes_qk_rope(c2.T, c2.n_q, c2.n_kv, c2.hd),
+            "swiglu": wl.bytes_swiglu(c2.T, c2.I)},
+            "Qwen3-0.6B decode: 64 rows, RMSNorm 1024, q/k RoPE 16q+8kv x 128 at random positions, SwiGLU I=3072")
 
     # Qwen3-4B prefill (the headline layer)
-    cfg, per_op, _ = gpu_bench(argparse.Namespace(only=None, copy_mib=0, steps=args.steps, warmup=args.warmup,
-                                                  no_flush=False))
-    out["qwen3_4b_prefill"] = {"workload": "Qwen3-4B prefill layer (headline)", "ops": per_op}
+    if want("qwen3_4b_prefill"):
+        cfg, per_op, _ = gpu_bench(argparse.Namespace(only=None, copy_mib=0, steps=args.steps, warmup=args.warmup,
+                                                      no_flush=False))
+        out["qwen3_4b_prefill"] = {"workload": "Qwen3-4B prefill layer (headline)", "ops": per_op}
 
     # Quantised gather: 151936 x 2048 tied table, 16384 Zipf(1.1) ids, FP16 / FP8 / FP4 rows
-    c4 = wl.QUANT_GATHER
-    src = wl.normal_f16((c4.vocab, c4.C), 0.0, 0.02, 31, dev).float().cpu().numpy()
-    ids4 = wl.zipf_ids(c4.T, c4.vocab, c4.s, 32)
-    ids4_t = torch.from_numpy(ids4).to(dev)
-    o4 = torch.empty((c4.T, c4.C), dtype=torch.float16, device=dev)
-    calls4, bytes4 = {}, {}
-    unique = int(np.unique(ids4).size)
-    for fmt, name in ((ops.FMT_F16, "gather_fp16"), (ops.FMT_FP8, "gather_fp8"), (ops.FMT_FP4, "gather_fp4")):
-        tab, _ = ops.quantize_rows(fmt, src)
-        tab_t = torch.from_numpy(tab).to(dev)
-        calls4[name] = ops.prepare(ops.embed, ids4_t, tab_t, fmt, c4.C, out=o4)[0]
-        bytes4[name] = wl.bytes_gather(c4.T, tab.shape[1], c4.C)
-        calls4[name].table = tab_t  # keep the table alive with its call
-    del src
-    run("quant_gather_qwen3_1.7b", calls4, bytes4,
-        f"Qwen3-1.7B tied table 151936x2048, 16384 Zipf(1.1) ids ({unique} unique rows): mostly cache-served")
+    if want("quant_gather_qwen3_1.7b"):
+        c4 = wl.QUANT_GATHER
+        src = wl.normal_f16((c4.vocab, c4.C), 0.0, 0.02, 31, dev).float().cpu().numpy()
+        ids4 = wl.zipf_ids(c4.T, c4.vocab, c4.s, 32)
+        ids4_t = torch.from_numpy(ids4).to(dev)
+        o4 = torch.empty((c4.T, c4.C), dtype=torch.float16, device=dev)
+        calls4, bytes4 = {}, {}
+        unique = int(np.unique(ids4).size)
+        for fmt, name in ((ops.FMT_F16, "gather_fp16"), (ops.FMT_FP8, "gather_fp8"), (ops.FMT_FP4, "gather_fp4")):
+            tab, _ = ops.quantize_rows(fmt, src)
+            tab_t = torch.from_numpy(tab).to(dev)
+            calls4[name] = ops.prepare(ops.embed, ids4_t, tab_t, fmt, c4.C, out=o4)[0]
+            bytes4[name] = wl.bytes_gather(c4.T, tab.shape[1], c4.C)
+            calls4[name].table = tab_t  # keep the table alive with its call
+        del src
+        run("quant_gather_qwen3_1.7b", calls4, bytes4,
+            f"Qwen3-1.7B tied table 151936x2048, 16384 Zipf(1.1) ids ({unique} unique rows): mostly cache-served")
 
     # Granite-4.0-H-style norms and SwiGLU
-    c5 = wl.GRANITE_NORMS
-    x5 = wl.normal_f16((c5.T, c5.C), 0.0, 1.0, 51, dev)
-    w5 = wl.weight_f32(c5.C, 1.0, 0.05, 52, dev)
-    y5 = torch.empty_like(x5)
-    ya = wl.normal_f16((c5.T, c5.D), 0.0, 1.0, 53, dev)
-    za = wl.normal_f16((c5.T, c5.D), 0.0, 1.0, 54, dev)
-    wg = wl.weight_f32(c5.D, 1.0, 0.05, 55, dev)
-    og = torch.empty_like(ya)
-    h5 = wl.normal_f16((c5.T, 2 * c5.I), 0.0, 1.0, 56, dev)
-    o5 = torch.empty((c5.T, c5.I), dtype=torch.float16, device=dev)
-    run("granite_4.0h_norms", {
-        "rmsnorm": ops.prepare(ops.rms_norm, x5, w5, c5.eps, out=y5)[0],
-        "gated_rmsnorm": ops.prepare(ops.gated_rms_norm, ya, za, wg, c5.groups, c5.eps, out=og)[0],
-        "swiglu": ops.prepare(ops.silu_mul, h5, out=o5)[0],
-    }, {"rmsnorm": wl.bytes_rmsnorm(c5.T, c5.C), "gated_rmsnorm": wl.bytes_gated(c5.T, c5.D),
-        "swiglu": wl.bytes_swiglu(c5.T, c5.I)},
-        "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096")
+    if want("granite_4.0h_norms"):
+        c5 = wl.GRANITE_NORMS
+        x5 = wl.normal_f16((c5.T, c5.C), 0.0, 1.0, 51, dev)
+        w5 = wl.weight_f32(c5.C, 1.0, 0.05, 52, dev)
+        y5 = torch.empty_like(x5)
+        ya = wl.normal_f16((c5.T, c5.D), 0.0, 1.0, 53, dev)
+        za = wl.normal_f16((c5.T, c5.D), 0.0, 1.0, 54, dev)
+        wg = wl.weight_f32(c5.D, 1.0, 0.05, 55, dev)
+        og = torch.empty_like(ya)
+        h5 = wl.normal_f16((c5.T, 2 * c5.I), 0.0, 1.0, 56, dev)
+        o5 = torch.empty((c5.T, c5.I), dtype=torch.float16, device=dev)
+        run("granite_4.0h_norms", {
+            "rmsnorm": ops.prepare(ops.rms_norm, x5, w5, c5.eps, out=y5)[0],
+            "gated_rmsnorm": ops.prepare(ops.gated_rms_norm, ya, za, wg, c5.groups, c5.eps, out=og)[0],
+            "swiglu": ops.prepare(ops.silu_mul, h5, out=o5)[0],
+        }, {"rmsnorm": wl.bytes_rmsnorm(c5.T, c5.C), "gated_rmsnorm": wl.bytes_gated(c5.T, c5.D),
+            "swiglu": wl.bytes_swiglu(c5.T, c5.I)},
+            "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096")
     return out
 
 

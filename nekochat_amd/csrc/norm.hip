@@ -1,11 +1,13 @@
 // Row norms for gfx950: LayerNorm (cpu_ops.cpp:483-500), RMSNorm (cpu_ops.cpp:502-511) and the
 // Granite-4.0-H gated group RMSNorm (granite_model.cpp:278-287).
 //
-// Fast path: one 64-wide wavefront per row, persistent. A grid of four 256-thread workgroups per CU
-// walks the rows; each wave keeps its norm weights in registers for all of its rows and issues the
-// 16-byte non-temporal loads of its next row before it reduces the current one, so HBM is read
-// once, written once, and always has loads in flight. Rows wider than one wave's registers use four
-// waves per row. Sums are accumulated in double, like the reference, and reduced across the wave
+// Fast path: one 64-wide wavefront per row, persistent. A grid of as many 256-thread workgroups as
+// stay resident walks the rows. RMSNorm / LayerNorm waves keep their norm weights in registers for
+// all of their rows and issue the 16-byte non-temporal loads of the next row before they reduce the
+// current one, so HBM is read once, written once, and always has loads in flight. The gated norm,
+// which holds two operands per row, reads its weights from one LDS copy per workgroup and runs
+// without the second row buffer, trading per-wave prefetch for three times the resident waves.
+// Rows wider than one wave's registers use four waves per row. Sums are accumulated in double, like the reference, and reduced across the wave
 // with DPP and v_readlane (LDS only joins the partial sums of multi-wave rows). The norm scale is
 // rounded to float exactly where the reference rounds it and the output is (x * s) * w unfused, so
 // results match the reference's CPU op bit for bit unless a double sum lands within an ulp of a
