@@ -164,6 +164,29 @@ void oracle_gated_rmsnorm(float* y, const float* z, int64_t z_stride, const floa
     }
 }
 
+/* KV-cache store (cpu_ops.cpp:535-542): row t's k and v, width floats each, rounded to f16 into cache
+ * row pos0 + t (toHalf, cpu_ops.cpp:98-104). */
+void oracle_store_kv(const float* k, const float* v, int64_t src_stride, uint16_t* kc, uint16_t* vc, int width,
+                     int64_t T, int64_t pos0) {
+    for (int64_t t = 0; t < T; t++) {
+        const int64_t dst = (pos0 + t) * (int64_t)width;
+        oracle_f32_to_f16_n(k + t * src_stride, kc + dst, width);
+        oracle_f32_to_f16_n(v + t * src_stride, vc + dst, width);
+    }
+}
+
+/* Residual add then RMSNorm: the matmul epilogue with kAccumulate adds the product into the residual
+ * row, dst = dst + v in float (cpu_ops.cpp:123), and the next op norms that row (qwen3_model.cpp:264,
+ * cpu_ops.cpp:502-511). Here v is the delta row d. */
+void oracle_add_rmsnorm(float* x, const float* d, float* xn, const float* w, int rows, int C, float eps) {
+    for (int t = 0; t < rows; t++) {
+        float* xr = x + (size_t)t * (size_t)C;
+        const float* dr = d + (size_t)t * (size_t)C;
+        for (int i = 0; i < C; i++) xr[i] = xr[i] + dr[i];
+        oracle_rmsnorm(xr, xn + (size_t)t * (size_t)C, w, 1, C, eps);
+    }
+}
+
 /* RoPE table in double, stored as float pairs (qwen3_model.cpp:102-114). */
 void oracle_rope_table(double theta, int hd, int n_pos, float* cs) {
     for (int i = 0; i < hd / 2; i++) {
@@ -412,6 +435,62 @@ void oracle_qk_norm_rope_f32(float* qkv, int64_t row_stride, int64_t rows, int n
         if (!row_position(r, pos0, positions, n_pos, &pos)) continue;
         qk_row_f32(qkv + r * row_stride, n_q, n_kv, hd, wqk, cs + pos * hd, eps);
     }
+}
+
+/* The KV store at the C ABI's argument meaning: cache row = positions[t] (or pos0 + t); rows whose
+ * cache row is outside [0, cache_rows) are skipped. f16 activations are copied bit for bit (a
+ * half widened to f32 and rounded back is itself); f32 activations are rounded by
+ * oracle_store_kv. */
+void oracle_store_kv_rows(const void* qkv, int is_f16, int64_t row_stride, int64_t k_off, int64_t v_off, int width,
+                          int64_t rows, int64_t pos0, const int32_t* positions, int64_t cache_rows, uint16_t* kc,
+                          uint16_t* vc) {
+    for (int64_t t = 0; t < rows; t++) {
+        int64_t p;
+        if (!row_position(t, pos0, positions, cache_rows, &p)) continue;
+        if (is_f16) {
+            const uint16_t* r = (const uint16_t*)qkv + t * row_stride;
+            memcpy(kc + p * width, r + k_off, (size_t)width * 2u);
+            memcpy(vc + p * width, r + v_off, (size_t)width * 2u);
+        } else {
+            const float* r = (const float*)qkv + t * row_stride;
+            oracle_store_kv(r + k_off, r + v_off, 0, kc, vc, width, 1, p);
+        }
+    }
+}
+
+/* q/k norm + RoPE then the KV store of the rotated keys and the values (qwen3_model.cpp:249-256),
+ * cache row = the row's position; rows outside [0, n_pos) are left untouched and store nothing. */
+void oracle_qk_norm_rope_kv_f16(uint16_t* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd,
+                                int64_t pos0, const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos,
+                                float eps, uint16_t* kc, uint16_t* vc) {
+    oracle_qk_norm_rope_f16(qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps);
+    const int64_t kw = (int64_t)n_kv * hd;
+    oracle_store_kv_rows(qkv, 1, row_stride, (int64_t)n_q * hd, (int64_t)n_q * hd + kw, (int)kw, rows, pos0, positions,
+                         n_pos, kc, vc);
+}
+
+void oracle_qk_norm_rope_kv_f32(float* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd, int64_t pos0,
+                                const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos, float eps,
+                                uint16_t* kc, uint16_t* vc) {
+    oracle_qk_norm_rope_f32(qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps);
+    const int64_t kw = (int64_t)n_kv * hd;
+    oracle_store_kv_rows(qkv, 0, row_stride, (int64_t)n_q * hd, (int64_t)n_q * hd + kw, (int)kw, rows, pos0, positions,
+                         n_pos, kc, vc);
+}
+
+/* fp16 residual add + RMSNorm: x = f16(f32(x) + f32(d)) stored back, then xn = rmsnorm of the stored
+ * halves (the unfused add-then-norm sequence with fp16 activations). */
+void oracle_add_rmsnorm_f16(uint16_t* x, int64_t xs, const uint16_t* d, int64_t ds, uint16_t* xn, int64_t xns,
+                            const float* w, int64_t rows, int C, float eps) {
+    float* t = scratch_f32((size_t)2 * (size_t)C);
+    for (int64_t r = 0; r < rows; r++) {
+        oracle_f16_to_f32_n(x + r * xs, t, C);
+        oracle_f16_to_f32_n(d + r * ds, t + C, C);
+        for (int i = 0; i < C; i++) t[i] = t[i] + t[C + i];
+        oracle_f32_to_f16_n(t, x + r * xs, C);
+    }
+    free(t);
+    oracle_rmsnorm_f16(x, xs, xn, xns, w, rows, C, eps);
 }
 
 void oracle_swiglu_f16(const uint16_t* h, int64_t hs, uint16_t* out, int64_t os, int64_t rows, int I) {

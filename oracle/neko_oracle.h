@@ -60,6 +60,13 @@ void oracle_gated_rmsnorm(float* y, const float* z, int64_t z_stride, const floa
 /* cs[p][i] = (cos(p * theta^(-2i/hd)), sin(...)) for p < n_pos, i < hd/2; row stride hd floats
  * (qwen3_model.cpp:102-114). */
 void oracle_rope_table(double theta, int hd, int n_pos, float* cs);
+/* KV-cache store (cpu_ops.cpp:535-542): k/v rows of width floats (stride src_stride) rounded to f16
+ * into cache rows pos0 + t. */
+void oracle_store_kv(const float* k, const float* v, int64_t src_stride, uint16_t* kc, uint16_t* vc, int width,
+                     int64_t T, int64_t pos0);
+/* Residual add (matmul kAccumulate epilogue, cpu_ops.cpp:123: x = x + d in float), then RMSNorm of
+ * the updated rows into xn (qwen3_model.cpp:264, cpu_ops.cpp:502-511). x is updated in place. */
+void oracle_add_rmsnorm(float* x, const float* d, float* xn, const float* w, int rows, int C, float eps);
 
 /* ---- weight row formats (quant.h:19-58, quant.cpp) ---- */
 enum { ORACLE_FMT_F16 = 0, ORACLE_FMT_FP8 = 1, ORACLE_FMT_FP4 = 2 };
@@ -90,6 +97,24 @@ void oracle_qk_norm_rope_f16(uint16_t* qkv, int64_t row_stride, int64_t rows, in
 void oracle_qk_norm_rope_f32(float* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd,
                              int64_t pos0, const int32_t* positions, const float* wqk, const float* cs,
                              int64_t n_pos, float eps);
+/* KV store at the C ABI's argument meaning: k = qkv row + k_off, v = qkv row + v_off (width values
+ * each), cache row = positions[t] or pos0 + t, rows outside [0, cache_rows) skipped; f16 activations
+ * are copied bit for bit, f32 activations rounded to f16 (oracle_store_kv). */
+void oracle_store_kv_rows(const void* qkv, int is_f16, int64_t row_stride, int64_t k_off, int64_t v_off, int width,
+                          int64_t rows, int64_t pos0, const int32_t* positions, int64_t cache_rows, uint16_t* kc,
+                          uint16_t* vc);
+/* q/k norm + RoPE, then the KV store of the rotated keys and the values into cache row = the row's
+ * position (qwen3_model.cpp:249-256); kc / vc rows are n_kv*hd halves; rows outside [0, n_pos) are
+ * untouched and store nothing. */
+void oracle_qk_norm_rope_kv_f16(uint16_t* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd,
+                                int64_t pos0, const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos,
+                                float eps, uint16_t* kc, uint16_t* vc);
+void oracle_qk_norm_rope_kv_f32(float* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd, int64_t pos0,
+                                const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos, float eps,
+                                uint16_t* kc, uint16_t* vc);
+/* fp16 residual add + RMSNorm: x = f16(f32(x) + f32(d)) in place, then xn = rmsnorm_f16(x). */
+void oracle_add_rmsnorm_f16(uint16_t* x, int64_t xs, const uint16_t* d, int64_t ds, uint16_t* xn, int64_t xns,
+                            const float* w, int64_t rows, int C, float eps);
 void oracle_swiglu_f16(const uint16_t* h, int64_t hs, uint16_t* out, int64_t os, int64_t rows, int I);
 void oracle_gelu_f16(const uint16_t* x, uint16_t* y, int64_t n);
 void oracle_gated_rmsnorm_f16(const uint16_t* y, int64_t ys, const uint16_t* z, int64_t zs, uint16_t* out,

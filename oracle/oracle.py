@@ -88,6 +88,12 @@ _ORACLE_SIGS = {
     "oracle_gelu_f16": (None, [_p, _p, _i64]),
     "oracle_gated_rmsnorm_f16": (None, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _i32, _f32]),
     "oracle_embed": (None, [_p, _i64, _p, _i64, _i32, _i32, _i64, _i64, _p, _i64, _p, _i64, _i32]),
+    "oracle_store_kv": (None, [_p, _p, _i64, _p, _p, _i32, _i64, _i64]),
+    "oracle_add_rmsnorm": (None, [_p, _p, _p, _p, _i32, _i32, _f32]),
+    "oracle_store_kv_rows": (None, [_p, _i32, _i64, _i64, _i64, _i32, _i64, _i64, _p, _i64, _p, _p]),
+    "oracle_qk_norm_rope_kv_f16": (None, [_p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p]),
+    "oracle_qk_norm_rope_kv_f32": (None, [_p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p]),
+    "oracle_add_rmsnorm_f16": (None, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _f32]),
 }
 
 _REF_SIGS = {
@@ -110,6 +116,8 @@ _REF_SIGS = {
     "ref_gelu_f16": (None, [_p, _p, _i32]),
     "ref_gated_rmsnorm_f16": (None, [_p, _p, _p, _p, _i32, _i32, _i32, _f32]),
     "ref_embed": (None, [_p, _i32, _p, _i32, _i32, _i32, _p, _i32, _p, _i32]),
+    "ref_store_kv": (None, [_p, _p, _i32, _p, _p, _i32, _i32, _i32]),
+    "ref_add_rmsnorm_f16": (None, [_p, _p, _p, _p, _p, _i32, _i32, _f32]),
 }
 
 _oracle = None
@@ -187,6 +195,44 @@ def qk_norm_rope_f32(qkv, n_q, n_kv, hd, cs, n_pos, eps, wqk=None, positions=Non
     lib().oracle_qk_norm_rope_f32(_ptr(out), stride, rows, n_q, n_kv, hd, pos0, _ptr(pos), _ptr(w), _ptr(_c32(cs)),
                                   n_pos, eps)
     return out
+
+
+def qk_norm_rope_kv(qkv, n_q, n_kv, hd, cs, n_pos, eps, wqk=None, positions=None, pos0=0):
+    """q/k norm + RoPE then the KV store; returns (qkv after, k cache, v cache) with n_pos cache rows
+    (rows the op does not write stay 0xFFFF so untouched rows are visible)."""
+    f16 = qkv.dtype == np.uint16
+    out = (_c16(qkv) if f16 else _c32(qkv)).copy()
+    rows, stride = out.shape
+    pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+    w = None if wqk is None else _c32(wqk)
+    kc = np.full((n_pos, n_kv * hd), 0xFFFF, np.uint16)
+    vc = kc.copy()
+    fn = lib().oracle_qk_norm_rope_kv_f16 if f16 else lib().oracle_qk_norm_rope_kv_f32
+    fn(_ptr(out), stride, rows, n_q, n_kv, hd, pos0, _ptr(pos), _ptr(w), _ptr(_c32(cs)), n_pos, eps, _ptr(kc), _ptr(vc))
+    return out, kc, vc
+
+
+def store_kv(qkv, k_off, v_off, width, cache_rows, positions=None, pos0=0):
+    """KV store at the C ABI's meaning; qkv uint16 (f16 bits) or float32. Unwritten cache rows stay 0xFFFF."""
+    f16 = qkv.dtype == np.uint16
+    src = _c16(qkv) if f16 else _c32(qkv)
+    rows, stride = src.shape
+    pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+    kc = np.full((cache_rows, width), 0xFFFF, np.uint16)
+    vc = kc.copy()
+    lib().oracle_store_kv_rows(_ptr(src), int(f16), stride, k_off, v_off, width, rows, pos0, _ptr(pos), cache_rows,
+                               _ptr(kc), _ptr(vc))
+    return kc, vc
+
+
+def add_rmsnorm_f16(x, d, w, eps):
+    """Returns (x + d rounded to f16, rmsnorm of it)."""
+    xo = _c16(x).copy()
+    d = _c16(d)
+    rows, C = xo.shape
+    xn = np.empty_like(xo)
+    lib().oracle_add_rmsnorm_f16(_ptr(xo), C, _ptr(d), d.shape[1], _ptr(xn), C, _ptr(_c32(w)), rows, C, eps)
+    return xo, xn
 
 
 def swiglu_f16(h):

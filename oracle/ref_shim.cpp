@@ -134,6 +134,30 @@ void ref_gated_rmsnorm_f16(const uint16_t* y, const uint16_t* z, uint16_t* out, 
     }
 }
 
+// KV-cache store: the compiled cpu::storeKv.
+void ref_store_kv(const float* k, const float* v, int src_stride, uint16_t* kc, uint16_t* vc, int width, int T, int pos0) {
+    cpu::storeKv(k, v, src_stride, kc, vc, width, T, pos0);
+}
+
+// Residual add + RMSNorm with f16 I/O, entirely through compiled reference code: the add is the
+// matmulF16 kAccumulate epilogue (cpu_ops.cpp:123) with an identity weight matrix, so each output
+// row is y = y + (sum of 1 * d[n] and exact zeros) = y + d (finite d); then cpu::rmsNorm of the
+// f16-rounded sum. x_out receives the rounded sum.
+void ref_add_rmsnorm_f16(const uint16_t* x, const uint16_t* d, uint16_t* x_out, uint16_t* xn, const float* w, int rows,
+                         int C, float eps) {
+    std::vector<float> xs(size_t(rows) * size_t(C)), ds(xs.size()), y(xs.size());
+    widen(x, xs.data(), xs.size());
+    widen(d, ds.data(), ds.size());
+    std::vector<uint16_t> eye(size_t(C) * size_t(C), 0);
+    for (int n = 0; n < C; n++) eye[size_t(n) * size_t(C) + size_t(n)] = 0x3C00;  // 1.0
+    ThreadPool pool(1);
+    cpu::matmulF16(pool, ds.data(), rows, C, eye.data(), nullptr, xs.data(), C, cpu::kAccumulate);
+    narrow(xs.data(), x_out, xs.size());
+    widen(x_out, xs.data(), xs.size());
+    cpu::rmsNorm(xs.data(), y.data(), w, rows, C, eps);
+    narrow(y.data(), xn, y.size());
+}
+
 // Embedding gather: dequantizeRow of each token's row, + the f32 position row (gpt2_model.cpp:182-187),
 // rounded to f16 when out_f16.
 void ref_embed(const int32_t* tokens, int T, const uint8_t* table, int fmt, int rows, int C, const uint16_t* wpe,

@@ -132,6 +132,29 @@ def main():
     R.ref_dequantize_row(2, 32, P(row4), P(dec4))
     g.update(fp8_decode=dec8, fp4_decode=dec4[:16].copy())
 
+    # KV-cache store (cpu_ops.cpp:535-542): f32 k/v rows of a qkv buffer into f16 caches at pos0 + t,
+    # with values that round to f16 subnormals, overflow to inf, and a NaN.
+    T, W, stride = 5, 256, 1024
+    src = (rng.standard_normal((T, stride)) * 3.0).astype(np.float32)
+    src[1, 300] = 1e-6
+    src[2, 260] = 70000.0
+    src[3, 700] = np.nan
+    kc = np.full((12, W), 0xFFFF, np.uint16)
+    vc = kc.copy()
+    base = src.ctypes.data  # k at column 256, v at column 640 of each 1024-float row
+    R.ref_store_kv(ctypes.c_void_p(base + 256 * 4), ctypes.c_void_p(base + 640 * 4), stride, P(kc), P(vc), W, T, 4)
+    g.update(kv_src=src, kv_k=kc, kv_v=vc)
+
+    # Residual add + RMSNorm with f16 I/O, through the compiled matmul kAccumulate epilogue and
+    # rmsNorm; a row whose sum cancels to zero and a row of large values.
+    x, d = f16(rng, (8, 512)), f16(rng, (8, 512), std=0.5)
+    d[2] = (-x[2].view(np.float16)).view(np.uint16)
+    x[5] = (x[5].view(np.float16) * np.float16(1000.0)).view(np.uint16)
+    w = w32(rng, 512)
+    xo, xn = np.empty_like(x), np.empty_like(x)
+    R.ref_add_rmsnorm_f16(P(x), P(d), P(xo), P(xn), P(w), 8, 512, F(1e-6))
+    g.update(addrms_x=x, addrms_d=d, addrms_w=w, addrms_xo=xo, addrms_xn=xn)
+
     path = os.path.join(HERE, "golden.npz")
     np.savez_compressed(path, **g)
     print(f"wrote {path}: {len(g)} arrays, {os.path.getsize(path)} bytes")

@@ -70,6 +70,18 @@ def test_golden_wpe(golden):
     assert np.array_equal(got, golden["embed_wpe_f16"])
 
 
+def test_golden_store_kv(golden):
+    """cpu::storeKv of f32 k/v rows (pos0 4), with values rounding to an f16 subnormal, inf and NaN."""
+    kc, vc = O.store_kv(golden["kv_src"], 256, 640, 256, 12, pos0=4)
+    assert np.array_equal(kc, golden["kv_k"]) and np.array_equal(vc, golden["kv_v"])
+
+
+def test_golden_add_rmsnorm(golden):
+    """Residual add (compiled matmul kAccumulate epilogue) + compiled rmsNorm, f16 I/O."""
+    xo, xn = O.add_rmsnorm_f16(golden["addrms_x"], golden["addrms_d"], golden["addrms_w"], 1e-6)
+    assert np.array_equal(xo, golden["addrms_xo"]) and np.array_equal(xn, golden["addrms_xn"])
+
+
 def test_golden_decoders(golden):
     d8 = np.array([O.lib().oracle_decode_fp8(c) for c in range(256)], np.float32)
     assert np.array_equal(d8.view(np.uint32), golden["fp8_decode"].view(np.uint32))
@@ -134,6 +146,23 @@ def test_ref_ops_bitexact(seed):
     xs = rng.standard_normal(4096).astype(np.float32) * 6
     assert np.array_equal(np.array([O.lib().oracle_gelu(v) for v in xs], np.float32).view(np.uint32),
                           np.array([R.ref_gelu(v) for v in xs], np.float32).view(np.uint32))
+    # KV store: f32 rows of a qkv buffer (k at 100, v at 900, width 300) into caches at pos0 + t.
+    src = (rng.standard_normal((7, 1300)) * 4).astype(np.float32)
+    src[2, 150] = 3e5
+    kc = np.full((20, 300), 0xFFFF, np.uint16)
+    vc = kc.copy()
+    R.ref_store_kv(ctypes.c_void_p(src.ctypes.data + 400), ctypes.c_void_p(src.ctypes.data + 3600), 1300, P(kc), P(vc),
+                   300, 7, 11)
+    ok, ov = O.store_kv(src, 100, 900, 300, 20, pos0=11)
+    assert np.array_equal(ok, kc) and np.array_equal(ov, vc)
+    # Residual add + RMSNorm (compiled kAccumulate epilogue and rmsNorm).
+    x = (rng.standard_normal((6, 384)) * 3).astype(np.float16).view(np.uint16)
+    d = rng.standard_normal((6, 384)).astype(np.float16).view(np.uint16)
+    w3 = rng.standard_normal(384).astype(np.float16).astype(np.float32)
+    xo, xn = np.empty_like(x), np.empty_like(x)
+    R.ref_add_rmsnorm_f16(P(x), P(d), P(xo), P(xn), P(w3), 6, 384, F(1e-5))
+    oxo, oxn = O.add_rmsnorm_f16(x, d, w3, 1e-5)
+    assert np.array_equal(oxo, xo) and np.array_equal(oxn, xn)
 
 
 @needs_ref
@@ -322,3 +351,62 @@ def test_rope_identities():
     cc, ss = cs[1234, 10], cs[1234, 11]
     assert v[0, 5] == np.float32(a * cc) - np.float32(b * ss)
     assert v[0, 69] == np.float32(a * ss) + np.float32(b * cc)
+
+
+def test_store_kv_closed_form():
+    """The KV store is numpy's IEEE RNE cast to f16 of each k/v value, written at the row's position;
+    f16 activations are copied bit for bit; rows outside the cache are skipped."""
+    rng = np.random.default_rng(21)
+    src = (rng.standard_normal((9, 700)) * 300).astype(np.float32)
+    src[0, 50:54] = [np.inf, -np.inf, 1e-8, -7e4]
+    pos = np.array([3, 0, 8, -1, 5, 12, 7, 1, 2], np.int32)  # -1 and 12 are outside 10 cache rows
+    kc, vc = O.store_kv(src, 40, 400, 256, 10, positions=pos)
+    for t, p in enumerate(pos):
+        if 0 <= p < 10:
+            assert np.array_equal(kc[p], src[t, 40:296].astype(np.float16).view(np.uint16))
+            assert np.array_equal(vc[p], src[t, 400:656].astype(np.float16).view(np.uint16))
+    assert (kc[[4, 6, 9]] == 0xFFFF).all()  # rows no token maps to stay untouched
+    h = rng.integers(0, 65536, (4, 64), dtype=np.uint16)
+    kh, vh = O.store_kv(h, 0, 32, 32, 6, pos0=2)
+    assert np.array_equal(kh[2:6], h[:, :32]) and np.array_equal(vh[2:6], h[:, 32:])
+
+
+def test_add_rmsnorm_closed_form():
+    """The residual sum is numpy's f32 add of the widened halves rounded to f16; the norm is the
+    oracle's (pinned) rmsnorm of that stored sum, and a cancelling row gives the eps-only scale."""
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal((5, 300)) * 8).astype(np.float16)
+    d = (rng.standard_normal((5, 300)) * 0.01).astype(np.float16)
+    d[3] = -x[3]
+    w = rng.standard_normal(300).astype(np.float16).astype(np.float32)
+    xo, xn = O.add_rmsnorm_f16(x.view(np.uint16), d.view(np.uint16), w, 1e-6)
+    want = (x.astype(np.float32) + d.astype(np.float32)).astype(np.float16).view(np.uint16)
+    assert np.array_equal(xo, want)
+    assert np.array_equal(xn, O.rmsnorm_f16(want, w, 1e-6))
+    assert (xo[3] == 0).all() and (xn[3].view(np.float16) == 0).all()  # +0 sums; -0 where w < 0
+
+
+def test_qk_norm_rope_kv_is_rope_then_store():
+    """The fused form equals q/k norm + RoPE followed by the KV store of the rotated rows."""
+    rng = np.random.default_rng(23)
+    H, KV, hd, n_pos = 4, 2, 64, 40
+    qkv = rng.standard_normal((11, (H + 2 * KV) * hd)).astype(np.float16).view(np.uint16)
+    cs = O.rope_table(1e6, hd, n_pos)
+    wq = rng.standard_normal(2 * hd).astype(np.float32)
+    pos = rng.permutation(n_pos)[:11].astype(np.int32)
+    pos[4] = n_pos  # out of range: untouched, stores nothing
+    out, kc, vc = O.qk_norm_rope_kv(qkv, H, KV, hd, cs, n_pos, 1e-6, wqk=wq, positions=pos)
+    rot = O.qk_norm_rope_f16(qkv, H, KV, hd, cs, n_pos, 1e-6, wqk=wq, positions=pos)
+    assert np.array_equal(out, rot)
+    kw = KV * hd
+    for t, p in enumerate(pos):
+        if p < n_pos:
+            assert np.array_equal(kc[p], rot[t, H * hd:H * hd + kw])
+            assert np.array_equal(vc[p], qkv[t, H * hd + kw:H * hd + 2 * kw])
+    assert np.count_nonzero((kc != 0xFFFF).any(axis=1)) == 10
+    f32 = rng.standard_normal((3, (H + 2 * KV) * hd)).astype(np.float32)
+    o32, k32, v32 = O.qk_norm_rope_kv(f32, H, KV, hd, cs, n_pos, 1e-6, wqk=wq, pos0=5)
+    r32 = O.qk_norm_rope_f32(f32, H, KV, hd, cs, n_pos, 1e-6, wqk=wq, pos0=5)
+    assert np.array_equal(o32, r32)
+    assert np.array_equal(k32[5:8], r32[:, H * hd:H * hd + kw].astype(np.float16).view(np.uint16))
+    assert np.array_equal(v32[5:8], f32[:, H * hd + kw:].astype(np.float16).view(np.uint16))
