@@ -34,7 +34,6 @@ METRIC = ("achieved HBM GB/s (% of 8 TB/s) per fused op; µs/layer non-GEMM ops,
 HBM_PEAK_GBS = 8000.0
 OPS = ("rmsnorm_in", "qk_norm_rope", "rmsnorm_post", "swiglu")
 DOMINANT = "swiglu"
-KERNEL_NAMES = {"swiglu": "swiglu_kernel", "rmsnorm_in": "norm_rows_kernel", "qk_norm_rope": "qk_rope_kernel"}
 
 
 def parse():
@@ -49,7 +48,7 @@ def parse():
                    help="time every configured workload's ops (one JSON line with all of them) instead")
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
-                        "quant_gather_qwen3_1.7b, granite_4.0h_norms)")
+                        "quant_gather_qwen3_1.7b, qwen3_4b_fused, granite_4.0h_norms)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -184,7 +183,8 @@ def all_configs(args):
     flush = torch.ones(256 << 20, dtype=torch.float32, device=dev)
     out = {}
 
-    labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "granite_4.0h_norms")
+    labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
+              "granite_4.0h_norms")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -263,6 +263,37 @@ def all_configs(args):
         del src
         run("quant_gather_qwen3_1.7b", calls4, bytes4,
             f"Qwen3-1.7B tied table 151936x2048, 16384 Zipf(1.1) ids ({unique} unique rows): mostly cache-served")
+
+    # The Qwen3-4B layer's fused neighbours: residual add + RMSNorm [8192, 2560], and q/k RoPE fused
+    # with the KV-cache store for one 8192-token sequence (positions 0..8191), beside the unfused
+    # q/k RoPE and KV store they replace.
+    if want("qwen3_4b_fused"):
+        c6 = wl.QWEN3_PREFILL
+        x6 = wl.normal_f16((c6.T, c6.C), 0.0, 1.0, 71, dev)
+        d6 = wl.normal_f16((c6.T, c6.C), 0.0, 0.5, 72, dev)
+        w6 = wl.weight_f32(c6.C, 1.0, 0.05, 73, dev)
+        xn6 = torch.empty_like(x6)
+        qkv6 = wl.normal_f16((c6.T, c6.qkv_stride), 0.0, 1.0, 74, dev)
+        wqk6 = wl.weight_f32(2 * c6.hd, 1.0, 0.05, 75, dev)
+        cs6 = torch.from_numpy(ops.rope_table(1e6, c6.hd, c6.T)).to(dev)
+        pos6 = torch.arange(c6.T, dtype=torch.int32, device=dev)
+        kw6 = c6.n_kv * c6.hd
+        kc6 = torch.empty((c6.T, kw6), dtype=torch.float16, device=dev)
+        vc6 = torch.empty_like(kc6)
+        qoff = c6.n_q * c6.hd
+        run("qwen3_4b_fused", {
+            "add_rmsnorm": ops.prepare(ops.add_rms_norm, x6, d6, w6, c6.eps, out=xn6)[0],
+            "qk_norm_rope_kv": ops.prepare(ops.qk_norm_rope_kv, qkv6, c6.n_q, c6.n_kv, c6.hd, cs6, c6.eps, kc6, vc6,
+                                           wqk=wqk6, positions=pos6)[0],
+            "qk_norm_rope": ops.prepare(ops.qk_norm_rope, qkv6, c6.n_q, c6.n_kv, c6.hd, cs6, c6.eps, wqk=wqk6,
+                                        positions=pos6)[0],
+            "store_kv": ops.prepare(ops.store_kv, qkv6, qoff, qoff + kw6, kw6, kc6, vc6, positions=pos6)[0],
+        }, {"add_rmsnorm": wl.bytes_add_rmsnorm(c6.T, c6.C),
+            "qk_norm_rope_kv": wl.bytes_qk_rope_kv(c6.T, c6.n_q, c6.n_kv, c6.hd),
+            "qk_norm_rope": wl.bytes_qk_rope(c6.T, c6.n_q, c6.n_kv, c6.hd),
+            "store_kv": wl.bytes_store_kv(c6.T, kw6)},
+            "Qwen3-4B fused neighbours: residual add + RMSNorm [8192,2560]; q/k RoPE + KV store of an 8192-token "
+            "sequence, beside the unfused q/k RoPE and KV store")
 
     # Granite-4.0-H-style norms and SwiGLU
     if want("granite_4.0h_norms"):

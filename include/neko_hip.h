@@ -112,6 +112,35 @@ int neko_hip_qk_norm_rope(neko_hip_ctx* ctx, void* qkv, int64_t row_stride, int6
                           int64_t pos0, const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos,
                           float eps, int dtype);
 
+/* The same, fused with the KV-cache store that follows it (qwen3_model.cpp:249-256: rope, then
+ * cpu::storeKv, cpu_ops.cpp:535-542; GPU kv_store.comp): after the q/k heads of a row are normed and
+ * rotated, its rotated k heads and its v heads are also written as f16 to cache row = the row's
+ * position, k_cache / v_cache being [cache_rows][n_kv*hd] halves. f16 activations are stored bit for
+ * bit; f32 activations are rounded to f16 (RNE). Rows outside [0, n_pos) are untouched and store
+ * nothing; cache_rows >= n_pos. Rows that share a position write the same cache row (which one lands
+ * last is unspecified). */
+int neko_hip_qk_norm_rope_kv(neko_hip_ctx* ctx, void* qkv, int64_t row_stride, int64_t rows, int n_q, int n_kv, int hd,
+                             int64_t pos0, const int32_t* positions, const float* wqk, const float* cs, int64_t n_pos,
+                             float eps, uint16_t* k_cache, uint16_t* v_cache, int64_t cache_rows, int dtype);
+
+/* KV-cache store alone (cpu_ops.cpp:535-542; the GPU kernel KvStore, kv_store.comp:1-21): for each
+ * row t, the width k values at qkv[t*row_stride + k_off] and v values at [... + v_off] are written as
+ * f16 (RNE from f32; bit copies from f16) to k_cache / v_cache row positions[t] (or pos0 + t), rows of
+ * width halves. Rows whose cache row is outside [0, cache_rows) are skipped. */
+int neko_hip_store_kv(neko_hip_ctx* ctx, const void* qkv, int64_t row_stride, int64_t k_off, int64_t v_off, int64_t rows,
+                      int64_t width, int64_t pos0, const int32_t* positions, uint16_t* k_cache, uint16_t* v_cache,
+                      int64_t cache_rows, int dtype);
+
+/* ---------------------------------------------------------------- residual */
+
+/* Residual add + RMSNorm: x[t] = x[t] + delta[t] (float add, rounded once to the activation type,
+ * written back to x), then xn[t] = RMSNorm(x[t]) with weights w -- the reference's matmul epilogue
+ * with kAccumulate (cpu_ops.cpp:123, dst = dst + v) followed by the next op's cpu::rmsNorm
+ * (qwen3_model.cpp:264, cpu_ops.cpp:502-511), with the add moved out of the GEMM so the residual row
+ * is read once for both. xn may not alias x or delta. */
+int neko_hip_add_rmsnorm(neko_hip_ctx* ctx, void* x, int64_t x_stride, const void* delta, int64_t delta_stride, void* xn,
+                         int64_t xn_stride, const float* w, int64_t rows, int64_t C, float eps, int dtype);
+
 /* ---------------------------------------------------------------- activations */
 
 /* SwiGLU: out[t][i] = gate / (1 + exp(-gate)) * up with gate = h[t][i], up = h[t][I + i]

@@ -46,6 +46,10 @@ SIGNATURES = {
     "neko_hip_rmsnorm": (_i32, [_p, _p, _i64, _p, _i64, _p, _i64, _i64, _f32, _i32]),
     "neko_hip_gated_rmsnorm": (_i32, [_p, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _i32, _f32, _i32]),
     "neko_hip_qk_norm_rope": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _i32]),
+    "neko_hip_qk_norm_rope_kv": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p, _i64,
+                                        _i32]),
+    "neko_hip_store_kv": (_i32, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i32]),
+    "neko_hip_add_rmsnorm": (_i32, [_p, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _f32, _i32]),
     "neko_hip_swiglu": (_i32, [_p, _p, _i64, _p, _i64, _i64, _i64, _i32]),
     "neko_hip_gelu_tanh": (_i32, [_p, _p, _p, _i64, _i32]),
     "neko_hip_embed": (_i32, [_p, _p, _i64, _p, _i64, _i32, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32]),

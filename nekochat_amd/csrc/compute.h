@@ -1,7 +1,8 @@
 // The engine's per-op GPU backend contract, kept as the reference declares it so a HIP backend drops
 // in beside its Vulkan and GLES backends (reference: shared/cpp/gpu/compute.h:14-58, common.h:26-31).
 // Names, argument meaning, the Kernel numbering and the throw-on-failure convention are unchanged;
-// GatedRmsNorm and Gelu extend the enum after MatmulQ4, so existing values keep their numbers.
+// GatedRmsNorm, Gelu and AddRmsNorm extend the enum after MatmulQ4, so existing values keep their
+// numbers.
 //
 // Per-kernel parameter blocks (PA = params[0..3], PB = params[4..7]; floats travel as raw bits, see
 // floatBits), activations f32, exactly as the reference's shaders take them:
@@ -13,7 +14,10 @@
 //   SiluMul    PA (T, I)                                     bindings h [T][2I], g [T][I]
 //   GatedRmsNorm PA (D, eps, groups, zStride)                bindings y (in/out), z, w; dispatch (rows, 1)
 //   Gelu       PA (n)                                        bindings x, y
-// Matmul, KvStore, Attention, MatmulQ8 and MatmulQ4 are dense contractions or attention and are not
+//   KvStore    PA (T, width, pos0), PB (rowStride, kOffset, vOffset)   bindings qkv, kCache, vCache
+//              (caches [ctx][width] f16)
+//   AddRmsNorm PA (C, eps)                                   bindings x (in/out), delta, xn, w; dispatch (rows, 1)
+// Matmul, Attention, MatmulQ8 and MatmulQ4 are dense contractions or attention and are not
 // implemented by the HIP backend: dispatching them throws NekoError.
 #pragma once
 
@@ -47,6 +51,7 @@ enum class Kernel : int {
     MatmulQ4,
     GatedRmsNorm,
     Gelu,
+    AddRmsNorm,
     Count
 };
 

@@ -6,6 +6,7 @@
 // nothing to do: work is submitted as it is dispatched. The reference's shaders rely on robust
 // buffer access for out-of-range indices; here every dispatch is checked against the bound buffer
 // sizes before launch and an out-of-range request throws instead.
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -20,8 +21,8 @@ struct HipBuffer : Buffer {
 };
 
 const char* kernelName(Kernel k) {
-    static const char* const names[] = {"Embed",   "LayerNorm", "Matmul",       "KvStore", "Attention", "Rope",
-                                        "SiluMul", "MatmulQ8",  "MatmulQ4",     "GatedRmsNorm", "Gelu"};
+    static const char* const names[] = {"Embed",    "LayerNorm", "Matmul",   "KvStore",      "Attention", "Rope",
+                                        "SiluMul",  "MatmulQ8",  "MatmulQ4", "GatedRmsNorm", "Gelu",      "AddRmsNorm"};
     const int i = static_cast<int>(k);
     return i >= 0 && i < static_cast<int>(Kernel::Count) ? names[i] : "?";
 }
@@ -84,6 +85,8 @@ public:
             case Kernel::SiluMul: siluMul(bindings, pa); return;
             case Kernel::GatedRmsNorm: gatedRmsNorm(bindings, pa, gx); return;
             case Kernel::Gelu: gelu(bindings, pa); return;
+            case Kernel::KvStore: kvStore(bindings, pa, pb); return;
+            case Kernel::AddRmsNorm: addRmsNorm(bindings, pa, gx); return;
             default: break;
         }
         fail(std::string("HIP backend: kernel ") + kernelName(k) + " is not implemented (dense contractions and attention)");
@@ -206,6 +209,35 @@ private:
         void* x = need(b, 0, uint64_t(n) * 4, "Gelu");
         void* y = need(b, 1, uint64_t(n) * 4, "Gelu");
         check(neko_hip_gelu_tanh(ctx_, x, y, n, NEKO_DT_F32));
+    }
+
+    // kv_store.comp: PA (T, width, pos0), PB (rowStride, kOffset, vOffset); caches [ctx][width] f16.
+    void kvStore(Buffer* const b[4], const int32_t* pa, const int32_t* pb) {
+        const int64_t T = pa[0], W = pa[1], pos0 = pa[2], stride = pb[0], kOff = pb[1], vOff = pb[2];
+        positive(T, "KvStore");
+        positive(W, "KvStore");
+        positive(pos0, "KvStore");
+        positive(kOff, "KvStore");
+        positive(vOff, "KvStore");
+        if (T == 0 || W == 0) return;
+        if (stride < kOff + W || stride < vOff + W) fail("HIP KvStore: k/v columns exceed the qkv row stride");
+        void* qkv = need(b, 0, (uint64_t(T - 1) * uint64_t(stride) + uint64_t(std::max(kOff, vOff) + W)) * 4, "KvStore");
+        auto* kc = static_cast<uint16_t*>(need(b, 1, uint64_t(pos0 + T) * uint64_t(W) * 2, "KvStore"));
+        auto* vc = static_cast<uint16_t*>(need(b, 2, uint64_t(pos0 + T) * uint64_t(W) * 2, "KvStore"));
+        check(neko_hip_store_kv(ctx_, qkv, stride, kOff, vOff, T, W, pos0, nullptr, kc, vc, pos0 + T, NEKO_DT_F32));
+    }
+
+    // Residual add + RMSNorm: PA (C, eps); bindings x (in/out), delta, xn, w; dispatch (rows, 1).
+    void addRmsNorm(Buffer* const b[4], const int32_t* pa, uint32_t gx) {
+        const int64_t C = pa[0], rows = gx;
+        const float eps = bitsFloat(pa[1]);
+        positive(C, "AddRmsNorm");
+        if (rows == 0 || C == 0) return;
+        void* x = need(b, 0, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
+        void* d = need(b, 1, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
+        void* xn = need(b, 2, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
+        auto* w = static_cast<const float*>(need(b, 3, uint64_t(C) * 4, "AddRmsNorm"));
+        check(neko_hip_add_rmsnorm(ctx_, x, C, d, C, xn, C, w, rows, C, eps, NEKO_DT_F32));
     }
 
     neko_hip_ctx* ctx_ = nullptr;

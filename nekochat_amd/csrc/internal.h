@@ -41,6 +41,12 @@ FastDiv make_fast_div(uint32_t d);
 int resident_blocks_per_cu(const void* kernel, int block, size_t lds_bytes = 0);
 int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_t work_blocks, size_t lds_bytes = 0);
 
+// The KV-cache store's launch (kv_store.hip), after argument checks; also the second half of the
+// unfused q/k RoPE + KV store path.
+int launch_store_kv(neko_hip_ctx* ctx, const char* what, const void* qkv, int64_t row_stride, int64_t k_off, int64_t v_off,
+                    int64_t rows, int64_t width, int64_t pos0, const int32_t* positions, uint16_t* k_cache,
+                    uint16_t* v_cache, int64_t cache_rows, int dtype);
+
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline size_t dtype_size(int dtype) { return dtype == NEKO_DT_F16 ? 2 : 4; }
 inline bool valid_dtype(int dtype) { return dtype == NEKO_DT_F16 || dtype == NEKO_DT_F32; }

@@ -1,14 +1,17 @@
-// Row norms for gfx950: LayerNorm (cpu_ops.cpp:483-500), RMSNorm (cpu_ops.cpp:502-511) and the
-// Granite-4.0-H gated group RMSNorm (granite_model.cpp:278-287).
+// Row norms for gfx950: LayerNorm (cpu_ops.cpp:483-500), RMSNorm (cpu_ops.cpp:502-511), the
+// Granite-4.0-H gated group RMSNorm (granite_model.cpp:278-287), and the residual add + RMSNorm
+// (the kAccumulate epilogue, cpu_ops.cpp:123, followed by cpu::rmsNorm, qwen3_model.cpp:264).
 //
 // Fast path: one 64-wide wavefront per row, persistent. A grid of as many 256-thread workgroups as
 // stay resident walks the rows. RMSNorm / LayerNorm waves keep their norm weights in registers for
 // all of their rows and issue the 16-byte non-temporal loads of the next row before they reduce the
 // current one, so HBM is read once, written once, and always has loads in flight. The gated norm,
 // which holds two operands per row, reads its weights from one LDS copy per workgroup and runs
-// without the second row buffer, trading per-wave prefetch for three times the resident waves.
-// Rows wider than one wave's registers use four waves per row. Sums are accumulated in double, like the reference, and reduced across the wave
-// with DPP and v_readlane (LDS only joins the partial sums of multi-wave rows). The norm scale is
+// without the second row buffer, trading per-wave prefetch for three times the resident waves; the
+// residual add + RMSNorm streams x and delta, writes the sum back over x and the norm to xn.
+// Rows wider than one wave's registers use four waves per row. Sums are accumulated in double, like
+// the reference, and reduced across the wave with DPP and v_readlane (LDS only joins the partial
+// sums of multi-wave rows). The norm scale is
 // rounded to float exactly where the reference rounds it and the output is (x * s) * w unfused, so
 // results match the reference's CPU op bit for bit unless a double sum lands within an ulp of a
 // float rounding boundary.
@@ -49,16 +52,26 @@
 #ifndef NEKO_TUNE_GATED_PF
 #define NEKO_TUNE_GATED_PF 0
 #endif
+// Residual add + RMSNorm: weights in LDS (1) or registers (0), and its prefetch mode.
+#ifndef NEKO_TUNE_NORM_WLDS_ADD
+#define NEKO_TUNE_NORM_WLDS_ADD 1
+#endif
+#ifndef NEKO_TUNE_ADD_PF
+#define NEKO_TUNE_ADD_PF 1
+#endif
 
 namespace neko_hip {
 namespace {
 
-enum class Norm : int { Rms = 0, Layer = 1, Gated = 2 };
+enum class Norm : int { Rms = 0, Layer = 1, Gated = 2, AddRms = 3 };
+
+// Kinds that stream a second operand row: the gate z (Gated) or the residual delta (AddRms).
+constexpr bool has_z(Norm k) { return k == Norm::Gated || k == Norm::AddRms; }
 
 struct NormArgs {
-    const void* x;  // input rows (the y operand of the gated norm)
+    const void* x;  // input rows (the y operand of the gated norm; in/out residual rows of AddRms)
     int64_t xs;
-    const void* z;  // gate rows (gated norm only)
+    const void* z;  // gate rows (gated norm) or delta rows (AddRms)
     int64_t zs;
     void* y;  // output rows
     int64_t ys;
@@ -84,9 +97,14 @@ __device__ __forceinline__ float silu_ref(float v) {
 }
 
 constexpr bool weights_in_lds(Norm k) {
-    return k == Norm::Rms ? NEKO_TUNE_NORM_WLDS_RMS : k == Norm::Layer ? NEKO_TUNE_NORM_WLDS_LAYER : NEKO_TUNE_NORM_WLDS_GATED;
+    return k == Norm::Rms     ? NEKO_TUNE_NORM_WLDS_RMS
+           : k == Norm::Layer ? NEKO_TUNE_NORM_WLDS_LAYER
+           : k == Norm::Gated ? NEKO_TUNE_NORM_WLDS_GATED
+                              : NEKO_TUNE_NORM_WLDS_ADD;
 }
-constexpr int prefetch_mode(Norm k) { return k == Norm::Gated ? NEKO_TUNE_GATED_PF : NEKO_TUNE_NORM_PF; }
+constexpr int prefetch_mode(Norm k) {
+    return k == Norm::Gated ? NEKO_TUNE_GATED_PF : k == Norm::AddRms ? NEKO_TUNE_ADD_PF : NEKO_TUNE_NORM_PF;
+}
 
 // Output stores: non-temporal (1) or plain (0), for the plain norms and for the gated norm.
 #ifndef NEKO_TUNE_NORM_NT_STORE
@@ -117,7 +135,7 @@ __device__ __forceinline__ RowPtrs<K, T> row_ptrs(const NormArgs& a, int64_t r) 
     const int64_t off = g * a.C;
     RowPtrs<K, T> p;
     p.x = static_cast<const T*>(a.x) + t * a.xs + off;
-    p.z = K == Norm::Gated ? static_cast<const T*>(a.z) + t * a.zs + off : nullptr;
+    p.z = has_z(K) ? static_cast<const T*>(a.z) + t * a.zs + off : nullptr;
     p.y = static_cast<T*>(a.y) + t * a.ys + off;
     p.w = a.w + off;
     p.b = a.b;
@@ -144,7 +162,33 @@ __device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K,
         rr.z[k] = V{};
         if (j < nch) {
             rr.x[k] = load_nt(reinterpret_cast<const V*>(p.x + j * N));
-            if constexpr (K == Norm::Gated) rr.z[k] = load_nt(reinterpret_cast<const V*>(p.z + j * N));
+            if constexpr (has_z(K)) rr.z[k] = load_nt(reinterpret_cast<const V*>(p.z + j * N));
+        }
+    }
+}
+
+// AddRms: the row becomes x + delta, added in float and rounded once to T (the residual the
+// reference's kAccumulate epilogue leaves, cpu_ops.cpp:123); the norm then reads that rounded row.
+template <Norm K, typename T, int CH>
+__device__ __forceinline__ void add_residual(RowRegs<K, T, CH>& rr) {
+    if constexpr (K == Norm::AddRms) {
+#pragma unroll
+        for (int k = 0; k < CH; k++)
+#pragma unroll
+            for (int e = 0; e < Chunk16<T>::N; e++) rr.x[k][e] = from_f32<T>(to_f32(rr.x[k][e]) + to_f32(rr.z[k][e]));
+    }
+}
+
+// AddRms: writes the updated residual chunks back over x.
+template <Norm K, typename T, int CH, int NT>
+__device__ __forceinline__ void store_residual(const RowRegs<K, T, CH>& rr, const RowPtrs<K, T>& p, int tid, int nch) {
+    if constexpr (K == Norm::AddRms) {
+        typedef typename Chunk16<T>::V V;
+        constexpr int N = Chunk16<T>::N;
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+            const int j = k * NT + tid;
+            if (j < nch) store_out<K>(reinterpret_cast<V*>(const_cast<T*>(p.x) + j * N), rr.x[k]);
         }
     }
 }
@@ -332,6 +376,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     for (; r < a.rows; r += nw) {
         const bool more = r + nw < a.rows;
         if (PF == 1 && more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
+        add_residual(cur);
         RowVals<K, T, CH> f;
         f.init(cur);
         float scale, mean_f = 0.0f;
@@ -347,20 +392,23 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
         if constexpr (PF == 2) {
             // Rolling: store chunk k, then load chunk k of the next row into the registers it used.
             typedef typename Chunk16<T>::V V;
-            T* y = row_ptrs<K, T>(a, r).y;
+            const RowPtrs<K, T> pc = row_ptrs<K, T>(a, r);
             const RowPtrs<K, T> pn = row_ptrs<K, T>(a, more ? r + nw : r);
 #pragma unroll
             for (int k = 0; k < CH; k++) {
                 const int j = k * kWave + lane;
                 if (j >= nch) continue;
-                store_out<K>(reinterpret_cast<V*>(y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
+                store_out<K>(reinterpret_cast<V*>(pc.y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
+                if constexpr (K == Norm::AddRms) store_out<K>(reinterpret_cast<V*>(const_cast<T*>(pc.x) + j * N), cur.x[k]);
                 if (more) {
                     cur.x[k] = load_nt(reinterpret_cast<const V*>(pn.x + j * N));
-                    if constexpr (K == Norm::Gated) cur.z[k] = load_nt(reinterpret_cast<const V*>(pn.z + j * N));
+                    if constexpr (has_z(K)) cur.z[k] = load_nt(reinterpret_cast<const V*>(pn.z + j * N));
                 }
             }
         } else {
-            store_row<K, T, CH, kWave>(row_ptrs<K, T>(a, r).y, f, scale, mean_f, wt, lane, nch);
+            const RowPtrs<K, T> pc = row_ptrs<K, T>(a, r);
+            store_row<K, T, CH, kWave>(pc.y, f, scale, mean_f, wt, lane, nch);
+            store_residual<K, T, CH, kWave>(cur, pc, lane, nch);
             if (PF == 1 && more) cur = nxt;
             else if (more) load_row<K, T, CH, kWave>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
         }
@@ -379,6 +427,7 @@ __global__ __launch_bounds__(256) void norm_wide_kernel(NormArgs a) {
     const RowPtrs<K, T> p = row_ptrs<K, T>(a, r);
     RowRegs<K, T, CH> rr;
     load_row<K, T, CH, NT>(rr, p, tid, nch);
+    add_residual(rr);
     Weights<K, T, CH, NT, false> wt;
     wt.init(p.w, p.b, tid, nch);
     RowVals<K, T, CH> f;
@@ -402,6 +451,7 @@ __global__ __launch_bounds__(256) void norm_wide_kernel(NormArgs a) {
         scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
     }
     store_row<K, T, CH, NT>(p.y, f, scale, mean_f, wt, tid, nch);
+    store_residual<K, T, CH, NT>(rr, p, tid, nch);
 }
 
 // ------------------------------------------------------------------ generic rows
@@ -442,6 +492,12 @@ __global__ __launch_bounds__(256) void norm_rows_generic(NormArgs a) {
         } else {
             double ss = 0.0;
             for (int c = threadIdx.x; c < a.C; c += 256) {
+                if constexpr (K == Norm::AddRms) {
+                    // The residual sum is written back at once; the store pass below reads the value
+                    // this same thread wrote.
+                    const T s = from_f32<T>(to_f32(p.x[c]) + to_f32(p.z[c]));
+                    const_cast<T*>(p.x)[c] = s;
+                }
                 const double d = static_cast<double>(gen_value<K, T>(p, c));
                 ss += d * d;
             }
@@ -514,7 +570,7 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
     // The register paths load 16-byte chunks of every operand row and 16-byte weight vectors.
     bool vec = a.C % N == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.w, 16) && (a.xs * esz) % 16 == 0 &&
                (a.ys * esz) % 16 == 0;
-    if (kind == Norm::Gated) vec = vec && aligned(a.z, 16) && (a.zs * esz) % 16 == 0;
+    if (kind == Norm::Gated || kind == Norm::AddRms) vec = vec && aligned(a.z, 16) && (a.zs * esz) % 16 == 0;
     if (kind == Norm::Layer) vec = vec && aligned(a.b, 16);
     int W = 0, CH = 0;
     if (vec) {
@@ -536,6 +592,7 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         case Norm::Rms: k = pick<Norm::Rms>(dtype, W, CH, wl); break;
         case Norm::Layer: k = pick<Norm::Layer>(dtype, W, CH, wl); break;
         case Norm::Gated: k = pick<Norm::Gated>(dtype, W, CH, wl); break;
+        case Norm::AddRms: k = pick<Norm::AddRms>(dtype, W, CH, wl); break;
     }
     if (!k) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: no kernel for C=%d", what, a.C);
     int64_t blocks;
@@ -600,6 +657,23 @@ int neko_hip_rmsnorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y
     if (int rc = check_rows(ctx, what, rows, C, y_stride, "y")) return rc;
     NormArgs a{x, x_stride, nullptr, 0, y, y_stride, w, nullptr, rows, static_cast<int>(C), 1, eps};
     return launch_norm(ctx, Norm::Rms, a, dtype, what);
+}
+
+int neko_hip_add_rmsnorm(neko_hip_ctx* ctx, void* x, int64_t x_stride, const void* delta, int64_t delta_stride, void* xn,
+                         int64_t xn_stride, const float* w, int64_t rows, int64_t C, float eps, int dtype) {
+    const char* what = "neko_hip_add_rmsnorm";
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, valid_dtype(dtype), "%s: bad dtype %d", what, dtype);
+    NEKO_REQUIRE(ctx, rows >= 0 && C > 0 && C <= 0x7fffffff, "%s: bad shape rows=%lld C=%lld", what, (long long)rows,
+                 (long long)C);
+    if (rows == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, x && delta && xn && w, "%s: null pointer", what);
+    NEKO_REQUIRE(ctx, xn != x && xn != delta, "%s: xn may not alias x or delta", what);
+    if (int rc = check_rows(ctx, what, rows, C, x_stride, "x")) return rc;
+    if (int rc = check_rows(ctx, what, rows, C, delta_stride, "delta")) return rc;
+    if (int rc = check_rows(ctx, what, rows, C, xn_stride, "xn")) return rc;
+    NormArgs a{x, x_stride, delta, delta_stride, xn, xn_stride, w, nullptr, rows, static_cast<int>(C), 1, eps};
+    return launch_norm(ctx, Norm::AddRms, a, dtype, what);
 }
 
 int neko_hip_gated_rmsnorm(neko_hip_ctx* ctx, const void* y, int64_t y_stride, const void* z, int64_t z_stride, void* out,

@@ -1,0 +1,490 @@
+// Qwen3 attention prologue for gfx950: per-head q/k RMSNorm fused with NeoX half-split RoPE, in
+// place on the q and k heads of each qkv row (rope.comp:1-55; CPU qwen3_model.cpp:249-253 =
+// cpu::rmsNorm per head, cpu_ops.cpp:502-511, then cpu::rope, cpu_ops.cpp:513-524).
+//
+// Fast path: one wavefront per token row, persistent over tokens. A head of hd elements is spread
+// over L lanes; lane l holds the V elements [lV, lV+V) of the first half AND their NeoX partners
+// [hd/2 + lV, ...), so the rotation needs no cross-lane exchange. 64/L heads are processed per wave
+// pass; all passes of a token are loaded at once, and the next token's heads and cos/sin row are in
+// flight while the current token is normalised and rotated. The head's sum of squares (double, like
+// the reference) is reduced over its L lanes with DPP only. The norm weights stay in registers for
+// all tokens of a wave. V heads are never touched.
+//
+// Fallback: one 64-thread workgroup per (head, row) staging the head in LDS (any even hd <= 512).
+#pragma once
+
+#include <cmath>
+
+#include "internal.h"
+
+// Build-time tuning knobs (measured defaults): persistent grid vs one token per wave, and the widest
+// per-lane vector (elements) a head half is split into.
+#ifndef NEKO_TUNE_QK_FULLGRID
+#define NEKO_TUNE_QK_FULLGRID 0
+#endif
+#ifndef NEKO_TUNE_QK_RSQ
+#define NEKO_TUNE_QK_RSQ 1
+#endif
+#ifndef NEKO_TUNE_QK_MAXV
+#define NEKO_TUNE_QK_MAXV 8
+#endif
+// Minimum waves per SIMD the rolling kernel is compiled for (caps its VGPRs at 512 / waves).
+#ifndef NEKO_TUNE_QK_WAVES
+#define NEKO_TUNE_QK_WAVES 3
+#endif
+
+namespace neko_hip {
+
+struct QkArgs {
+    void* qkv;
+    int64_t stride;
+    int64_t rows;
+    int n_q;
+    int n_kv;
+    int hd;
+    int64_t pos0;
+    const int32_t* positions;
+    const float* wqk;  // q_norm[hd] | k_norm[hd], or null
+    const float* cs;   // [n_pos][hd/2] (cos, sin)
+    int64_t n_pos;
+    float eps;
+    uint16_t* k_cache;  // [>= n_pos][n_kv * hd] f16, or null (no KV store)
+    uint16_t* v_cache;
+};
+
+// V values of type T as f16 at p: bit copies for f16, one RNE rounding each for f32.
+template <typename T, int V>
+__device__ __forceinline__ void store_f16(uint16_t* p, const typename VecOf<T, V>::V& v) {
+    typedef typename VecOf<half_t, V>::V VH;
+    if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<VH*>(p) = __builtin_bit_cast(VH, v);
+    } else {
+        VH h;
+        if constexpr (V == 1) h = static_cast<half_t>(v);
+        else
+#pragma unroll
+            for (int e = 0; e < V; e++) h[e] = static_cast<half_t>(v[e]);
+        *reinterpret_cast<VH*>(p) = h;
+    }
+}
+
+// The head's norm scale float(1 / sqrt(ss / hd + eps)) (cpu_ops.cpp:508 with C = hd). ss / hd is
+// the exact product with 1/hd when hd is a power of two (every Qwen3 head size); the reciprocal
+// square root comes from rsqrt_to_float (device.h) or, with the knob off, the libm-style expression.
+__device__ __forceinline__ float head_scale(const QkArgs& a, double ss) {
+    const double m = (a.hd & (a.hd - 1)) == 0 ? ss * (1.0 / a.hd) : ss / a.hd;
+    if constexpr (NEKO_TUNE_QK_RSQ) return rsqrt_to_float(m + static_cast<double>(a.eps));
+    else return static_cast<float>(1.0 / sqrt(m + static_cast<double>(a.eps)));
+}
+
+// Head stores: non-temporal (knob 1) or plain (0).
+#ifndef NEKO_TUNE_QK_NT_STORE
+#define NEKO_TUNE_QK_NT_STORE 0
+#endif
+template <typename VT>
+__device__ __forceinline__ void qk_store(VT* p, VT v) {
+    if constexpr (NEKO_TUNE_QK_NT_STORE) store_nt(p, v);
+    else *p = v;
+}
+// Head loads: non-temporal (knob 1) or plain (0).
+#ifndef NEKO_TUNE_QK_NT_LOAD
+#define NEKO_TUNE_QK_NT_LOAD 1
+#endif
+template <typename VT>
+__device__ __forceinline__ VT qk_load(const VT* p) {
+    if constexpr (NEKO_TUNE_QK_NT_LOAD) return load_nt(p);
+    else return *p;
+}
+
+__device__ __forceinline__ bool row_position(const QkArgs& a, int64_t t, int64_t& pos) {
+    pos = a.positions ? static_cast<int64_t>(a.positions[t]) : a.pos0 + t;
+    return pos >= 0 && pos < a.n_pos;
+}
+
+// One token's q/k heads held by one wave: U passes of 64/L heads, each lane V elements of the first
+// half of its head and their V partners in the second half.
+template <typename T, int V, int U>
+struct TokenRegs {
+    typedef typename VecOf<T, V>::V VT;
+    VT a[U];
+    VT b[U];
+    float c[V];
+    float s[V];
+};
+
+template <typename T, int L, int V, int U>
+__device__ __forceinline__ void load_token(TokenRegs<T, V, U>& tr, const QkArgs& a, int64_t t, int64_t pos, int p0, int hl,
+                                           int hs) {
+    typedef typename VecOf<T, V>::V VT;
+    constexpr int HPW = kWave / L;
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
+    const float* csr = a.cs + pos * a.hd + 2 * i0;
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+        const float2v c = *reinterpret_cast<const float2v*>(csr + 2 * e);
+        tr.c[e] = c[0];
+        tr.s[e] = c[1];
+    }
+    const T* row = static_cast<const T*>(a.qkv) + t * a.stride;
+    const int nh = a.n_q + a.n_kv;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int head = p0 + u * HPW + hs;
+        tr.a[u] = VT{};
+        tr.b[u] = VT{};
+        if (head < nh) {
+            const T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
+            tr.a[u] = qk_load(reinterpret_cast<const VT*>(hp));
+            tr.b[u] = qk_load(reinterpret_cast<const VT*>(hp + half));
+        }
+    }
+}
+
+template <typename T, int L, int V, int U>
+__device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const QkArgs& a, int64_t t, int p0, int hl,
+                                             int hs, bool norm, const float (&wqa)[V], const float (&wqb)[V],
+                                             const float (&wka)[V], const float (&wkb)[V]) {
+    typedef typename VecOf<T, V>::V VT;
+    constexpr int HPW = kWave / L;
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
+    const int nh = a.n_q + a.n_kv;
+    T* row = static_cast<T*>(a.qkv) + t * a.stride;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int head = p0 + u * HPW + hs;
+        float fa[V], fb[V];
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            if constexpr (V == 1) {
+                fa[e] = to_f32(tr.a[u]);
+                fb[e] = to_f32(tr.b[u]);
+            } else {
+                fa[e] = to_f32(tr.a[u][e]);
+                fb[e] = to_f32(tr.b[u][e]);
+            }
+        }
+        if (norm) {
+            // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
+            double ss = 0.0;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
+                ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
+            }
+            ss = group_sum_f64<L>(ss);
+            const float r = head_scale(a, ss);
+            const bool is_q = head < a.n_q;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                fa[e] = fa[e] * r * (is_q ? wqa[e] : wka[e]);
+                fb[e] = fb[e] * r * (is_q ? wqb[e] : wkb[e]);
+            }
+        }
+        VT oa, ob;
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            const float x0 = fa[e] * tr.c[e] - fb[e] * tr.s[e];
+            const float x1 = fa[e] * tr.s[e] + fb[e] * tr.c[e];
+            if constexpr (V == 1) {
+                oa = from_f32<T>(x0);
+                ob = from_f32<T>(x1);
+            } else {
+                oa[e] = from_f32<T>(x0);
+                ob[e] = from_f32<T>(x1);
+            }
+        }
+        if (head < nh) {
+            T* hp = row + static_cast<int64_t>(head) * a.hd + i0;
+            qk_store(reinterpret_cast<VT*>(hp), oa);
+            qk_store(reinterpret_cast<VT*>(hp + half), ob);
+        }
+    }
+}
+
+// Rolling pipeline for tokens whose heads fit in U passes: a wave holds one token's q/k heads in
+// registers; as each pass of token t is normalised, rotated and stored, the same registers receive
+// that pass of the wave's next token. A whole token of loads is therefore always in flight behind
+// the token being computed, with one token's worth of data registers, and because every load is
+// issued after the stores it follows, waiting for it never waits on later stores. The norm weights
+// are staged in LDS once per workgroup and read per pass; the cos/sin row of the next token is
+// loaded one token ahead.
+template <typename T, int L, int V, int U, bool KV>
+__global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(QkArgs a) {
+    constexpr int HPW = kWave / L;  // heads per wave pass
+    typedef typename VecOf<T, V>::V VT;
+    __shared__ float wsh[2 * 512];
+    const bool norm = a.wqk != nullptr;
+    if (norm)
+        for (int i = threadIdx.x; i < 2 * a.hd; i += 256) wsh[i] = a.wqk[i];
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, kept in SGPRs
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int hl = lane % L;
+    const int hs = lane / L;
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
+    const int nqk = a.n_q + a.n_kv;
+    const int nh = KV ? nqk + a.n_kv : nqk;  // with the KV store, the v heads ride along as extra passes
+    const int64_t kvw = static_cast<int64_t>(a.n_kv) * a.hd;
+    auto next_valid = [&](int64_t t, int64_t& pos) -> int64_t {
+        for (; t < a.rows; t += nw)
+            if (row_position(a, t, pos)) return t;
+        return a.rows;
+    };
+    auto load_cs = [&](int64_t pos, float (&c)[V], float (&s)[V]) {
+        const float* csr = a.cs + pos * a.hd + 2 * i0;
+#pragma unroll
+        for (int e = 0; e < V; e += 2) {
+            if constexpr (V == 1) {
+                const float2v v = *reinterpret_cast<const float2v*>(csr);
+                c[0] = v[0];
+                s[0] = v[1];
+            } else {
+                const float4v v = *reinterpret_cast<const float4v*>(csr + 2 * e);
+                c[e] = v[0];
+                s[e] = v[1];
+                c[e + 1] = v[2];
+                s[e + 1] = v[3];
+            }
+        }
+    };
+
+    int64_t pos;
+    int64_t t = next_valid(static_cast<int64_t>(blockIdx.x) * 4 + wave, pos);
+    if (t >= a.rows) return;
+
+    VT A[U], B[U];
+    float cc[V], sn[V];
+    load_cs(pos, cc, sn);
+    {
+        const T* row = static_cast<const T*>(a.qkv) + t * a.stride;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int head = u * HPW + hs;
+            A[u] = VT{};
+            B[u] = VT{};
+            if (head < nh) {
+                A[u] = qk_load(reinterpret_cast<const VT*>(row + head * a.hd + i0));
+                B[u] = qk_load(reinterpret_cast<const VT*>(row + head * a.hd + half + i0));
+            }
+        }
+    }
+    while (t < a.rows) {
+        int64_t npos;
+        const int64_t tn = next_valid(t + nw, npos);
+        const bool more = tn < a.rows;
+        float ncc[V], nsn[V];
+        if (more) load_cs(npos, ncc, nsn);
+        T* row = static_cast<T*>(a.qkv) + t * a.stride;
+        const T* nrow = static_cast<const T*>(a.qkv) + (more ? tn : t) * a.stride;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int head = u * HPW + hs;
+            float fa[V], fb[V];
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                if constexpr (V == 1) {
+                    fa[e] = to_f32(A[u]);
+                    fb[e] = to_f32(B[u]);
+                } else {
+                    fa[e] = to_f32(A[u][e]);
+                    fb[e] = to_f32(B[u][e]);
+                }
+            }
+            if (norm) {
+                // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
+                double ss = 0.0;
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
+                    ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
+                }
+                ss = group_sum_f64<L>(ss);
+                const float r = head_scale(a, ss);
+                const float* w = wsh + (head < a.n_q ? 0 : a.hd) + i0;
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    fa[e] = fa[e] * r * w[e];
+                    fb[e] = fb[e] * r * w[half + e];
+                }
+            }
+            VT oa, ob;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                const float x0 = fa[e] * cc[e] - fb[e] * sn[e];
+                const float x1 = fa[e] * sn[e] + fb[e] * cc[e];
+                if constexpr (V == 1) {
+                    oa = from_f32<T>(x0);
+                    ob = from_f32<T>(x1);
+                } else {
+                    oa[e] = from_f32<T>(x0);
+                    ob[e] = from_f32<T>(x1);
+                }
+            }
+            if (head < nh) {
+                T* hp = row + head * a.hd + i0;
+                if (!KV || head < nqk) {
+                    qk_store(reinterpret_cast<VT*>(hp), oa);
+                    qk_store(reinterpret_cast<VT*>(hp + half), ob);
+                }
+                if constexpr (KV) {
+                    if (head >= a.n_q) {  // rotated k heads and untouched v heads go to the caches
+                        const bool is_v = head >= nqk;
+                        uint16_t* cp = (is_v ? a.v_cache : a.k_cache) + pos * kvw +
+                                       static_cast<int64_t>(head - (is_v ? nqk : a.n_q)) * a.hd + i0;
+                        store_f16<T, V>(cp, is_v ? A[u] : oa);
+                        store_f16<T, V>(cp + half, is_v ? B[u] : ob);
+                    }
+                }
+                if (more) {
+                    A[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * a.hd + i0));
+                    B[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * a.hd + half + i0));
+                }
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                cc[e] = ncc[e];
+                sn[e] = nsn[e];
+            }
+            pos = npos;
+        }
+        t = tn;
+    }
+}
+
+// Tokens with more heads than U passes: persistent waves, each token in batches of U passes, the norm
+// weights in registers.
+template <typename T, int L, int V, int U>
+__global__ __launch_bounds__(256) void qk_rope_batch_kernel(QkArgs a) {
+    constexpr int HPW = kWave / L;  // heads per wave pass
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int hl = lane % L;
+    const int hs = lane / L;
+    const int half = a.hd / 2;
+    const int i0 = hl * V;
+    const bool norm = a.wqk != nullptr;
+    float wqa[V], wqb[V], wka[V], wkb[V];
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+        wqa[e] = norm ? a.wqk[i0 + e] : 1.0f;
+        wqb[e] = norm ? a.wqk[half + i0 + e] : 1.0f;
+        wka[e] = norm ? a.wqk[a.hd + i0 + e] : 1.0f;
+        wkb[e] = norm ? a.wqk[a.hd + half + i0 + e] : 1.0f;
+    }
+    const int nh = a.n_q + a.n_kv;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + wave; t < a.rows; t += nw) {
+        int64_t pos;
+        if (!row_position(a, t, pos)) continue;  // rows outside the table stay untouched
+        for (int p0 = 0; p0 < nh; p0 += HPW * U) {
+            TokenRegs<T, V, U> cur;
+            load_token<T, L, V, U>(cur, a, t, pos, p0, hl, hs);
+            rotate_token<T, L, V, U>(cur, a, t, p0, hl, hs, norm, wqa, wqb, wka, wkb);
+        }
+    }
+}
+
+// Any even hd <= 512: one 64-thread workgroup per (head, row).
+template <typename T>
+__global__ __launch_bounds__(64) void qk_rope_generic(QkArgs a) {
+    __shared__ float v[512];
+    const int head = blockIdx.x;
+    const int64_t t = blockIdx.y;
+    int64_t pos;
+    if (!row_position(a, t, pos)) return;
+    T* hp = static_cast<T*>(a.qkv) + t * a.stride + static_cast<int64_t>(head) * a.hd;
+    const int l = threadIdx.x;
+    double ss = 0.0;
+    for (int d = l; d < a.hd; d += 64) {
+        const float x = to_f32(hp[d]);
+        v[d] = x;
+        ss += static_cast<double>(x) * static_cast<double>(x);
+    }
+    ss = wave_sum_f64(ss);
+    __syncthreads();
+    const bool norm = a.wqk != nullptr;
+    const float r = norm ? static_cast<float>(1.0 / sqrt(ss / a.hd + static_cast<double>(a.eps))) : 1.0f;
+    const float* wn = a.wqk + (head >= a.n_q ? a.hd : 0);
+    const int half = a.hd / 2;
+    const float* csr = a.cs + pos * a.hd;
+    for (int i = l; i < half; i += 64) {
+        float x0 = v[i], x1 = v[i + half];
+        if (norm) {
+            x0 = x0 * r * wn[i];
+            x1 = x1 * r * wn[i + half];
+        }
+        const float c = csr[2 * i], s = csr[2 * i + 1];
+        hp[i] = from_f32<T>(x0 * c - x1 * s);
+        hp[i + half] = from_f32<T>(x0 * s + x1 * c);
+    }
+}
+
+typedef void (*QkKernel)(QkArgs);
+
+// The rolling kernel when a token's heads fit in U <= 8 passes, else (without the KV store) the
+// batch kernel; with the KV store there is no batch form and the caller runs the unfused pair.
+template <typename T, int L, int V, int U, bool KV>
+QkKernel pick_fit(bool fit) {
+    if constexpr (KV) return fit ? qk_rope_roll_kernel<T, L, V, U, true> : nullptr;
+    else return fit ? qk_rope_roll_kernel<T, L, V, U, false> : qk_rope_batch_kernel<T, L, V, U>;
+}
+
+template <typename T, int L, int V, bool KV>
+QkKernel pick_u(int passes) {
+    switch (passes) {
+        case 1: return pick_fit<T, L, V, 1, KV>(true);
+        case 2: return pick_fit<T, L, V, 2, KV>(true);
+        case 3: return pick_fit<T, L, V, 3, KV>(true);
+        case 4: return pick_fit<T, L, V, 4, KV>(true);
+        case 5: return pick_fit<T, L, V, 5, KV>(true);
+        case 6: return pick_fit<T, L, V, 6, KV>(true);
+        case 7: return pick_fit<T, L, V, 7, KV>(true);
+        case 8: return pick_fit<T, L, V, 8, KV>(true);
+    }
+    return pick_fit<T, L, V, 8, KV>(false);
+}
+
+template <typename T, int V, bool KV>
+QkKernel pick_l(int L, int nh) {
+    const int passes = (nh + kWave / L - 1) / (kWave / L);
+    switch (L) {
+        case 2: return pick_u<T, 2, V, KV>(passes);
+        case 4: return pick_u<T, 4, V, KV>(passes);
+        case 8: return pick_u<T, 8, V, KV>(passes);
+        case 16: return pick_u<T, 16, V, KV>(passes);
+        case 32: return pick_u<T, 32, V, KV>(passes);
+        case 64: return pick_u<T, 64, V, KV>(passes);
+    }
+    return nullptr;
+}
+
+template <typename T, bool KV>
+QkKernel pick_lv(int L, int V, int nh) {
+    // The fused KV store exists for 16-byte lane vectors only (every power-of-two head size); other
+    // shapes take the unfused pair.
+    if constexpr (KV) {
+        return V == Chunk16<T>::N ? pick_l<T, Chunk16<T>::N, true>(L, nh) : nullptr;
+    } else {
+        switch (V) {
+            case 1: return pick_l<T, 1, false>(L, nh);
+            case 2: return pick_l<T, 2, false>(L, nh);
+            case 4: return pick_l<T, 4, false>(L, nh);
+            case 8: return pick_l<T, 8, false>(L, nh);
+        }
+        return nullptr;
+    }
+}
+
+// Kernel pickers per activation type (qk_rope_f16.hip, qk_rope_f32.hip): the kernel for a head
+// split into L lanes of V elements and nh heads per row, with or without the fused KV store.
+QkKernel pick_qk_f16(int L, int V, int nh, bool kv);
+QkKernel pick_qk_f32(int L, int V, int nh, bool kv);
+
+}  // namespace neko_hip

@@ -19,7 +19,8 @@ import torch
 from ._lib import DT_F16, DT_F32, FMT_F16, FMT_FP4, FMT_FP8, NEKO_OK, NekoError, lib
 
 __all__ = [
-    "Context", "context", "layer_norm", "rms_norm", "qk_norm_rope", "silu_mul", "gelu", "gated_rms_norm", "embed",
+    "Context", "context", "layer_norm", "rms_norm", "qk_norm_rope", "qk_norm_rope_kv", "store_kv", "add_rms_norm",
+    "silu_mul", "gelu", "gated_rms_norm", "embed",
     "prepare", "quant_row_bytes", "quantize_rows", "rope_table", "FMT_F16", "FMT_FP8", "FMT_FP4", "NekoError",
 ]
 
@@ -98,6 +99,12 @@ def _rows(t: torch.Tensor, name: str):
         raise NekoError(f"{name} must be 2-D with unit stride along rows, got shape {tuple(t.shape)} "
                         f"strides {t.stride()}")
     return t.shape[0], t.shape[1], t.stride(0)
+
+
+def _on(t: torch.Tensor | None, name: str, device) -> None:
+    """Every buffer handed to the C ABI must live on the op's GPU: a host pointer would reach a kernel."""
+    if t is not None and (not t.is_cuda or t.device != device):
+        raise NekoError(f"{name} must be a tensor on {device}, got {t.device}")
 
 
 def _vec(t: torch.Tensor | None, n: int, name: str, device) -> int | None:
@@ -184,6 +191,7 @@ def gated_rms_norm(y: torch.Tensor, z: torch.Tensor, w: torch.Tensor, groups: in
     a column slice of a wider row (only its first D columns are read). out may be y."""
     rows, D, ys = _rows(y, "y")
     zr, zc, zs = _rows(z, "z")
+    _on(z, "z", y.device)
     if zr != rows or zc < D or z.dtype != y.dtype:
         raise NekoError(f"z must be {y.dtype} with {rows} rows of at least {D} columns")
     out = _out_like(y, rows, D, out, "out")
@@ -193,6 +201,24 @@ def gated_rms_norm(y: torch.Tensor, z: torch.Tensor, w: torch.Tensor, groups: in
     return out
 
 
+def _rope_inputs(qkv, rows, hd, cs, positions):
+    _on(cs, "cs", qkv.device)
+    if cs.dtype != torch.float32 or not cs.is_contiguous() or cs.dim() != 2 or cs.shape[1] != hd:
+        raise NekoError("cs must be a contiguous float32 [n_pos, hd] table")
+    if positions is None:
+        return None
+    _on(positions, "positions", qkv.device)
+    if positions.dtype != torch.int32 or not positions.is_contiguous() or positions.numel() < rows:
+        raise NekoError("positions must be a contiguous int32 vector with one entry per row")
+    return positions.data_ptr()
+
+
+def _cache(t: torch.Tensor, rows: int, width: int, name: str, device) -> None:
+    _on(t, name, device)
+    if t.dtype != torch.float16 or not t.is_contiguous() or t.dim() != 2 or t.shape[1] != width or t.shape[0] < rows:
+        raise NekoError(f"{name} must be a contiguous float16 [>= {rows}, {width}] cache")
+
+
 def qk_norm_rope(qkv: torch.Tensor, n_q: int, n_kv: int, hd: int, cs: torch.Tensor, eps: float,
                  wqk: torch.Tensor | None = None, positions: torch.Tensor | None = None, pos0: int = 0) -> torch.Tensor:
     """Qwen3 q/k head RMSNorm + NeoX RoPE in place on qkv rows (rope.comp; qwen3_model.cpp:249-253).
@@ -200,18 +226,69 @@ def qk_norm_rope(qkv: torch.Tensor, n_q: int, n_kv: int, hd: int, cs: torch.Tens
     rows, width, stride = _rows(qkv, "qkv")
     if width < (n_q + n_kv) * hd:
         raise NekoError(f"qkv rows hold {width} values, fewer than {n_q + n_kv} heads x {hd}")
-    if cs.dtype != torch.float32 or not cs.is_contiguous() or cs.dim() != 2 or cs.shape[1] != hd:
-        raise NekoError("cs must be a contiguous float32 [n_pos, hd] table")
-    pos_ptr = None
-    if positions is not None:
-        if positions.dtype != torch.int32 or not positions.is_contiguous() or positions.numel() < rows:
-            raise NekoError("positions must be a contiguous int32 vector with one entry per row")
-        pos_ptr = positions.data_ptr()
+    pos_ptr = _rope_inputs(qkv, rows, hd, cs, positions)
     ctx = _ctx_for(qkv)
     _issue(ctx, lib.neko_hip_qk_norm_rope, ctx.handle, qkv.data_ptr(), stride, rows, int(n_q), int(n_kv), int(hd),
            int(pos0), pos_ptr, _vec(wqk, 2 * hd, "wqk", qkv.device), cs.data_ptr(),
            cs.shape[0], float(eps), _dtype_code(qkv))
     return qkv
+
+
+def qk_norm_rope_kv(qkv: torch.Tensor, n_q: int, n_kv: int, hd: int, cs: torch.Tensor, eps: float,
+                    k_cache: torch.Tensor, v_cache: torch.Tensor, wqk: torch.Tensor | None = None,
+                    positions: torch.Tensor | None = None, pos0: int = 0) -> torch.Tensor:
+    """qk_norm_rope fused with the KV-cache store that follows it (qwen3_model.cpp:249-256): the
+    rotated k heads and the v heads of each row also go to k_cache / v_cache (float16 [>= n_pos,
+    n_kv * hd]) at row = the row's position."""
+    rows, width, stride = _rows(qkv, "qkv")
+    if width < (n_q + 2 * n_kv) * hd:
+        raise NekoError(f"qkv rows hold {width} values, fewer than {n_q + 2 * n_kv} heads x {hd}")
+    pos_ptr = _rope_inputs(qkv, rows, hd, cs, positions)
+    n_pos = cs.shape[0]
+    _cache(k_cache, n_pos, n_kv * hd, "k_cache", qkv.device)
+    _cache(v_cache, n_pos, n_kv * hd, "v_cache", qkv.device)
+    ctx = _ctx_for(qkv)
+    _issue(ctx, lib.neko_hip_qk_norm_rope_kv, ctx.handle, qkv.data_ptr(), stride, rows, int(n_q), int(n_kv), int(hd),
+           int(pos0), pos_ptr, _vec(wqk, 2 * hd, "wqk", qkv.device), cs.data_ptr(), n_pos, float(eps),
+           k_cache.data_ptr(), v_cache.data_ptr(), min(k_cache.shape[0], v_cache.shape[0]), _dtype_code(qkv))
+    return qkv
+
+
+def store_kv(qkv: torch.Tensor, k_off: int, v_off: int, width: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+             positions: torch.Tensor | None = None, pos0: int = 0) -> None:
+    """cpu::storeKv (cpu_ops.cpp:535-542): columns [k_off, +width) and [v_off, +width) of each qkv row
+    into float16 cache rows positions[t] (or pos0 + t); rows outside the caches are skipped."""
+    rows, cols, stride = _rows(qkv, "qkv")
+    if k_off < 0 or v_off < 0 or k_off + width > cols or v_off + width > cols:
+        raise NekoError("k/v columns exceed the qkv rows")
+    cache_rows = min(k_cache.shape[0], v_cache.shape[0])
+    _cache(k_cache, 0, width, "k_cache", qkv.device)
+    _cache(v_cache, 0, width, "v_cache", qkv.device)
+    pos_ptr = None
+    if positions is not None:
+        _on(positions, "positions", qkv.device)
+        if positions.dtype != torch.int32 or not positions.is_contiguous() or positions.numel() < rows:
+            raise NekoError("positions must be a contiguous int32 vector with one entry per row")
+        pos_ptr = positions.data_ptr()
+    ctx = _ctx_for(qkv)
+    _issue(ctx, lib.neko_hip_store_kv, ctx.handle, qkv.data_ptr(), stride, int(k_off), int(v_off), rows, int(width),
+           int(pos0), pos_ptr, k_cache.data_ptr(), v_cache.data_ptr(), cache_rows, _dtype_code(qkv))
+
+
+def add_rms_norm(x: torch.Tensor, delta: torch.Tensor, w: torch.Tensor, eps: float,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Residual add + RMSNorm: x += delta (float add, rounded to x's dtype, in place) -- the
+    kAccumulate matmul epilogue, cpu_ops.cpp:123 -- then returns rmsNorm(x) (cpu_ops.cpp:502-511)."""
+    rows, C, xs = _rows(x, "x")
+    dr, dc, ds = _rows(delta, "delta")
+    _on(delta, "delta", x.device)
+    if dr != rows or dc != C or delta.dtype != x.dtype:
+        raise NekoError(f"delta must be {x.dtype} [{rows}, {C}]")
+    out = _out_like(x, rows, C, out, "out")
+    ctx = _ctx_for(x)
+    _issue(ctx, lib.neko_hip_add_rmsnorm, ctx.handle, x.data_ptr(), xs, delta.data_ptr(), ds, out.data_ptr(),
+           out.stride(0), _vec(w, C, "w", x.device), rows, C, float(eps), _dtype_code(x))
+    return out
 
 
 def silu_mul(h: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -245,6 +322,11 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base:
     """Embedding gather with fused dequantisation (embed.comp, QMatrix::dequantizeRow).
     table: uint8 [rows, row_bytes] in format fmt; tokens: int32 [T]; wpe: float16 [P, C] or None.
     Tokens outside [row_base, row_base + rows) leave their out row untouched."""
+    if not tokens.is_cuda:
+        raise NekoError("tokens must be a GPU tensor")
+    _on(table, "table", tokens.device)
+    _on(wpe, "wpe", tokens.device)
+    _on(out, "out", tokens.device)
     if tokens.dtype != torch.int32 or not tokens.is_contiguous():
         raise NekoError("tokens must be a contiguous int32 vector")
     if table.dtype != torch.uint8 or table.dim() != 2 or not table.is_contiguous():

@@ -81,6 +81,21 @@ def bytes_gather(T: int, row_bytes: int, C: int, wpe: bool = False) -> int:
     return T * (row_bytes + C * 2 + 4 + (C * 2 if wpe else 0))
 
 
+def bytes_add_rmsnorm(T: int, C: int) -> int:
+    """x and delta read, x and xn written (fp16), the weights once."""
+    return 4 * T * C * 2 + C * 4
+
+
+def bytes_store_kv(T: int, width: int, positions: bool = True) -> int:
+    """k and v read (fp16), both written to the caches, plus the positions."""
+    return 4 * T * width * 2 + (T * 4 if positions else 0)
+
+
+def bytes_qk_rope_kv(T: int, n_q: int, n_kv: int, hd: int, positions: bool = True) -> int:
+    """q/k RoPE bytes plus the v heads read and the k and v heads written to the caches."""
+    return bytes_qk_rope(T, n_q, n_kv, hd, positions) + 3 * T * n_kv * hd * 2
+
+
 # ------------------------------------------------------------------ configurations
 
 @dataclasses.dataclass(frozen=True)

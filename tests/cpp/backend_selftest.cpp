@@ -205,6 +205,41 @@ struct Harness {
         closeOrFail(read(by, ref.size()), ref, 1e-3f, "gated-rmsnorm", false);
     }
 
+    void kvStore() {  // kv_store.comp / cpu::storeKv through the reference's KvStore parameter blocks
+        const int T = 3, KW = 64, QH = 128, QW = QH + 2 * KW, pos0 = 2, ctx = 8;
+        auto qkv = rnd(size_t(T * QW));
+        for (auto& v : qkv) v *= 3.0f;
+        std::vector<uint16_t> kref(size_t(ctx * KW), 0), vref(kref);
+        oracle_store_kv(qkv.data() + QH, qkv.data() + QH + KW, QW, kref.data(), vref.data(), KW, T, pos0);
+        std::vector<uint16_t> zero(kref.size(), 0);
+        Buffer* bk = be.create(zero.size() * 2, zero.data(), true);
+        Buffer* bv = be.create(zero.size() * 2, zero.data(), true);
+        be.begin();
+        run(Kernel::KvStore, {be.create(qkv.size() * 4, qkv.data()), bk, bv}, {T, KW, pos0, 0, QW, QH, QH + KW},
+            uint32_t((KW / 2 + 63) / 64), T);
+        be.submitAndWait();
+        std::vector<uint16_t> k(kref.size()), v(vref.size());
+        be.download(bk, 0, k.data(), k.size() * 2);
+        be.download(bv, 0, v.data(), v.size() * 2);
+        if (k != kref || v != vref) throw Failure{"self-test kv-store mismatch (bit-exact required)"};
+    }
+
+    void addRmsNorm() {  // the residual add of a kAccumulate matmul epilogue + RMSNorm, AddRmsNorm extension
+        const int T = 4, C = 96;
+        auto x = rnd(size_t(T * C)), d = rnd(size_t(T * C)), w = rnd(size_t(C));
+        halves(w);
+        std::vector<float> xr = x, xn(x.size());
+        oracle_add_rmsnorm(xr.data(), d.data(), xn.data(), w.data(), T, C, 1e-6f);
+        Buffer* bx = be.create(x.size() * 4, x.data(), true);
+        Buffer* bn = be.create(x.size() * 4, nullptr, true);
+        be.begin();
+        run(Kernel::AddRmsNorm, {bx, be.create(d.size() * 4, d.data()), bn, be.create(w.size() * 4, w.data())},
+            {C, floatBits(1e-6f)}, T, 1);
+        be.submitAndWait();
+        closeOrFail(read(bx, xr.size()), xr, 0.0f, "add-rmsnorm residual", true);
+        closeOrFail(read(bn, xn.size()), xn, 1e-3f, "add-rmsnorm", false);
+    }
+
     void unsupported() {  // dense kernels are outside the HIP backend and must throw, not run
         Buffer* b = be.create(64);
         try {
@@ -244,6 +279,8 @@ extern "C" int backend_selftest(char* err, int err_bytes) {
         h.siluMul();
         h.quantEmbed();
         h.gatedNorm();
+        h.kvStore();
+        h.addRmsNorm();
         h.unsupported();
         h.outOfRange();
         std::snprintf(err, size_t(err_bytes), "ok on %s (%s)", be->deviceName().c_str(), be->name());

@@ -258,6 +258,146 @@ def test_qk_rope_position_zero_is_norm_only(dev):
     assert np.array_equal(got, to_bits(normed))
 
 
+# ------------------------------------------------------------------ KV-cache store, fused and alone
+
+def _caches(rows, width, dev):
+    """float16 caches pre-filled with 0xFFFF (a NaN pattern) so rows the op must not write show up."""
+    kc = torch.full((rows, width), -1, dtype=torch.int16, device=dev).view(torch.float16)
+    return kc, kc.clone()
+
+
+def _kv_case(dev, T, n_q, n_kv, hd, n_pos, positions, dtype=torch.float16, stream=61, pos0=0):
+    stride = (n_q + 2 * n_kv) * hd
+    qkv = _f16((T, stride), stream, dev)
+    if dtype == torch.float32:
+        qkv = qkv.float()
+    wqk = _w(2 * hd, stream + 1, dev)
+    cs = ops.rope_table(1e6, hd, n_pos)
+    before = qkv.cpu().numpy().copy()
+    kc, vc = _caches(n_pos, n_kv * hd, dev)
+    pos_t = None if positions is None else torch.from_numpy(positions).to(dev)
+    ops.qk_norm_rope_kv(qkv, n_q, n_kv, hd, torch.from_numpy(cs).to(dev), 1e-6, kc, vc, wqk=wqk, positions=pos_t,
+                        pos0=pos0)
+    src = before.view(np.uint16) if dtype == torch.float16 else before
+    want, wk, wv = O.qk_norm_rope_kv(src, n_q, n_kv, hd, cs, n_pos, 1e-6, wqk=wqk.cpu().numpy(), positions=positions,
+                                     pos0=pos0)
+    gk, gv = to_bits(kc), to_bits(vc)
+    what = f"qk rope+kv T={T} heads={n_q}+{n_kv} hd={hd} {dtype}"
+    if dtype == torch.float16:
+        got = to_bits(qkv)
+        assert_f16_close(got, want, what=what)
+        # the k cache holds exactly the rotated k heads the op wrote back; v is copied bit for bit
+        kw = n_kv * hd
+        rows_k = got[:, n_q * hd:n_q * hd + kw]
+        p = positions if positions is not None else pos0 + np.arange(T)
+        ok = (p >= 0) & (p < n_pos)
+        assert np.array_equal(gk[p[ok]], rows_k[ok])
+        assert_f16_close(gk, wk, what=what + " k cache")
+        assert np.array_equal(gv, wv)
+        assert np.array_equal(got[:, (n_q + n_kv) * hd:], before.view(np.uint16)[:, (n_q + n_kv) * hd:])  # v untouched
+    else:
+        np.testing.assert_allclose(qkv.cpu().numpy(), want, rtol=1e-6, atol=1e-6)
+        assert_f16_close(gk, wk, what=what + " k cache")
+        assert np.array_equal(gv, wv)
+    untouched = ~(wk != 0xFFFF).any(axis=1)
+    assert (gk[untouched] == 0xFFFF).all() and (gv[untouched] == 0xFFFF).all()
+
+
+def test_qk_rope_kv_prefill(dev):
+    """Qwen3-4B prefill of one 8192-token sequence: every position's k and v land in the caches."""
+    _case("qk rope + kv store, Qwen3-4B 8192-token prefill")
+    cfg = wl.QWEN3_PREFILL
+    _kv_case(dev, cfg.T, cfg.n_q, cfg.n_kv, cfg.hd, cfg.T, np.arange(cfg.T, dtype=np.int32))
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,dtype", [
+    (16, 8, 128, torch.float16),   # Qwen3-0.6B decode
+    (2, 1, 64, torch.float16),
+    (3, 1, 96, torch.float16),     # no fused kernel for this head size: rope then store
+    (64, 8, 128, torch.float16),   # 80 heads > 8 passes: rope then store
+    (8, 2, 128, torch.float32),
+])
+def test_qk_rope_kv_shapes(dev, n_q, n_kv, hd, dtype):
+    _case(f"qk rope + kv n_q={n_q} n_kv={n_kv} hd={hd} {dtype}")
+    rng = np.random.default_rng(62)
+    pos = rng.permutation(512)[:37].astype(np.int32)
+    pos[[3, 9]] = [-1, 512]  # outside the table: untouched, no store
+    _kv_case(dev, 37, n_q, n_kv, hd, 512, pos, dtype=dtype)
+
+
+def test_qk_rope_kv_pos0(dev):
+    _case("qk rope + kv store, pos0 form")
+    _kv_case(dev, 9, 4, 2, 128, 16, None, pos0=5)  # rows 7 and 8 fall outside the 16-row table
+
+
+@pytest.mark.parametrize("dtype,width,k_off,v_off", [
+    (torch.float16, 1024, 4096, 5120),   # Qwen3-4B k/v columns
+    (torch.float32, 1024, 4096, 5120),
+    (torch.float16, 100, 7, 301),        # unaligned / odd width: per-element kernel
+    (torch.float32, 24, 40, 8),
+])
+def test_store_kv(dev, dtype, width, k_off, v_off):
+    """cpu::storeKv: f16 activations copied bit for bit, f32 rounded to f16; positions outside the
+    cache skipped."""
+    _case(f"store kv {dtype} width={width}")
+    T, cols, cache_rows = 50, 6144, 40
+    qkv = _f16((T, cols), 63, dev, std=300.0)
+    if dtype == torch.float32:
+        qkv = (qkv.float() * 3.3).contiguous()
+        qkv[1, k_off] = 1e-7
+        qkv[2, v_off] = 1e6
+    rng = np.random.default_rng(64)
+    pos = rng.integers(-3, cache_rows + 3, T).astype(np.int32)
+    pos[:cache_rows] = rng.permutation(cache_rows)[:cache_rows]  # unique rows, then some out of range
+    pos[cache_rows:] = np.array([-1, -2, cache_rows, cache_rows + 5, -7, cache_rows, 41, -1, 99, -3])[:T - cache_rows]
+    kc, vc = _caches(cache_rows, width, dev)
+    ops.store_kv(qkv, k_off, v_off, width, kc, vc, positions=torch.from_numpy(pos).to(dev))
+    src = to_bits(qkv) if dtype == torch.float16 else qkv.cpu().numpy()
+    wk, wv = O.store_kv(src, k_off, v_off, width, cache_rows, positions=pos)
+    assert np.array_equal(to_bits(kc), wk) and np.array_equal(to_bits(vc), wv)
+    kc, vc = _caches(cache_rows, width, dev)
+    ops.store_kv(qkv, k_off, v_off, width, kc, vc, pos0=30)  # rows 10.. of the batch fall past the cache
+    wk, wv = O.store_kv(src, k_off, v_off, width, cache_rows, pos0=30)
+    assert np.array_equal(to_bits(kc), wk) and np.array_equal(to_bits(vc), wv)
+
+
+# ------------------------------------------------------------------ residual add + RMSNorm
+
+@pytest.mark.parametrize("T,C,dtype", [
+    (8192, 2560, torch.float16),   # Qwen3-4B prefill
+    (64, 1024, torch.float16),
+    (7, 100, torch.float16),       # odd width: generic kernel
+    (3, 20000, torch.float16),     # four waves per row
+    (33, 1536, torch.float32),
+])
+def test_add_rmsnorm(dev, T, C, dtype):
+    _case(f"add + rmsnorm {T}x{C} {dtype}")
+    x = _f16((T, C), 65, dev, std=4.0)
+    d = _f16((T, C), 66, dev, std=0.5)
+    if dtype == torch.float32:
+        x, d = x.float(), d.float()
+    d[1] = -x[1]  # a row that cancels to zero: the eps-only scale
+    w = _w(C, 67, dev)
+    x0, d0 = x.cpu().numpy().copy(), d.cpu().numpy()
+    xn = ops.add_rms_norm(x, d, w, 1e-6)
+    if dtype == torch.float16:
+        wx, wn = O.add_rmsnorm_f16(x0.view(np.uint16), d0.view(np.uint16), w.cpu().numpy(), 1e-6)
+        assert np.array_equal(to_bits(x), wx)  # the residual sum is exact f32 then one RNE: bit-exact
+        assert_f16_close(to_bits(xn), wn, what=f"add+rmsnorm {T}x{C}")
+    else:
+        want_n = np.empty_like(x0)
+        O.lib().oracle_add_rmsnorm(O._ptr(x0), O._ptr(np.ascontiguousarray(d0)), O._ptr(want_n),
+                                   O._ptr(w.cpu().numpy()), T, C, 1e-6)
+        assert np.array_equal(x.cpu().numpy().view(np.uint32), x0.view(np.uint32))
+        np.testing.assert_allclose(xn.cpu().numpy(), want_n, rtol=2e-7, atol=0)
+
+
+def test_add_rmsnorm_rejects_aliasing(dev):
+    x = _f16((4, 256), 68, dev)
+    with pytest.raises(NekoError):
+        ops.add_rms_norm(x, x.clone(), _w(256, 69, dev), 1e-6, out=x)
+
+
 # ------------------------------------------------------------------ SwiGLU / GELU
 
 @pytest.mark.parametrize("T,I", [(64, 3072), (8192, 9728), (16384, 4096), (2, 100), (3, 7)])
