@@ -48,7 +48,7 @@ def parse():
                    help="time every configured workload's ops (one JSON line with all of them) instead")
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
-                        "quant_gather_qwen3_1.7b, qwen3_4b_fused, granite_4.0h_norms)")
+                        "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -184,7 +184,7 @@ def all_configs(args):
     out = {}
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
-              "granite_4.0h_norms")
+              "quantize_qwen3_1.7b_table", "granite_4.0h_norms")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -294,6 +294,21 @@ def all_configs(args):
             "store_kv": wl.bytes_store_kv(c6.T, kw6)},
             "Qwen3-4B fused neighbours: residual add + RMSNorm [8192,2560]; q/k RoPE + KV store of an 8192-token "
             "sequence, beside the unfused q/k RoPE and KV store")
+
+    # Load-time quantiser: the 151936 x 2048 tied table in f32 (1.24 GB) encoded on the device into each
+    # weight format; bytes = the f32 rows read + the encoded rows written.
+    if want("quantize_qwen3_1.7b_table"):
+        c7 = wl.QUANT_GATHER
+        src7 = wl.normal_f16((c7.vocab, c7.C), 0.0, 0.02, 31, dev).float()
+        calls7, bytes7 = {}, {}
+        for fmt, name in ((ops.FMT_F16, "quantize_fp16"), (ops.FMT_FP8, "quantize_fp8"), (ops.FMT_FP4, "quantize_fp4")):
+            run7, (tab7, _) = ops.prepare(ops.quantize, src7, fmt)
+            calls7[name] = run7
+            run7.table = tab7  # keep the output alive with its call
+            bytes7[name] = c7.vocab * c7.C * 4 + tab7.numel()
+        run("quantize_qwen3_1.7b_table", calls7, bytes7,
+            "quantizeMatrix on the device: 151936 x 2048 f32 table -> F16 / FP8 / FP4 rows")
+        del src7, calls7
 
     # Granite-4.0-H-style norms and SwiGLU
     if want("granite_4.0h_norms"):

@@ -167,6 +167,15 @@ int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const vo
                    int64_t C, int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t wpe_rows, int64_t pos0,
                    void* out, int64_t out_stride, int out_dtype);
 
+/* Load-time quantiser on the device (quantizeMatrix, quant.cpp:255-279, portable branch): rows x cols
+ * weights (src_dtype f32, or f16 widened exactly; row stride src_stride elements, device memory)
+ * encoded into device rows of neko_quant_row_bytes(*fmt_used, cols) bytes, bit-identical to
+ * neko_quantize_rows and the reference (FP8 block scale and RNE codes, FP4 scale search with its
+ * two least-squares refits, padding zeroed). cols % 32 != 0 stores F16, like the reference; FP8/FP4
+ * need 16-byte aligned source rows and output. */
+int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t cols, const void* src, int64_t src_stride,
+                           int src_dtype, uint8_t* dst, int* fmt_used);
+
 /* ---------------------------------------------------------------- host-side codecs */
 
 /* Bytes per stored row (quant.cpp:199-208): F16 2*cols; FP8 / FP4 the codes (cols or cols/2

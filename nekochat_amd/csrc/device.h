@@ -63,7 +63,8 @@ __device__ __forceinline__ void store_nt(V* p, V v) {
 // The exponent argument is clamped at 126 so d stays finite (no 0 * inf in the correction); gates
 // below about -87.3 then give a value of magnitude < 2^-119 instead of the reference's (also tiny
 // or -0) quotient, which rounds to the same signed zero once multiplied by an fp16 operand. A +inf
-// gate passes through as +inf and -inf / NaN give NaN, as in the reference. Measured against the
+// gate passes through as +inf, a zero gate keeps its sign (the correction step would turn -0 into
+// +0), and -inf / NaN give NaN, as in the reference. Measured against the
 // oracle over every fp16 gate value: SwiGLU outputs within 1 fp16 ulp.
 __device__ __forceinline__ float silu_fast(float gate) {
     const float kLog2e = 1.44269504088896341f, kLog2eLo = 1.925963033500011e-08f, kLn2 = 0.69314718055994531f;
@@ -74,7 +75,7 @@ __device__ __forceinline__ float silu_fast(float gate) {
     const float r = __builtin_amdgcn_rcpf(d);
     const float q0 = gate * r;
     float q = __builtin_fmaf(__builtin_fmaf(-q0, d, gate), r, q0);
-    if (gate == __builtin_inff()) q = gate;
+    if (gate == __builtin_inff() || gate == 0.0f) q = gate;  // +inf, and the sign of a zero gate
     return q;
 }
 
@@ -108,10 +109,20 @@ template <typename T>
 __device__ __forceinline__ float to_f32(T v) {
     return static_cast<float>(v);
 }
-// Conversion to T; for half this is one round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+// f32 -> f16, one round-to-nearest-even of v as computed (v_cvt_f16_f32). The empty asm keeps the
+// backend from folding a multiply that produced v into the conversion as v_fma_mix*_f16(a, b, +0):
+// that fused form returns +0 where the product is -0, so x*w = -0 would not round to 0x8000 as the
+// reference's separate multiply and conversion do.
+__device__ __forceinline__ half_t f16_rne(float v) {
+    __asm__("" : "+v"(v));
+    return static_cast<half_t>(v);
+}
+
+// Conversion to T; for half, f16_rne.
 template <typename T>
 __device__ __forceinline__ T from_f32(float v) {
-    return static_cast<T>(v);
+    if constexpr (sizeof(T) == 2) return f16_rne(v);
+    else return static_cast<T>(v);
 }
 
 // ---------------------------------------------------------------- DPP cross-lane moves

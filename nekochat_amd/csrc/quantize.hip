@@ -1,0 +1,328 @@
+// Load-time weight quantiser for gfx950: quantizeMatrix (quant.cpp:255-279) on the device, bit-identical
+// to the reference's portable (x86) branch, writing the row layout the gather reads (quant.h:30-36).
+//
+// One thread per 32-weight block, all of a block's arithmetic in that thread in the reference's order
+// (the FP4 least-squares sums are sequential float additions, so splitting a block across lanes would
+// change their rounding); FP8 waves load their 64 blocks coalesced and hand them out through LDS. Divisions are IEEE (correctly rounded, hipcc's default), products are not
+// contracted (-ffp-contract=off), nearbyint is v_rndne_f32 and halfBits is one RNE v_cvt_f16_f32
+// (subnormals kept). Consecutive threads take consecutive blocks of a row, so the code stores (16 or
+// 32 bytes per thread) and the f16 scales are contiguous across the wave; the thread of a row's last
+// block zero-fills the row's padding, as the reference's zero-initialised buffer leaves it.
+#include "internal.h"
+
+namespace neko_hip {
+namespace {
+
+constexpr int kBlock = 32;  // quant.h:17 kQuantBlock
+
+// halfBits: one RNE conversion of f as computed (f16_rne keeps a preceding multiply out of the
+// conversion, so -0 products stay -0).
+__device__ __forceinline__ uint32_t half_bits(float f) { return __builtin_bit_cast(uint16_t, f16_rne(f)); }
+__device__ __forceinline__ float half_value(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(h)));
+}
+
+// quant.cpp:43-49: the f16 pattern of y/256, rounded to nearest even over its 7 low bits, clamped to
+// 0x7E (448; 0x7F would decode as 480).
+__device__ __forceinline__ uint32_t encode_fp8(float y) {
+    const uint32_t h = half_bits(y * (1.0f / 256.0f));
+    const uint32_t mag = h & 0x7FFFu;
+    uint32_t c = (mag + 0x3Fu + ((mag >> 7) & 1u)) >> 7;
+    if (c > 0x7Eu) c = 0x7Eu;
+    return c | ((h >> 8) & 0x80u);
+}
+
+// quant.cpp:57-61: threshold ladder over |y|; a zero magnitude keeps no sign.
+__device__ __forceinline__ uint32_t encode_fp4(float y) {
+    const float a = fabsf(y);
+    const uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
+    return c == 0 ? 0u : (c | (y < 0.0f ? 8u : 0u));
+}
+
+// quant.cpp:93-97: nearest E2M1 magnitude of a >= 0.
+__device__ __forceinline__ float fp4_round(float a) {
+    if (a < 1.75f) return __builtin_rintf(a * 2.0f) * 0.5f;
+    if (a < 3.5f) return __builtin_rintf(a);
+    return a < 5.0f ? 4.0f : 6.0f;
+}
+
+struct Fit {
+    float err, xr, rr;
+};
+
+// quant.cpp:126-137 (the x86 branch): sequential sums over the block.
+__device__ __forceinline__ Fit fit_fp4(const float (&ax)[kBlock], float s) {
+    Fit f{0.0f, 0.0f, 0.0f};
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < kBlock; i++) {
+        const float r = fp4_round(ax[i] * inv);
+        const float d = ax[i] - r * s;
+        f.err = f.err + d * d;
+        f.xr = f.xr + ax[i] * r;
+        f.rr = f.rr + r * r;
+    }
+    return f;
+}
+
+// std::max(amax, v) as the reference evaluates it: (amax < v) ? v : amax.
+__device__ __forceinline__ float block_amax(const float (&x)[kBlock]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kBlock; i++) {
+        const float v = fabsf(x[i]);
+        amax = amax < v ? v : amax;
+    }
+    return amax;
+}
+
+// quant.cpp:142-165.
+__device__ __forceinline__ uint32_t fp4_block_scale(const float (&x)[kBlock]) {
+    const float amax = block_amax(x);
+    uint32_t best = half_bits(amax / 6.0f);
+    if (half_value(best) <= 0.0f) return 0;
+    float ax[kBlock];
+#pragma unroll
+    for (int i = 0; i < kBlock; i++) ax[i] = fabsf(x[i]);
+    Fit fit = fit_fp4(ax, half_value(best));
+    float best_err = fit.err;
+    for (int iter = 0; iter < 2 && fit.rr > 0.0f; iter++) {
+        const uint32_t s = half_bits(fit.xr / fit.rr);
+        if (half_value(s) <= 0.0f || s == best) break;
+        fit = fit_fp4(ax, half_value(s));
+        if (fit.err >= best_err) break;
+        best_err = fit.err;
+        best = s;
+    }
+    return best;
+}
+
+struct QuantArgs {
+    const void* src;
+    int64_t src_stride;  // elements
+    uint8_t* dst;
+    int64_t row_bytes;
+    int64_t cols;
+    int64_t pad_from;  // first padding byte of a row (codes + scales end)
+    uint32_t items;    // rows * blocks per row (< 2^31)
+    FastDiv nb;        // blocks per row
+};
+
+// One block read by its own thread (8 x 16 bytes; used where occupancy matters more than coalescing).
+template <typename TI>
+__device__ __forceinline__ void load_block(const TI* p, float (&x)[kBlock]) {
+    if constexpr (sizeof(TI) == 4) {
+#pragma unroll
+        for (int q = 0; q < kBlock / 4; q++) {
+            const float4v v = load_nt(reinterpret_cast<const float4v*>(p) + q);
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[4 * q + e] = v[e];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kBlock / 8; q++) {
+            const half8 v = load_nt(reinterpret_cast<const half8*>(p) + q);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[8 * q + e] = static_cast<float>(v[e]);
+        }
+    }
+}
+
+// A wave's 64 consecutive blocks go through LDS: the lanes load them as consecutive 16-byte chunks
+// (coalesced, whatever the row boundaries), store them with one pad word per 32 (block b starts at
+// word 33 b), and each lane then reads its own block, lanes b and b+1 landing in adjacent banks.
+constexpr int kStride = kBlock + 1;
+
+template <typename TI>
+__device__ __forceinline__ void stage_blocks(const QuantArgs& a, uint32_t wave_block0, float* lds, int lane,
+                                             float (&x)[kBlock]) {
+    constexpr int EPC = 16 / sizeof(TI);     // elements per 16-byte chunk
+    constexpr int CPB = kBlock / EPC;        // chunks per block
+#pragma unroll
+    for (int k = 0; k < CPB; k++) {
+        const uint32_t m = static_cast<uint32_t>(lane) + kWave * k;  // chunk index within the wave's span
+        const uint32_t blk = wave_block0 + m / CPB;
+        if (blk >= a.items) continue;
+        const uint32_t r = fast_div(blk, a.nb);
+        const int64_t col = static_cast<int64_t>(blk - r * a.nb.d) * kBlock + (m % CPB) * EPC;
+        const TI* p = static_cast<const TI*>(a.src) + static_cast<int64_t>(r) * a.src_stride + col;
+        float* d = lds + (m / CPB) * kStride + (m % CPB) * EPC;
+        if constexpr (sizeof(TI) == 4) {
+            const float4v v = load_nt(reinterpret_cast<const float4v*>(p));
+#pragma unroll
+            for (int e = 0; e < 4; e++) d[e] = v[e];
+        } else {
+            const half8 v = load_nt(reinterpret_cast<const half8*>(p));
+#pragma unroll
+            for (int e = 0; e < 8; e++) d[e] = static_cast<float>(v[e]);
+        }
+    }
+    // Only this wave's lanes wrote these words; the wave runs in lockstep, so a wave-local fence
+    // (not a workgroup barrier) orders the stores before the reads.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < kBlock; i++) x[i] = lds[lane * kStride + i];
+}
+
+// FMT 1: FP8 (quant.cpp:81-90), 2: FP4 (quant.cpp:167-178).
+// FP8 (light arithmetic, bound by the loads) stages its blocks through LDS; FP4 (bound by its scale
+// search's VALU work) reads them directly and keeps the occupancy the LDS would cost.
+template <int FMT, typename TI>
+__global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
+    constexpr bool kStage = FMT == 1;
+    __shared__ float lds[kStage ? 4 : 1][kStage ? kWave * kStride : 1];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave_block0 = blockIdx.x * 256u + static_cast<uint32_t>(wave) * kWave;
+    if (wave_block0 >= a.items) return;  // wave-uniform
+    float x[kBlock];
+    if constexpr (kStage) stage_blocks<TI>(a, wave_block0, lds[wave], lane, x);
+    const uint32_t idx = wave_block0 + static_cast<uint32_t>(lane);
+    if (idx >= a.items) return;
+    const uint32_t r = fast_div(idx, a.nb);
+    const uint32_t b = idx - r * a.nb.d;
+    if constexpr (!kStage)
+        load_block(static_cast<const TI*>(a.src) + static_cast<int64_t>(r) * a.src_stride + static_cast<int64_t>(b) * kBlock, x);
+    uint8_t* row = a.dst + static_cast<int64_t>(r) * a.row_bytes;
+    if constexpr (FMT == 1) {
+        const float amax = block_amax(x);
+        const uint32_t s = half_bits(amax / 448.0f);
+        const float sv = half_value(s);
+        const float inv = sv > 0.0f ? 1.0f / sv : 0.0f;
+        uint4v codes[2];
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) word |= encode_fp8(x[4 * w + e] * inv) << (8 * e);
+            codes[w / 4][w % 4] = word;
+        }
+        uint4v* out = reinterpret_cast<uint4v*>(row + static_cast<int64_t>(b) * kBlock);
+        out[0] = codes[0];
+        out[1] = codes[1];
+        reinterpret_cast<uint16_t*>(row + a.cols)[b] = static_cast<uint16_t>(sv > 0.0f ? s : 0u);
+    } else {
+        const uint32_t s = fp4_block_scale(x);
+        const float inv = s ? 1.0f / half_value(s) : 0.0f;
+        uint4v codes;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int j = 4 * w + e;
+                word |= (encode_fp4(x[j] * inv) | (encode_fp4(x[16 + j] * inv) << 4)) << (8 * e);
+            }
+            codes[w] = word;
+        }
+        *reinterpret_cast<uint4v*>(row + static_cast<int64_t>(b) * (kBlock / 2)) = codes;
+        reinterpret_cast<uint16_t*>(row + a.cols / 2)[b] = static_cast<uint16_t>(s);
+    }
+    if (b == a.nb.d - 1)
+        for (int64_t i = a.pad_from; i < a.row_bytes; i++) row[i] = 0;
+}
+
+// F16 rows (quant.cpp:180-186 rowToHalf): 8 elements per thread, flattened (row, chunk) space.
+template <typename TI>
+__global__ __launch_bounds__(256) void to_half8_kernel(const TI* src, int64_t src_stride, uint16_t* dst, int64_t cols,
+                                                       uint32_t items, FastDiv cpr) {
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= items) return;
+    const uint32_t r = fast_div(idx, cpr);
+    const int64_t c = static_cast<int64_t>(idx - r * cpr.d) * 8;
+    const TI* p = src + static_cast<int64_t>(r) * src_stride + c;
+    half8 h;
+    if constexpr (sizeof(TI) == 4) {
+        const float4v lo = load_nt(reinterpret_cast<const float4v*>(p));
+        const float4v hi = load_nt(reinterpret_cast<const float4v*>(p + 4));
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = f16_rne(lo[e]);
+            h[4 + e] = f16_rne(hi[e]);
+        }
+    } else {
+        h = load_nt(reinterpret_cast<const half8*>(p));
+    }
+    *reinterpret_cast<half8*>(dst + static_cast<int64_t>(r) * cols + c) = h;
+}
+
+// Any width (the cols % 32 != 0 fallback included): one thread per element.
+template <typename TI>
+__global__ __launch_bounds__(256) void to_half_kernel(const TI* src, int64_t src_stride, uint16_t* dst, int64_t cols,
+                                                      int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / cols, c = i - r * cols;
+    dst[i] = static_cast<uint16_t>(half_bits(static_cast<float>(src[r * src_stride + c])));
+}
+
+template <typename TI>
+int launch_typed(neko_hip_ctx* ctx, const char* what, int fmt, int64_t rows, int64_t cols, const void* src,
+                 int64_t src_stride, uint8_t* dst, int64_t row_bytes) {
+    if (fmt == NEKO_FMT_F16 && cols % 8 == 0 && aligned(src, 16) && (src_stride * sizeof(TI)) % 16 == 0 &&
+        aligned(dst, 16)) {
+        const int64_t cpr = cols / 8;
+        const int64_t slice = 0x7fffff00LL / cpr;
+        for (int64_t r0 = 0; r0 < rows; r0 += slice) {
+            const int64_t n = rows - r0 < slice ? rows - r0 : slice;
+            const uint32_t items = static_cast<uint32_t>(n * cpr);
+            hipLaunchKernelGGL(to_half8_kernel<TI>, dim3((items + 255u) / 256u), dim3(256), 0, ctx->stream,
+                               static_cast<const TI*>(src) + r0 * src_stride, src_stride,
+                               reinterpret_cast<uint16_t*>(dst + r0 * row_bytes), cols, items,
+                               make_fast_div(static_cast<uint32_t>(cpr)));
+            if (int rc = after_launch(ctx, what)) return rc;
+        }
+        return NEKO_OK;
+    }
+    if (fmt == NEKO_FMT_F16) {
+        const int64_t n = rows * cols;
+        const int64_t blocks = (n + 255) / 256;
+        if (blocks > 0x7fffffff) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: too many elements", what);
+        hipLaunchKernelGGL(to_half_kernel<TI>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream,
+                           static_cast<const TI*>(src), src_stride, reinterpret_cast<uint16_t*>(dst), cols, n);
+        return after_launch(ctx, what);
+    }
+    const int64_t nb = cols / kBlock;
+    const int64_t slice = 0x7fffff00LL / nb;  // rows per launch, keeping block indices < 2^31
+    for (int64_t r0 = 0; r0 < rows; r0 += slice) {
+        const int64_t n = rows - r0 < slice ? rows - r0 : slice;
+        QuantArgs a{static_cast<const TI*>(src) + r0 * src_stride, src_stride, dst + r0 * row_bytes, row_bytes, cols,
+                    fmt == NEKO_FMT_FP8 ? cols + 2 * nb : cols / 2 + 2 * nb, static_cast<uint32_t>(n * nb),
+                    make_fast_div(static_cast<uint32_t>(nb))};
+        const uint32_t blocks = (a.items + 255u) / 256u;
+        if (fmt == NEKO_FMT_FP8) hipLaunchKernelGGL((quantize_kernel<1, TI>), dim3(blocks), dim3(256), 0, ctx->stream, a);
+        else hipLaunchKernelGGL((quantize_kernel<2, TI>), dim3(blocks), dim3(256), 0, ctx->stream, a);
+        if (int rc = after_launch(ctx, what)) return rc;
+    }
+    return NEKO_OK;
+}
+
+}  // namespace
+}  // namespace neko_hip
+
+using namespace neko_hip;
+
+extern "C" int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t cols, const void* src,
+                                      int64_t src_stride, int src_dtype, uint8_t* dst, int* fmt_used) {
+    const char* what = "neko_hip_quantize_rows";
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, fmt == NEKO_FMT_F16 || fmt == NEKO_FMT_FP8 || fmt == NEKO_FMT_FP4, "%s: bad format %d", what, fmt);
+    NEKO_REQUIRE(ctx, valid_dtype(src_dtype), "%s: bad source dtype %d", what, src_dtype);
+    NEKO_REQUIRE(ctx, rows >= 0 && cols > 0 && cols <= 0x7fffffff, "%s: bad shape rows=%lld cols=%lld", what,
+                 (long long)rows, (long long)cols);
+    const int used = cols % kBlock != 0 ? NEKO_FMT_F16 : fmt;  // quant.cpp:257
+    if (fmt_used) *fmt_used = used;
+    if (rows == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, src && dst, "%s: null pointer", what);
+    NEKO_REQUIRE(ctx, src_stride >= cols, "%s: source stride %lld < cols %lld", what, (long long)src_stride, (long long)cols);
+    const int64_t row_bytes = static_cast<int64_t>(neko_quant_row_bytes(used, cols));
+    if (used != NEKO_FMT_F16) {
+        const size_t esz = dtype_size(src_dtype);
+        NEKO_REQUIRE(ctx, aligned(src, 16) && (src_stride * esz) % 16 == 0 && aligned(dst, 16),
+                     "%s: FP8/FP4 need 16-byte aligned source rows and output", what);
+    }
+    return src_dtype == NEKO_DT_F32 ? launch_typed<float>(ctx, what, used, rows, cols, src, src_stride, dst, row_bytes)
+                                    : launch_typed<half_t>(ctx, what, used, rows, cols, src, src_stride, dst, row_bytes);
+}

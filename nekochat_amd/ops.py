@@ -21,7 +21,7 @@ from ._lib import DT_F16, DT_F32, FMT_F16, FMT_FP4, FMT_FP8, NEKO_OK, NekoError,
 __all__ = [
     "Context", "context", "layer_norm", "rms_norm", "qk_norm_rope", "qk_norm_rope_kv", "store_kv", "add_rms_norm",
     "silu_mul", "gelu", "gated_rms_norm", "embed",
-    "prepare", "quant_row_bytes", "quantize_rows", "rope_table", "FMT_F16", "FMT_FP8", "FMT_FP4", "NekoError",
+    "prepare", "quantize", "quant_row_bytes", "quantize_rows", "rope_table", "FMT_F16", "FMT_FP8", "FMT_FP4", "NekoError",
 ]
 
 
@@ -350,6 +350,25 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base:
            int(row_base), n_rows, wpe_ptr, wpe_rows, int(pos0), out.data_ptr(), os_,
            _dtype_code(out))
     return out
+
+
+def quantize(src: torch.Tensor, fmt: int, out: torch.Tensor | None = None) -> tuple[torch.Tensor, int]:
+    """quantizeMatrix (quant.cpp:255-279) on the GPU: float32 or float16 rows [rows, cols] -> uint8 rows of
+    quant_row_bytes(fmt_used, cols) in the weight format, bit-identical to the host quantize_rows.
+    cols % 32 != 0 stores F16 (fmt_used says so)."""
+    rows, cols, stride = _rows(src, "src")
+    used = fmt if cols % 32 == 0 else FMT_F16
+    rb = quant_row_bytes(used, cols)
+    if out is None:
+        out = torch.empty((rows, rb), dtype=torch.uint8, device=src.device)
+    _on(out, "out", src.device)
+    if out.dtype != torch.uint8 or not out.is_contiguous() or tuple(out.shape) != (rows, rb):
+        raise NekoError(f"out must be a contiguous uint8 [{rows}, {rb}] tensor")
+    got = ctypes.c_int()
+    ctx = _ctx_for(src)
+    _issue(ctx, lib.neko_hip_quantize_rows, ctx.handle, int(fmt), rows, cols, src.data_ptr(), stride, _dtype_code(src),
+           out.data_ptr(), ctypes.byref(got))
+    return out, used
 
 
 # ------------------------------------------------------------------ host-side codecs

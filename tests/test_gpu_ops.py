@@ -569,6 +569,77 @@ def test_embed_empty_and_invalid(dev):
         ops.embed(torch.zeros(2, dtype=torch.int32, device=dev), tab, ops.FMT_FP8, 48)  # C % 32 != 0
 
 
+# ------------------------------------------------------------------ load-time quantiser
+
+def _quant_source(rows, cols, seed):
+    """~N(0, 0.02) weights with blocks that reach every branch of the encoders: all-zero rows and
+    blocks, outliers, tiny blocks whose scales are f16 subnormals or round to zero, a block whose
+    FP8/FP4 scale overflows f16, exact code values, and sign mixes."""
+    rng = np.random.default_rng(seed)
+    x = (0.02 * rng.standard_normal((rows, cols))).astype(np.float32)
+    x[0] = 0.0
+    x[1, 32:64] = 0.0
+    x[2, 5] = 1.5
+    x[2, 40] = -3e-6
+    x[3, :64] *= 1e-5                 # scales near and below the smallest f16 subnormals
+    x[3, 64:96] = 1e-12               # rounds to a zero scale
+    x[4, :32] *= 1e9                  # FP8 and FP4 scales overflow to inf (codes 0)
+    x[5, :32] = np.tile(np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float32), 4) * np.float32(0.125)
+    x[5, 32:64] = -x[5, :32]
+    x[6] = rng.standard_normal(cols).astype(np.float32) * (10.0 ** rng.integers(-6, 3, cols)).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("fmt", [ops.FMT_F16, ops.FMT_FP8, ops.FMT_FP4])
+@pytest.mark.parametrize("src_dtype", [torch.float32, torch.float16])
+def test_quantize_gpu_bitexact(dev, fmt, src_dtype):
+    """The device quantiser writes the same bytes as the oracle (itself pinned to the reference's
+    quantizeMatrix) and as the host C-ABI encoder, codes, scales and padding."""
+    _case(f"quantize fmt={fmt} src={src_dtype}")
+    x = _quant_source(512, 2048, 81 + fmt)
+    if src_dtype == torch.float16:
+        x = np.clip(x, -60000, 60000).astype(np.float16).astype(np.float32)  # f16 sources: exact widening
+    src = torch.from_numpy(x).to(dev).to(src_dtype)
+    got, used = ops.quantize(src, fmt)
+    assert used == fmt
+    want = O.quantize_rows(fmt, x)
+    g = got.cpu().numpy()
+    bad = np.argwhere(g != want)
+    if bad.size:
+        r, c = (int(v) for v in bad[0])
+        cols = x.shape[1]
+        codes = cols if fmt == ops.FMT_FP8 else cols // 2 if fmt == ops.FMT_FP4 else 2 * cols
+        per = 32 if fmt == ops.FMT_FP8 else 16
+        part = "code" if c < codes else "scale" if c < codes + cols // 16 else "padding"
+        blk = c // per if part == "code" else (c - codes) // 2
+        xb = x[r, 32 * blk:32 * blk + 32] if fmt != ops.FMT_F16 else x[r, c // 2:c // 2 + 1]
+        pytest.fail(f"{len(bad)} bytes differ; first at row {r} byte {c} ({part}, block {blk}): got {g[r, c]:#04x} "
+                    f"want {want[r, c]:#04x}; block amax {np.abs(xb).max():.9g}, scale want "
+                    f"{want[r, codes + 2 * blk:codes + 2 * blk + 2].view(np.uint16)} got "
+                    f"{g[r, codes + 2 * blk:codes + 2 * blk + 2].view(np.uint16)}; values {xb[:8]}")
+    if src_dtype == torch.float32:
+        host, _ = ops.quantize_rows(fmt, x)
+        assert np.array_equal(host, want)
+
+
+def test_quantize_gpu_shapes(dev):
+    _case("quantize: cols % 32 != 0 stores F16, strided source, then the gather reads the table back")
+    x = _quant_source(40, 100, 91)
+    got, used = ops.quantize(torch.from_numpy(x).to(dev), ops.FMT_FP4)
+    assert used == ops.FMT_F16 and np.array_equal(got.cpu().numpy(), O.quantize_rows(ops.FMT_FP4, x))
+    wide = torch.from_numpy(_quant_source(33, 512, 92)).to(dev)
+    view = wide[:, :256]  # row stride 512, 256 columns
+    for fmt in (ops.FMT_FP8, ops.FMT_FP4):
+        got, _ = ops.quantize(view, fmt)
+        want = O.quantize_rows(fmt, view.cpu().numpy())
+        assert np.array_equal(got.cpu().numpy(), want)
+        ids = np.arange(33, dtype=np.int32)[::-1].copy()
+        out = ops.embed(torch.from_numpy(ids).to(dev), got, fmt, 256)
+        assert np.array_equal(to_bits(out), O.embed(ids, want, fmt, 256))
+    with pytest.raises(NekoError):
+        ops.quantize(torch.zeros((4, 64), dtype=torch.float64, device=dev), ops.FMT_FP8)
+
+
 # ------------------------------------------------------------------ the GPT-2 op chain
 
 def test_gpt2_chain(dev):
