@@ -15,8 +15,8 @@ ms_per_step is that per-layer kernel time; wall_ms_per_step (the barrier-to-barr
 timed steps, divided by K) also contains the flushes.
 
 cpu_baseline: the reference's portable C++ ops (oracle/_ref, compiled from its sources) -- or the
-oracle's C restatement where that is absent -- on one pinned core, over a bounded row sample of the
-same workload.
+oracle's C restatement where that is absent -- on f32 activations, one pinned core, over a bounded
+row sample of the same workload. With --all, every op carries the same kind of figure (cpu_us).
 """
 from __future__ import annotations
 
@@ -169,6 +169,262 @@ def gpu_bench(args):
     per_op, wall = time_ops(calls, cfg.op_bytes(), names, args.steps, args.warmup,
                             None if args.no_flush else flush, timer)
     return cfg, per_op, wall
+
+
+def _pin_one_core():
+    """Pins the calling thread to its first allowed core; returns the previous mask."""
+    try:
+        mask = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {sorted(mask)[0]})
+        return mask
+    except (AttributeError, OSError):
+        return None
+
+
+def _unpin(mask):
+    if mask is not None:
+        os.sched_setaffinity(0, mask)
+
+
+def _f32(shape, mean, std, stream):
+    """Host f32 activations with the same generator as the device inputs (fp16-rounded values)."""
+    from nekochat_amd import workloads as wl
+
+    return wl.normal_f16(shape, mean, std, stream, "cpu").float().numpy()
+
+
+class CpuLeg:
+    """The reference's CPU path beside each device op of --all: its compiled ops (oracle/_ref, built
+    from its sources) on f32 activations as its CPU forward passes hold them, one pinned core, a
+    bounded sample of the workload's rows, median of `reps`, scaled to the full workload. An op whose
+    reference form exists only inside a GEMM epilogue is timed as the oracle's restatement ("port")."""
+
+    def __init__(self, reps: int = 3):
+        from oracle import oracle as O
+
+        self.O = O
+        self.R = O.ref() if O.ref_available() else None
+        self.reps = reps
+        self.jobs = []
+
+    def add(self, label, op, make, scale, sample, port=False):
+        """make() builds the sample's inputs and returns (run_once, release or None)."""
+        self.jobs.append((label, op, make, scale, sample, port))
+
+    def run(self, out):
+        if self.R is None:
+            for label, op, *_ in self.jobs:
+                out[label]["ops"][op]["cpu_kind"] = "not run: oracle/_ref (the compiled reference ops) is not built"
+            return
+        for label, op, make, scale, sample, port in self.jobs:
+            fn, release = make()
+            mask = _pin_one_core()
+            fn()
+            samples = []
+            for _ in range(self.reps):
+                t0 = time.perf_counter()
+                fn()
+                samples.append(time.perf_counter() - t0)
+            _unpin(mask)
+            if release is not None:
+                release()
+            us = statistics.median(samples) * scale * 1e6
+            d = out[label]["ops"][op]
+            d["cpu_us"] = round(us, 1)
+            d["cpu_kind"] = "port" if port else "reference"
+            d["cpu_sample"] = sample
+            d["speedup_vs_cpu"] = round(us / d["us"], 1)
+
+
+def add_cpu_jobs(leg, want):
+    """Registers the CPU counterpart of every device op that all_configs times."""
+    import numpy as np
+
+    from nekochat_amd import ops
+    from nekochat_amd import workloads as wl
+
+    O, R, P = leg.O, leg.R, leg.O._ptr
+    core = f"1 pinned core of {os.cpu_count()}, g++ -O3 portable x86-64 build, f32 activations"
+
+    def every(what):
+        return f"{what}; {core}"
+
+    def rows_of(n, total):
+        return f"{n} of {total} rows (median of {leg.reps}), scaled to all {total}; {core}"
+
+    def gpt2_jobs():  # gpt2_small_chain
+        c = wl.GPT2_CHAIN
+
+        def gather():
+            table = wl.normal_f16((c.vocab, c.C), 0.0, 0.02, 41, "cpu").numpy().view(np.uint8).copy()
+            h = R.ref_qmatrix_new(ops.FMT_F16, c.vocab, c.C, P(table))
+            del table
+            ids = wl.uniform_ids(c.T, c.vocab, 43)
+            wpe = _f32((c.n_ctx, c.C), 0.0, 0.02, 42)[:c.T].copy()
+            x = np.empty((c.T, c.C), np.float32)
+            return (lambda: R.ref_qmatrix_gather(h, P(ids), c.T, P(wpe), P(x))), (lambda: R.ref_qmatrix_free(h))
+
+        def layernorm():
+            x = _f32((c.T, c.C), 0.0, 1.0, 46)
+            g, b = wl.weight_f32(c.C, 1.0, 0.02, 44, "cpu").numpy(), wl.weight_f32(c.C, 0.0, 0.02, 45, "cpu").numpy()
+            y = np.empty_like(x)
+            return (lambda: R.ref_layernorm(P(x), P(y), P(g), P(b), c.T, c.C, c.eps)), None
+
+        def gelu():
+            x = _f32((c.T, c.F), 0.0, 1.0, 46)
+            y = np.empty_like(x)
+            return (lambda: R.ref_gelu_n(P(x), P(y), x.size)), None
+
+        leg.add("gpt2_small_chain", "gather_wte_wpe", gather, 1, every("all 128 tokens: dequantizeRow + wpe add"))
+        leg.add("gpt2_small_chain", "layernorm", layernorm, 1, every("all 128 rows"))
+        leg.add("gpt2_small_chain", "gelu", gelu, 1, every("all 128 x 3072 values"))
+
+    def rms_job(T, C, eps, stream):
+        def make():
+            x = _f32((T, C), 0.0, 1.0, stream)
+            w = wl.weight_f32(C, 1.0, 0.05, stream + 1, "cpu").numpy()
+            y = np.empty_like(x)
+            return (lambda: R.ref_rmsnorm(P(x), P(y), P(w), T, C, eps)), None
+        return make
+
+    def swiglu_job(T, I, stream):
+        def make():
+            h = _f32((T, 2 * I), 0.0, 1.0, stream)
+            o = np.empty((T, I), np.float32)
+            return (lambda: R.ref_silu_mul(P(h), P(o), T, I)), None
+        return make
+
+    def qk_state(T, n_q, n_kv, hd, theta, n_pos, pos, stream):
+        stride = (n_q + 2 * n_kv) * hd
+        qkv = _f32((T, stride), 0.0, 1.0, stream)
+        wqk = wl.weight_f32(2 * hd, 1.0, 0.05, stream + 1, "cpu").numpy()
+        wq, wk = wqk[:hd].copy(), wqk[hd:].copy()
+        cs = O.rope_table(theta, hd, n_pos)
+        return stride, qkv, wq, wk, cs, np.ascontiguousarray(pos, dtype=np.int32)
+
+    def qk_job(T, n_q, n_kv, hd, theta, n_pos, pos, eps, stream):
+        def make():
+            stride, qkv, wq, wk, cs, p = qk_state(T, n_q, n_kv, hd, theta, n_pos, pos, stream)
+            return (lambda: R.ref_qk_norm_rope(P(qkv), stride, T, n_q, n_kv, hd, P(p), P(wq), P(wk), P(cs), eps)), None
+        return make
+
+    def decode_jobs():  # qwen3_0.6b_decode
+        c = wl.QWEN3_DECODE
+        pos = wl.uniform_ids(c.T, c.n_pos, 7)
+        full = every("all 64 rows")
+        leg.add("qwen3_0.6b_decode", "rmsnorm", rms_job(c.T, c.C, c.eps, 1), 1, full)
+        leg.add("qwen3_0.6b_decode", "qk_norm_rope", qk_job(c.T, c.n_q, c.n_kv, c.hd, c.theta, c.n_pos, pos, c.eps, 4),
+                1, every("all 64 rows: per-token q/k rmsNorm + rope"))
+        leg.add("qwen3_0.6b_decode", "swiglu", swiglu_job(c.T, c.I, 6), 1, full)
+
+    def prefill_jobs():  # qwen3_4b_prefill
+        c, n = wl.QWEN3_PREFILL, 256
+        s = rows_of(n, c.T)
+        pos = np.arange(n) % c.seq
+        leg.add("qwen3_4b_prefill", "rmsnorm_in", rms_job(n, c.C, c.eps, 1), c.T / n, s)
+        leg.add("qwen3_4b_prefill", "qk_norm_rope", qk_job(n, c.n_q, c.n_kv, c.hd, c.theta, c.seq, pos, c.eps, 4),
+                c.T / n, s)
+        leg.add("qwen3_4b_prefill", "rmsnorm_post", rms_job(n, c.C, c.eps, 1), c.T / n, s)
+        leg.add("qwen3_4b_prefill", "swiglu", swiglu_job(n, c.I, 6), c.T / n, s)
+
+    def gather_jobs():  # quant_gather_qwen3_1.7b
+        c, n = wl.QUANT_GATHER, 2048
+        ids = wl.zipf_ids(c.T, c.vocab, c.s, 32)[:n].copy()
+        held = {}
+
+        def gather(fmt):
+            def make():
+                if "src" not in held:
+                    held["src"] = _f32((c.vocab, c.C), 0.0, 0.02, 31)
+                tab, used = ops.quantize_rows(fmt, held["src"])
+                h = R.ref_qmatrix_new(used, c.vocab, c.C, P(tab))
+                del tab
+                x = np.empty((n, c.C), np.float32)
+                if fmt == ops.FMT_FP4:
+                    held.clear()
+                return (lambda: R.ref_qmatrix_gather(h, P(ids), n, None, P(x))), (lambda: R.ref_qmatrix_free(h))
+            return make
+
+        s = f"first {n} of the {c.T} Zipf ids (median of {leg.reps}), scaled to all {c.T}; {core}"
+        for fmt, name in ((ops.FMT_F16, "gather_fp16"), (ops.FMT_FP8, "gather_fp8"), (ops.FMT_FP4, "gather_fp4")):
+            leg.add("quant_gather_qwen3_1.7b", name, gather(fmt), c.T / n, s)
+
+    def fused_jobs():  # qwen3_4b_fused
+        c, n = wl.QWEN3_PREFILL, 256
+        s = rows_of(n, c.T)
+        pos = np.arange(n)
+        kw = c.n_kv * c.hd
+        koff, voff = c.n_q * c.hd, (c.n_q + c.n_kv) * c.hd
+
+        def add_rms():
+            x = _f32((n, c.C), 0.0, 1.0, 71)
+            d = _f32((n, c.C), 0.0, 0.5, 72)
+            w = wl.weight_f32(c.C, 1.0, 0.05, 73, "cpu").numpy()
+            xn = np.empty_like(x)
+            return (lambda: O.lib().oracle_add_rmsnorm(P(x), P(d), P(xn), P(w), n, c.C, c.eps)), None
+
+        def qk_kv(with_rope, with_store):
+            def make():
+                stride, qkv, wq, wk, cs, p = qk_state(n, c.n_q, c.n_kv, c.hd, 1e6, n, pos, 74)
+                kc = np.empty((n, kw), np.uint16)
+                vc = np.empty_like(kc)
+
+                def once():
+                    if with_rope:
+                        R.ref_qk_norm_rope(P(qkv), stride, n, c.n_q, c.n_kv, c.hd, P(p), P(wq), P(wk), P(cs), c.eps)
+                    if with_store:
+                        R.ref_store_kv(P(qkv[:, koff:]), P(qkv[:, voff:]), stride, P(kc), P(vc), kw, n, 0)
+                return once, None
+            return make
+
+        leg.add("qwen3_4b_fused", "add_rmsnorm", add_rms, c.T / n,
+                rows_of(n, c.T) + "; the reference adds the residual in its output GEMM's epilogue, so the "
+                "oracle's restatement of add + rmsNorm is timed", port=True)
+        leg.add("qwen3_4b_fused", "qk_norm_rope_kv", qk_kv(True, True), c.T / n, s + ": q/k loop, then storeKv")
+        leg.add("qwen3_4b_fused", "qk_norm_rope", qk_kv(True, False), c.T / n, s)
+        leg.add("qwen3_4b_fused", "store_kv", qk_kv(False, True), c.T / n, s + ": storeKv")
+
+    def quantize_jobs():  # quantize_qwen3_1.7b_table
+        c, n = wl.QUANT_GATHER, 512
+
+        def quant(fmt):
+            def make():
+                src = _f32((n, c.C), 0.0, 0.02, 31)
+                dst = np.empty((n, O.quant_row_bytes(fmt, c.C)), np.uint8)
+                return (lambda: R.ref_quantize_rows(fmt, n, c.C, P(src), P(dst))), None
+            return make
+
+        s = (f"{n} of {c.vocab} rows (median of {leg.reps}), scaled to all {c.vocab}; quantizeMatrix with no "
+             f"thread pool; {core}")
+        for fmt, name in ((ops.FMT_F16, "quantize_fp16"), (ops.FMT_FP8, "quantize_fp8"), (ops.FMT_FP4, "quantize_fp4")):
+            leg.add("quantize_qwen3_1.7b_table", name, quant(fmt), c.vocab / n, s)
+
+    def granite_jobs():  # granite_4.0h_norms
+        c, n = wl.GRANITE_NORMS, 512
+        s = rows_of(n, c.T)
+
+        def gated():
+            y = _f32((n, c.D), 0.0, 1.0, 53)
+            z = _f32((n, c.D), 0.0, 1.0, 54)
+            w = wl.weight_f32(c.D, 1.0, 0.05, 55, "cpu").numpy()
+            return (lambda: R.ref_gated_rmsnorm(P(y), P(z), P(w), n, c.D, c.groups, c.eps)), None
+
+        leg.add("granite_4.0h_norms", "rmsnorm", rms_job(n, c.C, c.eps, 51), c.T / n, s)
+        leg.add("granite_4.0h_norms", "gated_rmsnorm", gated, c.T / n, s + ": y *= silu(z), then rmsNorm per group")
+        leg.add("granite_4.0h_norms", "swiglu", swiglu_job(n, c.I, 56), c.T / n, s)
+
+    # Each workload in its own scope: the closures above read their configuration when they run.
+    for label, jobs in (
+            ("gpt2_small_chain", gpt2_jobs),
+            ("qwen3_0.6b_decode", decode_jobs),
+            ("qwen3_4b_prefill", prefill_jobs),
+            ("quant_gather_qwen3_1.7b", gather_jobs),
+            ("qwen3_4b_fused", fused_jobs),
+            ("quantize_qwen3_1.7b_table", quantize_jobs),
+            ("granite_4.0h_norms", granite_jobs),
+    ):
+        if want(label):
+            jobs()
 
 
 def all_configs(args):
@@ -329,50 +585,56 @@ def all_configs(args):
         }, {"rmsnorm": wl.bytes_rmsnorm(c5.T, c5.C), "gated_rmsnorm": wl.bytes_gated(c5.T, c5.D),
             "swiglu": wl.bytes_swiglu(c5.T, c5.I)},
             "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096")
+
+    if not args.no_cpu:
+        del flush
+        torch.cuda.synchronize()
+        leg = CpuLeg()
+        add_cpu_jobs(leg, want)
+        leg.run(out)
     return out
 
 
 def cpu_baseline(cfg, rows=256, reps=5):
-    """The reference CPU ops on one core over `rows` tokens of the same workload, scaled to GB/s."""
-    import ctypes
-
+    """The reference's CPU path for the layer's four ops (its compiled cpu::rmsNorm, the Qwen3 q/k loop
+    of rmsNorm + rope, cpu::siluMul on f32 activations, as its CPU forward pass holds them) on one
+    pinned core over `rows` tokens of the same workload, scaled to the full layer; the oracle's f32
+    restatement when oracle/_ref is not built."""
     import numpy as np
 
     from nekochat_amd import workloads as wl
     from oracle import oracle as O
 
-    try:
-        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
-    except (AttributeError, OSError):
-        pass
-    x = wl.normal_f16((rows, cfg.C), 0.0, 1.0, 1, "cpu").numpy().view(np.uint16)
+    x = _f32((rows, cfg.C), 0.0, 1.0, 1)
     w = wl.weight_f32(cfg.C, 1.0, 0.05, 2, "cpu").numpy()
-    qkv = wl.normal_f16((rows, cfg.qkv_stride), 0.0, 1.0, 4, "cpu").numpy().view(np.uint16).copy()
+    qkv = _f32((rows, cfg.qkv_stride), 0.0, 1.0, 4)
     wqk = wl.weight_f32(2 * cfg.hd, 1.0, 0.05, 5, "cpu").numpy()
+    wq, wk = wqk[:cfg.hd].copy(), wqk[cfg.hd:].copy()
     pos = (np.arange(rows) % cfg.seq).astype(np.int32)
     cs = O.rope_table(cfg.theta, cfg.hd, cfg.seq)
-    h = wl.normal_f16((rows, 2 * cfg.I), 0.0, 1.0, 6, "cpu").numpy().view(np.uint16)
+    h = _f32((rows, 2 * cfg.I), 0.0, 1.0, 6)
     y = np.empty_like(x)
-    g = np.empty((rows, cfg.I), np.uint16)
+    g = np.empty((rows, cfg.I), np.float32)
     P = O._ptr
     if O.ref_available():
         R = O.ref()
         kind = "reference"
         run = {
-            "rmsnorm": lambda: R.ref_rmsnorm_f16(P(x), P(y), P(w), rows, cfg.C, ctypes.c_float(cfg.eps)),
-            "qk_norm_rope": lambda: R.ref_qk_norm_rope_f16(P(qkv), cfg.qkv_stride, rows, cfg.n_q, cfg.n_kv, cfg.hd,
-                                                           P(pos), P(wqk[:cfg.hd].copy()), P(wqk[cfg.hd:].copy()),
-                                                           P(cs), ctypes.c_float(cfg.eps)),
-            "swiglu": lambda: R.ref_silu_mul_f16(P(h), P(g), rows, cfg.I),
+            "rmsnorm": lambda: R.ref_rmsnorm(P(x), P(y), P(w), rows, cfg.C, cfg.eps),
+            "qk_norm_rope": lambda: R.ref_qk_norm_rope(P(qkv), cfg.qkv_stride, rows, cfg.n_q, cfg.n_kv, cfg.hd,
+                                                       P(pos), P(wq), P(wk), P(cs), cfg.eps),
+            "swiglu": lambda: R.ref_silu_mul(P(h), P(g), rows, cfg.I),
         }
     else:
         kind = "port"
+        L = O.lib()
         run = {
-            "rmsnorm": lambda: O.lib().oracle_rmsnorm_f16(P(x), cfg.C, P(y), cfg.C, P(w), rows, cfg.C, cfg.eps),
-            "qk_norm_rope": lambda: O.lib().oracle_qk_norm_rope_f16(P(qkv), cfg.qkv_stride, rows, cfg.n_q, cfg.n_kv,
-                                                                    cfg.hd, 0, P(pos), P(wqk), P(cs), cfg.seq, cfg.eps),
-            "swiglu": lambda: O.lib().oracle_swiglu_f16(P(h), 2 * cfg.I, P(g), cfg.I, rows, cfg.I),
+            "rmsnorm": lambda: L.oracle_rmsnorm(P(x), P(y), P(w), rows, cfg.C, cfg.eps),
+            "qk_norm_rope": lambda: L.oracle_qk_norm_rope_f32(P(qkv), cfg.qkv_stride, rows, cfg.n_q, cfg.n_kv,
+                                                              cfg.hd, 0, P(pos), P(wqk), P(cs), cfg.seq, cfg.eps),
+            "swiglu": lambda: L.oracle_silu_mul(P(h), P(g), rows, cfg.I),
         }
+    mask = _pin_one_core()
     t = {}
     for name, fn in run.items():
         fn()
@@ -382,6 +644,7 @@ def cpu_baseline(cfg, rows=256, reps=5):
             fn()
             samples.append(time.perf_counter() - t0)
         t[name] = statistics.median(samples) * cfg.T / rows  # seconds for the full 8192 rows
+    _unpin(mask)
     layer_s = 2 * t["rmsnorm"] + t["qk_norm_rope"] + t["swiglu"]
     total_bytes = sum(cfg.op_bytes().values())
     return {
@@ -389,7 +652,7 @@ def cpu_baseline(cfg, rows=256, reps=5):
         "us_per_layer": round(layer_s * 1e6, 1),
         "per_op_us": {k: round(v * 1e6, 1) for k, v in t.items()},
         "sample": f"{rows} of {cfg.T} tokens per op (median of {reps}), scaled to the full layer; "
-                  f"1 pinned core of {os.cpu_count()}; g++ -O3 portable x86-64 build",
+                  f"1 pinned core of {os.cpu_count()}; g++ -O3 portable x86-64 build; f32 activations",
     }
 
 

@@ -118,6 +118,12 @@ _REF_SIGS = {
     "ref_embed": (None, [_p, _i32, _p, _i32, _i32, _i32, _p, _i32, _p, _i32]),
     "ref_store_kv": (None, [_p, _p, _i32, _p, _p, _i32, _i32, _i32]),
     "ref_add_rmsnorm_f16": (None, [_p, _p, _p, _p, _p, _i32, _i32, _f32]),
+    "ref_gelu_n": (None, [_p, _p, _i64]),
+    "ref_qk_norm_rope": (None, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32]),
+    "ref_gated_rmsnorm": (None, [_p, _p, _p, _i32, _i32, _i32, _f32]),
+    "ref_qmatrix_new": (_p, [_i32, _i32, _i32, _p]),
+    "ref_qmatrix_gather": (None, [_p, _p, _i32, _p, _p]),
+    "ref_qmatrix_free": (None, [_p]),
 }
 
 _oracle = None

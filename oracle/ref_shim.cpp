@@ -158,6 +158,64 @@ void ref_add_rmsnorm_f16(const uint16_t* x, const uint16_t* d, uint16_t* x_out, 
     narrow(y.data(), xn, y.size());
 }
 
+// ---- f32 activations, as the reference's CPU forward passes hold them (its CPU path, timed beside
+// the device kernels; same compiled ops, no f16 widening or narrowing).
+
+// GELU over n values: what the matmul epilogue applies per output under kGelu (cpu_ops.cpp:121,143).
+void ref_gelu_n(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = cpu::gelu(x[i]);
+}
+
+// The Qwen3 per-token q/k norm + RoPE loop on f32 rows of `stride` floats (qwen3_model.cpp:249-253).
+void ref_qk_norm_rope(float* qkv, int stride, int rows, int H, int KV, int hd, const int32_t* positions,
+                      const float* qNorm, const float* kNorm, const float* cs, float eps) {
+    const int kOff = H * hd;
+    for (int t = 0; t < rows; t++) {
+        float* r = qkv + size_t(t) * size_t(stride);
+        cpu::rmsNorm(r, r, qNorm, H, hd, eps);
+        cpu::rmsNorm(r + kOff, r + kOff, kNorm, KV, hd, eps);
+        cpu::rope(r, H + KV, hd, cs + size_t(positions[t]) * size_t(hd));
+    }
+}
+
+// The Granite gate + group norm in place on f32 rows (granite_model.cpp:21,278-285).
+void ref_gated_rmsnorm(float* y, const float* z, const float* w, int rows, int D, int groups, float eps) {
+    const int GS = D / groups;
+    for (int t = 0; t < rows; t++) {
+        float* yr = y + size_t(t) * size_t(D);
+        const float* zr = z + size_t(t) * size_t(D);
+        for (int i = 0; i < D; i++) yr[i] *= zr[i] / (1.0f + std::exp(-zr[i]));
+        for (int g = 0; g < groups; g++)
+            cpu::rmsNorm(yr + size_t(g) * size_t(GS), yr + size_t(g) * size_t(GS), w + size_t(g) * size_t(GS), 1, GS, eps);
+    }
+}
+
+// A weight table held as the reference's QMatrix, so a gather can be timed without copying the table
+// per call: the embedding loop dequantizeRow(tokens[t]) into f32 rows (qwen3_model.cpp:236), plus,
+// when wpe (T f32 position rows) is given, GPT-2's position add (gpt2_model.cpp:182-187).
+void* ref_qmatrix_new(int fmt, int rows, int C, const uint8_t* table) {
+    QMatrix* m = new QMatrix();
+    m->format = WeightFormat(fmt);
+    m->rows = rows;
+    m->cols = C;
+    m->rowBytes = quantRowBytes(m->format, C);
+    m->data.assign(table, table + m->rowBytes * size_t(rows));
+    return m;
+}
+void ref_qmatrix_gather(const void* h, const int32_t* tokens, int T, const float* wpe, float* out) {
+    const QMatrix* m = static_cast<const QMatrix*>(h);
+    const int C = m->cols;
+    for (int t = 0; t < T; t++) {
+        float* xr = out + size_t(t) * size_t(C);
+        m->dequantizeRow(tokens[t], xr);
+        if (wpe) {
+            const float* pe = wpe + size_t(t) * size_t(C);
+            for (int c = 0; c < C; c++) xr[c] += pe[c];
+        }
+    }
+}
+void ref_qmatrix_free(void* h) { delete static_cast<QMatrix*>(h); }
+
 // Embedding gather: dequantizeRow of each token's row, + the f32 position row (gpt2_model.cpp:182-187),
 // rounded to f16 when out_f16.
 void ref_embed(const int32_t* tokens, int T, const uint8_t* table, int fmt, int rows, int C, const uint16_t* wpe,

@@ -166,6 +166,58 @@ def test_ref_ops_bitexact(seed):
 
 
 @needs_ref
+def test_ref_f32_entry_points_match_oracle():
+    """The f32-activation forms the CPU baseline times compute what the oracle's f32 functions do."""
+    R = O.ref()
+    L = O.lib()
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(5000) * 6).astype(np.float32)
+    a, b = np.empty_like(x), np.empty_like(x)
+    R.ref_gelu_n(P(x), P(a), x.size)
+    b[:] = [L.oracle_gelu(v) for v in x]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    H, KV, hd, T = 4, 2, 64, 9
+    stride = (H + 2 * KV) * hd
+    qkv = rng.standard_normal((T, stride)).astype(np.float32)
+    cs = O.rope_table(1e4, hd, 100)
+    pos = rng.integers(0, 100, T).astype(np.int32)
+    wqk = rng.standard_normal(2 * hd).astype(np.float32)
+    r, o = qkv.copy(), qkv.copy()
+    R.ref_qk_norm_rope(P(r), stride, T, H, KV, hd, P(pos), P(wqk[:hd].copy()), P(wqk[hd:].copy()), P(cs),
+                       ctypes.c_float(1e-6))
+    L.oracle_qk_norm_rope_f32(P(o), stride, T, H, KV, hd, 0, P(pos), P(wqk), P(cs), 100, 1e-6)
+    assert np.array_equal(r.view(np.uint32), o.view(np.uint32))
+    assert not np.array_equal(r, qkv)
+    y = rng.standard_normal((4, 640)).astype(np.float32)
+    z = (rng.standard_normal((4, 640)) * 3).astype(np.float32)
+    wg = rng.standard_normal(640).astype(np.float32)
+    for groups in (1, 5):
+        r, o = y.copy(), y.copy()
+        R.ref_gated_rmsnorm(P(r), P(z), P(wg), 4, 640, groups, ctypes.c_float(1e-5))
+        L.oracle_gated_rmsnorm(P(o), P(z), 640, P(wg), 4, 640, groups, 1e-5)
+        assert np.array_equal(r.view(np.uint32), o.view(np.uint32))
+    cols, rows = 256, 50
+    src = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    ids = rng.integers(0, rows, 17).astype(np.int32)
+    wpe = rng.standard_normal((17, cols)).astype(np.float32)
+    for fmt in (0, 1, 2):
+        tab = O.quantize_rows(fmt, src)
+        h = R.ref_qmatrix_new(fmt, rows, cols, P(tab))
+        try:
+            for pe in (None, wpe):
+                got = np.empty((17, cols), np.float32)
+                R.ref_qmatrix_gather(h, P(ids), 17, P(pe), P(got))
+                want = np.empty_like(got)
+                for t, i in enumerate(ids):
+                    L.oracle_dequantize_row(fmt, cols, P(tab[i]), P(want[t]))
+                if pe is not None:
+                    want += pe
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        finally:
+            R.ref_qmatrix_free(h)
+
+
+@needs_ref
 @pytest.mark.parametrize("fmt", [0, 1, 2])
 @pytest.mark.parametrize("cols,scale", [(256, 0.02), (1024, 1.0), (96, 1e-4), (100, 0.02), (64, 3e4)])
 def test_ref_quantizer_bitexact(fmt, cols, scale):
