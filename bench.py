@@ -48,7 +48,8 @@ def parse():
                    help="time every configured workload's ops (one JSON line with all of them) instead")
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
-                        "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms)")
+                        "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
+                        "qwen3_4b_decode_matmul)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -413,6 +414,25 @@ def add_cpu_jobs(leg, want):
         leg.add("granite_4.0h_norms", "gated_rmsnorm", gated, c.T / n, s + ": y *= silu(z), then rmsNorm per group")
         leg.add("granite_4.0h_norms", "swiglu", swiglu_job(n, c.I, 56), c.T / n, s)
 
+    def matmul_jobs():  # qwen3_4b_decode_matmul
+        c, n = wl.QWEN3_DECODE_MATMUL, 256
+
+        def mm(fmt, N, K):
+            def make():
+                src = _f32((n, K), 0.0, 0.02, 81)
+                tab, used = ops.quantize_rows(fmt, src)
+                h = R.ref_qmatrix_new(used, n, K, P(tab))
+                x = _f32((c.T, K), 0.0, 1.0, 82)
+                y = np.zeros((c.T, n), np.float32)
+                return (lambda: R.ref_qmatrix_matmul(h, P(x), c.T, None, P(y), 0)), (lambda: R.ref_qmatrix_free(h))
+            return make
+
+        for pname, N, K in c.projections:
+            for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
+                leg.add("qwen3_4b_decode_matmul", f"{pname}_{fname}", mm(fmt, N, K), N / n,
+                        f"{n} of {N} weight rows through cpu::matmul on a one-thread pool (median of {leg.reps}), "
+                        f"scaled to all {N}; {core}")
+
     # Each workload in its own scope: the closures above read their configuration when they run.
     for label, jobs in (
             ("gpt2_small_chain", gpt2_jobs),
@@ -422,6 +442,7 @@ def add_cpu_jobs(leg, want):
             ("qwen3_4b_fused", fused_jobs),
             ("quantize_qwen3_1.7b_table", quantize_jobs),
             ("granite_4.0h_norms", granite_jobs),
+            ("qwen3_4b_decode_matmul", matmul_jobs),
     ):
         if want(label):
             jobs()
@@ -440,7 +461,7 @@ def all_configs(args):
     out = {}
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
-              "quantize_qwen3_1.7b_table", "granite_4.0h_norms")
+              "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -585,6 +606,27 @@ def all_configs(args):
         }, {"rmsnorm": wl.bytes_rmsnorm(c5.T, c5.C), "gated_rmsnorm": wl.bytes_gated(c5.T, c5.D),
             "swiglu": wl.bytes_swiglu(c5.T, c5.I)},
             "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096")
+
+    # Qwen3-4B decode step (T = 1): the four weight matmuls in each weight format, f16 activations,
+    # f32 outputs; bytes = the weight rows once + activations + outputs.
+    if want("qwen3_4b_decode_matmul"):
+        c8 = wl.QWEN3_DECODE_MATMUL
+        calls8, bytes8 = {}, {}
+        for pname, N, K in c8.projections:
+            wsrc = wl.normal_f16((N, K), 0.0, 0.02, 81, dev).float()
+            x8 = wl.normal_f16((c8.T, K), 0.0, 1.0, 82, dev)
+            y8 = torch.empty((c8.T, N), dtype=torch.float32, device=dev)
+            for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
+                tab8, _ = ops.quantize(wsrc, fmt)
+                name = f"{pname}_{fname}"
+                calls8[name] = ops.prepare(ops.matmul, x8, tab8, fmt, K, out=y8)[0]
+                calls8[name].table = tab8
+                bytes8[name] = wl.bytes_matmul(c8.T, K, N, tab8.shape[1])
+            del wsrc
+        run("qwen3_4b_decode_matmul", calls8, bytes8,
+            "Qwen3-4B decode step, T=1: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
+            "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs")
+        del calls8
 
     if not args.no_cpu:
         del flush

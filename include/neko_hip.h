@@ -176,6 +176,28 @@ int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const vo
 int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t cols, const void* src, int64_t src_stride,
                            int src_dtype, uint8_t* dst, int* fmt_used);
 
+/* ---------------------------------------------------------------- weight matmul */
+
+/* y[t][n] (+)= act(x[t] . W[n] + bias[n]) for t < T, n < N: the reference's weight matmul,
+ * cpu::matmul (cpu_ops.cpp:474-490, with matmulF16 :108-127 and matmulGeneric :455-472) and its GPU
+ * kernels Matmul / MatmulQ8 / MatmulQ4 (gpu/compute.h:17; matmul.comp, matmul_q8.comp,
+ * matmul_q4.comp), whose flags this keeps: NEKO_MM_GELU applies the GELU tanh form to the biased
+ * sum, NEKO_MM_ACCUMULATE adds the result into y (dst = dst + v) instead of storing it.
+ *   x      T rows of K activations (x_stride elements apart) of x_dtype.
+ *   w      N weight rows of row_bytes bytes in format fmt (quant.h:30-36 layout, as written by
+ *          neko_quantize_rows / neko_hip_quantize_rows); FP8/FP4 need K % 32 == 0.
+ *   bias   f32 [N] or NULL.
+ *   y      T rows of y_stride elements of y_dtype; may not overlap x or w. Column offsets (the
+ *          shaders' nOffset) are a pointer offset into y.
+ * The dot products are summed in f32 (f16 activations and weight codes exactly, each 32-block scaled
+ * by its f16 scale) in a different order from the reference's sequential loop: results agree to f32
+ * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows. */
+#define NEKO_MM_GELU 1
+#define NEKO_MM_ACCUMULATE 2
+int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
+                    int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags,
+                    int x_dtype, int y_dtype);
+
 /* ---------------------------------------------------------------- host-side codecs */
 
 /* Bytes per stored row (quant.cpp:199-208): F16 2*cols; FP8 / FP4 the codes (cols or cols/2

@@ -16,31 +16,7 @@ namespace {
 // SwiGLU element: silu(gate) * up in float (silu_fast, device.h).
 __device__ __forceinline__ float swiglu_ref(float gate, float up) { return silu_fast(gate) * up; }
 
-// tanh with the structure of fdlibm's s_tanhf.c (the C library the reference calls through
-// std::tanh): expm1-based branches around |x| = 1, saturation at |x| >= 22, identity below 2^-55.
-__device__ __forceinline__ float tanh_ref(float x) {
-    const float ax = fabsf(x);
-    float z;
-    if (!(ax < 22.0f)) {
-        if (ax != ax) return x + x;
-        z = 1.0f;
-    } else if (ax < 0x1p-55f) {
-        return x;
-    } else if (ax >= 1.0f) {
-        const float t = expm1f(2.0f * ax);
-        z = 1.0f - 2.0f / (t + 2.0f);
-    } else {
-        const float t = expm1f(-2.0f * ax);
-        z = -t / (t + 2.0f);
-    }
-    return x < 0.0f ? -z : z;
-}
-
-// GPT-2 gelu_new, left to right in float.
-__device__ __forceinline__ float gelu_ref(float x) {
-    const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.0f + tanh_ref(inner));
-}
+// GELU: gelu_ref (device.h).
 
 template <typename VT, typename T, int N>
 __device__ __forceinline__ T lane_elem(const VT& v, int e) {

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
+
 // The reference rounds every float product and sum separately (its portable path has no FMA), so
 // kernels must not contract a*b+c into fma. The build passes -ffp-contract=off as well.
 #pragma clang fp contract(off)
@@ -103,6 +105,43 @@ __device__ __forceinline__ float rsqrt_to_float(double d) {
 __device__ __forceinline__ float silu_lite(float g) {
     const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
     return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// Two weight codes, one in the low byte of each 16-bit half of p, -> the f16 bit patterns whose
+// values are the codes' values / 2^8 (FP8 E4M3: (c & 0x7F) << 7 with the sign moved to bit 15) or
+// / 2^14 (FP4 E2M1: (c & 7) << 9, sign to bit 15; the high nibble of each byte is ignored). Exact:
+// every E4M3 and E2M1 value, scaled so, is an f16 normal or subnormal.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t fp8_pair_bits(uint32_t p) { return (p + (p & 0x00800080u)) << 7; }
+__device__ __forceinline__ uint32_t fp4_pair_bits(uint32_t p) {
+    const uint32_t m = p & 0x000F000Fu;
+    return (m + 7u * (m & 0x00080008u)) << 9;  // sign bit 3 -> bit 6 before the shift -> bit 15
+}
+
+// tanh with the structure of fdlibm's s_tanhf.c (the C library the reference calls through
+// std::tanh): expm1-based branches around |x| = 1, saturation at |x| >= 22, identity below 2^-55.
+__device__ __forceinline__ float tanh_ref(float x) {
+    const float ax = fabsf(x);
+    float z;
+    if (!(ax < 22.0f)) {
+        if (ax != ax) return x + x;
+        z = 1.0f;
+    } else if (ax < 0x1p-55f) {
+        return x;
+    } else if (ax >= 1.0f) {
+        const float t = expm1f(2.0f * ax);
+        z = 1.0f - 2.0f / (t + 2.0f);
+    } else {
+        const float t = expm1f(-2.0f * ax);
+        z = -t / (t + 2.0f);
+    }
+    return x < 0.0f ? -z : z;
+}
+
+// GPT-2 gelu_new (cpu_ops.cpp:20-23), left to right in float.
+__device__ __forceinline__ float gelu_ref(float x) {
+    const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanh_ref(inner));
 }
 
 template <typename T>

@@ -50,12 +50,7 @@ __device__ __forceinline__ float fp4_code(uint32_t n) { return half_bits_to_f32(
 // product of two f16 values is exact in f32, so the single RNE rounding of the f16 multiply equals
 // the reference's f32 product rounded to f16 (f16 subnormals are kept, as the hardware does by
 // default for f16).
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t fp8_pair_bits(uint32_t p) { return (p + (p & 0x00800080u)) << 7; }
-__device__ __forceinline__ uint32_t fp4_pair_bits(uint32_t p) {
-    const uint32_t m = p & 0x000F000Fu;
-    return (m + 7u * (m & 0x00080008u)) << 9;  // sign bit 3 -> bit 6 before the shift -> bit 15
-}
+// (fp8_pair_bits / fp4_pair_bits, device.h)
 
 // 32-bit word w of a loaded chunk (a scalar when the chunk is one word).
 template <typename R>

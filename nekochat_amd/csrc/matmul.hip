@@ -1,0 +1,507 @@
+// Weight matmul for gfx950: y[t][n] (+)= act(x[t] . W[n] + bias[n]) with W stored in the reference's
+// weight row formats -- F16, FP8 (E4M3 codes + f16 block scales) and FP4 (E2M1 nibbles + f16 block
+// scales), quant.h:30-36. The reference's Matmul / MatmulQ8 / MatmulQ4 kernels (matmul.comp,
+// matmul_q8.comp, matmul_q4.comp) and cpu::matmul (cpu_ops.cpp:474-490).
+//
+// Fast path (f16 activations, K % 32 == 0): one wave owns a tile of 16 weight rows and up to 64
+// tokens and walks a slice of K in 32-wide blocks -- exactly one FP8/FP4 scale block -- with
+// v_mfma_f32_16x16x32_f16. The weight codes enter the MFMA as the exact f16 values code/2^8 (FP8) or
+// code/2^14 (FP4), the activations as they are, so every product is exact and summed in f32; the
+// block's f32 sum is then multiplied by its f16 scale (times 2^8 or 2^14, exact) and accumulated
+// with one fma. F16 rows feed the MFMA directly. The workgroup's waves split K and add their
+// partial tiles in LDS in a fixed order, then apply bias, GELU and the accumulate epilogue. Rows
+// are read once per 64 tokens, so for decode-sized T the kernel is a stream of the weight bytes.
+//
+// Generic path (f32 activations, unaligned or odd shapes): one wave per weight row and 4 tokens,
+// lanes striding K, each weight decoded exactly to f32 and multiplied and added in f32.
+//
+// Summation order differs from the reference's sequential dot (and the reference's own GPU shaders
+// differ from its CPU loop), so results agree to f32 rounding of the sum, not bit for bit.
+#include <algorithm>
+
+#include "internal.h"
+
+namespace neko_hip {
+namespace {
+
+constexpr int kBlockK = 32;  // quant.h kQuantBlock
+
+struct MmArgs {
+    const void* x;
+    int64_t xs;
+    int64_t T;
+    const uint8_t* w;
+    int64_t rb;
+    int K;
+    int N;
+    const float* bias;
+    void* y;
+    int64_t ys;
+    int flags;
+    int fmt;
+    int blocks_per_wave;  // 32-wide blocks of K per wave, a multiple of kGroup (fast path)
+};
+
+constexpr int kGelu = 1, kAccumulate = 2;  // cpu_ops.h MatmulFlags
+
+template <typename TY>
+__device__ __forceinline__ void epilogue(const MmArgs& a, int64_t t, int64_t n, float v) {
+    if (a.bias) v += a.bias[n];
+    if (a.flags & kGelu) v = gelu_ref(v);
+    TY* yp = static_cast<TY*>(a.y) + t * a.ys + n;
+    if (a.flags & kAccumulate) v += to_f32(*yp);
+    *yp = from_f32<TY>(v);
+}
+
+// ---------------------------------------------------------------- fast path: MFMA tiles
+
+// The B operand of one 32-wide block for weight row `row`: the 8 k values lane group g supplies.
+// FP8: codes g*8 .. g*8+7 of the block (8 bytes). FP4: bytes g*4 .. g*4+3 of the 16-byte block, low
+// nibbles (k = g*4 + i) then high nibbles (k = 16 + g*4 + i). F16: halves g*8 .. g*8+7. Loaded raw
+// (so a group can be fetched ahead) and decoded to exact f16 values just before its MFMA.
+#ifndef NEKO_TUNE_MM_FP4_CVT
+#define NEKO_TUNE_MM_FP4_CVT 1
+#endif
+constexpr bool kFp4Cvt = NEKO_TUNE_MM_FP4_CVT;
+
+template <int FMT>
+struct BRaw {
+    typedef half8 T;
+};
+template <>
+struct BRaw<1> {
+    typedef uint2v T;
+};
+template <>
+struct BRaw<2> {
+    typedef uint32_t T;
+};
+
+template <int FMT>
+__device__ __forceinline__ typename BRaw<FMT>::T load_b_raw(const uint8_t* row, int b, int g) {
+    if constexpr (FMT == 0) return *reinterpret_cast<const half8*>(row + 2 * (b * kBlockK + g * 8));
+    else if constexpr (FMT == 1) return *reinterpret_cast<const uint2v*>(row + b * kBlockK + g * 8);
+    else return *reinterpret_cast<const uint32_t*>(row + b * (kBlockK / 2) + g * 4);
+}
+
+template <int FMT>
+__device__ __forceinline__ half8 decode_b(typename BRaw<FMT>::T q) {
+    if constexpr (FMT == 0) {
+        return q;
+    } else if constexpr (FMT == 1) {
+        uint4v h;
+        h[0] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q[0], 0x0C010C00u));
+        h[1] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q[0], 0x0C030C02u));
+        h[2] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q[1], 0x0C010C00u));
+        h[3] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q[1], 0x0C030C02u));
+        return __builtin_bit_cast(half8, h);
+    } else if constexpr (kFp4Cvt) {
+        // gfx950's E2M1 -> f16 conversion (scale 1: the code values themselves, exact, -0 for code 8):
+        // byte i -> [low nibble, high nibble]; regrouped into the low nibbles of bytes 0..3 then the
+        // high nibbles.
+        const uint32_t c[4] = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 1.0f, 0)),
+                               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 1.0f, 1)),
+                               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 1.0f, 2)),
+                               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q, 1.0f, 3))};
+        uint4v h;
+        h[0] = __builtin_amdgcn_perm(c[1], c[0], 0x05040100u);
+        h[1] = __builtin_amdgcn_perm(c[3], c[2], 0x05040100u);
+        h[2] = __builtin_amdgcn_perm(c[1], c[0], 0x07060302u);
+        h[3] = __builtin_amdgcn_perm(c[3], c[2], 0x07060302u);
+        return __builtin_bit_cast(half8, h);
+    } else {
+        const uint32_t hi = q >> 4;
+        uint4v h;
+        h[0] = fp4_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+        h[1] = fp4_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+        h[2] = fp4_pair_bits(__builtin_amdgcn_perm(0u, hi, 0x0C010C00u));
+        h[3] = fp4_pair_bits(__builtin_amdgcn_perm(0u, hi, 0x0C030C02u));
+        return __builtin_bit_cast(half8, h);
+    }
+}
+
+// The matching A operand: activations of one token at the same 8 k positions.
+template <int FMT>
+__device__ __forceinline__ half8 load_a(const half_t* xr, int b, int g) {
+    if constexpr (FMT == 2) {
+        const uint2v lo = *reinterpret_cast<const uint2v*>(xr + b * kBlockK + g * 4);
+        const uint2v hi = *reinterpret_cast<const uint2v*>(xr + b * kBlockK + 16 + g * 4);
+        return __builtin_bit_cast(half8, uint4v{lo[0], lo[1], hi[0], hi[1]});
+    } else {
+        return *reinterpret_cast<const half8*>(xr + b * kBlockK + g * 8);
+    }
+}
+
+// What the block sum is multiplied by besides the f16 scale: decoded FP8 codes are value / 2^8, FP4
+// codes value / 2^14 with the bit-pattern decode and the value itself with the hardware conversion.
+template <int FMT>
+__device__ __forceinline__ float block_scale_factor() {
+    return FMT == 1 ? 256.0f : (kFp4Cvt ? 1.0f : 16384.0f);
+}
+
+// One 32-wide block: acc[tt] += scale * (x-tile . codes) (FP8/FP4) or acc[tt] += x-tile . w (F16).
+template <int FMT, int TT>
+__device__ __forceinline__ void mma_block(float4v (&acc)[TT], const half8 (&A)[TT], half8 B, float s) {
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        if constexpr (FMT == 0) {
+            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt], B, acc[tt], 0, 0, 0);
+        } else {
+            const float4v blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[tt], B, float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[tt][i] = __builtin_fmaf(s, blk[i], acc[tt][i]);
+        }
+    }
+}
+
+#ifndef NEKO_TUNE_MM_WAVE_TARGET
+#define NEKO_TUNE_MM_WAVE_TARGET 4096
+#endif
+#ifndef NEKO_TUNE_MM_MAXW
+#define NEKO_TUNE_MM_MAXW 16
+#endif
+// Weights travel in groups of four 32-wide blocks of each of the tile's 16 rows (256 / 128 / 64
+// contiguous bytes per row for F16 / FP8 / FP4): lanes load a group coalesced, 16 bytes each along
+// the rows, write it to the wave's LDS tile and read their MFMA operands back from there -- a direct
+// MFMA-layout load would touch 16 rows per instruction for 4-16 bytes of each. Launch shape: waves per row tile (the K split) chosen for about kWaveTarget waves in
+// the grid, at most kMaxWaves per workgroup.
+constexpr int64_t kWaveTarget = NEKO_TUNE_MM_WAVE_TARGET;
+constexpr int kMaxWaves = NEKO_TUNE_MM_MAXW;
+constexpr int kGroup = 4;  // 32-wide blocks per group: one 8-byte load of a row's 4 block scales
+
+// Bytes of one row's 32-wide block; a group's bytes of one row; 16-byte pieces per lane per group.
+__host__ __device__ constexpr int block_bytes(int fmt) { return fmt == 0 ? 64 : fmt == 1 ? 32 : 16; }
+__host__ __device__ constexpr int group_row_bytes(int fmt) { return kGroup * block_bytes(fmt); }
+__host__ __device__ constexpr int pieces(int fmt) { return group_row_bytes(fmt) / 64; }  // 16 rows / 64 lanes / 16 B
+__host__ __device__ constexpr int stage_row(int fmt) { return group_row_bytes(fmt) + 16; }  // padded: no bank conflicts
+__host__ __device__ constexpr int stage_bytes(int fmt) { return 16 * stage_row(fmt); }      // one wave's tile
+
+template <int FMT>
+struct MmStage {
+    uint4v w[pieces(FMT)];  // this lane's 16-byte pieces of the group
+    uint2v s;               // this lane's row's 4 block scales (FP8 / FP4)
+};
+
+// Requests group b0's weight pieces and scales. Piece i of lane l is chunk c = 64 i + l of the
+// group: row c / (pieces per row), 16-byte column c % (pieces per row); rows[i] are those rows.
+template <int FMT>
+__device__ __forceinline__ void load_stage(MmStage<FMT>& st, const uint8_t* const (&rows)[pieces(FMT)], int col16,
+                                           const uint8_t* wrow, int soff, int b0) {
+#pragma unroll
+    for (int i = 0; i < pieces(FMT); i++)
+        st.w[i] = *reinterpret_cast<const uint4v*>(rows[i] + b0 * block_bytes(FMT) + col16 * 16);
+    if constexpr (FMT != 0) st.s = *reinterpret_cast<const uint2v*>(wrow + soff + 2 * b0);
+}
+
+// Activations of a group. Every lane loads, without a branch: a lane whose token row is past T
+// reads row 0 (a valid address) and feeds it to MFMA output rows that are never stored (each
+// output row depends only on its own A row). Loads under divergent control flow, or values used
+// at once, would make the compiler wait for every outstanding load and drain the weight prefetch.
+template <int FMT, int TT>
+__device__ __forceinline__ void load_acts(half8 (&A)[kGroup][TT], const half_t* const (&xr)[TT], int b0, int g) {
+#pragma unroll
+    for (int j = 0; j < kGroup; j++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) A[j][tt] = load_a<FMT>(xr[tt], b0 + j, g);
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int FMT>
+__device__ __forceinline__ typename BRaw<FMT>::T read_b(const uint8_t* tile, int n, int j, int g) {
+    const uint8_t* p = tile + n * stage_row(FMT) + j * block_bytes(FMT) + g * (block_bytes(FMT) / 4);
+    return *reinterpret_cast<const typename BRaw<FMT>::T*>(p);
+}
+
+// One group: request the next group's activations, write this group's weights to the wave's LDS
+// tile, request the weights two groups ahead into the same registers, then the group's MFMAs.
+template <int FMT, int TT>
+__device__ __forceinline__ void mm_step(float4v (&acc)[TT], MmStage<FMT>& st, const half8 (&A)[kGroup][TT],
+                                        half8 (&A_next)[kGroup][TT], const uint8_t* const (&prow)[pieces(FMT)],
+                                        int col16, const uint8_t* wrow, int soff, const half_t* const (&xr)[TT], int g,
+                                        int n, uint8_t* tile, const int (&slot)[pieces(FMT)], int b_acts, int b_stage) {
+    load_acts<FMT, TT>(A_next, xr, b_acts, g);
+    wave_sync_lds();  // the previous group's operand reads are done
+#pragma unroll
+    for (int q = 0; q < pieces(FMT); q++) *reinterpret_cast<uint4v*>(tile + slot[q]) = st.w[q];
+    const uint2v sc = st.s;
+    load_stage<FMT>(st, prow, col16, wrow, soff, b_stage);
+    wave_sync_lds();
+#pragma unroll
+    for (int j = 0; j < kGroup; j++) {
+        float s = 0.0f;
+        if constexpr (FMT != 0) {
+            // Copied out first: hipcc miscompiles __builtin_bit_cast of a vector element expression
+            // (it reads element 0 whatever the index).
+            const uint32_t sw = sc[j >> 1];
+            const half2v s2 = __builtin_bit_cast(half2v, sw);
+            s = static_cast<float>(s2[j & 1]) * block_scale_factor<FMT>();
+        }
+        mma_block<FMT, TT>(acc, A[j], decode_b<FMT>(read_b<FMT>(tile, n, j, g)), s);
+    }
+}
+
+// Waves per workgroup the kernel is compiled for: more than one token tile needs more than 128
+// VGPRs, which allows at most 8 waves.
+__host__ __device__ constexpr int max_waves(int fmt, int tt) { return tt == 1 ? 16 : 8; }
+
+// Dynamic LDS of a workgroup: the waves' staging tiles and, with more than one wave, the partial
+// tiles of the K split.
+__host__ __device__ constexpr size_t tile_lds_bytes(int fmt, int waves, int tt) {
+    return static_cast<size_t>(waves) * stage_bytes(fmt) + (waves > 1 ? static_cast<size_t>(waves) * tt * 64 * 16 : 0);
+}
+
+// Grid: x = tiles of 16 weight rows, y = chunks of 16*TT tokens. Block: 64 * waves threads; wave w
+// takes K blocks [w * blocks_per_wave, ...). Dynamic LDS: one staging tile per wave, then
+// waves * TT * 64 float4 partial tiles.
+template <int FMT, int TT, typename TY>
+__global__ __launch_bounds__(64 * max_waves(FMT, TT)) void mm_tile_kernel(MmArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int G = kGroup, NP = pieces(FMT), PR = group_row_bytes(FMT) / 16;  // pieces per row
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);  // uniform: scalar loop control
+    const int waves = static_cast<int>(blockDim.x) >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t t_base = static_cast<int64_t>(blockIdx.y) * (16 * TT);
+    const int64_t last = a.N - 1;
+    const uint8_t* wrow = a.w + min(row0 + n, last) * a.rb;
+    const int soff = FMT == 1 ? a.K : a.K / 2;  // scale area of FP8 / FP4 rows
+    uint8_t* tile = lds + wave * stage_bytes(FMT);
+
+    // This lane's staging pieces: rows and LDS slots (fixed for every group).
+    const uint8_t* prow[NP];
+    int slot[NP];
+    const int col16 = lane % PR;
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int r = (64 * i + lane) / PR;
+        prow[i] = a.w + min(row0 + r, last) * a.rb;
+        slot[i] = r * stage_row(FMT) + col16 * 16;
+    }
+
+    const half_t* xr[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int64_t t = t_base + tt * 16 + n;
+        xr[tt] = static_cast<const half_t*>(a.x) + (t < a.T ? t : 0) * a.xs;
+    }
+
+    const int nblk = a.K / kBlockK;
+    const int b_begin = wave * a.blocks_per_wave;
+    const int b_end = min(nblk, b_begin + a.blocks_per_wave);
+    float4v acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) acc[tt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nfull = (b_end - b_begin) / G;  // whole groups of this wave's K slice
+    if (nfull > 0) {
+        // Two register sets (weights + activations) alternate, so no register with a load in
+        // flight is ever copied. Issue order per step: the next group's activations, this group's
+        // LDS write, the weights two groups ahead, this group's MFMAs -- every wait covers only the
+        // group being computed. Requests past the last group re-read it (from L2): the number of
+        // loads in flight is the same on every path, so the compiler's waits stay partial.
+        const int lastg = nfull - 1;
+        MmStage<FMT> st0, st1;
+        half8 A0[G][TT], A1[G][TT];
+        load_stage<FMT>(st0, prow, col16, wrow, soff, b_begin);
+        load_stage<FMT>(st1, prow, col16, wrow, soff, b_begin + min(1, lastg) * G);
+        load_acts<FMT, TT>(A0, xr, b_begin, g);
+        for (int i = 0;; i += 2) {
+            mm_step<FMT, TT>(acc, st0, A0, A1, prow, col16, wrow, soff, xr, g, n, tile, slot,
+                             b_begin + min(i + 1, lastg) * G, b_begin + min(i + 2, lastg) * G);
+            if (i + 1 >= nfull) break;
+            mm_step<FMT, TT>(acc, st1, A1, A0, prow, col16, wrow, soff, xr, g, n, tile, slot,
+                             b_begin + min(i + 2, lastg) * G, b_begin + min(i + 3, lastg) * G);
+            if (i + 2 >= nfull) break;
+        }
+    }
+    for (int b = b_begin + nfull * G; b < b_end; b++) {  // K tail of fewer than a group: direct loads
+        half8 A[TT];
+        const half8 B = decode_b<FMT>(load_b_raw<FMT>(wrow, b, g));
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) A[tt] = load_a<FMT>(xr[tt], b, g);
+        float s = 0.0f;
+        if constexpr (FMT != 0)
+            s = static_cast<float>(*reinterpret_cast<const half_t*>(wrow + soff + 2 * b)) * block_scale_factor<FMT>();
+        mma_block<FMT, TT>(acc, A, B, s);
+    }
+
+    if (waves > 1) {
+        float4v* red = reinterpret_cast<float4v*>(lds + waves * stage_bytes(FMT));
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) red[(wave * TT + tt) * 64 + lane] = acc[tt];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            float4v s = red[tt * 64 + lane];
+            for (int w = 1; w < waves; w++) s += red[(w * TT + tt) * 64 + lane];
+            acc[tt] = s;
+        }
+    }
+    // Lane (n, g) holds C[token 4g + i][row n] of each 16 x 16 tile.
+    const int64_t out_row = row0 + n;
+    if (out_row >= a.N) return;
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t t = t_base + tt * 16 + 4 * g + i;
+            if (t < a.T) epilogue<TY>(a, t, out_row, acc[tt][i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- generic path
+
+// W[row][k] as f32, exact: the code's f16 pattern widened, times 2^8 / 2^14, times the f16 scale.
+__device__ __forceinline__ float weight_at(int fmt, const uint8_t* row, int K, int k) {
+    if (fmt == NEKO_FMT_F16) return static_cast<float>(reinterpret_cast<const half_t*>(row)[k]);
+    const int b = k / kBlockK;
+    if (fmt == NEKO_FMT_FP8) {
+        const uint32_t c = row[k];
+        const half_t s = *reinterpret_cast<const half_t*>(row + K + 2 * b);
+        const uint16_t h = static_cast<uint16_t>(((c & 0x7Fu) << 7) | ((c & 0x80u) << 8));
+        return static_cast<float>(__builtin_bit_cast(half_t, h)) * (static_cast<float>(s) * 256.0f);
+    }
+    const int j = k % kBlockK;
+    const uint32_t byte = row[b * (kBlockK / 2) + (j & 15)];
+    const uint32_t c = j < 16 ? (byte & 0xFu) : (byte >> 4);
+    const half_t s = *reinterpret_cast<const half_t*>(row + K / 2 + 2 * b);
+    const uint16_t h = static_cast<uint16_t>(((c & 7u) << 9) | ((c & 8u) << 12));
+    return static_cast<float>(__builtin_bit_cast(half_t, h)) * (static_cast<float>(s) * 16384.0f);
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// Grid: x = weight rows, y = groups of 4 tokens; one wave each.
+template <typename TX, typename TY>
+__global__ __launch_bounds__(64) void mm_generic_kernel(MmArgs a) {
+    const int lane = static_cast<int>(threadIdx.x);
+    const int64_t n = blockIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * 4;
+    const int nt = static_cast<int>(min(static_cast<int64_t>(4), a.T - t0));
+    const uint8_t* row = a.w + n * a.rb;
+    const TX* x = static_cast<const TX*>(a.x) + t0 * a.xs;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = lane; k < a.K; k += kWave) {
+        const float wk = weight_at(a.fmt, row, a.K, k);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (j < nt) acc[j] += to_f32(x[j * a.xs + k]) * wk;
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float s = wave_sum_f32(acc[j]);
+        if (lane == j) mine = s;
+    }
+    if (lane < nt) epilogue<TY>(a, t0 + lane, n, mine);
+}
+
+// ---------------------------------------------------------------- launch
+
+template <int FMT, int TT>
+int launch_tile(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int waves) {
+    const size_t lds = tile_lds_bytes(FMT, waves, TT);
+    if (y_dtype == NEKO_DT_F16)
+        hipLaunchKernelGGL((mm_tile_kernel<FMT, TT, half_t>), grid, dim3(64 * waves), lds, ctx->stream, a);
+    else
+        hipLaunchKernelGGL((mm_tile_kernel<FMT, TT, float>), grid, dim3(64 * waves), lds, ctx->stream, a);
+    return after_launch(ctx, "neko_hip_matmul");
+}
+
+template <int FMT>
+int launch_tile_tt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int waves, int tt) {
+    switch (tt) {
+        case 1: return launch_tile<FMT, 1>(ctx, a, y_dtype, grid, waves);
+        case 2: return launch_tile<FMT, 2>(ctx, a, y_dtype, grid, waves);
+        case 3: return launch_tile<FMT, 3>(ctx, a, y_dtype, grid, waves);
+        default: return launch_tile<FMT, 4>(ctx, a, y_dtype, grid, waves);
+    }
+}
+
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return an && bn && pa < pb + bn && pb < pa + an;
+}
+
+}  // namespace
+}  // namespace neko_hip
+
+using namespace neko_hip;
+
+extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
+                               int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride,
+                               int flags, int x_dtype, int y_dtype) {
+    const char* what = "neko_hip_matmul";
+    NEKO_ENTER(ctx);
+    NEKO_REQUIRE(ctx, valid_dtype(x_dtype) && valid_dtype(y_dtype), "%s: bad dtype x=%d y=%d", what, x_dtype, y_dtype);
+    NEKO_REQUIRE(ctx, fmt == NEKO_FMT_F16 || fmt == NEKO_FMT_FP8 || fmt == NEKO_FMT_FP4, "%s: bad weight format %d", what,
+                 fmt);
+    NEKO_REQUIRE(ctx, (flags & ~(kGelu | kAccumulate)) == 0, "%s: bad flags %d", what, flags);
+    NEKO_REQUIRE(ctx, T >= 0 && K > 0 && N >= 0 && K <= (1 << 30) && N <= (1 << 30),
+                 "%s: bad shape T=%lld K=%lld N=%lld", what, (long long)T, (long long)K, (long long)N);
+    NEKO_REQUIRE(ctx, fmt == NEKO_FMT_F16 || K % kBlockK == 0, "%s: FP8/FP4 rows need K %% 32 == 0 (K=%lld)", what,
+                 (long long)K);
+    NEKO_REQUIRE(ctx, row_bytes >= static_cast<int64_t>(neko_quant_row_bytes(fmt, K)) && row_bytes % 2 == 0,
+                 "%s: row_bytes %lld below the %zu bytes of a K=%lld row", what, (long long)row_bytes,
+                 neko_quant_row_bytes(fmt, K), (long long)K);
+    NEKO_REQUIRE(ctx, x_stride >= K && y_stride >= N, "%s: strides x=%lld y=%lld below K=%lld / N=%lld", what,
+                 (long long)x_stride, (long long)y_stride, (long long)K, (long long)N);
+    if (T == 0 || N == 0) return NEKO_OK;
+    NEKO_REQUIRE(ctx, x && w && y, "%s: null pointer", what);
+    NEKO_REQUIRE(ctx, T <= INT64_MAX / x_stride && T <= INT64_MAX / y_stride, "%s: too many rows", what);
+    const size_t xbytes = static_cast<size_t>((T - 1) * x_stride + K) * dtype_size(x_dtype);
+    const size_t ybytes = static_cast<size_t>((T - 1) * y_stride + N) * dtype_size(y_dtype);
+    const size_t wbytes = static_cast<size_t>(N) * static_cast<size_t>(row_bytes);
+    NEKO_REQUIRE(ctx, !overlaps(y, ybytes, x, xbytes) && !overlaps(y, ybytes, w, wbytes),
+                 "%s: y may not overlap x or the weights", what);
+
+    MmArgs a{x, x_stride, T, static_cast<const uint8_t*>(w), row_bytes, static_cast<int>(K), static_cast<int>(N), bias,
+             y, y_stride, flags, fmt, 0};
+    const bool fast = x_dtype == NEKO_DT_F16 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 8 == 0 &&
+                      aligned(w, 16) && row_bytes % 16 == 0;
+    if (fast) {
+        const int tt = static_cast<int>(std::min<int64_t>(4, (T + 15) / 16));
+        const int64_t chunks = (T + 16 * tt - 1) / (16 * tt);
+        const int64_t tiles = (N + 15) / 16;
+        NEKO_REQUIRE(ctx, chunks <= 65535, "%s: T=%lld exceeds this kernel's grid", what, (long long)T);
+        // Enough waves to fill the chip, each with at least one group of K.
+        const int gb = kGroup;
+        const int groups = static_cast<int>((K / kBlockK + gb - 1) / gb);
+        const int64_t want = (kWaveTarget + tiles * chunks - 1) / (tiles * chunks);
+        int cap = std::min(kMaxWaves, max_waves(fmt, tt));
+        while (cap > 1 && tile_lds_bytes(fmt, cap, tt) > 65536) cap--;
+        int waves = static_cast<int>(std::min<int64_t>({cap, static_cast<int64_t>(groups), std::max<int64_t>(1, want)}));
+        const int gpw = (groups + waves - 1) / waves;
+        a.blocks_per_wave = gpw * gb;
+        waves = (groups + gpw - 1) / gpw;
+        const dim3 grid(static_cast<uint32_t>(tiles), static_cast<uint32_t>(chunks));
+        switch (fmt) {
+            case NEKO_FMT_F16: return launch_tile_tt<0>(ctx, a, y_dtype, grid, waves, tt);
+            case NEKO_FMT_FP8: return launch_tile_tt<1>(ctx, a, y_dtype, grid, waves, tt);
+            default: return launch_tile_tt<2>(ctx, a, y_dtype, grid, waves, tt);
+        }
+    }
+    const int64_t tgroups = (T + 3) / 4;
+    NEKO_REQUIRE(ctx, tgroups <= 65535, "%s: T=%lld exceeds this kernel's grid", what, (long long)T);
+    const dim3 grid(static_cast<uint32_t>(N), static_cast<uint32_t>(tgroups));
+    if (x_dtype == NEKO_DT_F16) {
+        if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_generic_kernel<half_t, half_t>), grid, dim3(64), 0, ctx->stream, a);
+        else hipLaunchKernelGGL((mm_generic_kernel<half_t, float>), grid, dim3(64), 0, ctx->stream, a);
+    } else {
+        if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_generic_kernel<float, half_t>), grid, dim3(64), 0, ctx->stream, a);
+        else hipLaunchKernelGGL((mm_generic_kernel<float, float>), grid, dim3(64), 0, ctx->stream, a);
+    }
+    return after_launch(ctx, what);
+}

@@ -20,7 +20,7 @@ from ._lib import DT_F16, DT_F32, FMT_F16, FMT_FP4, FMT_FP8, NEKO_OK, NekoError,
 
 __all__ = [
     "Context", "context", "layer_norm", "rms_norm", "qk_norm_rope", "qk_norm_rope_kv", "store_kv", "add_rms_norm",
-    "silu_mul", "gelu", "gated_rms_norm", "embed",
+    "silu_mul", "gelu", "gated_rms_norm", "embed", "matmul", "MM_GELU", "MM_ACCUMULATE",
     "prepare", "quantize", "quant_row_bytes", "quantize_rows", "rope_table", "FMT_F16", "FMT_FP8", "FMT_FP4", "NekoError",
 ]
 
@@ -349,6 +349,37 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base:
     _issue(ctx, lib.neko_hip_embed, ctx.handle, tokens.data_ptr(), T, table.data_ptr(), table.shape[1], int(fmt), int(C),
            int(row_base), n_rows, wpe_ptr, wpe_rows, int(pos0), out.data_ptr(), os_,
            _dtype_code(out))
+    return out
+
+
+MM_GELU, MM_ACCUMULATE = 1, 2  # cpu_ops.h MatmulFlags
+
+
+def matmul(x: torch.Tensor, table: torch.Tensor, fmt: int, K: int, bias: torch.Tensor | None = None,
+           out: torch.Tensor | None = None, flags: int = 0, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """cpu::matmul / matmul*.comp (cpu_ops.cpp:474-490): out[t][n] (+)= act(x[t] . W[n] + bias[n]).
+    x: float16 or float32 [T, K] rows; table: uint8 [N, row_bytes] weight rows in format fmt; bias: float32
+    [N] or None; out: [T, >= N] rows of float32 or float16 (a column slice of a wider buffer is fine).
+    flags: MM_GELU applies GELU to the biased sum, MM_ACCUMULATE adds into out."""
+    T, xk, xs = _rows(x, "x")
+    if xk < K:
+        raise NekoError("x rows are narrower than K")
+    _on(table, "table", x.device)
+    if table.dtype != torch.uint8 or table.dim() != 2 or not table.is_contiguous():
+        raise NekoError("table must be a contiguous uint8 [N, row_bytes] tensor")
+    N = table.shape[0]
+    bias_ptr = _vec(bias, N, "bias", x.device)
+    if out is None:
+        if flags & MM_ACCUMULATE:
+            raise NekoError("MM_ACCUMULATE needs an out tensor to add into")
+        out = torch.empty((T, N), dtype=out_dtype, device=x.device)
+    _on(out, "out", x.device)
+    ot, oc, os_ = _rows(out, "out")
+    if ot != T or oc < N:
+        raise NekoError(f"out must have {T} rows of at least {N} columns")
+    ctx = _ctx_for(x)
+    _issue(ctx, lib.neko_hip_matmul, ctx.handle, x.data_ptr(), xs, T, int(K), table.data_ptr(), table.shape[1], int(fmt),
+           N, bias_ptr, out.data_ptr(), os_, int(flags), _dtype_code(x), _dtype_code(out))
     return out
 
 

@@ -91,6 +91,12 @@ def bytes_store_kv(T: int, width: int, positions: bool = True) -> int:
     return 4 * T * width * 2 + (T * 4 if positions else 0)
 
 
+def bytes_matmul(T: int, K: int, N: int, row_bytes: int, y_bytes: int = 4, accumulate: bool = False) -> int:
+    """The weight rows read once, the fp16 activations read, the outputs written (and read when
+    accumulating)."""
+    return N * row_bytes + T * K * 2 + T * N * y_bytes * (2 if accumulate else 1)
+
+
 def bytes_qk_rope_kv(T: int, n_q: int, n_kv: int, hd: int, positions: bool = True) -> int:
     """q/k RoPE bytes plus the v heads read and the k and v heads written to the caches."""
     return bytes_qk_rope(T, n_q, n_kv, hd, positions) + 3 * T * n_kv * hd * 2
@@ -160,6 +166,14 @@ class QuantGather:
 
 
 @dataclasses.dataclass(frozen=True)
+class Qwen3DecodeMatmul:
+    """Qwen3-4B decode: the layer's four weight matmuls for T tokens (one decode step of T sequences):
+    q/k/v [6144, 2560], o [2560, 4096], gate/up [19456, 2560], down [2560, 9728]."""
+    T: int = 1
+    projections: tuple = (("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728))
+
+
+@dataclasses.dataclass(frozen=True)
 class GraniteNorms:
     """Granite-4.0-H-style: 16384 tokens, RMSNorm over 1536, gated norm over d_inner 3072, SwiGLU I = 4096."""
     T: int = 16384
@@ -175,6 +189,7 @@ QWEN3_DECODE = Qwen3Decode()
 GPT2_CHAIN = Gpt2Chain()
 QUANT_GATHER = QuantGather()
 GRANITE_NORMS = GraniteNorms()
+QWEN3_DECODE_MATMUL = Qwen3DecodeMatmul()
 
 
 def qwen3_prefill_inputs(cfg: Qwen3Prefill, device) -> dict:

@@ -538,3 +538,34 @@ void oracle_embed(const int32_t* tokens, int64_t T, const uint8_t* table, int64_
     }
     free(t);
 }
+
+/* ------------------------------------------------------------------ weight matmul */
+
+/* cpu::matmul on the portable (non-aarch64) path, cpu_ops.cpp:474-490. F16 rows go through matmulF16
+ * (:108-127): the dot starts at 0 and runs k = 0..K-1 in float (dotRow4's scalar loop, :60-63), then
+ * v = dot + bias. FP8 / FP4 rows go through matmulGeneric (:455-472): dequantizeRow, then the sum starts
+ * at the bias and adds x[k] * w[k] for k = 0..K-1. Both then apply gelu (flags & 1) and add into y
+ * (flags & 2); y rows have stride N. */
+void oracle_matmul(int fmt, const float* x, int64_t T, int K, const uint8_t* w, int64_t row_bytes, int64_t N,
+                   const float* bias, float* y, int flags) {
+    float* wr = scratch_f32((size_t)K);
+    for (int64_t n = 0; n < N; n++) {
+        oracle_dequantize_row(fmt, K, w + n * row_bytes, wr);
+        for (int64_t t = 0; t < T; t++) {
+            const float* xt = x + t * (int64_t)K;
+            float v;
+            if (fmt == ORACLE_FMT_F16) {
+                float acc = 0.0f;
+                for (int k = 0; k < K; k++) acc += wr[k] * xt[k];
+                v = acc + (bias ? bias[n] : 0.0f);
+            } else {
+                v = bias ? bias[n] : 0.0f;
+                for (int k = 0; k < K; k++) v += xt[k] * wr[k];
+            }
+            if (flags & 1) v = oracle_gelu(v);
+            float* dst = y + t * N + n;
+            *dst = (flags & 2) ? *dst + v : v;
+        }
+    }
+    free(wr);
+}

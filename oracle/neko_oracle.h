@@ -127,6 +127,12 @@ void oracle_embed(const int32_t* tokens, int64_t T, const uint8_t* table, int64_
                   int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t pos0, void* out,
                   int64_t out_stride, int out_f16);
 
+/* Weight matmul, cpu::matmul on the portable path (cpu_ops.cpp:108-127 for F16 rows, :455-472 for FP8 /
+ * FP4 rows): y[t][n] (+)= gelu?(x[t] . dequant(W[n]) + bias[n]) in float, k ascending; x is [T][K] f32,
+ * W is N rows of row_bytes in `fmt`, y is [T][N]; flags 1 = gelu, 2 = accumulate into y. bias may be NULL. */
+void oracle_matmul(int fmt, const float* x, int64_t T, int K, const uint8_t* w, int64_t row_bytes, int64_t N,
+                   const float* bias, float* y, int flags);
+
 #ifdef __cplusplus
 }
 #endif

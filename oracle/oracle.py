@@ -94,6 +94,7 @@ _ORACLE_SIGS = {
     "oracle_qk_norm_rope_kv_f16": (None, [_p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p]),
     "oracle_qk_norm_rope_kv_f32": (None, [_p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p]),
     "oracle_add_rmsnorm_f16": (None, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _f32]),
+    "oracle_matmul": (None, [_i32, _p, _i64, _i32, _p, _i64, _i64, _p, _p, _i32]),
 }
 
 _REF_SIGS = {
@@ -119,11 +120,13 @@ _REF_SIGS = {
     "ref_store_kv": (None, [_p, _p, _i32, _p, _p, _i32, _i32, _i32]),
     "ref_add_rmsnorm_f16": (None, [_p, _p, _p, _p, _p, _i32, _i32, _f32]),
     "ref_gelu_n": (None, [_p, _p, _i64]),
+    "ref_matmul": (None, [_i32, _p, _i32, _i32, _p, _i32, _p, _p, _i32]),
     "ref_qk_norm_rope": (None, [_p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32]),
     "ref_gated_rmsnorm": (None, [_p, _p, _p, _i32, _i32, _i32, _f32]),
     "ref_qmatrix_new": (_p, [_i32, _i32, _i32, _p]),
     "ref_qmatrix_gather": (None, [_p, _p, _i32, _p, _p]),
     "ref_qmatrix_free": (None, [_p]),
+    "ref_qmatrix_matmul": (None, [_p, _p, _i32, _p, _p, _i32]),
 }
 
 _oracle = None
@@ -304,4 +307,16 @@ def embed(tokens, table, fmt, C, row_base=0, rows=None, wpe=None, pos0=0, out_f1
     pe = None if wpe is None else _c16(wpe)
     lib().oracle_embed(_ptr(tokens), T, _ptr(table), table.shape[1], fmt, C, row_base, rows, _ptr(pe), pos0,
                        _ptr(out), out.shape[1], 1 if out_f16 else 0)
+    return out
+
+
+def matmul(fmt, x, table, K, bias=None, y=None, flags=0):
+    """cpu::matmul on the portable path: x float32 [T, K], table uint8 [N, row_bytes] in `fmt`; returns y
+    float32 [T, N] (a copy of `y` accumulated into when flags & 2)."""
+    x = _c32(x)
+    table = np.ascontiguousarray(table, dtype=np.uint8)
+    T, N = x.shape[0], table.shape[0]
+    out = np.zeros((T, N), np.float32) if y is None else _c32(y).copy()
+    b = None if bias is None else _c32(bias)
+    lib().oracle_matmul(fmt, _ptr(x), T, K, _ptr(table), table.shape[1], N, _ptr(b), _ptr(out), flags)
     return out

@@ -158,6 +158,20 @@ void ref_add_rmsnorm_f16(const uint16_t* x, const uint16_t* d, uint16_t* x_out, 
     narrow(y.data(), xn, y.size());
 }
 
+// Weight matmul: the compiled cpu::matmul on a one-thread pool (x86: matmulF16 for F16 rows,
+// matmulGeneric for FP8 / FP4).
+void ref_matmul(int fmt, const float* x, int T, int K, const uint8_t* table, int N, const float* bias, float* y,
+                int flags) {
+    QMatrix m;
+    m.format = WeightFormat(fmt);
+    m.rows = N;
+    m.cols = K;
+    m.rowBytes = quantRowBytes(m.format, K);
+    m.data.assign(table, table + m.rowBytes * size_t(N));
+    static ThreadPool pool(1);
+    cpu::matmul(pool, x, T, K, m, bias, y, N, flags);
+}
+
 // ---- f32 activations, as the reference's CPU forward passes hold them (its CPU path, timed beside
 // the device kernels; same compiled ops, no f16 widening or narrowing).
 
@@ -215,6 +229,12 @@ void ref_qmatrix_gather(const void* h, const int32_t* tokens, int T, const float
     }
 }
 void ref_qmatrix_free(void* h) { delete static_cast<QMatrix*>(h); }
+// cpu::matmul over a held QMatrix (no per-call copy of the table), one-thread pool.
+void ref_qmatrix_matmul(const void* h, const float* x, int T, const float* bias, float* y, int flags) {
+    const QMatrix* m = static_cast<const QMatrix*>(h);
+    static ThreadPool pool(1);
+    cpu::matmul(pool, x, T, m->cols, *m, bias, y, m->rows, flags);
+}
 
 // Embedding gather: dequantizeRow of each token's row, + the f32 position row (gpt2_model.cpp:182-187),
 // rounded to f16 when out_f16.

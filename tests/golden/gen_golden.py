@@ -155,6 +155,22 @@ def main():
     R.ref_add_rmsnorm_f16(P(x), P(d), P(xo), P(xn), P(w), 8, 512, F(1e-6))
     g.update(addrms_x=x, addrms_d=d, addrms_w=w, addrms_xo=xo, addrms_xn=xn)
 
+    # Weight matmul (cpu::matmul on one thread; x86: matmulF16 / matmulGeneric): f16-valued
+    # activations, weights quantised by the compiled quantizeMatrix, bias, each flag combination.
+    x = f16(rng, (6, 256)).view(np.float16).astype(np.float32)
+    wm = (rng.standard_normal((40, 256)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(40) * 0.1).astype(np.float32)
+    y0 = (rng.standard_normal((6, 40))).astype(np.float32)
+    g.update(mm_x=x, mm_bias=bias, mm_y0=y0)
+    for fmt, name in ((0, "f16"), (1, "fp8"), (2, "fp4")):
+        tab = np.zeros((40, int(R.ref_quant_row_bytes(fmt, 256))), np.uint8)
+        assert R.ref_quantize_rows(fmt, 40, 256, P(wm), P(tab)) == fmt
+        g[f"mm_w_{name}"] = tab
+        for flags in (0, 1, 2, 3):
+            y = y0.copy()
+            R.ref_matmul(fmt, P(x), 6, 256, P(tab), 40, P(bias) if flags != 2 else None, P(y), flags)
+            g[f"mm_y_{name}_{flags}"] = y
+
     path = os.path.join(HERE, "golden.npz")
     np.savez_compressed(path, **g)
     print(f"wrote {path}: {len(g)} arrays, {os.path.getsize(path)} bytes")

@@ -1,0 +1,157 @@
+"""GPU parity of the weight matmul (neko_hip_matmul) against the oracle and exact arithmetic.
+
+The reference sums each dot product sequentially in f32 on the CPU and in a reduction tree on its
+GPU, so no summation order is canonical. The bars:
+  - integer-valued weights (codes times power-of-two scales) and activations: every partial sum is
+    exact, so outputs are bit-identical to the oracle in any order -- a dropped, repeated or
+    misplaced term, a wrong scale or a wrong token/row mapping changes the bits;
+  - random data: |y - exact| <= (K + 64) * 2^-24 * (sum_k |x_k w_k| + |bias|) against the float64
+    product of the oracle's dequantised weights (the worst-case bound of an f32 sum of K exact
+    products in any order, with the per-block scale, cross-wave and bias additions); the observed
+    error is reported and is a few units of 2^-24 * that magnitude.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mm_tables as M
+from nekochat_amd import NekoError, ops
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+FMTS = [ops.FMT_F16, ops.FMT_FP8, ops.FMT_FP4]
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _bound_check(got, exact, mag, K, what):
+    err = np.abs(got.astype(np.float64) - exact)
+    ratio = float((err / np.maximum(mag * U, 1e-300)).max())
+    print(f"[parity] {what}: max |y - exact| = {ratio:.2f} * 2^-24 * sum|x w| (bound {K + 64})", flush=True)
+    assert (err <= (K + 64) * U * mag + 1e-30).all(), f"{what}: error beyond the f32 summation bound"
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T", [1, 5, 16, 17, 64, 100])
+def test_matmul_integer_rows_bitexact(dev, fmt, T):
+    """K = 320 (ten 32-blocks: two 4-block groups and a 2-block tail), N = 37 (a partial row tile)."""
+    _case(f"matmul integer fmt={fmt} T={T}")
+    rng = np.random.default_rng(100 + 10 * fmt + T)
+    K, N = 320, 37
+    tab, w = M.integer_table(fmt, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev).half()
+    td = torch.from_numpy(tab).to(dev)
+    bd = torch.from_numpy(bias).to(dev)
+    for flags, b in ((0, None), (0, bias), (ops.MM_ACCUMULATE, bias), (ops.MM_GELU, bias),
+                     (ops.MM_GELU | ops.MM_ACCUMULATE, None)):
+        want = O.matmul(fmt, x, tab, K, b, y0, flags)
+        out = torch.from_numpy(y0).to(dev)
+        ops.matmul(xd, td, fmt, K, bias=None if b is None else bd, out=out, flags=flags)
+        got = out.cpu().numpy()
+        if flags & ops.MM_GELU:  # device GELU vs libm tanh: within 2 f32 ulp of the same argument
+            d = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+            assert d.max() <= 2, (flags, int(d.max()))
+        else:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (flags, b is None)
+    # f16 output: one rounding of the exact value
+    out16 = ops.matmul(xd, td, fmt, K, bias=bd, out_dtype=torch.float16)
+    want16 = O.f32_to_f16(O.matmul(fmt, x, tab, K, bias))
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), want16)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,K,N", [
+    (1, 2560, 6144),    # Qwen3-4B decode: q/k/v projection
+    (1, 9728, 2560),    # Qwen3-4B decode: down projection
+    (8, 2560, 19456),   # Qwen3-4B batch-8 decode: gate/up projection
+    (33, 4096, 2560),   # o projection, three token tiles
+    (3, 32, 40),        # one block
+    (200, 768, 96),     # GPT-2 width, several token chunks
+])
+def test_matmul_random_within_bound(dev, fmt, T, K, N):
+    _case(f"matmul random fmt={fmt} T={T} K={K} N={N}")
+    rng = np.random.default_rng(7 * T + K + N + fmt)
+    w = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    tab, used = ops.quantize_rows(fmt, w)
+    assert used == fmt
+    wd = M.dequant(fmt, tab, K)
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    y = ops.matmul(torch.from_numpy(x).to(dev), torch.from_numpy(tab).to(dev), fmt, K,
+                   bias=torch.from_numpy(bias).to(dev)).cpu().numpy()
+    exact, mag = M.exact_and_bound(x.astype(np.float32), wd, bias)
+    _bound_check(y, exact, mag, K, f"fmt={fmt} T={T} K={K} N={N}")
+    if T * N <= 4096:
+        want = O.matmul(fmt, x.astype(np.float32), tab, K, bias)
+        assert np.abs(y - want).max() <= float(((2 * K + 65) * U * mag).max())
+
+
+def test_matmul_generic_paths(dev):
+    """f32 activations, misaligned rows, K not a multiple of 32 (F16 only), f16 output."""
+    _case("matmul generic paths")
+    rng = np.random.default_rng(5)
+    for fmt, K, xdt, off in ((ops.FMT_F16, 100, torch.float32, 0), (ops.FMT_FP8, 256, torch.float32, 3),
+                             (ops.FMT_FP4, 96, torch.float16, 3), (ops.FMT_F16, 64, torch.float16, 1)):
+        T, N = 6, 21
+        w = (rng.standard_normal((N, K)) * 0.1).astype(np.float32)
+        tab, used = ops.quantize_rows(fmt, w)
+        wd = M.dequant(used, tab, K)
+        buf = torch.from_numpy(rng.standard_normal((T, K + 8)).astype(np.float32)).to(dev).to(xdt)
+        x = buf[:, off:off + K]
+        xh = x.float().cpu().numpy()
+        for ydt in (torch.float32, torch.float16):
+            y = ops.matmul(x, torch.from_numpy(tab).to(dev), used, K, out_dtype=ydt).float().cpu().numpy()
+            exact, mag = M.exact_and_bound(xh, wd)
+            if ydt == torch.float32:
+                _bound_check(y, exact, mag, K, f"generic fmt={used} K={K} x={xdt}")
+            else:
+                assert np.abs(y - exact).max() <= np.abs(exact).max() * 2.0 ** -10 + 1e-6
+
+
+def test_matmul_accumulate_into_column_slice(dev):
+    """y is columns [64, 64 + N) of a wider f32 buffer (the shaders' nOffset): bias + GELU added into it;
+    the columns outside stay untouched."""
+    _case("matmul accumulate into a column slice")
+    rng = np.random.default_rng(9)
+    T, K, N = 20, 512, 48
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    tab, _ = ops.quantize_rows(ops.FMT_FP8, w)
+    wd = M.dequant(ops.FMT_FP8, tab, K)
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    base = rng.standard_normal((T, 256)).astype(np.float32)
+    buf = torch.from_numpy(base).to(dev)
+    ops.matmul(torch.from_numpy(x).to(dev), torch.from_numpy(tab).to(dev), ops.FMT_FP8, K,
+               bias=torch.from_numpy(bias).to(dev), out=buf[:, 64:64 + N], flags=ops.MM_GELU | ops.MM_ACCUMULATE)
+    got = buf.cpu().numpy()
+    assert np.array_equal(got[:, :64], base[:, :64]) and np.array_equal(got[:, 64 + N:], base[:, 64 + N:])
+    exact, mag = M.exact_and_bound(x.astype(np.float32), wd, bias)
+    gel = np.array([O.lib().oracle_gelu(float(v)) for v in exact.ravel()], np.float64).reshape(T, N)
+    want = base[:, 64:64 + N].astype(np.float64) + gel
+    tol = 1.2 * (K + 64) * U * mag + 4 * U * (np.abs(gel) + np.abs(want))
+    assert (np.abs(got[:, 64:64 + N] - want) <= tol).all()
+
+
+def test_matmul_empty_and_invalid(dev):
+    _case("matmul empty / invalid")
+    x = torch.zeros((4, 64), dtype=torch.float16, device=dev)
+    tab = torch.zeros((8, O.lib().oracle_quant_row_bytes(1, 64)), dtype=torch.uint8, device=dev)
+    out = ops.matmul(x[:0], tab, ops.FMT_FP8, 64)
+    assert out.shape == (0, 8)
+    with pytest.raises(NekoError):
+        ops.matmul(x, tab, 7, 64)  # bad format
+    with pytest.raises(NekoError):
+        ops.matmul(x, tab, ops.FMT_FP8, 64, flags=4)  # bad flags
+    with pytest.raises(NekoError):
+        ops.matmul(x[:, :48], tab, ops.FMT_FP8, 48)  # FP8 rows need K % 32 == 0
+    with pytest.raises(NekoError):
+        ops.matmul(x, tab, ops.FMT_FP8, 64, out=x.view(torch.float32)[:, :8])  # y overlaps x
+    with pytest.raises(NekoError):
+        ops.matmul(x, tab[:, :40], ops.FMT_FP8, 64)  # rows shorter than a K=64 FP8 row

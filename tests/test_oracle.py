@@ -82,6 +82,15 @@ def test_golden_add_rmsnorm(golden):
     assert np.array_equal(xo, golden["addrms_xo"]) and np.array_equal(xn, golden["addrms_xn"])
 
 
+@pytest.mark.parametrize("fmt,name", [(0, "f16"), (1, "fp8"), (2, "fp4")])
+def test_golden_matmul(golden, fmt, name):
+    """Compiled cpu::matmul (matmulF16 / matmulGeneric) for each flag combination, bit-exact."""
+    for flags in (0, 1, 2, 3):
+        bias = golden["mm_bias"] if flags != 2 else None
+        y = O.matmul(fmt, golden["mm_x"], golden[f"mm_w_{name}"], 256, bias, golden["mm_y0"], flags)
+        assert np.array_equal(y.view(np.uint32), golden[f"mm_y_{name}_{flags}"].view(np.uint32)), flags
+
+
 def test_golden_decoders(golden):
     d8 = np.array([O.lib().oracle_decode_fp8(c) for c in range(256)], np.float32)
     assert np.array_equal(d8.view(np.uint32), golden["fp8_decode"].view(np.uint32))
@@ -215,6 +224,27 @@ def test_ref_f32_entry_points_match_oracle():
                 assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         finally:
             R.ref_qmatrix_free(h)
+
+
+@needs_ref
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_ref_matmul_bitexact(fmt):
+    R = O.ref()
+    rng = np.random.default_rng(40 + fmt)
+    for T, K, N in ((1, 64, 7), (5, 256, 33), (9, 96, 4), (4, 32, 1)):
+        if fmt != 0 and K % 32:
+            continue
+        w = (rng.standard_normal((N, K)) * 0.1).astype(np.float32)
+        tab = O.quantize_rows(fmt, w)
+        x = rng.standard_normal((T, K)).astype(np.float16).astype(np.float32)
+        b = rng.standard_normal(N).astype(np.float32)
+        for flags in (0, 1, 2, 3):
+            for bias in (None, b):
+                y0 = rng.standard_normal((T, N)).astype(np.float32)
+                want = y0.copy()
+                R.ref_matmul(fmt, P(x), T, K, P(tab), N, P(bias), P(want), flags)
+                got = O.matmul(fmt, x, tab, K, bias, y0, flags)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (T, K, N, flags, bias is None)
 
 
 @needs_ref
@@ -462,3 +492,48 @@ def test_qk_norm_rope_kv_is_rope_then_store():
     assert np.array_equal(o32, r32)
     assert np.array_equal(k32[5:8], r32[:, H * hd:H * hd + kw].astype(np.float16).view(np.uint16))
     assert np.array_equal(v32[5:8], f32[:, H * hd + kw:].astype(np.float16).view(np.uint16))
+
+
+# ------------------------------------------------------------------ weight matmul
+
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_matmul_integer_rows_exact(fmt):
+    """Integer weights (codes times power-of-two scales) and integer activations: every partial sum
+    is exact, so the matmul equals the integer dot product; GELU and accumulate apply to that value."""
+    import mm_tables as M
+
+    rng = np.random.default_rng(60 + fmt)
+    T, K, N = 7, 320, 19
+    tab, w = M.integer_table(fmt, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    exact = (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float64) + bias
+    assert np.array_equal(O.matmul(fmt, x, tab, K, bias), exact.astype(np.float32))
+    g = O.matmul(fmt, x, tab, K, bias, None, 1)
+    want = np.array([O.lib().oracle_gelu(float(v)) for v in exact.ravel()], np.float32).reshape(T, N)
+    assert np.array_equal(g.view(np.uint32), want.view(np.uint32))
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    a = O.matmul(fmt, x, tab, K, None, y0, 2)
+    assert np.array_equal(a, y0 + (exact - bias).astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_matmul_float_within_summation_bound(fmt):
+    """Random rows: within K * 2^-24 * sum|x_k w_k| of the float64 product of the dequantised weights
+    (the bound of a sequential f32 sum), and far from it when one term is dropped."""
+    import mm_tables as M
+
+    rng = np.random.default_rng(70 + fmt)
+    T, K, N = 3, 512, 24
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    tab = O.quantize_rows(fmt, w)
+    wd = M.dequant(fmt, tab, K)
+    x = rng.standard_normal((T, K)).astype(np.float16).astype(np.float32)
+    exact, mag = M.exact_and_bound(x, wd)
+    err = np.abs(O.matmul(fmt, x, tab, K).astype(np.float64) - exact)
+    assert (err <= (K + 1) * 2.0 ** -24 * mag).all()
+    x2 = x.copy()
+    x2[:, 100] = 0.0
+    dropped = np.abs(O.matmul(fmt, x2, tab, K).astype(np.float64) - exact)
+    assert (dropped > (K + 1) * 2.0 ** -24 * mag)[np.abs(x[:, 100:101] * wd[None, :, 100]) > 1e-3 * mag].all()
+
