@@ -17,8 +17,10 @@
 //   KvStore    PA (T, width, pos0), PB (rowStride, kOffset, vOffset)   bindings qkv, kCache, vCache
 //              (caches [ctx][width] f16)
 //   AddRmsNorm PA (C, eps)                                   bindings x (in/out), delta, xn, w; dispatch (rows, 1)
-// Matmul, Attention, MatmulQ8 and MatmulQ4 are dense contractions or attention and are not
-// implemented by the HIP backend: dispatching them throws NekoError.
+//   Matmul / MatmulQ8 / MatmulQ4  PA (K, N = row stride of y, T, flags{1: GELU, 2: accumulate, 4: bias})
+//              PB (xRow0, nOffset)                            bindings x, W rows (F16 / FP8 / FP4), bias, y;
+//              dispatch (weight rows, ceil(T / 4))
+// Attention is not implemented by the HIP backend: dispatching it throws NekoError.
 #pragma once
 
 #include <cstddef>

@@ -87,9 +87,12 @@ public:
             case Kernel::Gelu: gelu(bindings, pa); return;
             case Kernel::KvStore: kvStore(bindings, pa, pb); return;
             case Kernel::AddRmsNorm: addRmsNorm(bindings, pa, gx); return;
+            case Kernel::Matmul: matmul(bindings, pa, pb, gx, NEKO_FMT_F16); return;
+            case Kernel::MatmulQ8: matmul(bindings, pa, pb, gx, NEKO_FMT_FP8); return;
+            case Kernel::MatmulQ4: matmul(bindings, pa, pb, gx, NEKO_FMT_FP4); return;
             default: break;
         }
-        fail(std::string("HIP backend: kernel ") + kernelName(k) + " is not implemented (dense contractions and attention)");
+        fail(std::string("HIP backend: kernel ") + kernelName(k) + " is not implemented (attention)");
     }
 
 private:
@@ -238,6 +241,29 @@ private:
         void* xn = need(b, 2, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
         auto* w = static_cast<const float*>(need(b, 3, uint64_t(C) * 4, "AddRmsNorm"));
         check(neko_hip_add_rmsnorm(ctx_, x, C, d, C, xn, C, w, rows, C, eps, NEKO_DT_F32));
+    }
+
+    // matmul.comp / matmul_q8.comp / matmul_q4.comp: PA (K, N = the row stride of y, T, flags: 1 GELU,
+    // 2 accumulate, 4 bias), PB (xRow0, nOffset); bindings x rows of K, the weight rows, bias, y;
+    // dispatch (weight rows, ceil(T / 4)). y[t][nOffset + n] (+)= act(x[xRow0 + t] . W[n] + bias[n]).
+    void matmul(Buffer* const b[4], const int32_t* pa, const int32_t* pb, uint32_t gx, int fmt) {
+        const int64_t K = pa[0], N = pa[1], T = pa[2], row0 = pb[0], nOff = pb[1], rows = gx;
+        const int flags = pa[3];
+        const char* what = fmt == NEKO_FMT_F16 ? "Matmul" : fmt == NEKO_FMT_FP8 ? "MatmulQ8" : "MatmulQ4";
+        positive(K, what);
+        positive(N, what);
+        positive(T, what);
+        positive(row0, what);
+        positive(nOff, what);
+        if (T == 0 || rows == 0) return;
+        if (nOff + rows > N) fail(std::string("HIP ") + what + ": output columns exceed the row stride of y");
+        const uint64_t rb = neko_quant_row_bytes(fmt, K);
+        auto* x = static_cast<char*>(need(b, 0, uint64_t(row0 + T) * uint64_t(K) * 4, what)) + row0 * K * 4;
+        void* w = need(b, 1, uint64_t(rows) * rb, what);
+        const float* bias = (flags & 4) ? static_cast<const float*>(need(b, 2, uint64_t(rows) * 4, what)) : nullptr;
+        auto* y = static_cast<char*>(need(b, 3, (uint64_t(T - 1) * uint64_t(N) + uint64_t(nOff + rows)) * 4, what)) + nOff * 4;
+        check(neko_hip_matmul(ctx_, x, K, T, K, w, int64_t(rb), fmt, rows, bias, y, N, flags & 3, NEKO_DT_F32,
+                              NEKO_DT_F32));
     }
 
     neko_hip_ctx* ctx_ = nullptr;

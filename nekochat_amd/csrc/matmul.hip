@@ -357,6 +357,182 @@ __global__ __launch_bounds__(64 * max_waves(FMT, TT)) void mm_tile_kernel(MmArgs
     }
 }
 
+// ---------------------------------------------------------------- decode path: VALU GEMV
+
+// Sum over each DPP row of 16 lanes; every lane of the row receives the same bits.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    v += dpp_f32<kDppQuadXor2>(v);
+    v += dpp_f32<kDppRowHalfMirror>(v);
+    v += dpp_f32<kDppRowMirror>(v);
+    return v;
+}
+
+// Two weights as f16 (exact values / 2^8 for FP8, the values for FP4) paired with the activation
+// pair at the same positions of the staged x block; dot of one 32-wide block against token t.
+template <int FMT>
+__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const half_t* xb) {
+    const uint4v* xv = reinterpret_cast<const uint4v*>(xb);
+    float d = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {  // 4 x 8 activations
+        const uint4v xc = xv[c];
+        uint32_t wp[4];
+        if constexpr (FMT == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) wp[i] = q[c][i];
+        } else if constexpr (FMT == 1) {
+            const uint32_t w0 = q[c >> 1][(c & 1) * 2], w1 = q[c >> 1][(c & 1) * 2 + 1];
+            wp[0] = fp8_pair_bits(__builtin_amdgcn_perm(0u, w0, 0x0C010C00u));
+            wp[1] = fp8_pair_bits(__builtin_amdgcn_perm(0u, w0, 0x0C030C02u));
+            wp[2] = fp8_pair_bits(__builtin_amdgcn_perm(0u, w1, 0x0C010C00u));
+            wp[3] = fp8_pair_bits(__builtin_amdgcn_perm(0u, w1, 0x0C030C02u));
+        } else {
+            // Bytes 4c .. 4c+3 of the block: (weight j, weight 16 + j) pairs, matching the staged
+            // x order (x_j, x_16+j).
+            const uint32_t w = q[0][c];
+            wp[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0));
+            wp[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1));
+            wp[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2));
+            wp[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t xw = xc[i];
+            d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wp[i]), __builtin_bit_cast(half2v, xw), d, false);
+        }
+    }
+    return d;
+}
+
+#ifndef NEKO_TUNE_MM_GEMV_MAX_T
+#define NEKO_TUNE_MM_GEMV_MAX_T 4
+#endif
+#ifndef NEKO_TUNE_MM_GEMV_WAVE_TARGET
+#define NEKO_TUNE_MM_GEMV_WAVE_TARGET 8192
+#endif
+constexpr int64_t kGemvMaxT = NEKO_TUNE_MM_GEMV_MAX_T;  // largest T taking the GEMV path
+constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
+constexpr int kGemvRows = 4;    // weight rows per wave: 16 lanes each
+constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw slices of K
+#ifndef NEKO_TUNE_MM_GEMV_BATCH
+#define NEKO_TUNE_MM_GEMV_BATCH 2
+#endif
+constexpr int kGemvBatch = NEKO_TUNE_MM_GEMV_BATCH;  // 32-wide blocks per lane whose weights are requested together
+
+// Grid: x = workgroups of 4 * 8 / kw weight rows, y = chunks of NT tokens. Wave w works on row
+// group w / kw and K slice w % kw (a.blocks_per_wave blocks). Dynamic LDS: the chunk's activations as f16 [NT][K] (FP4: each 32-block
+// stored as (x_j, x_16+j) pairs), then 8 * 4 * NT partial sums.
+template <int FMT, int NT, typename TY>
+__global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int kw) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NW = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;  // 16-byte weight loads per block
+    constexpr int U = kGemvBatch;
+    half_t* xs = reinterpret_cast<half_t*>(lds);
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int rg = wave / kw, ks = wave - rg * kw;  // row group, K slice
+    const int r = lane >> 4, sl = lane & 15;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * NT;
+    const int nt = static_cast<int>(min(static_cast<int64_t>(NT), a.T - t0));
+    const int K = a.K;
+
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * (kGemvWaves / kw) + rg) * kGemvRows + r;
+    const uint8_t* wrow = a.w + min(row, static_cast<int64_t>(a.N) - 1) * a.rb;
+    const int soff = FMT == 1 ? K : K / 2;
+    const int nblk = K / kBlockK;
+    const int b_begin = min(nblk, ks * a.blocks_per_wave);
+    const int b_end = min(nblk, b_begin + a.blocks_per_wave);
+    const int steps = (b_end - b_begin + 15) / 16;  // wave-uniform; 0 for an empty slice
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = 0.0f;
+
+    // Every wave runs at least one batch (the x staging and its barrier are in the first).
+    for (int j0 = 0; j0 == 0 || j0 < steps; j0 += U) {
+        uint4v q[U][NW];
+        float sc[U];
+        bool valid[U];
+        int bl[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int b = b_begin + sl + 16 * (j0 + u);
+            valid[u] = b < b_end;
+            bl[u] = valid[u] ? b : max(b_begin, b_end - 1);  // in bounds and unconditional
+            bl[u] = min(bl[u], nblk - 1);
+#pragma unroll
+            for (int i = 0; i < NW; i++)
+                q[u][i] = *reinterpret_cast<const uint4v*>(wrow + bl[u] * block_bytes(FMT) + 16 * i);
+            sc[u] = 1.0f;
+            if constexpr (FMT != 0)
+                sc[u] = static_cast<float>(*reinterpret_cast<const half_t*>(wrow + soff + 2 * bl[u])) *
+                        block_scale_factor<FMT>();
+        }
+        if (j0 == 0) {
+            // Stage x rows t0 .. t0 + NT - 1 (rows past T are zero) in 16-byte pieces, while the
+            // first weights are in flight.
+            const int kc = K / 8;
+            for (int i = static_cast<int>(threadIdx.x); i < NT * kc; i += static_cast<int>(blockDim.x)) {
+                const int t = i / kc, c = i - t * kc;
+                uint4v v = {0u, 0u, 0u, 0u};
+                if (t < nt) v = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + (t0 + t) * a.xs + 8 * c);
+                half_t* dst = xs + static_cast<int64_t>(t) * K;
+                if constexpr (FMT == 2) {
+                    // Piece c of a block holds k = 8 (c & 3) .. + 7: to 2 k (k < 16) or 2 (k - 16) + 1.
+                    const int kb = 8 * (c & 3), base = (c >> 2) * 32;
+                    const half8 h = __builtin_bit_cast(half8, v);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const int k = kb + e;
+                        dst[base + (k < 16 ? 2 * k : 2 * (k - 16) + 1)] = h[e];
+                    }
+                } else {
+                    *reinterpret_cast<uint4v*>(dst + 8 * c) = v;
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (j0 + u >= steps) break;  // wave-uniform
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float d = block_dot<FMT>(q[u], xs + static_cast<int64_t>(t) * K + bl[u] * kBlockK);
+                const float v = FMT == 0 ? d : d * sc[u];
+                acc[t] += valid[u] ? v : 0.0f;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = row16_sum(acc[t]);
+
+    if (kw > 1) {
+        float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(NT) * K * sizeof(half_t));
+        if (sl == 0) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) red[(wave * kGemvRows + r) * NT + t] = acc[t];
+        }
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            float v = red[(wave * kGemvRows + r) * NT + t];
+            for (int w = 1; w < kw; w++) v += red[((wave + w) * kGemvRows + r) * NT + t];
+            acc[t] = v;
+        }
+    }
+    if (row >= a.N || sl >= nt) return;
+    float v = acc[0];
+#pragma unroll
+    for (int t = 1; t < NT; t++)
+        if (sl == t) v = acc[t];
+    epilogue<TY>(a, t0 + sl, row, v);
+}
+
+__host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
+    return static_cast<size_t>(nt) * K * 2 + static_cast<size_t>(kGemvWaves) * kGemvRows * nt * 4;
+}
+
 // ---------------------------------------------------------------- generic path
 
 // W[row][k] as f32, exact: the code's f16 pattern widened, times 2^8 / 2^14, times the f16 scale.
@@ -409,6 +585,25 @@ __global__ __launch_bounds__(64) void mm_generic_kernel(MmArgs a) {
 }
 
 // ---------------------------------------------------------------- launch
+
+template <int FMT, int NT>
+int launch_gemv(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int kw) {
+    const size_t lds = gemv_lds_bytes(a.K, NT);
+    if (y_dtype == NEKO_DT_F16)
+        hipLaunchKernelGGL((mm_gemv_kernel<FMT, NT, half_t>), grid, dim3(64 * kGemvWaves), lds, ctx->stream, a, kw);
+    else
+        hipLaunchKernelGGL((mm_gemv_kernel<FMT, NT, float>), grid, dim3(64 * kGemvWaves), lds, ctx->stream, a, kw);
+    return after_launch(ctx, "neko_hip_matmul");
+}
+
+template <int FMT>
+int launch_gemv_nt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int kw, int nt) {
+    switch (nt) {
+        case 1: return launch_gemv<FMT, 1>(ctx, a, y_dtype, grid, kw);
+        case 2: return launch_gemv<FMT, 2>(ctx, a, y_dtype, grid, kw);
+        default: return launch_gemv<FMT, 4>(ctx, a, y_dtype, grid, kw);
+    }
+}
 
 template <int FMT, int TT>
 int launch_tile(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int waves) {
@@ -471,6 +666,32 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
              y, y_stride, flags, fmt, 0};
     const bool fast = x_dtype == NEKO_DT_F16 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 8 == 0 &&
                       aligned(w, 16) && row_bytes % 16 == 0;
+    // Decode-sized T: the GEMV path, NT tokens per pass with their activations staged in 64 KB of LDS.
+    int gemv_nt = 0;
+    if (fast && T <= kGemvMaxT) {
+        int nt = T <= 1 ? 1 : T <= 2 ? 2 : 4;
+        while (nt > 1 && gemv_lds_bytes(static_cast<int>(K), nt) > 65536) nt /= 2;
+        if (gemv_lds_bytes(static_cast<int>(K), nt) <= 65536) gemv_nt = nt;
+    }
+    if (gemv_nt > 0) {
+        // kw waves share 4 rows, splitting K; a workgroup holds 8 / kw such row groups. kw: the
+        // smallest power of two giving about kGemvWaveTarget waves, while every lane keeps a block.
+        const int64_t chunks = (T + gemv_nt - 1) / gemv_nt;
+        NEKO_REQUIRE(ctx, chunks <= 65535, "%s: T=%lld exceeds this kernel's grid", what, (long long)T);
+        const int nblk = static_cast<int>(K / kBlockK);
+        int kw = 1;
+        while (kw < kGemvWaves && 2 * kw * 16 <= nblk &&
+               (N + kGemvRows - 1) / kGemvRows * kw * chunks < kGemvWaveTarget)
+            kw *= 2;
+        a.blocks_per_wave = (nblk + kw - 1) / kw;
+        const int64_t rows_per_wg = static_cast<int64_t>(kGemvRows) * (kGemvWaves / kw);
+        const dim3 grid(static_cast<uint32_t>((N + rows_per_wg - 1) / rows_per_wg), static_cast<uint32_t>(chunks));
+        switch (fmt) {
+            case NEKO_FMT_F16: return launch_gemv_nt<0>(ctx, a, y_dtype, grid, kw, gemv_nt);
+            case NEKO_FMT_FP8: return launch_gemv_nt<1>(ctx, a, y_dtype, grid, kw, gemv_nt);
+            default: return launch_gemv_nt<2>(ctx, a, y_dtype, grid, kw, gemv_nt);
+        }
+    }
     if (fast) {
         const int tt = static_cast<int>(std::min<int64_t>(4, (T + 15) / 16));
         const int64_t chunks = (T + 16 * tt - 1) / (16 * tt);

@@ -240,14 +240,81 @@ struct Harness {
         closeOrFail(read(bn, xn.size()), xn, 1e-3f, "add-rmsnorm", false);
     }
 
-    void unsupported() {  // dense kernels are outside the HIP backend and must throw, not run
+    // y[t][nOff + n] = y0 + oracle matmul (bias, no accumulate), the reference cases' expected value.
+    static std::vector<float> expected(int fmt, const std::vector<float>& x, int T, int K, const std::vector<uint8_t>& w,
+                                       int N, const std::vector<float>& bias, int flags, const std::vector<float>& y0,
+                                       int NS, int nOff) {
+        std::vector<float> v(size_t(T) * size_t(N), 0.0f), ref = y0;
+        oracle_matmul(fmt, x.data(), T, K, w.data(), int64_t(w.size() / size_t(N)), N, bias.data(), v.data(), flags & 1);
+        for (int t = 0; t < T; t++)
+            for (int n = 0; n < N; n++) {
+                float& dst = ref[size_t(t * NS + nOff + n)];
+                dst = (flags & 2) ? dst + v[size_t(t * N + n)] : v[size_t(t * N + n)];
+            }
+        return ref;
+    }
+
+    void matmul() {  // compute.cpp:63-104 (F16 rows) and 208-244 (FP8 / FP4 rows)
+        {   // bias + GELU, T = 5 (a partial 4-token tile)
+            const int K = 64, N = 37, T = 5;
+            auto x = rnd(size_t(T * K)), bias = rnd(size_t(N)), wf = rnd(size_t(N * K));
+            auto w = halves(wf);
+            std::vector<uint8_t> wb(w.size() * 2);
+            std::memcpy(wb.data(), w.data(), wb.size());
+            const auto ref = expected(ORACLE_FMT_F16, x, T, K, wb, N, bias, 1, std::vector<float>(size_t(T * N)), N, 0);
+            Buffer* by = be.create(ref.size() * 4, nullptr, true);
+            be.begin();
+            run(Kernel::Matmul, {be.create(x.size() * 4, x.data()), be.create(wb.size(), wb.data()),
+                                 be.create(bias.size() * 4, bias.data()), by},
+                {K, N, T, 4 | 1}, uint32_t(N), uint32_t((T + 3) / 4));
+            be.submitAndWait();
+            closeOrFail(read(by, ref.size()), ref, 2e-3f, "matmul", false);
+        }
+        {   // K = 768, x row offset, accumulate, output column offset
+            const int BK = 768, BN = 96, BT = 6, row0 = 1, nOff = 5, NS = BN + 8;
+            auto bx = rnd(size_t((BT + row0) * BK)), bb = rnd(size_t(BN)), bwf = rnd(size_t(BN * BK));
+            auto y0 = rnd(size_t(BT * NS));
+            auto bw = halves(bwf);
+            std::vector<uint8_t> wb(bw.size() * 2);
+            std::memcpy(wb.data(), bw.data(), wb.size());
+            const std::vector<float> xs(bx.begin() + row0 * BK, bx.end());
+            const auto ref = expected(ORACLE_FMT_F16, xs, BT, BK, wb, BN, bb, 2, y0, NS, nOff);
+            Buffer* by = be.create(y0.size() * 4, y0.data(), true);
+            be.begin();
+            run(Kernel::Matmul, {be.create(bx.size() * 4, bx.data()), be.create(wb.size(), wb.data()),
+                                 be.create(bb.size() * 4, bb.data()), by},
+                {BK, NS, BT, 4 | 2, row0, nOff}, uint32_t(BN), uint32_t((BT + 3) / 4));
+            be.submitAndWait();
+            closeOrFail(read(by, ref.size()), ref, 2e-3f, "matmul-768", false);
+        }
+        // FP8 / FP4 rows: bias + accumulate + output offset, K = 96 and 1024, T = 5.
+        for (int fmt : {ORACLE_FMT_FP8, ORACLE_FMT_FP4}) {
+            for (int K : {96, 1024}) {
+                const int N = 37, T = 5, nOff = 3, NS = N + 5;
+                auto x = rnd(size_t(T * K)), bias = rnd(size_t(N)), wf = rnd(size_t(N * K)), y0 = rnd(size_t(T * NS));
+                std::vector<uint8_t> wb(size_t(N) * oracle_quant_row_bytes(fmt, K));
+                oracle_quantize_rows(fmt, N, K, wf.data(), wb.data());
+                const auto ref = expected(fmt, x, T, K, wb, N, bias, 2, y0, NS, nOff);
+                Buffer* by = be.create(y0.size() * 4, y0.data(), true);
+                be.begin();
+                run(fmt == ORACLE_FMT_FP8 ? Kernel::MatmulQ8 : Kernel::MatmulQ4,
+                    {be.create(x.size() * 4, x.data()), be.create(wb.size(), wb.data()),
+                     be.create(bias.size() * 4, bias.data()), by},
+                    {K, NS, T, 4 | 2, 0, nOff}, uint32_t(N), uint32_t((T + 3) / 4));
+                be.submitAndWait();
+                closeOrFail(read(by, ref.size()), ref, 2e-3f, fmt == ORACLE_FMT_FP8 ? "FP8 matmul" : "FP4 matmul", false);
+            }
+        }
+    }
+
+    void unsupported() {  // attention is outside the HIP backend and must throw, not run
         Buffer* b = be.create(64);
         try {
-            run(Kernel::Matmul, {b, b, nullptr, b}, {4, 4, 1, 0}, 4, 1);
+            run(Kernel::Attention, {b, b, b, b}, {4, 4, 1, 0}, 4, 1);
         } catch (const NekoError&) {
             return;
         }
-        throw Failure{"Matmul dispatch did not throw"};
+        throw Failure{"Attention dispatch did not throw"};
     }
 
     void outOfRange() {  // a dispatch reading past a buffer throws instead of faulting
@@ -281,6 +348,7 @@ extern "C" int backend_selftest(char* err, int err_bytes) {
         h.gatedNorm();
         h.kvStore();
         h.addRmsNorm();
+        h.matmul();
         h.unsupported();
         h.outOfRange();
         std::snprintf(err, size_t(err_bytes), "ok on %s (%s)", be->deviceName().c_str(), be->name());

@@ -36,7 +36,7 @@ def _bound_check(got, exact, mag, K, what):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T", [1, 5, 16, 17, 64, 100])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 16, 17, 64, 100])
 def test_matmul_integer_rows_bitexact(dev, fmt, T):
     """K = 320 (ten 32-blocks: two 4-block groups and a 2-block tail), N = 37 (a partial row tile)."""
     _case(f"matmul integer fmt={fmt} T={T}")
@@ -74,6 +74,9 @@ def test_matmul_integer_rows_bitexact(dev, fmt, T):
     (33, 4096, 2560),   # o projection, three token tiles
     (3, 32, 40),        # one block
     (200, 768, 96),     # GPT-2 width, several token chunks
+    (2, 4096, 2560),    # two-token decode
+    (4, 9728, 64),      # four tokens whose activations exceed one LDS stage: two token chunks
+    (4, 768, 3072),     # GPT-2 MLP, four tokens
 ])
 def test_matmul_random_within_bound(dev, fmt, T, K, N):
     _case(f"matmul random fmt={fmt} T={T} K={K} N={N}")
@@ -115,12 +118,13 @@ def test_matmul_generic_paths(dev):
                 assert np.abs(y - exact).max() <= np.abs(exact).max() * 2.0 ** -10 + 1e-6
 
 
-def test_matmul_accumulate_into_column_slice(dev):
+@pytest.mark.parametrize("T", [3, 20])
+def test_matmul_accumulate_into_column_slice(dev, T):
     """y is columns [64, 64 + N) of a wider f32 buffer (the shaders' nOffset): bias + GELU added into it;
-    the columns outside stay untouched."""
-    _case("matmul accumulate into a column slice")
-    rng = np.random.default_rng(9)
-    T, K, N = 20, 512, 48
+    the columns outside stay untouched (T = 3: the decode path, T = 20: the tile path)."""
+    _case(f"matmul accumulate into a column slice T={T}")
+    rng = np.random.default_rng(9 + T)
+    K, N = 512, 48
     w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
     tab, _ = ops.quantize_rows(ops.FMT_FP8, w)
     wd = M.dequant(ops.FMT_FP8, tab, K)
