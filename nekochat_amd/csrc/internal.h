@@ -20,6 +20,8 @@ struct neko_hip_ctx {
     std::string name;
     std::string err;
     std::unordered_set<void*> allocs;
+    void* workspace = nullptr;  // device scratch for split reductions, grown on demand
+    size_t workspace_bytes = 0;
 };
 
 namespace neko_hip {
@@ -35,6 +37,10 @@ int enter(neko_hip_ctx* ctx);
 int after_launch(neko_hip_ctx* ctx, const char* what);
 
 FastDiv make_fast_div(uint32_t d);
+
+// The context's device workspace, at least `bytes` long (grown on demand: growing waits for the
+// context's stream, since queued work may still read the old one). Shared by every op on ctx.
+int workspace(neko_hip_ctx* ctx, size_t bytes, void** out);
 
 // Workgroups of `block` threads of `kernel` that fit on one CU at once (cached per kernel), and the
 // grid of a persistent kernel: that many per CU, or fewer when there is less work.

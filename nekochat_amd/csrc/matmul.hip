@@ -533,6 +533,242 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
     return static_cast<size_t>(nt) * K * 2 + static_cast<size_t>(kGemvWaves) * kGemvRows * nt * 4;
 }
 
+// ---------------------------------------------------------------- prefill path: MFMA GEMM
+
+// Workgroup tile: BM tokens x BN weight rows (BM = 32 MF, BN = 32 NF), K in 32-wide steps (one
+// FP8/FP4 scale block). Four waves in 2 x 2, each an (16 MF) x (16 NF) tile of
+// v_mfma_f32_16x16x32_f16. Per step the workgroup stages the activation tile and the weight tile --
+// codes decoded once to exact f16 values -- in double-buffered LDS; the next step's global loads are
+// in flight during this step's MFMAs. LDS bytes per MFMA fall as the wave tile grows (both operand
+// fragments are reused across the other dimension), which is what bounds a 64 x 64 wave tile.
+#ifndef NEKO_TUNE_MM_GEMM_MIN_T
+#define NEKO_TUNE_MM_GEMM_MIN_T 128
+#endif
+#ifndef NEKO_TUNE_MM_GEMM_MF
+#define NEKO_TUNE_MM_GEMM_MF 4
+#endif
+#ifndef NEKO_TUNE_MM_GEMM_NF
+#define NEKO_TUNE_MM_GEMM_NF 4
+#endif
+constexpr int64_t kGemmMinT = NEKO_TUNE_MM_GEMM_MIN_T;  // smallest T taking the GEMM path
+constexpr int kGemmMF = NEKO_TUNE_MM_GEMM_MF, kGemmNF = NEKO_TUNE_MM_GEMM_NF;
+constexpr int kGemmBM = 32 * kGemmMF, kGemmBN = 32 * kGemmNF, kGemmBK = 32;
+constexpr int kGemmRow = kGemmBK + 8;  // halves per LDS row: 80 bytes, staggering the banks of rows
+static_assert(kGemmBN == 128, "the weight-tile load split assumes 128 rows per workgroup");
+
+struct GemmLds {
+    half_t a[2][kGemmBM][kGemmRow];
+    half_t b[2][kGemmBN][kGemmRow];
+    float s[2][kGemmBN];  // the step's block scale of each row (times the decode factor)
+};
+
+template <int FMT>
+struct GemmRegs {
+    uint4v a[kGemmBM / 64];                                          // 16-byte activation pieces
+    typename VecOf<uint32_t, FMT == 0 ? 8 : FMT == 1 ? 4 : 2>::V w;  // 32 / 16 / 8 weight bytes
+    half_t s;
+};
+
+// Thread tid's pieces of step k0: activations rows (tid + 256 i) / 4, 16-byte column (tid % 4);
+// weights: F16 the same split of 64-byte row blocks, FP8 row tid / 2 half tid % 2 (16 codes), FP4 row
+// tid / 2 half tid % 2 (8 bytes); scales: thread tid < 128 takes row tid.
+template <int FMT>
+__device__ __forceinline__ void gemm_load(GemmRegs<FMT>& r, const MmArgs& a, int64_t m0, int64_t n0, int k0, int tid) {
+    const int64_t lastT = a.T - 1, lastN = a.N - 1;
+#pragma unroll
+    for (int i = 0; i < kGemmBM / 64; i++) {
+        const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+        const half_t* xr = static_cast<const half_t*>(a.x) + min(m0 + row, lastT) * a.xs;
+        r.a[i] = *reinterpret_cast<const uint4v*>(xr + k0 + 8 * c);
+    }
+    if constexpr (FMT == 0) {
+        uint4v w[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+            w[i] = *reinterpret_cast<const uint4v*>(a.w + min(n0 + row, lastN) * a.rb + 2 * (k0 + 8 * c));
+        }
+        r.w = __builtin_shufflevector(w[0], w[1], 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+        const int row = tid >> 1, h = tid & 1;
+        const uint8_t* wr = a.w + min(n0 + row, lastN) * a.rb;
+        const int bb = block_bytes(FMT);
+        if constexpr (FMT == 1) r.w = *reinterpret_cast<const uint4v*>(wr + (k0 / kBlockK) * bb + 16 * h);
+        else r.w = *reinterpret_cast<const uint2v*>(wr + (k0 / kBlockK) * bb + 8 * h);
+        if (tid < kGemmBN) {
+            const uint8_t* sr = a.w + min(n0 + tid, lastN) * a.rb + (FMT == 1 ? a.K : a.K / 2);
+            r.s = *reinterpret_cast<const half_t*>(sr + 2 * (k0 / kBlockK));
+        }
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void gemm_store(GemmLds& L, int buf, const GemmRegs<FMT>& r, int tid) {
+#pragma unroll
+    for (int i = 0; i < kGemmBM / 64; i++) {
+        const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+        *reinterpret_cast<uint4v*>(&L.a[buf][row][8 * c]) = r.a[i];
+    }
+    if constexpr (FMT == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+            const uint4v v = {r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]};
+            *reinterpret_cast<uint4v*>(&L.b[buf][row][8 * c]) = v;
+        }
+    } else {
+        const int row = tid >> 1, h = tid & 1;
+        if constexpr (FMT == 1) {
+            // 16 codes -> 16 halves at positions 16 h ..
+            uint32_t o[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t q = r.w[i];
+                o[2 * i] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+                o[2 * i + 1] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+            }
+            *reinterpret_cast<uint4v*>(&L.b[buf][row][16 * h]) = uint4v{o[0], o[1], o[2], o[3]};
+            *reinterpret_cast<uint4v*>(&L.b[buf][row][16 * h + 8]) = uint4v{o[4], o[5], o[6], o[7]};
+        } else {
+            // Bytes 8 h .. 8 h + 7: byte i holds weights 8 h + i (low nibble) and 16 + 8 h + i (high):
+            // the hardware conversion yields those pairs, regrouped into natural order.
+            const uint32_t q0 = r.w[0], q1 = r.w[1];
+            const uint32_t c[8] = {
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q0, 1.0f, 0)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q0, 1.0f, 1)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q0, 1.0f, 2)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q0, 1.0f, 3)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q1, 1.0f, 0)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q1, 1.0f, 1)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q1, 1.0f, 2)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(q1, 1.0f, 3))};
+            uint4v lo, hi;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = __builtin_amdgcn_perm(c[2 * i + 1], c[2 * i], 0x05040100u);
+                hi[i] = __builtin_amdgcn_perm(c[2 * i + 1], c[2 * i], 0x07060302u);
+            }
+            *reinterpret_cast<uint4v*>(&L.b[buf][row][8 * h]) = lo;
+            *reinterpret_cast<uint4v*>(&L.b[buf][row][16 + 8 * h]) = hi;
+        }
+        if (tid < kGemmBN) L.s[buf][tid] = static_cast<float>(r.s) * block_scale_factor<FMT>();
+    }
+}
+
+// One 32-wide step of the wave's (16 MF) x (16 NF) tile from LDS buffer buf.
+template <int FMT>
+__device__ __forceinline__ void gemm_step(float4v (&acc)[kGemmMF][kGemmNF], const GemmLds& L, int buf, int wm, int wn,
+                                          int n16, int g) {
+    constexpr int MF = kGemmMF, NF = kGemmNF;
+    half8 B[NF];
+    float sc[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        B[j] = *reinterpret_cast<const half8*>(&L.b[buf][wn * 16 * NF + j * 16 + n16][8 * g]);
+        sc[j] = FMT == 0 ? 1.0f : L.s[buf][wn * 16 * NF + j * 16 + n16];
+    }
+#pragma unroll
+    for (int i = 0; i < MF; i++) {
+        const half8 A = *reinterpret_cast<const half8*>(&L.a[buf][wm * 16 * MF + i * 16 + n16][8 * g]);
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            if constexpr (FMT == 0) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[i][j], 0, 0, 0);
+            } else {
+                const float4v blk =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][j][e] = __builtin_fmaf(sc[j], blk[e], acc[i][j][e]);
+            }
+        }
+    }
+}
+
+// Grid: one workgroup per BM x BN output tile (1-D, remapped: each XCD -- the hardware deals
+// workgroups round-robin over the 8 -- takes a contiguous range, walked in groups of 8 token tiles
+// so that concurrent workgroups share activation and weight tiles in that XCD's L2).
+// With partial != nullptr the grid holds `slices` workgroups per tile, each summing one slice of
+// K's steps into partial[slice][t][n] (f32, row stride N); mm_splitk_reduce adds the slices and
+// applies the epilogue.
+template <int FMT, typename TY>
+__global__ __launch_bounds__(256, 2) void mm_gemm_kernel(MmArgs a, int tiles_m, int tiles_n, int slices, float* partial) {
+    __shared__ __align__(16) GemmLds L;
+    constexpr int MF = kGemmMF, NF = kGemmNF;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6, wm = wave & 1, wn = wave >> 1;
+    const int n16 = lane & 15, g = lane >> 4;
+
+    uint32_t b = blockIdx.x;
+    const uint32_t nb = gridDim.x;
+    if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
+    const int slice = static_cast<int>(b % static_cast<uint32_t>(slices));
+    b /= static_cast<uint32_t>(slices);
+    constexpr int GM = 8;
+    const int group = static_cast<int>(b) / (GM * tiles_n);
+    const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
+    const int in_group = static_cast<int>(b) - group * GM * tiles_n;
+    const int64_t m0 = static_cast<int64_t>(first_m + in_group % gm) * kGemmBM;
+    const int64_t n0 = static_cast<int64_t>(in_group / gm) * kGemmBN;
+
+    float4v acc[MF][NF];
+#pragma unroll
+    for (int i = 0; i < MF; i++)
+#pragma unroll
+        for (int j = 0; j < NF; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Two register sets alternate: each step's global pieces are requested two steps before they are
+    // written to LDS (requests past the last step re-read it: in bounds, never stored), so the loads
+    // have two steps of MFMAs to arrive.
+    const int nk_all = a.K / kGemmBK, per = (nk_all + slices - 1) / slices;
+    const int k_first = slice * per, nk = min(nk_all - k_first, per), lastk = k_first + nk - 1;
+    if (nk > 0) {  // a slice past the end of K (possible only in the last tile's tail) adds zeros
+        GemmRegs<FMT> r0, r1;
+        gemm_load<FMT>(r0, a, m0, n0, k_first * kGemmBK, tid);
+        gemm_load<FMT>(r1, a, m0, n0, min(k_first + 1, lastk) * kGemmBK, tid);
+        gemm_store<FMT>(L, 0, r0, tid);
+        __syncthreads();
+        gemm_load<FMT>(r0, a, m0, n0, min(k_first + 2, lastk) * kGemmBK, tid);
+        for (int ks = 0;; ks += 2) {
+            gemm_step<FMT>(acc, L, 0, wm, wn, n16, g);
+            if (ks + 1 >= nk) break;
+            gemm_store<FMT>(L, 1, r1, tid);
+            __syncthreads();
+            gemm_load<FMT>(r1, a, m0, n0, min(k_first + ks + 3, lastk) * kGemmBK, tid);
+            gemm_step<FMT>(acc, L, 1, wm, wn, n16, g);
+            if (ks + 2 >= nk) break;
+            gemm_store<FMT>(L, 0, r0, tid);
+            __syncthreads();
+            gemm_load<FMT>(r0, a, m0, n0, min(k_first + ks + 4, lastk) * kGemmBK, tid);
+        }
+    }
+    // Lane (n16, g) holds C[token 4g + e][row n16] of each 16 x 16 tile.
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        const int64_t n = n0 + wn * 16 * NF + j * 16 + n16;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < MF; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int64_t t = m0 + wm * 16 * MF + i * 16 + 4 * g + e;
+                if (t >= a.T) continue;
+                if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = acc[i][j][e];
+                else epilogue<TY>(a, t, n, acc[i][j][e]);
+            }
+    }
+}
+
+// y = epilogue(sum over slices of partial[slice][t][n]), slices added in order.
+template <typename TY>
+__global__ __launch_bounds__(256) void mm_splitk_reduce(MmArgs a, const float* partial, int slices) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.T * static_cast<int64_t>(a.N)) return;
+    float v = partial[i];
+    for (int sl = 1; sl < slices; sl++) v += partial[static_cast<int64_t>(sl) * a.T * a.N + i];
+    const int64_t t = i / a.N, n = i - t * a.N;
+    epilogue<TY>(a, t, n, v);
+}
+
 // ---------------------------------------------------------------- generic path
 
 // W[row][k] as f32, exact: the code's f16 pattern widened, times 2^8 / 2^14, times the f16 scale.
@@ -691,6 +927,44 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
             case NEKO_FMT_FP8: return launch_gemv_nt<1>(ctx, a, y_dtype, grid, kw, gemv_nt);
             default: return launch_gemv_nt<2>(ctx, a, y_dtype, grid, kw, gemv_nt);
         }
+    }
+    if (fast && T >= kGemmMinT) {
+        const int64_t tiles_m = (T + kGemmBM - 1) / kGemmBM, tiles_n = (N + kGemmBN - 1) / kGemmBN;
+        const int64_t tiles = tiles_m * tiles_n, nk = K / kGemmBK;
+        // Split K when the tiles alone would leave CUs idle: enough slices for about two workgroups
+        // per CU, each at least 8 steps long.
+        int slices = 1;
+        while (slices < 16 && tiles * slices * 2 <= 2 * ctx->cu_count && nk / (2 * slices) >= 8) slices *= 2;
+        NEKO_REQUIRE(ctx, tiles * slices <= 0x7fffffff, "%s: too many output tiles", what);
+        float* partial = nullptr;
+        if (slices > 1) {
+            void* ws = nullptr;
+            if (int rc = workspace(ctx, static_cast<size_t>(slices) * T * N * sizeof(float), &ws)) return rc;
+            partial = static_cast<float*>(ws);
+        }
+        const dim3 grid(static_cast<uint32_t>(tiles * slices));
+        const int tm = static_cast<int>(tiles_m), tn = static_cast<int>(tiles_n);
+        if (fmt == NEKO_FMT_F16) {
+            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<0, half_t>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+            else hipLaunchKernelGGL((mm_gemm_kernel<0, float>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+        } else if (fmt == NEKO_FMT_FP8) {
+            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<1, half_t>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+            else hipLaunchKernelGGL((mm_gemm_kernel<1, float>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+        } else {
+            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<2, half_t>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+            else hipLaunchKernelGGL((mm_gemm_kernel<2, float>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+        }
+        if (int rc = after_launch(ctx, what)) return rc;
+        if (slices > 1) {
+            const int64_t blocks = (T * N + 255) / 256;
+            NEKO_REQUIRE(ctx, blocks <= 0x7fffffff, "%s: output too large", what);
+            if (y_dtype == NEKO_DT_F16)
+                hipLaunchKernelGGL((mm_splitk_reduce<half_t>), dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a, partial, slices);
+            else
+                hipLaunchKernelGGL((mm_splitk_reduce<float>), dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a, partial, slices);
+            return after_launch(ctx, what);
+        }
+        return NEKO_OK;
     }
     if (fast) {
         const int tt = static_cast<int>(std::min<int64_t>(4, (T + 15) / 16));

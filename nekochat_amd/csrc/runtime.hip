@@ -69,6 +69,23 @@ int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_
     return work_blocks < cap ? work_blocks : cap;
 }
 
+int workspace(neko_hip_ctx* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->workspace_bytes) {
+        if (ctx->workspace) {
+            if (int rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return rc;
+            (void)hipFree(ctx->workspace);
+            ctx->workspace = nullptr;
+            ctx->workspace_bytes = 0;
+        }
+        void* p = nullptr;
+        if (int rc = check(ctx, hipMalloc(&p, bytes), "hipMalloc (workspace)")) return rc;
+        ctx->workspace = p;
+        ctx->workspace_bytes = bytes;
+    }
+    *out = ctx->workspace;
+    return NEKO_OK;
+}
+
 }  // namespace neko_hip
 
 using namespace neko_hip;
@@ -107,6 +124,7 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     int rc = enter(ctx);
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (void* p : ctx->allocs) (void)hipFree(p);
+    if (ctx->workspace) (void)hipFree(ctx->workspace);
     delete ctx;
     return rc;
 }

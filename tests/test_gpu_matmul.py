@@ -36,9 +36,10 @@ def _bound_check(got, exact, mag, K, what):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 16, 17, 64, 100])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 16, 17, 64, 100, 128, 300])
 def test_matmul_integer_rows_bitexact(dev, fmt, T):
-    """K = 320 (ten 32-blocks: two 4-block groups and a 2-block tail), N = 37 (a partial row tile)."""
+    """K = 320 (ten 32-blocks: two 4-block groups and a 2-block tail), N = 37 (a partial row tile).
+    T <= 4: the decode path; 5..127: the MFMA tiles; >= 128: the GEMM (300: a partial token tile)."""
     _case(f"matmul integer fmt={fmt} T={T}")
     rng = np.random.default_rng(100 + 10 * fmt + T)
     K, N = 320, 37
@@ -67,6 +68,24 @@ def test_matmul_integer_rows_bitexact(dev, fmt, T):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+def test_matmul_split_k_integer_bitexact(dev, fmt):
+    """A long K over few output tiles (T = 130, N = 37: two tiles) runs as K slices whose partial
+    sums are reduced afterwards; with integer values every partial is exact, so the result is."""
+    _case(f"matmul split-K integer fmt={fmt}")
+    rng = np.random.default_rng(400 + fmt)
+    T, K, N = 130, 2048, 37
+    tab, w = M.integer_table(fmt, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    out = torch.from_numpy(y0).to(dev)
+    ops.matmul(torch.from_numpy(x).to(dev).half(), torch.from_numpy(tab).to(dev), fmt, K,
+               bias=torch.from_numpy(bias).to(dev), out=out, flags=ops.MM_ACCUMULATE)
+    want = O.matmul(fmt, x, tab, K, bias, y0, ops.MM_ACCUMULATE)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
     (1, 2560, 6144),    # Qwen3-4B decode: q/k/v projection
     (1, 9728, 2560),    # Qwen3-4B decode: down projection
@@ -77,6 +96,9 @@ def test_matmul_integer_rows_bitexact(dev, fmt, T):
     (2, 4096, 2560),    # two-token decode
     (4, 9728, 64),      # four tokens whose activations exceed one LDS stage: two token chunks
     (4, 768, 3072),     # GPT-2 MLP, four tokens
+    (256, 2560, 6144),  # prefill chunk: GEMM tiles
+    (300, 1024, 700),   # partial token and row tiles
+    (512, 9728, 2560),  # down projection, long K
 ])
 def test_matmul_random_within_bound(dev, fmt, T, K, N):
     _case(f"matmul random fmt={fmt} T={T} K={K} N={N}")
