@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = ("achieved HBM GB/s (% of 8 TB/s) per fused op; µs/layer non-GEMM ops, Qwen3-4B")
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 OPS = ("rmsnorm_in", "qk_norm_rope", "rmsnorm_post", "swiglu")
 DOMINANT = "swiglu"
 
@@ -49,7 +50,7 @@ def parse():
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
-                        "qwen3_4b_decode_matmul)")
+                        "qwen3_4b_decode_matmul, qwen3_4b_prefill_matmul)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -433,6 +434,26 @@ def add_cpu_jobs(leg, want):
                         f"{n} of {N} weight rows through cpu::matmul on a one-thread pool (median of {leg.reps}), "
                         f"scaled to all {N}; {core}")
 
+    def prefill_matmul_jobs():  # qwen3_4b_prefill_matmul
+        c, n = wl.QWEN3_PREFILL_MATMUL, 4
+
+        def mm(fmt, N, K):
+            def make():
+                src = _f32((N, K), 0.0, 0.02, 91)
+                tab, used = ops.quantize_rows(fmt, src)
+                h = R.ref_qmatrix_new(used, N, K, P(tab))
+                del tab, src
+                x = _f32((n, K), 0.0, 1.0, 92)
+                y = np.zeros((n, N), np.float32)
+                return (lambda: R.ref_qmatrix_matmul(h, P(x), n, None, P(y), 0)), (lambda: R.ref_qmatrix_free(h))
+            return make
+
+        for pname, N, K in c.projections:
+            for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
+                leg.add("qwen3_4b_prefill_matmul", f"{pname}_{fname}", mm(fmt, N, K), c.T / n,
+                        f"{n} of {c.T} tokens through cpu::matmul on a one-thread pool (median of {leg.reps}), "
+                        f"scaled to all {c.T}; {core}")
+
     # Each workload in its own scope: the closures above read their configuration when they run.
     for label, jobs in (
             ("gpt2_small_chain", gpt2_jobs),
@@ -443,6 +464,7 @@ def add_cpu_jobs(leg, want):
             ("quantize_qwen3_1.7b_table", quantize_jobs),
             ("granite_4.0h_norms", granite_jobs),
             ("qwen3_4b_decode_matmul", matmul_jobs),
+            ("qwen3_4b_prefill_matmul", prefill_matmul_jobs),
     ):
         if want(label):
             jobs()
@@ -461,16 +483,19 @@ def all_configs(args):
     out = {}
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
-              "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul")
+              "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_prefill_matmul")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
     def want(label):
         return args.workload is None or args.workload == label
 
-    def run(label, calls, op_bytes, workload):
+    def run(label, calls, op_bytes, workload, op_flops=None):
         timer = HipTimer(torch.cuda.current_stream().cuda_stream)
         per_op, _ = time_ops(calls, op_bytes, list(calls), args.steps, args.warmup, flush, timer)
+        for n, f in (op_flops or {}).items():  # MFMA-bound ops: their roofline is the dense f16 peak
+            tf = f / (per_op[n]["us"] * 1e-6) / 1e12
+            per_op[n].update({"flops": f, "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
         out[label] = {"workload": workload, "ops": per_op}
         torch.cuda.synchronize()
 
@@ -627,6 +652,27 @@ def all_configs(args):
             "Qwen3-4B decode step, T=1: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
             "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs")
         del calls8
+
+    # Qwen3-4B prefill (T = 8192): the same four weight matmuls, MFMA-bound; flops = 2 T N K.
+    if want("qwen3_4b_prefill_matmul"):
+        c9 = wl.QWEN3_PREFILL_MATMUL
+        calls9, bytes9, flops9 = {}, {}, {}
+        for pname, N, K in c9.projections:
+            wsrc = wl.normal_f16((N, K), 0.0, 0.02, 91, dev).float()
+            x9 = wl.normal_f16((c9.T, K), 0.0, 1.0, 92, dev)
+            y9 = torch.empty((c9.T, N), dtype=torch.float32, device=dev)
+            for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
+                tab9, _ = ops.quantize(wsrc, fmt)
+                name = f"{pname}_{fname}"
+                calls9[name] = ops.prepare(ops.matmul, x9, tab9, fmt, K, out=y9)[0]
+                calls9[name].table = tab9
+                bytes9[name] = wl.bytes_matmul(c9.T, K, N, tab9.shape[1])
+                flops9[name] = 2 * c9.T * N * K
+            del wsrc
+        run("qwen3_4b_prefill_matmul", calls9, bytes9,
+            "Qwen3-4B prefill, T=8192: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
+            "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs", flops9)
+        del calls9
 
     if not args.no_cpu:
         del flush

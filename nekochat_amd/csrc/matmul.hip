@@ -542,7 +542,7 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
 // in flight during this step's MFMAs. LDS bytes per MFMA fall as the wave tile grows (both operand
 // fragments are reused across the other dimension), which is what bounds a 64 x 64 wave tile.
 #ifndef NEKO_TUNE_MM_GEMM_MIN_T
-#define NEKO_TUNE_MM_GEMM_MIN_T 128
+#define NEKO_TUNE_MM_GEMM_MIN_T 48
 #endif
 #ifndef NEKO_TUNE_MM_GEMM_MF
 #define NEKO_TUNE_MM_GEMM_MF 4
@@ -550,21 +550,43 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
 #ifndef NEKO_TUNE_MM_GEMM_NF
 #define NEKO_TUNE_MM_GEMM_NF 4
 #endif
+#ifndef NEKO_TUNE_MM_GEMM_WM
+#define NEKO_TUNE_MM_GEMM_WM 2
+#endif
+#ifndef NEKO_TUNE_MM_GEMM_WN
+#define NEKO_TUNE_MM_GEMM_WN 2
+#endif
 constexpr int64_t kGemmMinT = NEKO_TUNE_MM_GEMM_MIN_T;  // smallest T taking the GEMM path
-constexpr int kGemmMF = NEKO_TUNE_MM_GEMM_MF, kGemmNF = NEKO_TUNE_MM_GEMM_NF;
-constexpr int kGemmBM = 32 * kGemmMF, kGemmBN = 32 * kGemmNF, kGemmBK = 32;
-constexpr int kGemmRow = kGemmBK + 8;  // halves per LDS row: 80 bytes, staggering the banks of rows
-static_assert(kGemmBN == 128, "the weight-tile load split assumes 128 rows per workgroup");
+constexpr int kGemmMF = NEKO_TUNE_MM_GEMM_MF, kGemmNF = NEKO_TUNE_MM_GEMM_NF;  // 16 x 16 fragments per wave
+constexpr int kGemmWM = NEKO_TUNE_MM_GEMM_WM, kGemmWN = NEKO_TUNE_MM_GEMM_WN;  // waves per workgroup
+constexpr int kGemmThreads = 64 * kGemmWM * kGemmWN;
+constexpr int kGemmBM = 16 * kGemmMF * kGemmWM, kGemmBN = 16 * kGemmNF * kGemmWN, kGemmBK = 32;
+#ifndef NEKO_TUNE_MM_GEMM_ROW
+#define NEKO_TUNE_MM_GEMM_ROW 40
+#endif
+#ifndef NEKO_TUNE_MM_GEMM_SWZ
+#define NEKO_TUNE_MM_GEMM_SWZ 0
+#endif
+constexpr int kGemmRow = NEKO_TUNE_MM_GEMM_ROW;  // halves per LDS row (>= 32)
+constexpr int kGemmSwz = NEKO_TUNE_MM_GEMM_SWZ;  // XOR of the 16-byte chunk index with row bits
+static_assert(kGemmBN == kGemmThreads / 2, "the weight-tile load split: two threads per weight row");
+static_assert((kGemmBM * 4) % kGemmThreads == 0, "activation pieces per thread");
+
+// Half offset of 16-byte chunk c (0..3) of row r in a staged tile.
+__device__ __forceinline__ int gemm_off(int r, int c) {
+    const int x = kGemmSwz == 0 ? 0 : kGemmSwz == 1 ? (r & 3) : kGemmSwz == 2 ? ((r >> 1) & 3) : ((r >> 2) & 3);
+    return r * kGemmRow + 8 * (c ^ x);
+}
 
 struct GemmLds {
-    half_t a[2][kGemmBM][kGemmRow];
-    half_t b[2][kGemmBN][kGemmRow];
+    half_t a[2][kGemmBM * kGemmRow];
+    half_t b[2][kGemmBN * kGemmRow];
     float s[2][kGemmBN];  // the step's block scale of each row (times the decode factor)
 };
 
 template <int FMT>
 struct GemmRegs {
-    uint4v a[kGemmBM / 64];                                          // 16-byte activation pieces
+    uint4v a[kGemmBM * 4 / kGemmThreads];                            // 16-byte activation pieces
     typename VecOf<uint32_t, FMT == 0 ? 8 : FMT == 1 ? 4 : 2>::V w;  // 32 / 16 / 8 weight bytes
     half_t s;
 };
@@ -576,8 +598,8 @@ template <int FMT>
 __device__ __forceinline__ void gemm_load(GemmRegs<FMT>& r, const MmArgs& a, int64_t m0, int64_t n0, int k0, int tid) {
     const int64_t lastT = a.T - 1, lastN = a.N - 1;
 #pragma unroll
-    for (int i = 0; i < kGemmBM / 64; i++) {
-        const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+    for (int i = 0; i < kGemmBM * 4 / kGemmThreads; i++) {
+        const int p = tid + kGemmThreads * i, row = p >> 2, c = p & 3;
         const half_t* xr = static_cast<const half_t*>(a.x) + min(m0 + row, lastT) * a.xs;
         r.a[i] = *reinterpret_cast<const uint4v*>(xr + k0 + 8 * c);
     }
@@ -585,7 +607,7 @@ __device__ __forceinline__ void gemm_load(GemmRegs<FMT>& r, const MmArgs& a, int
         uint4v w[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+            const int p = tid + kGemmThreads * i, row = p >> 2, c = p & 3;
             w[i] = *reinterpret_cast<const uint4v*>(a.w + min(n0 + row, lastN) * a.rb + 2 * (k0 + 8 * c));
         }
         r.w = __builtin_shufflevector(w[0], w[1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -605,16 +627,16 @@ __device__ __forceinline__ void gemm_load(GemmRegs<FMT>& r, const MmArgs& a, int
 template <int FMT>
 __device__ __forceinline__ void gemm_store(GemmLds& L, int buf, const GemmRegs<FMT>& r, int tid) {
 #pragma unroll
-    for (int i = 0; i < kGemmBM / 64; i++) {
-        const int p = tid + 256 * i, row = p >> 2, c = p & 3;
-        *reinterpret_cast<uint4v*>(&L.a[buf][row][8 * c]) = r.a[i];
+    for (int i = 0; i < kGemmBM * 4 / kGemmThreads; i++) {
+        const int p = tid + kGemmThreads * i, row = p >> 2, c = p & 3;
+        *reinterpret_cast<uint4v*>(&L.a[buf][gemm_off(row, c)]) = r.a[i];
     }
     if constexpr (FMT == 0) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int p = tid + 256 * i, row = p >> 2, c = p & 3;
+            const int p = tid + kGemmThreads * i, row = p >> 2, c = p & 3;
             const uint4v v = {r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]};
-            *reinterpret_cast<uint4v*>(&L.b[buf][row][8 * c]) = v;
+            *reinterpret_cast<uint4v*>(&L.b[buf][gemm_off(row, c)]) = v;
         }
     } else {
         const int row = tid >> 1, h = tid & 1;
@@ -627,8 +649,8 @@ __device__ __forceinline__ void gemm_store(GemmLds& L, int buf, const GemmRegs<F
                 o[2 * i] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C010C00u));
                 o[2 * i + 1] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C030C02u));
             }
-            *reinterpret_cast<uint4v*>(&L.b[buf][row][16 * h]) = uint4v{o[0], o[1], o[2], o[3]};
-            *reinterpret_cast<uint4v*>(&L.b[buf][row][16 * h + 8]) = uint4v{o[4], o[5], o[6], o[7]};
+            *reinterpret_cast<uint4v*>(&L.b[buf][gemm_off(row, 2 * h)]) = uint4v{o[0], o[1], o[2], o[3]};
+            *reinterpret_cast<uint4v*>(&L.b[buf][gemm_off(row, 2 * h + 1)]) = uint4v{o[4], o[5], o[6], o[7]};
         } else {
             // Bytes 8 h .. 8 h + 7: byte i holds weights 8 h + i (low nibble) and 16 + 8 h + i (high):
             // the hardware conversion yields those pairs, regrouped into natural order.
@@ -648,8 +670,8 @@ __device__ __forceinline__ void gemm_store(GemmLds& L, int buf, const GemmRegs<F
                 lo[i] = __builtin_amdgcn_perm(c[2 * i + 1], c[2 * i], 0x05040100u);
                 hi[i] = __builtin_amdgcn_perm(c[2 * i + 1], c[2 * i], 0x07060302u);
             }
-            *reinterpret_cast<uint4v*>(&L.b[buf][row][8 * h]) = lo;
-            *reinterpret_cast<uint4v*>(&L.b[buf][row][16 + 8 * h]) = hi;
+            *reinterpret_cast<uint4v*>(&L.b[buf][gemm_off(row, h)]) = lo;
+            *reinterpret_cast<uint4v*>(&L.b[buf][gemm_off(row, 2 + h)]) = hi;
         }
         if (tid < kGemmBN) L.s[buf][tid] = static_cast<float>(r.s) * block_scale_factor<FMT>();
     }
@@ -664,12 +686,12 @@ __device__ __forceinline__ void gemm_step(float4v (&acc)[kGemmMF][kGemmNF], cons
     float sc[NF];
 #pragma unroll
     for (int j = 0; j < NF; j++) {
-        B[j] = *reinterpret_cast<const half8*>(&L.b[buf][wn * 16 * NF + j * 16 + n16][8 * g]);
+        B[j] = *reinterpret_cast<const half8*>(&L.b[buf][gemm_off(wn * 16 * NF + j * 16 + n16, g)]);
         sc[j] = FMT == 0 ? 1.0f : L.s[buf][wn * 16 * NF + j * 16 + n16];
     }
 #pragma unroll
     for (int i = 0; i < MF; i++) {
-        const half8 A = *reinterpret_cast<const half8*>(&L.a[buf][wm * 16 * MF + i * 16 + n16][8 * g]);
+        const half8 A = *reinterpret_cast<const half8*>(&L.a[buf][gemm_off(wm * 16 * MF + i * 16 + n16, g)]);
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             if constexpr (FMT == 0) {
@@ -691,11 +713,11 @@ __device__ __forceinline__ void gemm_step(float4v (&acc)[kGemmMF][kGemmNF], cons
 // K's steps into partial[slice][t][n] (f32, row stride N); mm_splitk_reduce adds the slices and
 // applies the epilogue.
 template <int FMT, typename TY>
-__global__ __launch_bounds__(256, 2) void mm_gemm_kernel(MmArgs a, int tiles_m, int tiles_n, int slices, float* partial) {
+__global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int tiles_m, int tiles_n, int slices, float* partial) {
     __shared__ __align__(16) GemmLds L;
     constexpr int MF = kGemmMF, NF = kGemmNF;
     const int tid = static_cast<int>(threadIdx.x);
-    const int lane = tid & 63, wave = tid >> 6, wm = wave & 1, wn = wave >> 1;
+    const int lane = tid & 63, wave = tid >> 6, wm = wave % kGemmWM, wn = wave / kGemmWM;
     const int n16 = lane & 15, g = lane >> 4;
 
     uint32_t b = blockIdx.x;
@@ -945,14 +967,14 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         const dim3 grid(static_cast<uint32_t>(tiles * slices));
         const int tm = static_cast<int>(tiles_m), tn = static_cast<int>(tiles_n);
         if (fmt == NEKO_FMT_F16) {
-            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<0, half_t>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
-            else hipLaunchKernelGGL((mm_gemm_kernel<0, float>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<0, half_t>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
+            else hipLaunchKernelGGL((mm_gemm_kernel<0, float>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
         } else if (fmt == NEKO_FMT_FP8) {
-            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<1, half_t>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
-            else hipLaunchKernelGGL((mm_gemm_kernel<1, float>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<1, half_t>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
+            else hipLaunchKernelGGL((mm_gemm_kernel<1, float>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
         } else {
-            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<2, half_t>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
-            else hipLaunchKernelGGL((mm_gemm_kernel<2, float>), grid, dim3(256), 0, ctx->stream, a, tm, tn, slices, partial);
+            if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<2, half_t>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
+            else hipLaunchKernelGGL((mm_gemm_kernel<2, float>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
         }
         if (int rc = after_launch(ctx, what)) return rc;
         if (slices > 1) {

@@ -174,6 +174,13 @@ class Qwen3DecodeMatmul:
 
 
 @dataclasses.dataclass(frozen=True)
+class Qwen3PrefillMatmul:
+    """Qwen3-4B prefill: the layer's four weight matmuls over 4 x 2048 = 8192 tokens."""
+    T: int = 8192
+    projections: tuple = (("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728))
+
+
+@dataclasses.dataclass(frozen=True)
 class GraniteNorms:
     """Granite-4.0-H-style: 16384 tokens, RMSNorm over 1536, gated norm over d_inner 3072, SwiGLU I = 4096."""
     T: int = 16384
@@ -190,6 +197,7 @@ GPT2_CHAIN = Gpt2Chain()
 QUANT_GATHER = QuantGather()
 GRANITE_NORMS = GraniteNorms()
 QWEN3_DECODE_MATMUL = Qwen3DecodeMatmul()
+QWEN3_PREFILL_MATMUL = Qwen3PrefillMatmul()
 
 
 def qwen3_prefill_inputs(cfg: Qwen3Prefill, device) -> dict:
