@@ -6,8 +6,8 @@ V heads in the qkv buffer and the RoPE cos/sin table are not counted.
 
 Inputs are drawn with torch's Philox generator (seed 0, one stream id per tensor), normals in f32
 then rounded once to fp16; weights are rounded to fp16 (as a checkpoint would hold them) and kept as
-f32. Token ids use numpy's PCG64 with the same seeding. Everything is deterministic for a given
-seed, so tests, the oracle and the benchmark see identical data.
+f32. Token ids use numpy's PCG64 with the same seeding. Everything is deterministic for a given seed
+and device (torch's CPU and GPU generators give different streams; tests draw on the CPU and copy).
 """
 from __future__ import annotations
 

@@ -5,10 +5,17 @@ Run in the container that holds the reference checkout:  python tests/golden/gen
 The fixture is data only (numeric arrays, no pickles); tests/test_oracle.py checks the oracle against it
 and tests/test_gpu_ops.py checks the HIP kernels against it.
 
+It also writes tests/golden/table_sha256.json: the sha256 of the Qwen3-1.7B-shaped tied table
+(151936 x 2048 f32, ~N(0, 0.02), tests/mm_tables.py:qwen3_table_source) and of that table encoded by the
+reference's compiled quantizeMatrix into F16, FP8 and FP4 rows, so the full-size encoders can be pinned
+without storing 1.1 GB of tables.
+
 Inputs are drawn with numpy's PCG64 (seed 0): normals are rounded to fp16 once; weights are fp16-rounded
 then kept as f32, as the reference's loader keeps them.
 """
 import ctypes
+import hashlib
+import json
 import os
 import sys
 
@@ -17,8 +24,10 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.dirname(HERE))
 
 from oracle import oracle as O  # noqa: E402
+from mm_tables import qwen3_table_source  # noqa: E402
 
 P = O._ptr
 F = ctypes.c_float
@@ -174,6 +183,26 @@ def main():
     path = os.path.join(HERE, "golden.npz")
     np.savez_compressed(path, **g)
     print(f"wrote {path}: {len(g)} arrays, {os.path.getsize(path)} bytes")
+    table_hashes(R)
+
+
+def table_hashes(R):
+    """sha256 of the full-size source table and of its F16 / FP8 / FP4 encodings by quantizeMatrix."""
+    x = qwen3_table_source()
+    V, C = x.shape
+    h = {"rows": V, "cols": C, "source": "tests/mm_tables.py:qwen3_table_source (f32, row-major)",
+         "source_sha256": hashlib.sha256(x.data).hexdigest()}
+    for fmt, name in ((0, "f16"), (1, "fp8"), (2, "fp4")):
+        tab = np.empty((V, int(R.ref_quant_row_bytes(fmt, C))), np.uint8)
+        assert R.ref_quantize_rows(fmt, V, C, P(x), P(tab)) == fmt
+        h[f"{name}_row_bytes"] = tab.shape[1]
+        h[f"{name}_sha256"] = hashlib.sha256(tab.data).hexdigest()
+        del tab
+    path = os.path.join(HERE, "table_sha256.json")
+    with open(path, "w") as f:
+        json.dump(h, f, indent=1)
+        f.write("\n")
+    print(f"wrote {path}")
 
 
 if __name__ == "__main__":

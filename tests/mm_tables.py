@@ -83,3 +83,12 @@ def exact_and_bound(x, w, bias=None):
         exact = exact + bias.astype(np.float64)
         mag = mag + np.abs(bias.astype(np.float64))
     return exact, mag
+
+
+def qwen3_table_source(vocab=151936, cols=2048):
+    """The Qwen3-1.7B-shaped tied embedding table in f32, ~N(0, 0.02) from numpy's PCG64 (seed [0, 41]):
+    identical on every machine, so its encoded tables can be pinned by sha256."""
+    rng = np.random.default_rng([0, 41])
+    x = rng.standard_normal((vocab, cols), dtype=np.float32)
+    x *= np.float32(0.02)
+    return x

@@ -640,6 +640,37 @@ def test_quantize_gpu_shapes(dev):
         ops.quantize(torch.zeros((4, 64), dtype=torch.float64, device=dev), ops.FMT_FP8)
 
 
+def test_quantize_and_gather_full_table(dev):
+    """Full size: the device quantiser encodes the 151936 x 2048 f32 table into the bytes whose sha256
+    the reference's compiled quantizeMatrix gave (tests/golden/table_sha256.json), and the gather of
+    16384 Zipf(1.1) ids from each encoded table equals the oracle's, bit for bit."""
+    import hashlib
+    import json
+    import os
+
+    import mm_tables as M
+
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "table_sha256.json")) as f:
+        want = json.load(f)
+    x = M.qwen3_table_source(want["rows"], want["cols"])
+    assert hashlib.sha256(x.data).hexdigest() == want["source_sha256"], "source table generator changed"
+    C = want["cols"]
+    src = torch.from_numpy(x).to(dev)
+    del x
+    cfg = wl.QUANT_GATHER
+    ids = wl.zipf_ids(cfg.T, cfg.vocab, cfg.s, 32)
+    idd = torch.from_numpy(ids).to(dev)
+    for fmt, name in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
+        _case(f"quantize + gather full table fmt={fmt}")
+        tab, used = ops.quantize(src, fmt)
+        assert used == fmt and tab.shape[1] == want[f"{name}_row_bytes"]
+        host = tab.cpu().numpy()
+        assert hashlib.sha256(host.data).hexdigest() == want[f"{name}_sha256"], name
+        out = ops.embed(idd, tab, fmt, C)
+        assert np.array_equal(to_bits(out), O.embed(ids, host, fmt, C))
+        del tab, host, out
+
+
 # ------------------------------------------------------------------ the GPT-2 op chain
 
 def test_gpt2_chain(dev):

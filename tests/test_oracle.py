@@ -7,12 +7,15 @@
    activations, RoPE identities (position 0, norm preservation, the angle table), encoder invariants.
 """
 import ctypes
+import hashlib
+import json
 import math
 import os
 
 import numpy as np
 import pytest
 
+import mm_tables as M
 from conftest import f32_line
 from oracle import oracle as O
 
@@ -267,6 +270,21 @@ def test_ref_quantizer_bitexact(fmt, cols, scale):
         O.lib().oracle_dequantize_row(used, cols, P(got[r]), P(a))
         R.ref_dequantize_row(used, cols, P(got[r]), P(b))
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_full_table_encodings_match_reference_sha256():
+    """The oracle's encoder over the full Qwen3-1.7B tied table (151936 x 2048 f32) gives the same bytes
+    as the reference's compiled quantizeMatrix, pinned by the sha256 values it wrote
+    (tests/golden/table_sha256.json) -- every row, block scale, code and padding byte at full size."""
+    with open(os.path.join(os.path.dirname(GOLDEN), "table_sha256.json")) as f:
+        want = json.load(f)
+    x = M.qwen3_table_source(want["rows"], want["cols"])
+    assert hashlib.sha256(x.data).hexdigest() == want["source_sha256"], "source table generator changed"
+    for fmt, name in ((0, "f16"), (1, "fp8"), (2, "fp4")):
+        tab = O.quantize_rows(fmt, x)
+        assert tab.shape[1] == want[f"{name}_row_bytes"]
+        assert hashlib.sha256(tab.data).hexdigest() == want[f"{name}_sha256"], name
+        del tab
 
 
 # ------------------------------------------------------------------ 3. what the mathematics fixes
