@@ -10,9 +10,12 @@ write back and invalidate the caches; their intervals then match rocprofv3's ker
 the stream it runs on, after a 1 GiB streaming read that
 evicts L2 and the 256 MB Infinity Cache, so every op reads its operands from HBM (the flush is
 outside the event pair). The sweep reads, so it leaves no dirty lines whose write-back the timed op
-would pay for. value = algorithmic bytes of the four ops / sum of their median times.
-ms_per_step is that per-layer kernel time; wall_ms_per_step (the barrier-to-barrier clock of the K
-timed steps, divided by K) also contains the flushes.
+would pay for. The step is then timed as the layer runs it: after one flush, the four ops issued
+back-to-back on the stream inside one event pair (the post-attention RMSNorm reads its own residual
+buffer, so no op finds its input in a cache). value = algorithmic bytes of the four ops / the median
+step time (ms_per_step, us_per_layer); us_per_layer_sum_of_ops adds the per-op medians instead (it
+also counts one event pair's overhead per op, ~1.3 us). wall_ms_per_step (the barrier-to-barrier
+clock of the K timed rounds, divided by K) also contains the flushes.
 
 cpu_baseline: the reference's portable C++ ops (oracle/_ref, compiled from its sources) -- or the
 oracle's C restatement where that is absent -- on f32 activations, one pinned core, over a bounded
@@ -136,6 +139,33 @@ def time_ops(calls, op_bytes, names, steps, warmup, flush, timer):
     return per_op, wall
 
 
+def time_layer(calls, names, steps, warmup, flush, timer):
+    """Times the layer as it runs: per step a cache flush (unless flush is None), then the named ops
+    issued back-to-back inside one event pair. Returns the per-step times in ms."""
+    import torch
+
+    def step(pair):
+        if flush is not None:
+            flush.sum()
+        if pair is not None:
+            timer.record(pair[0])
+        for name in names:
+            calls[name]()
+        if pair is not None:
+            timer.record(pair[1])
+
+    for _ in range(warmup):
+        step(None)
+    pairs = [timer.pair() for _ in range(steps)]
+    torch.cuda.synchronize()
+    for k in range(steps):
+        step(pairs[k])
+    torch.cuda.synchronize()
+    times = [timer.elapsed_ms(*p) for p in pairs]
+    timer.close()
+    return times
+
+
 def gpu_bench(args):
     import torch
 
@@ -146,6 +176,7 @@ def gpu_bench(args):
     cfg = wl.QWEN3_PREFILL
     inp = wl.qwen3_prefill_inputs(cfg, dev)
     xn = torch.empty_like(inp["x"])
+    xn_post = torch.empty_like(inp["x_post"])
     g = torch.empty((cfg.T, cfg.I), dtype=torch.float16, device=dev)
     # 1 GiB swept by a sum: longer than the host needs to queue the next op, so the GPU never waits
     # for Python between the start event and the kernel.
@@ -156,7 +187,7 @@ def gpu_bench(args):
         "rmsnorm_in": ops.prepare(ops.rms_norm, inp["x"], inp["w_in"], cfg.eps, out=xn)[0],
         "qk_norm_rope": ops.prepare(ops.qk_norm_rope, inp["qkv"], cfg.n_q, cfg.n_kv, cfg.hd, inp["cs"], cfg.eps,
                                     wqk=inp["wqk"], positions=inp["positions"])[0],
-        "rmsnorm_post": ops.prepare(ops.rms_norm, inp["x"], inp["w_post"], cfg.eps, out=xn)[0],
+        "rmsnorm_post": ops.prepare(ops.rms_norm, inp["x_post"], inp["w_post"], cfg.eps, out=xn_post)[0],
         "swiglu": ops.prepare(ops.silu_mul, inp["h"], out=g)[0],
     }
     names = [args.only] if args.only else list(OPS)
@@ -170,7 +201,11 @@ def gpu_bench(args):
     timer = HipTimer(torch.cuda.current_stream().cuda_stream)
     per_op, wall = time_ops(calls, cfg.op_bytes(), names, args.steps, args.warmup,
                             None if args.no_flush else flush, timer)
-    return cfg, per_op, wall
+    layer = None
+    if not args.only:
+        layer = time_layer(calls, names, args.steps, args.warmup, None if args.no_flush else flush,
+                           HipTimer(torch.cuda.current_stream().cuda_stream))
+    return cfg, per_op, wall, layer
 
 
 def _pin_one_core():
@@ -763,9 +798,12 @@ def main():
         print(json.dumps({"metric": METRIC, "unit": "GB/s", "data": "synthetic", "configs": all_configs(args)}),
               flush=True)
         return
-    cfg, per_op, wall = gpu_bench(args)
-    total_us = sum(v["us"] for v in per_op.values())
+    cfg, per_op, wall, layer = gpu_bench(args)
+    sum_us = sum(v["us"] for v in per_op.values())
     total_bytes = sum(v["bytes"] for v in per_op.values())
+    # The step: the layer's ops back-to-back after one flush, one event pair (median over steps);
+    # with --only, the one op.
+    total_us = statistics.median(layer) * 1e3 if layer else sum_us
     value = total_bytes / (total_us * 1e-6) / 1e9
     line = {
         "metric": METRIC,
@@ -789,8 +827,11 @@ def main():
         },
         "us_per_layer": round(total_us, 3),
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "us_per_layer_sum_of_ops": round(sum_us, 3),
         "ops": per_op,
     }
+    if layer:
+        line["layer_mean_us"] = round(statistics.fmean(layer) * 1e3, 3)
     if not args.only or args.only == DOMINANT:
         d = per_op[DOMINANT]
         achieved = d["bytes"] / (d["mean_us"] * 1e-6) / 1e9

@@ -208,6 +208,7 @@ def qwen3_prefill_inputs(cfg: Qwen3Prefill, device) -> dict:
         "x": normal_f16((cfg.T, cfg.C), 0.0, 1.0, 1, device),
         "w_in": weight_f32(cfg.C, 1.0, 0.05, 2, device),
         "w_post": weight_f32(cfg.C, 1.0, 0.05, 3, device),
+        "x_post": normal_f16((cfg.T, cfg.C), 0.0, 1.0, 7, device),  # the post-attention residual
         "qkv": normal_f16((cfg.T, cfg.qkv_stride), 0.0, 1.0, 4, device),
         "wqk": weight_f32(2 * cfg.hd, 1.0, 0.05, 5, device),
         "positions": torch.from_numpy(pos).to(device),
