@@ -691,11 +691,15 @@ def all_configs(args):
     # Qwen3-4B prefill (T = 8192): the same four weight matmuls, MFMA-bound; flops = 2 T N K.
     if want("qwen3_4b_prefill_matmul"):
         c9 = wl.QWEN3_PREFILL_MATMUL
-        calls9, bytes9, flops9 = {}, {}, {}
+        calls9, bytes9, flops9, lib9 = {}, {}, {}, {}
         for pname, N, K in c9.projections:
             wsrc = wl.normal_f16((N, K), 0.0, 0.02, 91, dev).float()
             x9 = wl.normal_f16((c9.T, K), 0.0, 1.0, 92, dev)
             y9 = torch.empty((c9.T, N), dtype=torch.float32, device=dev)
+            # The vendor library on the same F16 product (torch.matmul -> hipBLASLt; f16 output):
+            # a reference point for the MFMA kernel, not part of the path.
+            w16, y16 = wsrc.half(), torch.empty((c9.T, N), dtype=torch.float16, device=dev)
+            lib9[f"{pname}_f16"] = (lambda x=x9, w=w16, y=y16: torch.matmul(x, w.t(), out=y))
             for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
                 tab9, _ = ops.quantize(wsrc, fmt)
                 name = f"{pname}_{fname}"
@@ -707,7 +711,13 @@ def all_configs(args):
         run("qwen3_4b_prefill_matmul", calls9, bytes9,
             "Qwen3-4B prefill, T=8192: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
             "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs", flops9)
-        del calls9
+        lib_ops, _ = time_ops(lib9, bytes9, list(lib9), args.steps, args.warmup, flush,
+                              HipTimer(torch.cuda.current_stream().cuda_stream))
+        for n, v in lib_ops.items():
+            tf = flops9[n] / (v["us"] * 1e-6) / 1e12
+            out["qwen3_4b_prefill_matmul"]["ops"][n].update(
+                {"library_us": v["us"], "library_TFLOPs": round(tf, 1), "library": "torch.matmul f16 x f16 -> f16 (hipBLASLt)"})
+        del calls9, lib9
 
     if not args.no_cpu:
         del flush

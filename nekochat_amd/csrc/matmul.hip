@@ -677,10 +677,69 @@ __device__ __forceinline__ void gemm_store(GemmLds& L, int buf, const GemmRegs<F
     }
 }
 
-// One 32-wide step of the wave's (16 MF) x (16 NF) tile from LDS buffer buf.
+// The wave's (16 MF) x (16 NF) accumulator tile, held as 16 x 16 MFMA tiles (v_mfma_f32_16x16x32_f16:
+// lane (n16, g) holds C[4g + e][n16]) or, with kGemm32, as 32 x 32 tiles (v_mfma_f32_32x32x16_f16:
+// lane (l32, h) holds C[8 (v / 4) + 4 h + v % 4][l32] in register v). Measured on MI355X, independent
+// 32 x 32 x 16 MFMAs sustain ~98% of the dense fp16 peak at one wave per SIMD; 16 x 16 x 32 ones need
+// 16 chains per wave at many waves per SIMD to pass ~55%.
+#ifndef NEKO_TUNE_MM_GEMM_M32
+#define NEKO_TUNE_MM_GEMM_M32 1
+#endif
+constexpr bool kGemm32 = NEKO_TUNE_MM_GEMM_M32;
+static_assert(!kGemm32 || (kGemmMF % 2 == 0 && kGemmNF % 2 == 0), "32 x 32 tiles need even fragment counts");
+
+template <bool M32>
+struct GemmAcc {
+    float4v v[kGemmMF][kGemmNF];
+};
+template <>
+struct GemmAcc<true> {
+    float16v v[kGemmMF / 2][kGemmNF / 2];
+};
+
+// One 32-wide step (one scale block) of the wave's tile from LDS buffer buf, 32 x 32 MFMA tiles: the
+// block's k range in two halves of 16, lane (l32, h) supplying 16-byte chunk 2 q + h of its row to
+// MFMA q -- the same chunks on both operands.
 template <int FMT>
-__device__ __forceinline__ void gemm_step(float4v (&acc)[kGemmMF][kGemmNF], const GemmLds& L, int buf, int wm, int wn,
-                                          int n16, int g) {
+__device__ __forceinline__ void gemm_step(GemmAcc<true>& acc, const GemmLds& L, int buf, int wm, int wn, int lane) {
+    constexpr int MF = kGemmMF / 2, NF = kGemmNF / 2;
+    const int l32 = lane & 31, h = lane >> 5;
+    half8 B[NF][2];
+    float sc[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        const int r = wn * 32 * NF + j * 32 + l32;
+#pragma unroll
+        for (int q = 0; q < 2; q++) B[j][q] = *reinterpret_cast<const half8*>(&L.b[buf][gemm_off(r, 2 * q + h)]);
+        sc[j] = FMT == 0 ? 1.0f : L.s[buf][r];
+    }
+#pragma unroll
+    for (int i = 0; i < MF; i++) {
+        const int r = wm * 32 * MF + i * 32 + l32;
+        half8 A[2];
+#pragma unroll
+        for (int q = 0; q < 2; q++) A[q] = *reinterpret_cast<const half8*>(&L.a[buf][gemm_off(r, 2 * q + h)]);
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            if constexpr (FMT == 0) {
+                acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[j][0], acc.v[i][j], 0, 0, 0);
+                acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[j][1], acc.v[i][j], 0, 0, 0);
+            } else {
+                float16v blk = {};
+                blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[j][0], blk, 0, 0, 0);
+                blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[j][1], blk, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc.v[i][j][e] = __builtin_fmaf(sc[j], blk[e], acc.v[i][j][e]);
+            }
+        }
+    }
+}
+
+// One 32-wide step of the wave's (16 MF) x (16 NF) tile from LDS buffer buf, 16 x 16 MFMA tiles.
+template <int FMT>
+__device__ __forceinline__ void gemm_step(GemmAcc<false>& acc_t, const GemmLds& L, int buf, int wm, int wn, int lane) {
+    float4v (&acc)[kGemmMF][kGemmNF] = acc_t.v;
+    const int n16 = lane & 15, g = lane >> 4;
     constexpr int MF = kGemmMF, NF = kGemmNF;
     half8 B[NF];
     float sc[NF];
@@ -732,11 +791,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int 
     const int64_t m0 = static_cast<int64_t>(first_m + in_group % gm) * kGemmBM;
     const int64_t n0 = static_cast<int64_t>(in_group / gm) * kGemmBN;
 
-    float4v acc[MF][NF];
-#pragma unroll
-    for (int i = 0; i < MF; i++)
-#pragma unroll
-        for (int j = 0; j < NF; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    GemmAcc<kGemm32> acc = {};
 
     // Two register sets alternate: each step's global pieces are requested two steps before they are
     // written to LDS (requests past the last step re-read it: in bounds, never stored), so the loads
@@ -751,32 +806,43 @@ __global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int 
         __syncthreads();
         gemm_load<FMT>(r0, a, m0, n0, min(k_first + 2, lastk) * kGemmBK, tid);
         for (int ks = 0;; ks += 2) {
-            gemm_step<FMT>(acc, L, 0, wm, wn, n16, g);
+            gemm_step<FMT>(acc, L, 0, wm, wn, lane);
             if (ks + 1 >= nk) break;
             gemm_store<FMT>(L, 1, r1, tid);
             __syncthreads();
             gemm_load<FMT>(r1, a, m0, n0, min(k_first + ks + 3, lastk) * kGemmBK, tid);
-            gemm_step<FMT>(acc, L, 1, wm, wn, n16, g);
+            gemm_step<FMT>(acc, L, 1, wm, wn, lane);
             if (ks + 2 >= nk) break;
             gemm_store<FMT>(L, 0, r0, tid);
             __syncthreads();
             gemm_load<FMT>(r0, a, m0, n0, min(k_first + ks + 4, lastk) * kGemmBK, tid);
         }
     }
-    // Lane (n16, g) holds C[token 4g + e][row n16] of each 16 x 16 tile.
+    auto put = [&](int64_t t, int64_t n, float v) {
+        if (t >= a.T || n >= a.N) return;
+        if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = v;
+        else epilogue<TY>(a, t, n, v);
+    };
+    if constexpr (kGemm32) {
+        // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
+        const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int j = 0; j < NF; j++) {
-        const int64_t n = n0 + wn * 16 * NF + j * 16 + n16;
-        if (n >= a.N) continue;
+        for (int j = 0; j < NF / 2; j++)
 #pragma unroll
-        for (int i = 0; i < MF; i++)
+            for (int i = 0; i < MF / 2; i++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int64_t t = m0 + wm * 16 * MF + i * 16 + 4 * g + e;
-                if (t >= a.T) continue;
-                if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = acc[i][j][e];
-                else epilogue<TY>(a, t, n, acc[i][j][e]);
-            }
+                for (int e = 0; e < 16; e++)
+                    put(m0 + wm * 16 * MF + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3), n0 + wn * 16 * NF + j * 32 + l32,
+                        acc.v[i][j][e]);
+    } else {
+        // Lane (n16, g) holds C[token 4g + e][row n16] of each 16 x 16 tile.
+#pragma unroll
+        for (int j = 0; j < NF; j++)
+#pragma unroll
+            for (int i = 0; i < MF; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    put(m0 + wm * 16 * MF + i * 16 + 4 * g + e, n0 + wn * 16 * NF + j * 16 + n16, acc.v[i][j][e]);
     }
 }
 
@@ -789,6 +855,318 @@ __global__ __launch_bounds__(256) void mm_splitk_reduce(MmArgs a, const float* p
     for (int sl = 1; sl < slices; sl++) v += partial[static_cast<int64_t>(sl) * a.T * a.N + i];
     const int64_t t = i / a.N, n = i - t * a.N;
     epilogue<TY>(a, t, n, v);
+}
+
+// ---------------------------------------------------------------- prefill GEMM, 64-wide stages
+//
+// Workgroup tiles of BM tokens x BN weight rows over WGM x WGN waves, each wave a (32 TM) x (32 TN)
+// grid of v_mfma_f32_32x32x16_f16 tiles; K staged 64 at a time -- two scale blocks per LDS stage --
+// with one set of prefetch registers a stage ahead (the loads have a whole stage of MFMAs to
+// arrive) and double-buffered LDS (one barrier per stage). LDS rows are 64 halves padded to 72
+// (144 bytes: the 16 rows a ds_read_b128 serves per pass fall on distinct 16-byte bank groups).
+// Tile size sets the reuse: every stage loads (BM + BN) x 64 operands for BM x BN x 64 MACs, and at
+// 128 x 128 feeding the MFMAs at full rate would take all of the L2's bandwidth (measured: the L1s
+// then wait on L2 half the time). Large FP8 / FP4 problems take 256-token x 128-row tiles (one
+// workgroup of eight waves per CU, 110 KB of LDS), which also decode each weight tile once per 256
+// tokens: measured 10-20% faster than 128 x 128 there, and slightly slower for F16, which keeps
+// 128 x 128. (256 x 256 tiles need 128 accumulators per lane besides the staging registers and
+// spill at two waves per SIMD.) Needs K % 64 == 0; other K take the 32-wide kernel above.
+#ifndef NEKO_TUNE_MM_GEMM_V2
+#define NEKO_TUNE_MM_GEMM_V2 1
+#endif
+#ifndef NEKO_TUNE_MM_G2_ROW
+#define NEKO_TUNE_MM_G2_ROW 72
+#endif
+#ifndef NEKO_TUNE_MM_GEMM_BIG
+#define NEKO_TUNE_MM_GEMM_BIG 1
+#endif
+constexpr bool kGemmV2 = NEKO_TUNE_MM_GEMM_V2;
+constexpr bool kGemmBig = NEKO_TUNE_MM_GEMM_BIG;  // FP8 / FP4 take the 256-token tiles when their grid fills the GPU
+constexpr int kG2Row = NEKO_TUNE_MM_G2_ROW;     // halves per staged row (>= 64, a multiple of 8)
+constexpr int kG2BK = 64;
+#ifndef NEKO_TUNE_MM_G2_DEPTH
+#define NEKO_TUNE_MM_G2_DEPTH 2
+#endif
+constexpr int kG2Depth = NEKO_TUNE_MM_G2_DEPTH;  // F16: stages of global prefetch in registers (1 or 2)
+
+template <int BM_, int BN_, int WGM_, int WGN_>
+struct G2Cfg {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int threads = 64 * WGM * WGN;
+    static constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;  // 32 x 32 tiles per wave
+    static_assert(TM * 32 * WGM == BM && TN * 32 * WGN == BN, "wave tiles of whole 32 x 32 MFMA tiles");
+    static_assert(BM * 8 % threads == 0 && BN * 4 % threads == 0 && BN * 2 <= threads,
+                  "load split: whole pieces per thread, at most one scale per thread");
+};
+typedef G2Cfg<128, 128, 2, 2> G2Small;
+typedef G2Cfg<256, 128, 4, 2> G2Big;
+
+template <class C>
+struct Gemm2Lds {
+    half_t a[2][C::BM * kG2Row];
+    half_t b[2][C::BN * kG2Row];
+    float s[2][2][C::BN];  // [buffer][block of the stage][row]: f16 scale times the decode factor
+};
+
+template <int FMT, class C>
+struct Gemm2Regs {
+    static constexpr int NA = C::BM * 8 / C::threads;   // activation pieces (16 bytes) per thread
+    static constexpr int NW = C::BN * (FMT == 0 ? 8 : 4) / C::threads;
+    uint4v a[NA];
+    typename VecOf<uint32_t, FMT == 2 ? 2 : 4>::V w[NW];  // F16: 8 halves; FP8: 16 codes; FP4: half a block (16 codes)
+    half_t s;  // FP8 / FP4: the scale of (row tid / 2, block tid % 2), threads below 2 BN
+};
+
+// Stage k0 (a multiple of 64). Activation piece p = tid + threads i: row p / 8, 16-byte column p % 8
+// (each row's 128 bytes from 8 neighbouring threads). F16 weights the same; FP8 piece p: row p / 4,
+// 16 codes at byte 16 (p % 4) of the stage's 64; FP4 piece p: row p / 4, 8 bytes at byte 8 (p % 4) of
+// the stage's 32 (half of block (p % 4) / 2).
+template <int FMT, class C>
+__device__ __forceinline__ void gemm2_load(Gemm2Regs<FMT, C>& r, const MmArgs& a, int64_t m0, int64_t n0, int k0, int tid) {
+    typedef Gemm2Regs<FMT, C> R;
+    const int64_t lastT = a.T - 1, lastN = a.N - 1;
+#pragma unroll
+    for (int i = 0; i < R::NA; i++) {
+        const int p = tid + C::threads * i, row = p >> 3, c = p & 7;
+        const half_t* xr = static_cast<const half_t*>(a.x) + min(m0 + row, lastT) * a.xs;
+        r.a[i] = *reinterpret_cast<const uint4v*>(xr + k0 + 8 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < R::NW; i++) {
+        const int p = tid + C::threads * i;
+        if constexpr (FMT == 0) {
+            const int row = p >> 3, c = p & 7;
+            r.w[i] = *reinterpret_cast<const uint4v*>(a.w + min(n0 + row, lastN) * a.rb + 2 * (k0 + 8 * c));
+        } else if constexpr (FMT == 1) {
+            const int row = p >> 2, c = p & 3;
+            r.w[i] = *reinterpret_cast<const uint4v*>(a.w + min(n0 + row, lastN) * a.rb + k0 + 16 * c);
+        } else {
+            const int row = p >> 2, c = p & 3;
+            r.w[i] = *reinterpret_cast<const uint2v*>(a.w + min(n0 + row, lastN) * a.rb + k0 / 2 + 8 * c);
+        }
+    }
+    if (FMT != 0 && (C::BN * 2 == C::threads || tid < C::BN * 2)) {
+        const int row = tid >> 1, bb = tid & 1;
+        const uint8_t* sr = a.w + min(n0 + row, lastN) * a.rb + (FMT == 1 ? a.K : a.K / 2);
+        r.s = *reinterpret_cast<const half_t*>(sr + 2 * (k0 / kBlockK + bb));
+    }
+}
+
+// FP4 byte SEL of word q -> its two weights as f16 (low nibble first); SEL must be a literal.
+#define NEKO_FP4_PAIR(q, SEL) __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4((q), 1.0f, SEL))
+
+template <int FMT, class C>
+__device__ __forceinline__ void gemm2_store(Gemm2Lds<C>& L, int buf, const Gemm2Regs<FMT, C>& r, int tid) {
+    typedef Gemm2Regs<FMT, C> R;
+#pragma unroll
+    for (int i = 0; i < R::NA; i++) {
+        const int p = tid + C::threads * i, row = p >> 3, c = p & 7;
+        *reinterpret_cast<uint4v*>(&L.a[buf][row * kG2Row + 8 * c]) = r.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < R::NW; i++) {
+        const int p = tid + C::threads * i;
+        if constexpr (FMT == 0) {
+            const int row = p >> 3, c = p & 7;
+            *reinterpret_cast<uint4v*>(&L.b[buf][row * kG2Row + 8 * c]) = r.w[i];
+        } else if constexpr (FMT == 1) {
+            const int row = p >> 2, c = p & 3;  // 16 codes -> halves 16 c .. 16 c + 15
+            uint32_t o[8];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint32_t q = r.w[i][w];
+                o[2 * w] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+                o[2 * w + 1] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+            }
+            half_t* dst = &L.b[buf][row * kG2Row + 16 * c];
+            *reinterpret_cast<uint4v*>(dst) = uint4v{o[0], o[1], o[2], o[3]};
+            *reinterpret_cast<uint4v*>(dst + 8) = uint4v{o[4], o[5], o[6], o[7]};
+        } else {
+            // Bytes 8 u .. 8 u + 7 of block v (c = 2 v + u): byte j holds weights j (low nibble) and
+            // 16 + j (high nibble); the conversion yields those pairs, regrouped into natural order at
+            // halves 32 v + 8 u (low) and 32 v + 16 + 8 u (high).
+            const int row = p >> 2, c = p & 3, v = c >> 1, u = c & 1;
+            uint32_t pr[8];
+#pragma unroll
+            for (int w = 0; w < 2; w++) {
+                const uint32_t q = r.w[i][w];
+                pr[4 * w] = NEKO_FP4_PAIR(q, 0);
+                pr[4 * w + 1] = NEKO_FP4_PAIR(q, 1);
+                pr[4 * w + 2] = NEKO_FP4_PAIR(q, 2);
+                pr[4 * w + 3] = NEKO_FP4_PAIR(q, 3);
+            }
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                lo[j] = __builtin_amdgcn_perm(pr[2 * j + 1], pr[2 * j], 0x05040100u);
+                hi[j] = __builtin_amdgcn_perm(pr[2 * j + 1], pr[2 * j], 0x07060302u);
+            }
+            half_t* dst = &L.b[buf][row * kG2Row + 32 * v + 8 * u];
+            *reinterpret_cast<uint4v*>(dst) = uint4v{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<uint4v*>(dst + 16) = uint4v{hi[0], hi[1], hi[2], hi[3]};
+        }
+    }
+    if (FMT != 0 && (C::BN * 2 == C::threads || tid < C::BN * 2))
+        L.s[buf][tid & 1][tid >> 1] = static_cast<float>(r.s) * block_scale_factor<FMT>();
+}
+#undef NEKO_FP4_PAIR
+
+template <class C>
+struct Gemm2Acc {
+    float16v v[C::TM][C::TN];
+};
+
+// The stage in LDS buffer buf: for each of its two blocks, lane (l32, h) reads 16-byte chunk
+// 4 bb + 2 q + h of its rows for MFMA q -- the same chunks on both operands.
+template <int FMT, class C>
+__device__ __forceinline__ void gemm2_step(Gemm2Acc<C>& acc, const Gemm2Lds<C>& L, int buf, int wm, int wn, int lane) {
+    constexpr int TM = C::TM, TN = C::TN;
+    const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int bb = 0; bb < 2; bb++) {
+        half8 B[TN][2];
+        float sc[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int r = wn * 32 * TN + j * 32 + l32;
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+                B[j][q] = *reinterpret_cast<const half8*>(&L.b[buf][r * kG2Row + 8 * (4 * bb + 2 * q + h)]);
+            sc[j] = FMT == 0 ? 1.0f : L.s[buf][bb][r];
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int r = wm * 32 * TM + i * 32 + l32;
+            half8 A[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+                A[q] = *reinterpret_cast<const half8*>(&L.a[buf][r * kG2Row + 8 * (4 * bb + 2 * q + h)]);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (FMT == 0) {
+                    acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[j][0], acc.v[i][j], 0, 0, 0);
+                    acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[j][1], acc.v[i][j], 0, 0, 0);
+                } else {
+                    float16v blk = {};
+                    blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[j][0], blk, 0, 0, 0);
+                    blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[j][1], blk, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc.v[i][j][e] = __builtin_fmaf(sc[j], blk[e], acc.v[i][j][e]);
+                }
+            }
+        }
+    }
+}
+
+// Grid and split of K as mm_gemm_kernel (tiles of BM x BN), in stages of 64.
+template <int FMT, typename TY, class C>
+__global__ __launch_bounds__(C::threads, 2) void mm_gemm2_kernel(MmArgs a, int tiles_m, int tiles_n, int slices, float* partial) {
+    extern __shared__ __align__(16) uint8_t g2_lds[];
+    Gemm2Lds<C>& L = *reinterpret_cast<Gemm2Lds<C>*>(g2_lds);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & 63, wave = tid >> 6, wm = wave % C::WGM, wn = wave / C::WGM;
+
+    uint32_t b = blockIdx.x;
+    const uint32_t nb = gridDim.x;
+    if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
+    const int slice = static_cast<int>(b % static_cast<uint32_t>(slices));
+    b /= static_cast<uint32_t>(slices);
+    constexpr int GM = 8;
+    const int group = static_cast<int>(b) / (GM * tiles_n);
+    const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
+    const int in_group = static_cast<int>(b) - group * GM * tiles_n;
+    const int64_t m0 = static_cast<int64_t>(first_m + in_group % gm) * C::BM;
+    const int64_t n0 = static_cast<int64_t>(in_group / gm) * C::BN;
+
+    Gemm2Acc<C> acc = {};
+    const int nk_all = a.K / kG2BK, per = (nk_all + slices - 1) / slices;
+    const int k_first = slice * per, nk = min(nk_all - k_first, per), lastk = k_first + nk - 1;
+    constexpr int depth = FMT == 0 ? kG2Depth : 1;  // the scaled formats have no registers for a second set
+    if (nk > 0 && depth == 1) {
+        Gemm2Regs<FMT, C> r;
+        gemm2_load<FMT, C>(r, a, m0, n0, k_first * kG2BK, tid);
+        gemm2_store<FMT, C>(L, 0, r, tid);
+        __syncthreads();
+        gemm2_load<FMT, C>(r, a, m0, n0, min(k_first + 1, lastk) * kG2BK, tid);
+        for (int s = 0;; s++) {
+            gemm2_step<FMT, C>(acc, L, s & 1, wm, wn, lane);
+            if (s + 1 >= nk) break;
+            gemm2_store<FMT, C>(L, (s + 1) & 1, r, tid);
+            __syncthreads();
+            gemm2_load<FMT, C>(r, a, m0, n0, min(k_first + s + 2, lastk) * kG2BK, tid);
+        }
+    } else if (nk > 0) {
+        // Two register sets alternate, each stage's loads requested two stages before they are
+        // stored (requests past the last stage re-read it: in bounds, never stored).
+        Gemm2Regs<FMT, C> r0, r1;
+        gemm2_load<FMT, C>(r0, a, m0, n0, k_first * kG2BK, tid);
+        gemm2_load<FMT, C>(r1, a, m0, n0, min(k_first + 1, lastk) * kG2BK, tid);
+        gemm2_store<FMT, C>(L, 0, r0, tid);
+        __syncthreads();
+        gemm2_load<FMT, C>(r0, a, m0, n0, min(k_first + 2, lastk) * kG2BK, tid);
+        for (int s = 0;; s += 2) {
+            gemm2_step<FMT, C>(acc, L, 0, wm, wn, lane);
+            if (s + 1 >= nk) break;
+            gemm2_store<FMT, C>(L, 1, r1, tid);
+            __syncthreads();
+            gemm2_load<FMT, C>(r1, a, m0, n0, min(k_first + s + 3, lastk) * kG2BK, tid);
+            gemm2_step<FMT, C>(acc, L, 1, wm, wn, lane);
+            if (s + 2 >= nk) break;
+            gemm2_store<FMT, C>(L, 0, r0, tid);
+            __syncthreads();
+            gemm2_load<FMT, C>(r0, a, m0, n0, min(k_first + s + 4, lastk) * kG2BK, tid);
+        }
+    }
+    // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
+    const int l32 = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) {
+        const int64_t n = n0 + wn * 32 * C::TN + j * 32 + l32;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int64_t t = m0 + wm * 32 * C::TM + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (t >= a.T) continue;
+                if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = acc.v[i][j][e];
+                else epilogue<TY>(a, t, n, acc.v[i][j][e]);
+            }
+    }
+}
+
+template <int FMT, typename TY, class C>
+int launch_gemm2(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn, int slices, float* partial) {
+    constexpr size_t lds = sizeof(Gemm2Lds<C>);
+    static bool attr_set = false;  // dynamic LDS above 64 KB is enabled once per instantiation
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mm_gemm2_kernel<FMT, TY, C>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return fail(ctx, NEKO_ERR_HIP, "matmul: hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((mm_gemm2_kernel<FMT, TY, C>), grid, dim3(C::threads), lds, ctx->stream, a, tm, tn, slices, partial);
+    return NEKO_OK;
+}
+
+template <class C>
+int launch_gemm2_fmt(neko_hip_ctx* ctx, int fmt, int y_dtype, dim3 grid, const MmArgs& a, int tm, int tn, int slices,
+                     float* partial) {
+    const bool f16 = y_dtype == NEKO_DT_F16;
+    switch (fmt) {
+        case NEKO_FMT_F16:
+            if constexpr (C::BM == G2Small::BM)
+                return f16 ? launch_gemm2<0, half_t, C>(ctx, grid, a, tm, tn, slices, partial)
+                           : launch_gemm2<0, float, C>(ctx, grid, a, tm, tn, slices, partial);
+            else
+                return fail(ctx, NEKO_ERR_INVALID, "matmul: F16 rows take the 128 x 128 tiles");
+        case NEKO_FMT_FP8:
+            return f16 ? launch_gemm2<1, half_t, C>(ctx, grid, a, tm, tn, slices, partial)
+                       : launch_gemm2<1, float, C>(ctx, grid, a, tm, tn, slices, partial);
+        default:
+            return f16 ? launch_gemm2<2, half_t, C>(ctx, grid, a, tm, tn, slices, partial)
+                       : launch_gemm2<2, float, C>(ctx, grid, a, tm, tn, slices, partial);
+    }
 }
 
 // ---------------------------------------------------------------- generic path
@@ -951,6 +1329,17 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         }
     }
     if (fast && T >= kGemmMinT) {
+        const bool v2 = kGemmV2 && K % kG2BK == 0;
+        // FP8 / FP4: 256-token x 128-row tiles (one workgroup per CU) when they alone give every CU a
+        // workgroup.
+        const int64_t big_m = (T + G2Big::BM - 1) / G2Big::BM, big_n = (N + G2Big::BN - 1) / G2Big::BN;
+        if (v2 && kGemmBig && fmt != NEKO_FMT_F16 && big_m * big_n >= ctx->cu_count) {
+            NEKO_REQUIRE(ctx, big_m * big_n <= 0x7fffffff, "%s: too many output tiles", what);
+            if (int rc = launch_gemm2_fmt<G2Big>(ctx, fmt, y_dtype, dim3(static_cast<uint32_t>(big_m * big_n)), a,
+                                                 static_cast<int>(big_m), static_cast<int>(big_n), 1, nullptr))
+                return rc;
+            return after_launch(ctx, what);
+        }
         const int64_t tiles_m = (T + kGemmBM - 1) / kGemmBM, tiles_n = (N + kGemmBN - 1) / kGemmBN;
         const int64_t tiles = tiles_m * tiles_n, nk = K / kGemmBK;
         // Split K when the tiles alone would leave CUs idle: enough slices for about two workgroups
@@ -966,7 +1355,9 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         }
         const dim3 grid(static_cast<uint32_t>(tiles * slices));
         const int tm = static_cast<int>(tiles_m), tn = static_cast<int>(tiles_n);
-        if (fmt == NEKO_FMT_F16) {
+        if (v2) {
+            if (int rc = launch_gemm2_fmt<G2Small>(ctx, fmt, y_dtype, grid, a, tm, tn, slices, partial)) return rc;
+        } else if (fmt == NEKO_FMT_F16) {
             if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_gemm_kernel<0, half_t>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
             else hipLaunchKernelGGL((mm_gemm_kernel<0, float>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
         } else if (fmt == NEKO_FMT_FP8) {

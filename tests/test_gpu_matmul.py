@@ -87,6 +87,32 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
+    (1000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
+    (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
+    (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
+])
+def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
+    """Integer-valued weights and activations through each GEMM tiling: every partial sum is exact,
+    so y = bias + x . w (+ y0 with accumulate) is bit-identical to the float64 product rounded once."""
+    _case(f"matmul GEMM tiling integer fmt={fmt} T={T} K={K} N={N}")
+    rng = np.random.default_rng(500 + fmt + T + K)
+    tab, w = M.integer_table(fmt, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T + bias
+    assert np.abs(exact).max() < 2 ** 24
+    xd, td, bd = (torch.from_numpy(v).to(dev) for v in (x.astype(np.float16), tab, bias))
+    got = ops.matmul(xd, td, fmt, K, bias=bd).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), exact.astype(np.float32).view(np.uint32))
+    out = torch.from_numpy(y0).to(dev)
+    ops.matmul(xd, td, fmt, K, bias=bd, out=out, flags=ops.MM_ACCUMULATE)
+    want = (y0.astype(np.float64) + exact).astype(np.float32)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,K,N", [
     (1, 2560, 6144),    # Qwen3-4B decode: q/k/v projection
     (1, 9728, 2560),    # Qwen3-4B decode: down projection
     (8, 2560, 19456),   # Qwen3-4B batch-8 decode: gate/up projection
@@ -99,6 +125,7 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
     (256, 2560, 6144),  # prefill chunk: GEMM tiles
     (300, 1024, 700),   # partial token and row tiles
     (512, 9728, 2560),  # down projection, long K
+    (512, 2560, 16384), # FP8 / FP4: 256-token x 128-row tiles
 ])
 def test_matmul_random_within_bound(dev, fmt, T, K, N):
     _case(f"matmul random fmt={fmt} T={T} K={K} N={N}")
