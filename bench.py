@@ -578,9 +578,10 @@ def all_configs(args):
 
     # Qwen3-4B prefill (the headline layer)
     if want("qwen3_4b_prefill"):
-        cfg, per_op, _ = gpu_bench(argparse.Namespace(only=None, copy_mib=0, steps=args.steps, warmup=args.warmup,
-                                                      no_flush=False))
-        out["qwen3_4b_prefill"] = {"workload": "Qwen3-4B prefill layer (headline)", "ops": per_op}
+        cfg, per_op, _, layer = gpu_bench(argparse.Namespace(only=None, copy_mib=0, steps=args.steps,
+                                                             warmup=args.warmup, no_flush=False))
+        out["qwen3_4b_prefill"] = {"workload": "Qwen3-4B prefill layer (headline)", "ops": per_op,
+                                   "layer_step_us": round(statistics.median(layer) * 1e3, 3)}
 
     # Quantised gather: 151936 x 2048 tied table, 16384 Zipf(1.1) ids, FP16 / FP8 / FP4 rows
     if want("quant_gather_qwen3_1.7b"):
