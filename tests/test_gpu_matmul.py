@@ -87,7 +87,7 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
-    (1000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
+    (2000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
     (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
 ])
