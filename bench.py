@@ -53,7 +53,7 @@ def parse():
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
-                        "qwen3_4b_decode_matmul, qwen3_4b_prefill_matmul)")
+                        "qwen3_4b_decode_matmul, qwen3_4b_decode16_matmul, qwen3_4b_prefill_matmul)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -450,8 +450,8 @@ def add_cpu_jobs(leg, want):
         leg.add("granite_4.0h_norms", "gated_rmsnorm", gated, c.T / n, s + ": y *= silu(z), then rmsNorm per group")
         leg.add("granite_4.0h_norms", "swiglu", swiglu_job(n, c.I, 56), c.T / n, s)
 
-    def matmul_jobs():  # qwen3_4b_decode_matmul
-        c, n = wl.QWEN3_DECODE_MATMUL, 256
+    def matmul_jobs(label, c):  # qwen3_4b_decode_matmul, qwen3_4b_decode16_matmul
+        n = 256
 
         def mm(fmt, N, K):
             def make():
@@ -465,7 +465,7 @@ def add_cpu_jobs(leg, want):
 
         for pname, N, K in c.projections:
             for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
-                leg.add("qwen3_4b_decode_matmul", f"{pname}_{fname}", mm(fmt, N, K), N / n,
+                leg.add(label, f"{pname}_{fname}", mm(fmt, N, K), N / n,
                         f"{n} of {N} weight rows through cpu::matmul on a one-thread pool (median of {leg.reps}), "
                         f"scaled to all {N}; {core}")
 
@@ -498,7 +498,8 @@ def add_cpu_jobs(leg, want):
             ("qwen3_4b_fused", fused_jobs),
             ("quantize_qwen3_1.7b_table", quantize_jobs),
             ("granite_4.0h_norms", granite_jobs),
-            ("qwen3_4b_decode_matmul", matmul_jobs),
+            ("qwen3_4b_decode_matmul", lambda: matmul_jobs("qwen3_4b_decode_matmul", wl.QWEN3_DECODE_MATMUL)),
+            ("qwen3_4b_decode16_matmul", lambda: matmul_jobs("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL)),
             ("qwen3_4b_prefill_matmul", prefill_matmul_jobs),
     ):
         if want(label):
@@ -518,7 +519,8 @@ def all_configs(args):
     out = {}
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
-              "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_prefill_matmul")
+              "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode16_matmul",
+              "qwen3_4b_prefill_matmul")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -670,8 +672,11 @@ def all_configs(args):
 
     # Qwen3-4B decode step (T = 1): the four weight matmuls in each weight format, f16 activations,
     # f32 outputs; bytes = the weight rows once + activations + outputs.
-    if want("qwen3_4b_decode_matmul"):
-        c8 = wl.QWEN3_DECODE_MATMUL
+    # Qwen3-4B decode steps of 1 and 16 sequences: the layer's four weight matmuls, weight-bandwidth bound.
+    for label8, c8 in (("qwen3_4b_decode_matmul", wl.QWEN3_DECODE_MATMUL),
+                       ("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL)):
+        if not want(label8):
+            continue
         calls8, bytes8 = {}, {}
         for pname, N, K in c8.projections:
             wsrc = wl.normal_f16((N, K), 0.0, 0.02, 81, dev).float()
@@ -684,8 +689,8 @@ def all_configs(args):
                 calls8[name].table = tab8
                 bytes8[name] = wl.bytes_matmul(c8.T, K, N, tab8.shape[1])
             del wsrc
-        run("qwen3_4b_decode_matmul", calls8, bytes8,
-            "Qwen3-4B decode step, T=1: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
+        run(label8, calls8, bytes8,
+            f"Qwen3-4B decode step, T={c8.T}: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
             "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs")
         del calls8
 

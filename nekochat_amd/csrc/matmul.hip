@@ -357,6 +357,168 @@ __global__ __launch_bounds__(64 * max_waves(FMT, TT)) void mm_tile_kernel(MmArgs
     }
 }
 
+// ---------------------------------------------------------------- mid-size T: activations shared in LDS
+//
+// 5 <= T < 48 (FP4; FP8 above 8 tokens; F16 above 16), second form: each wave of a 4-wave workgroup
+// owns its own 16-row tile, and the workgroup stages its token chunk's activations for one slice of
+// K in LDS once, with coalesced loads (FP4 blocks pre-permuted to the MFMA k order), so every wave
+// reads its A fragments from LDS. (Re-reading them from L1 per wave and group, 16 token rows per instruction, left the L1 tag
+// lookups at their issue rate -- measured.) Weights stream through each wave's LDS staging tile as
+// in mm_tile_kernel. K is split over the grid's z: with several slices the waves write f32 partials
+// that mm_splitk_reduce adds in order. (Adding them in the kernel, by the last workgroup of each row
+// group to arrive, measured several times slower: the device-scope fences that publish the partials
+// write back / invalidate an XCD's whole L2.)
+#ifndef NEKO_TUNE_MM_TILE2
+#define NEKO_TUNE_MM_TILE2 1
+#endif
+#ifndef NEKO_TUNE_MM_T2_LDS
+#define NEKO_TUNE_MM_T2_LDS 65536
+#endif
+constexpr bool kTile2 = NEKO_TUNE_MM_TILE2;
+constexpr int kT2Waves = 4;
+constexpr int kT2Lds = NEKO_TUNE_MM_T2_LDS;  // LDS per workgroup (two per CU at 64 KB)
+
+// Halves per staged token row for nb blocks: 32 nb plus 8 of padding (16-byte bank groups differ
+// between the 16 token rows a ds_read_b128 pass serves: the row stride over 16 is odd).
+__host__ __device__ constexpr int t2_row(int nb) { return 32 * nb + 8; }
+
+template <int TT>
+__host__ __device__ constexpr size_t t2_acts_bytes(int nb) { return static_cast<size_t>(16 * TT) * t2_row(nb) * 2; }
+
+template <int FMT, int TT>
+__device__ __forceinline__ void t2_load_acts(half8 (&A)[kGroup][TT], const half_t* xl, int xr_stride, int b0, int n, int g) {
+#pragma unroll
+    for (int j = 0; j < kGroup; j++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+            A[j][tt] = *reinterpret_cast<const half8*>(xl + (tt * 16 + n) * xr_stride + (b0 + j) * kBlockK + 8 * g);
+}
+
+// One group, as mm_step, with the next group's activation fragments read from LDS.
+template <int FMT, int TT>
+__device__ __forceinline__ void t2_step(float4v (&acc)[TT], MmStage<FMT>& st, const half8 (&A)[kGroup][TT],
+                                        half8 (&A_next)[kGroup][TT], const uint8_t* const (&prow)[pieces(FMT)],
+                                        int col16, const uint8_t* wrow, int soff, const half_t* xl, int xr_stride,
+                                        int g, int n, uint8_t* tile, const int (&slot)[pieces(FMT)], int b_acts_rel,
+                                        int b_stage) {
+    t2_load_acts<FMT, TT>(A_next, xl, xr_stride, b_acts_rel, n, g);
+    wave_sync_lds();  // the previous group's operand reads are done
+#pragma unroll
+    for (int q = 0; q < pieces(FMT); q++) *reinterpret_cast<uint4v*>(tile + slot[q]) = st.w[q];
+    const uint2v sc = st.s;
+    load_stage<FMT>(st, prow, col16, wrow, soff, b_stage);
+    wave_sync_lds();
+#pragma unroll
+    for (int j = 0; j < kGroup; j++) {
+        float s = 0.0f;
+        if constexpr (FMT != 0) {
+            const uint32_t sw = sc[j >> 1];  // copied out first (see mm_step)
+            const half2v s2 = __builtin_bit_cast(half2v, sw);
+            s = static_cast<float>(s2[j & 1]) * block_scale_factor<FMT>();
+        }
+        mma_block<FMT, TT>(acc, A[j], decode_b<FMT>(read_b<FMT>(tile, n, j, g)), s);
+    }
+}
+
+// Grid: x = groups of 4 row tiles (64 rows), y = chunks of 16 TT tokens, z = K slices of
+// `slice_blocks` blocks. Dynamic LDS: the staged activations (16 TT rows of t2_row(slice_blocks)
+// halves), then one weight staging tile per wave.
+template <int FMT, int TT, typename TY>
+__global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int slice_blocks, float* partial) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int G = kGroup, NP = pieces(FMT), PR = group_row_bytes(FMT) / 16;
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, g = lane >> 4;
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kT2Waves + wave) * 16;
+    const int64_t t_base = static_cast<int64_t>(blockIdx.y) * (16 * TT);
+    const int nblk = a.K / kBlockK;
+    const int kb0 = static_cast<int>(blockIdx.z) * slice_blocks;
+    const int nb = min(nblk - kb0, slice_blocks);  // > 0: the host sizes the slices
+    const int xr_stride = t2_row(slice_blocks);
+    half_t* xl = reinterpret_cast<half_t*>(lds);
+    uint8_t* tile = lds + t2_acts_bytes<TT>(slice_blocks) + wave * stage_bytes(FMT);
+
+    // Stage the activations: 16-byte chunk c = (token, block, h) holds halves 8h .. 8h+7 of the block.
+    // FP4 groups lane g's k set {4g..4g+3, 16+4g..16+4g+3} at halves 8g .. 8g+7 of the staged block.
+    const int chunks = 16 * TT * nb * 4;
+    for (int c = tid; c < chunks; c += 64 * kT2Waves) {
+        const int t = c / (nb * 4), q = c - t * (nb * 4), b = q >> 2, h = q & 3;
+        const int64_t tok = min(t_base + t, a.T - 1);  // rows past T read the last token, never stored
+        const uint4v v = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + tok * a.xs +
+                                                           (kb0 + b) * kBlockK + 8 * h);
+        half_t* dst = xl + t * xr_stride + b * kBlockK;
+        if constexpr (FMT == 2) {
+            // Chunk h covers k 8h .. 8h+7: its halves k 8h..8h+3 and 8h+4..8h+7 belong to groups
+            // 2 (h & 1) and 2 (h & 1) + 1, in their low (h < 2) or high (h >= 2) four halves.
+            const int g0 = 2 * (h & 1), hi = 4 * (h >> 1);
+            *reinterpret_cast<uint2v*>(dst + 8 * g0 + hi) = uint2v{v[0], v[1]};
+            *reinterpret_cast<uint2v*>(dst + 8 * (g0 + 1) + hi) = uint2v{v[2], v[3]};
+        } else {
+            *reinterpret_cast<uint4v*>(dst + 8 * h) = v;
+        }
+    }
+    __syncthreads();
+
+    const int64_t last = a.N - 1;
+    const uint8_t* wrow = a.w + min(row0 + n, last) * a.rb;
+    const int soff = FMT == 1 ? a.K : a.K / 2;
+    const uint8_t* prow[NP];
+    int slot[NP];
+    const int col16 = lane % PR;
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int r = (64 * i + lane) / PR;
+        prow[i] = a.w + min(row0 + r, last) * a.rb;
+        slot[i] = r * stage_row(FMT) + col16 * 16;
+    }
+
+    float4v acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) acc[tt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const int nfull = nb / G;
+    if (nfull > 0) {
+        const int lastg = nfull - 1;
+        MmStage<FMT> st0, st1;
+        half8 A0[G][TT], A1[G][TT];
+        load_stage<FMT>(st0, prow, col16, wrow, soff, kb0);
+        load_stage<FMT>(st1, prow, col16, wrow, soff, kb0 + min(1, lastg) * G);
+        t2_load_acts<FMT, TT>(A0, xl, xr_stride, 0, n, g);
+        for (int i = 0;; i += 2) {
+            t2_step<FMT, TT>(acc, st0, A0, A1, prow, col16, wrow, soff, xl, xr_stride, g, n, tile, slot,
+                             min(i + 1, lastg) * G, kb0 + min(i + 2, lastg) * G);
+            if (i + 1 >= nfull) break;
+            t2_step<FMT, TT>(acc, st1, A1, A0, prow, col16, wrow, soff, xl, xr_stride, g, n, tile, slot,
+                             min(i + 2, lastg) * G, kb0 + min(i + 3, lastg) * G);
+            if (i + 2 >= nfull) break;
+        }
+    }
+    for (int b = nfull * G; b < nb; b++) {  // K tail of fewer than a group: direct weight loads
+        half8 A[TT];
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+            A[tt] = *reinterpret_cast<const half8*>(xl + (tt * 16 + n) * xr_stride + b * kBlockK + 8 * g);
+        const half8 B = decode_b<FMT>(load_b_raw<FMT>(wrow, kb0 + b, g));
+        float s = 0.0f;
+        if constexpr (FMT != 0)
+            s = static_cast<float>(*reinterpret_cast<const half_t*>(wrow + soff + 2 * (kb0 + b))) * block_scale_factor<FMT>();
+        mma_block<FMT, TT>(acc, A, B, s);
+    }
+
+    // Lane (n, g) holds C[token 4g + i][row n] of each 16 x 16 tile.
+    const int64_t out_row = row0 + n;
+    if (out_row >= a.N) return;
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t t = t_base + tt * 16 + 4 * g + i;
+            if (t >= a.T) continue;
+            if (partial) partial[(static_cast<int64_t>(blockIdx.z) * a.T + t) * a.N + out_row] = acc[tt][i];
+            else epilogue<TY>(a, t, out_row, acc[tt][i]);
+        }
+}
+
 // ---------------------------------------------------------------- decode path: VALU GEMV
 
 // Sum over each DPP row of 16 lanes; every lane of the row receives the same bits.
@@ -851,10 +1013,41 @@ template <typename TY>
 __global__ __launch_bounds__(256) void mm_splitk_reduce(MmArgs a, const float* partial, int slices) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= a.T * static_cast<int64_t>(a.N)) return;
+    const int64_t total = a.T * static_cast<int64_t>(a.N);
     float v = partial[i];
-    for (int sl = 1; sl < slices; sl++) v += partial[static_cast<int64_t>(sl) * a.T * a.N + i];
+    int sl = 1;
+    for (; sl + 4 <= slices; sl += 4) {  // four slices' loads in flight, added in slice order
+        float p[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) p[q] = partial[static_cast<int64_t>(sl + q) * total + i];
+#pragma unroll
+        for (int q = 0; q < 4; q++) v += p[q];
+    }
+    for (; sl < slices; sl++) v += partial[static_cast<int64_t>(sl) * total + i];
     const int64_t t = i / a.N, n = i - t * a.N;
     epilogue<TY>(a, t, n, v);
+}
+
+// The same, four neighbouring outputs of one token row per thread (N % 4 == 0: 16-byte loads).
+template <typename TY>
+__global__ __launch_bounds__(256) void mm_splitk_reduce4(MmArgs a, const float* partial, int slices) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    const int64_t total = a.T * static_cast<int64_t>(a.N);
+    if (i >= total) return;
+    // Loads four slices at a time (one memory round trip each), added in slice order.
+    float4v v = *reinterpret_cast<const float4v*>(partial + i);
+    int sl = 1;
+    for (; sl + 4 <= slices; sl += 4) {
+        float4v p[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) p[q] = *reinterpret_cast<const float4v*>(partial + static_cast<int64_t>(sl + q) * total + i);
+#pragma unroll
+        for (int q = 0; q < 4; q++) v += p[q];
+    }
+    for (; sl < slices; sl++) v += *reinterpret_cast<const float4v*>(partial + static_cast<int64_t>(sl) * total + i);
+    const int64_t t = i / a.N, n = i - t * a.N;
+#pragma unroll
+    for (int e = 0; e < 4; e++) epilogue<TY>(a, t, n + e, v[e]);
 }
 
 // ---------------------------------------------------------------- prefill GEMM, 64-wide stages
@@ -1261,6 +1454,41 @@ int launch_tile_tt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, i
     }
 }
 
+template <int FMT, int TT>
+int launch_tile2(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, size_t lds, int slice_blocks, float* partial) {
+    if (y_dtype == NEKO_DT_F16)
+        hipLaunchKernelGGL((mm_tile2_kernel<FMT, TT, half_t>), grid, dim3(64 * kT2Waves), lds, ctx->stream, a, slice_blocks, partial);
+    else
+        hipLaunchKernelGGL((mm_tile2_kernel<FMT, TT, float>), grid, dim3(64 * kT2Waves), lds, ctx->stream, a, slice_blocks, partial);
+    return after_launch(ctx, "neko_hip_matmul");
+}
+
+template <int FMT>
+int launch_tile2_tt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, size_t lds, int slice_blocks, float* partial, int tt) {
+    switch (tt) {
+        case 1: return launch_tile2<FMT, 1>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
+        case 2: return launch_tile2<FMT, 2>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
+        default: return launch_tile2<FMT, 3>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
+    }
+}
+
+// y = epilogue(partial slices added in order), after a split-K launch.
+int launch_splitk_reduce(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const float* partial, int slices, const char* what) {
+    const int64_t total = a.T * a.N;
+    const bool vec = a.N % 4 == 0;
+    const int64_t blocks = (total + (vec ? 1023 : 255)) / (vec ? 1024 : 256);
+    NEKO_REQUIRE(ctx, blocks <= 0x7fffffff, "%s: output too large", what);
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    if (vec) {
+        if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_splitk_reduce4<half_t>), grid, dim3(256), 0, ctx->stream, a, partial, slices);
+        else hipLaunchKernelGGL((mm_splitk_reduce4<float>), grid, dim3(256), 0, ctx->stream, a, partial, slices);
+    } else {
+        if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((mm_splitk_reduce<half_t>), grid, dim3(256), 0, ctx->stream, a, partial, slices);
+        else hipLaunchKernelGGL((mm_splitk_reduce<float>), grid, dim3(256), 0, ctx->stream, a, partial, slices);
+    }
+    return after_launch(ctx, what);
+}
+
 bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
     const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
     return an && bn && pa < pb + bn && pb < pa + an;
@@ -1368,16 +1596,43 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
             else hipLaunchKernelGGL((mm_gemm_kernel<2, float>), grid, dim3(kGemmThreads), 0, ctx->stream, a, tm, tn, slices, partial);
         }
         if (int rc = after_launch(ctx, what)) return rc;
-        if (slices > 1) {
-            const int64_t blocks = (T * N + 255) / 256;
-            NEKO_REQUIRE(ctx, blocks <= 0x7fffffff, "%s: output too large", what);
-            if (y_dtype == NEKO_DT_F16)
-                hipLaunchKernelGGL((mm_splitk_reduce<half_t>), dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a, partial, slices);
-            else
-                hipLaunchKernelGGL((mm_splitk_reduce<float>), dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a, partial, slices);
-            return after_launch(ctx, what);
-        }
+        if (slices > 1) return launch_splitk_reduce(ctx, a, y_dtype, partial, slices, what);
         return NEKO_OK;
+    }
+    // The shared-activation kernel where it measured faster: FP4 at every T, FP8 above 8 tokens, F16
+    // above 16 (below that the per-wave kernel's single launch wins over the slices' reduction).
+    const bool tile2 = kTile2 && T < 48 && (fmt == NEKO_FMT_FP4 || (fmt == NEKO_FMT_FP8 && T > 8) || T > 16);
+    if (fast && tile2) {
+        const int tt = static_cast<int>((T + 15) / 16);  // 1..3: one chunk of 16 tt tokens
+        const int64_t tiles = (N + 16 * kT2Waves - 1) / (16 * kT2Waves);
+        const int nblk = static_cast<int>(K / kBlockK);
+        const size_t stage = static_cast<size_t>(kT2Waves) * stage_bytes(fmt);
+        // The largest slice of K whose staged activations fit beside the staging tiles; then more
+        // slices (halving) until the grid holds about two workgroups per CU, each slice at least 8
+        // blocks long.
+        const int cap = static_cast<int>(((kT2Lds - stage) / (32 * tt) - 8) / 32);
+        int slices = (nblk + cap - 1) / cap;
+        while (tiles * slices < 2 * ctx->cu_count && nblk / (2 * slices) >= 8) slices *= 2;
+        int slice_blocks = (nblk + slices - 1) / slices;
+        slice_blocks = std::min(cap, (slice_blocks + kGroup - 1) / kGroup * kGroup);  // whole groups where possible
+        slices = (nblk + slice_blocks - 1) / slice_blocks;
+        NEKO_REQUIRE(ctx, tiles <= 0x7fffffff && slices <= 65535, "%s: grid too large", what);
+        float* partial = nullptr;
+        if (slices > 1) {
+            void* ws = nullptr;
+            if (int rc = workspace(ctx, static_cast<size_t>(slices) * T * N * sizeof(float), &ws)) return rc;
+            partial = static_cast<float*>(ws);
+        }
+        const size_t lds = static_cast<size_t>(16 * tt) * (32 * slice_blocks + 8) * 2 + stage;
+        const dim3 grid(static_cast<uint32_t>(tiles), 1u, static_cast<uint32_t>(slices));
+        int rc;
+        switch (fmt) {
+            case NEKO_FMT_F16: rc = launch_tile2_tt<0>(ctx, a, y_dtype, grid, lds, slice_blocks, partial, tt); break;
+            case NEKO_FMT_FP8: rc = launch_tile2_tt<1>(ctx, a, y_dtype, grid, lds, slice_blocks, partial, tt); break;
+            default: rc = launch_tile2_tt<2>(ctx, a, y_dtype, grid, lds, slice_blocks, partial, tt); break;
+        }
+        if (rc || slices == 1) return rc;
+        return launch_splitk_reduce(ctx, a, y_dtype, partial, slices, what);
     }
     if (fast) {
         const int tt = static_cast<int>(std::min<int64_t>(4, (T + 15) / 16));

@@ -90,9 +90,11 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
     (2000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
     (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
+    (20, 4096, 100),    # 5 <= T < 48: activations staged per K slice, several slices reduced in order
+    (47, 2080, 300),    # three token tiles, K slices ending in a partial group
 ])
 def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
-    """Integer-valued weights and activations through each GEMM tiling: every partial sum is exact,
+    """Integer-valued weights and activations through each MFMA tiling: every partial sum is exact,
     so y = bias + x . w (+ y0 with accumulate) is bit-identical to the float64 product rounded once."""
     _case(f"matmul GEMM tiling integer fmt={fmt} T={T} K={K} N={N}")
     rng = np.random.default_rng(500 + fmt + T + K)
