@@ -357,6 +357,135 @@ __global__ __launch_bounds__(64 * max_waves(FMT, TT)) void mm_tile_kernel(MmArgs
     }
 }
 
+// ---------------------------------------------------------------- prefill GEMM, F16, direct-to-LDS loads
+//
+// F16 rows on large grids: 256 x 256 workgroup tiles over eight waves of 128 x 64 (4 x 2
+// v_mfma_f32_32x32x16_f16 tiles, 128 accumulators per lane) at two waves per SIMD, K staged 64 at a
+// time in double-buffered LDS (128 KB). Operands go from global memory straight into LDS
+// (global_load_lds_dwordx4: lane l of an instruction writes bytes [16 l, 16 l + 16) past the wave's
+// LDS base), so no staging registers are needed -- with them the 128 accumulators spill. Each
+// instruction fills 8 unpadded 128-byte rows; within a row, 16-byte chunk c sits at slot
+// c ^ ((row / 2) % 8), so the 16 rows one ds_read_b128 pass serves fall on distinct bank groups.
+// A stage's loads are issued before the previous stage's MFMAs and waited for (vmcnt) before the
+// barrier that publishes them.
+#ifndef NEKO_TUNE_MM_GEMM3
+#define NEKO_TUNE_MM_GEMM3 1
+#endif
+constexpr bool kGemm3 = NEKO_TUNE_MM_GEMM3;
+constexpr int kG3BM = 256, kG3BN = 256, kG3Threads = 512;
+
+struct Gemm3Lds {
+    half_t a[2][kG3BM * 64];
+    half_t b[2][kG3BN * 64];
+};
+
+__device__ __forceinline__ int g3_slot(int row, int c) { return c ^ ((row >> 1) & 7); }
+
+template <typename TY>
+__global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int tiles_m, int tiles_n) {
+    extern __shared__ __align__(16) uint8_t g3_lds[];
+    Gemm3Lds& L = *reinterpret_cast<Gemm3Lds*>(g3_lds);
+    constexpr int TM = 4, TN = 2;
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 1, wn = wave >> 1;
+
+    uint32_t b = blockIdx.x;
+    const uint32_t nb = gridDim.x;
+    if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
+    constexpr int GM = 8;
+    const int group = static_cast<int>(b) / (GM * tiles_n);
+    const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
+    const int in_group = static_cast<int>(b) - group * GM * tiles_n;
+    const int64_t m0 = static_cast<int64_t>(first_m + in_group % gm) * kG3BM;
+    const int64_t n0 = static_cast<int64_t>(in_group / gm) * kG3BN;
+
+    // This lane's four load instructions per operand and stage: rows (4 wave + i) * 8 + lane / 8, the
+    // global chunk whose swizzled slot is lane % 8.
+    const half_t* xa[4];
+    const uint8_t* wb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (wave * 4 + i) * 8 + (lane >> 3), c = g3_slot(row, lane & 7);
+        xa[i] = static_cast<const half_t*>(a.x) + min(m0 + row, a.T - 1) * a.xs + 8 * c;
+        wb[i] = a.w + min(n0 + row, static_cast<int64_t>(a.N) - 1) * a.rb + 16 * c;
+    }
+    auto issue = [&](int k0, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r0 = (wave * 4 + i) * 8;
+            // (address-space conversions: C casts, which reinterpret_cast does not allow)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(xa[i] + k0),
+                                             (__attribute__((address_space(3))) void*)(&L.a[buf][r0 * 64]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(wb[i] + 2 * k0),
+                                             (__attribute__((address_space(3))) void*)(&L.b[buf][r0 * 64]), 16, 0, 0);
+        }
+    };
+
+    float16v acc[TM][TN] = {};
+    const int l32 = lane & 31, h = lane >> 5;
+    const int nk = a.K / 64;
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int s = 0; s < nk; s++) {
+        const int buf = s & 1;
+        if (s + 1 < nk) issue((s + 1) * 64, buf ^ 1);  // that buffer's last readers passed the barrier
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            half8 B[TN][2];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int r = wn * 64 + j * 32 + l32;
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+                    B[j][q] = *reinterpret_cast<const half8*>(&L.b[buf][r * 64 + 8 * g3_slot(r, 4 * bb + 2 * q + h)]);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int r = wm * 128 + i * 32 + l32;
+                half8 A[2];
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+                    A[q] = *reinterpret_cast<const half8*>(&L.a[buf][r * 64 + 8 * g3_slot(r, 4 * bb + 2 * q + h)]);
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[j][0], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[j][1], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next stage have landed
+        __syncthreads();                // and every wave's; this stage's reads are done
+    }
+    // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int64_t n = n0 + wn * 64 + j * 32 + l32;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int64_t t = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (t < a.T) epilogue<TY>(a, t, n, acc[i][j][e]);
+            }
+    }
+}
+
+template <typename TY>
+int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) {
+    constexpr size_t lds = sizeof(Gemm3Lds);
+    static bool attr_set = false;  // dynamic LDS above 64 KB is enabled once per instantiation
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mm_gemm3_kernel<TY>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) return fail(ctx, NEKO_ERR_HIP, "matmul: hipFuncSetAttribute: %s", hipGetErrorString(e));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((mm_gemm3_kernel<TY>), grid, dim3(kG3Threads), lds, ctx->stream, a, tm, tn);
+    return NEKO_OK;
+}
+
 // ---------------------------------------------------------------- mid-size T: activations shared in LDS
 //
 // 5 <= T < 48 (FP4; FP8 above 8 tokens; F16 above 16), second form: each wave of a 4-wave workgroup
@@ -1558,6 +1687,19 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
     }
     if (fast && T >= kGemmMinT) {
         const bool v2 = kGemmV2 && K % kG2BK == 0;
+        // F16: 256 x 256 tiles with direct-to-LDS loads when they give every CU at least two (with
+        // fewer, the partial last round of one-per-CU workgroups cost more than the wider tiles save:
+        // measured on the 2560-row projections at T = 8192, 320 tiles).
+        const int64_t g3_m = (T + kG3BM - 1) / kG3BM, g3_n = (N + kG3BN - 1) / kG3BN;
+        if (v2 && kGemm3 && fmt == NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
+            NEKO_REQUIRE(ctx, g3_m * g3_n <= 0x7fffffff, "%s: too many output tiles", what);
+            const dim3 grid(static_cast<uint32_t>(g3_m * g3_n));
+            const int rc = y_dtype == NEKO_DT_F16
+                               ? launch_gemm3<half_t>(ctx, grid, a, static_cast<int>(g3_m), static_cast<int>(g3_n))
+                               : launch_gemm3<float>(ctx, grid, a, static_cast<int>(g3_m), static_cast<int>(g3_n));
+            if (rc) return rc;
+            return after_launch(ctx, what);
+        }
         // FP8 / FP4: 256-token x 128-row tiles (one workgroup per CU) when they alone give every CU a
         // workgroup.
         const int64_t big_m = (T + G2Big::BM - 1) / G2Big::BM, big_n = (N + G2Big::BN - 1) / G2Big::BN;

@@ -88,6 +88,7 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
     (2000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
+    (4000, 320, 8200),  # F16: 256 x 256 tiles, direct-to-LDS loads (two per CU), partial in both
     (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
     (20, 4096, 100),    # 5 <= T < 48: activations staged per K slice, several slices reduced in order
