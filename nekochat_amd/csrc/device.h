@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <cmath>
+#include <utility>
 
 // The reference rounds every float product and sum separately (its portable path has no FMA), so
 // kernels must not contract a*b+c into fma. The build passes -ffp-contract=off as well.
@@ -163,6 +164,18 @@ template <typename T>
 __device__ __forceinline__ T from_f32(float v) {
     if constexpr (sizeof(T) == 2) return f16_rne(v);
     else return static_cast<T>(v);
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}): a loop with
+// compile-time indices, whatever the unroller decides (an element loop over a vector of accumulators
+// that is left rolled indexes it at run time and sends the whole array to scratch memory).
+template <typename F, int... E>
+__device__ __forceinline__ void unrolled_impl(F&& f, std::integer_sequence<int, E...>) {
+    (f(std::integral_constant<int, E>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unrolled(F&& f) {
+    unrolled_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // ---------------------------------------------------------------- DPP cross-lane moves

@@ -457,19 +457,22 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int t
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next stage have landed
         __syncthreads();                // and every wave's; this stage's reads are done
     }
-    // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
+    // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile. (Indices
+    // fixed at compile time: with f16 output a rolled loop here sent acc to scratch memory.)
+    unrolled<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
         const int64_t n = n0 + wn * 64 + j * 32 + l32;
-        if (n >= a.N) continue;
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
+        if (n >= a.N) return;
+        unrolled<TM>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            const float16v v = acc[i][j];
+            unrolled<16>([&](auto ec) {
+                constexpr int e = decltype(ec)::value;
                 const int64_t t = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (t < a.T) epilogue<TY>(a, t, n, acc[i][j][e]);
-            }
-    }
+                if (t < a.T) epilogue<TY>(a, t, n, v[e]);
+            });
+        });
+    });
 }
 
 template <typename TY>
@@ -1446,14 +1449,16 @@ __global__ __launch_bounds__(C::threads, 2) void mm_gemm2_kernel(MmArgs a, int t
         const int64_t n = n0 + wn * 32 * C::TN + j * 32 + l32;
         if (n >= a.N) continue;
 #pragma unroll
-        for (int i = 0; i < C::TM; i++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
+        for (int i = 0; i < C::TM; i++) {
+            const float16v v = acc.v[i][j];
+            unrolled<16>([&](auto ec) {
+                constexpr int e = decltype(ec)::value;
                 const int64_t t = m0 + wm * 32 * C::TM + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (t >= a.T) continue;
-                if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = acc.v[i][j][e];
-                else epilogue<TY>(a, t, n, acc.v[i][j][e]);
-            }
+                if (t >= a.T) return;
+                if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = v[e];
+                else epilogue<TY>(a, t, n, v[e]);
+            });
+        }
     }
 }
 
@@ -1694,9 +1699,9 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         if (v2 && kGemm3 && fmt == NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
             NEKO_REQUIRE(ctx, g3_m * g3_n <= 0x7fffffff, "%s: too many output tiles", what);
             const dim3 grid(static_cast<uint32_t>(g3_m * g3_n));
-            const int rc = y_dtype == NEKO_DT_F16
-                               ? launch_gemm3<half_t>(ctx, grid, a, static_cast<int>(g3_m), static_cast<int>(g3_n))
-                               : launch_gemm3<float>(ctx, grid, a, static_cast<int>(g3_m), static_cast<int>(g3_n));
+            const int tm = static_cast<int>(g3_m), tn = static_cast<int>(g3_n);
+            const int rc = y_dtype == NEKO_DT_F16 ? launch_gemm3<half_t>(ctx, grid, a, tm, tn)
+                                                  : launch_gemm3<float>(ctx, grid, a, tm, tn);
             if (rc) return rc;
             return after_launch(ctx, what);
         }
