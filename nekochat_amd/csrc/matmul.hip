@@ -510,6 +510,7 @@ constexpr bool kTile2 = NEKO_TUNE_MM_TILE2;
 constexpr int kT2Waves = 4;
 constexpr int kT2Lds = NEKO_TUNE_MM_T2_LDS;  // LDS per workgroup (two per CU at 64 KB)
 
+
 // Halves per staged token row for nb blocks: 32 nb plus 8 of padding (16-byte bank groups differ
 // between the 16 token rows a ds_read_b128 pass serves: the row stride over 16 is odd).
 __host__ __device__ constexpr int t2_row(int nb) { return 32 * nb + 8; }
@@ -571,27 +572,6 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
     half_t* xl = reinterpret_cast<half_t*>(lds);
     uint8_t* tile = lds + t2_acts_bytes<TT>(slice_blocks) + wave * stage_bytes(FMT);
 
-    // Stage the activations: 16-byte chunk c = (token, block, h) holds halves 8h .. 8h+7 of the block.
-    // FP4 groups lane g's k set {4g..4g+3, 16+4g..16+4g+3} at halves 8g .. 8g+7 of the staged block.
-    const int chunks = 16 * TT * nb * 4;
-    for (int c = tid; c < chunks; c += 64 * kT2Waves) {
-        const int t = c / (nb * 4), q = c - t * (nb * 4), b = q >> 2, h = q & 3;
-        const int64_t tok = min(t_base + t, a.T - 1);  // rows past T read the last token, never stored
-        const uint4v v = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + tok * a.xs +
-                                                           (kb0 + b) * kBlockK + 8 * h);
-        half_t* dst = xl + t * xr_stride + b * kBlockK;
-        if constexpr (FMT == 2) {
-            // Chunk h covers k 8h .. 8h+7: its halves k 8h..8h+3 and 8h+4..8h+7 belong to groups
-            // 2 (h & 1) and 2 (h & 1) + 1, in their low (h < 2) or high (h >= 2) four halves.
-            const int g0 = 2 * (h & 1), hi = 4 * (h >> 1);
-            *reinterpret_cast<uint2v*>(dst + 8 * g0 + hi) = uint2v{v[0], v[1]};
-            *reinterpret_cast<uint2v*>(dst + 8 * (g0 + 1) + hi) = uint2v{v[2], v[3]};
-        } else {
-            *reinterpret_cast<uint4v*>(dst + 8 * h) = v;
-        }
-    }
-    __syncthreads();
-
     const int64_t last = a.N - 1;
     const uint8_t* wrow = a.w + min(row0 + n, last) * a.rb;
     const int soff = FMT == 1 ? a.K : a.K / 2;
@@ -604,17 +584,53 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
         prow[i] = a.w + min(row0 + r, last) * a.rb;
         slot[i] = r * stage_row(FMT) + col16 * 16;
     }
+    // The first two groups' weights do not depend on the activations: requested before staging them.
+    const int nfull = nb / G, lastg = max(nfull - 1, 0);
+    MmStage<FMT> st0, st1;
+    if (nfull > 0) {
+        load_stage<FMT>(st0, prow, col16, wrow, soff, kb0);
+        load_stage<FMT>(st1, prow, col16, wrow, soff, kb0 + min(1, lastg) * G);
+    }
+
+    // Stage the activations: 16-byte chunk c = (token, block, h) holds halves 8h .. 8h+7 of the block.
+    // FP4 groups lane g's k set {4g..4g+3, 16+4g..16+4g+3} at halves 8g .. 8g+7 of the staged block.
+    // Eight chunks per thread are requested before any is stored (one memory round trip per batch;
+    // chunk indices past the end re-read the last chunk and are not stored).
+    constexpr int kBatch = 8, kThreads = 64 * kT2Waves;
+    const int chunks = 16 * TT * nb * 4;
+    for (int c0 = tid; c0 < chunks; c0 += kThreads * kBatch) {
+        uint4v v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; u++) {
+            const int c = min(c0 + kThreads * u, chunks - 1);
+            const int t = c / (nb * 4), q = c - t * (nb * 4);
+            const int64_t tok = min(t_base + t, a.T - 1);  // rows past T read the last token, never stored
+            v[u] = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + tok * a.xs + kb0 * kBlockK + 8 * q);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; u++) {
+            const int c = c0 + kThreads * u;
+            if (c >= chunks) break;
+            const int t = c / (nb * 4), q = c - t * (nb * 4), b = q >> 2, h = q & 3;
+            half_t* dst = xl + t * xr_stride + b * kBlockK;
+            if constexpr (FMT == 2) {
+                // Chunk h covers k 8h .. 8h+7: its halves k 8h..8h+3 and 8h+4..8h+7 belong to groups
+                // 2 (h & 1) and 2 (h & 1) + 1, in their low (h < 2) or high (h >= 2) four halves.
+                const int g0 = 2 * (h & 1), hi = 4 * (h >> 1);
+                *reinterpret_cast<uint2v*>(dst + 8 * g0 + hi) = uint2v{v[u][0], v[u][1]};
+                *reinterpret_cast<uint2v*>(dst + 8 * (g0 + 1) + hi) = uint2v{v[u][2], v[u][3]};
+            } else {
+                *reinterpret_cast<uint4v*>(dst + 8 * h) = v[u];
+            }
+        }
+    }
+    __syncthreads();
 
     float4v acc[TT];
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) acc[tt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
-    const int nfull = nb / G;
     if (nfull > 0) {
-        const int lastg = nfull - 1;
-        MmStage<FMT> st0, st1;
         half8 A0[G][TT], A1[G][TT];
-        load_stage<FMT>(st0, prow, col16, wrow, soff, kb0);
-        load_stage<FMT>(st1, prow, col16, wrow, soff, kb0 + min(1, lastg) * G);
         t2_load_acts<FMT, TT>(A0, xl, xr_stride, 0, n, g);
         for (int i = 0;; i += 2) {
             t2_step<FMT, TT>(acc, st0, A0, A1, prow, col16, wrow, soff, xl, xr_stride, g, n, tile, slot,
