@@ -557,7 +557,8 @@ __device__ __forceinline__ void t2_step(float4v (&acc)[TT], MmStage<FMT>& st, co
 // `slice_blocks` blocks. Dynamic LDS: the staged activations (16 TT rows of t2_row(slice_blocks)
 // halves), then one weight staging tile per wave.
 template <int FMT, int TT, typename TY>
-__global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int slice_blocks, float* partial) {
+__global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int slice_blocks, float* partial,
+                                                                  FastDiv div_full, FastDiv div_last) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int G = kGroup, NP = pieces(FMT), PR = group_row_bytes(FMT) / 16;
     const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
@@ -598,12 +599,13 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
     // chunk indices past the end re-read the last chunk and are not stored).
     constexpr int kBatch = 8, kThreads = 64 * kT2Waves;
     const int chunks = 16 * TT * nb * 4;
+    const FastDiv per_row = nb == slice_blocks ? div_full : div_last;  // chunk -> token: by nb * 4
     for (int c0 = tid; c0 < chunks; c0 += kThreads * kBatch) {
         uint4v v[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; u++) {
             const int c = min(c0 + kThreads * u, chunks - 1);
-            const int t = c / (nb * 4), q = c - t * (nb * 4);
+            const int t = static_cast<int>(fast_div(static_cast<uint32_t>(c), per_row)), q = c - t * (nb * 4);
             const int64_t tok = min(t_base + t, a.T - 1);  // rows past T read the last token, never stored
             v[u] = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + tok * a.xs + kb0 * kBlockK + 8 * q);
         }
@@ -611,7 +613,8 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
         for (int u = 0; u < kBatch; u++) {
             const int c = c0 + kThreads * u;
             if (c >= chunks) break;
-            const int t = c / (nb * 4), q = c - t * (nb * 4), b = q >> 2, h = q & 3;
+            const int t = static_cast<int>(fast_div(static_cast<uint32_t>(c), per_row));
+            const int q = c - t * (nb * 4), b = q >> 2, h = q & 3;
             half_t* dst = xl + t * xr_stride + b * kBlockK;
             if constexpr (FMT == 2) {
                 // Chunk h covers k 8h .. 8h+7: its halves k 8h..8h+3 and 8h+4..8h+7 belong to groups
@@ -1606,10 +1609,16 @@ int launch_tile_tt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, i
 
 template <int FMT, int TT>
 int launch_tile2(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, size_t lds, int slice_blocks, float* partial) {
+    const int nblk = static_cast<int>(a.K / kBlockK);
+    const int last_blocks = nblk - (static_cast<int>(grid.z) - 1) * slice_blocks;
+    const FastDiv full = make_fast_div(static_cast<uint32_t>(4 * slice_blocks));
+    const FastDiv last = make_fast_div(static_cast<uint32_t>(4 * last_blocks));
     if (y_dtype == NEKO_DT_F16)
-        hipLaunchKernelGGL((mm_tile2_kernel<FMT, TT, half_t>), grid, dim3(64 * kT2Waves), lds, ctx->stream, a, slice_blocks, partial);
+        hipLaunchKernelGGL((mm_tile2_kernel<FMT, TT, half_t>), grid, dim3(64 * kT2Waves), lds, ctx->stream, a, slice_blocks,
+                           partial, full, last);
     else
-        hipLaunchKernelGGL((mm_tile2_kernel<FMT, TT, float>), grid, dim3(64 * kT2Waves), lds, ctx->stream, a, slice_blocks, partial);
+        hipLaunchKernelGGL((mm_tile2_kernel<FMT, TT, float>), grid, dim3(64 * kT2Waves), lds, ctx->stream, a, slice_blocks,
+                           partial, full, last);
     return after_launch(ctx, "neko_hip_matmul");
 }
 
