@@ -129,6 +129,8 @@ def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
     (300, 1024, 700),   # partial token and row tiles
     (512, 9728, 2560),  # down projection, long K
     (512, 2560, 16384), # FP8 / FP4: 256-token x 128-row tiles
+    (2048, 1024, 16384),  # F16: 256 x 256 tiles with direct-to-LDS loads
+    (47, 9728, 2560),   # three token tiles, activations staged per K slice, slices reduced in order
 ])
 def test_matmul_random_within_bound(dev, fmt, T, K, N):
     _case(f"matmul random fmt={fmt} T={T} K={K} N={N}")
