@@ -89,6 +89,7 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
 @pytest.mark.parametrize("T,K,N", [
     (2000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
     (4000, 320, 8200),  # F16: 256 x 256 tiles, direct-to-LDS loads (two per CU), partial in both
+    (4000, 320, 4100),  # F16: 128 x 128 tiles (too few 256 x 256 tiles for two per CU), partial in both
     (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
     (20, 4096, 100),    # 5 <= T < 48: activations staged per K slice, several slices reduced in order
@@ -130,6 +131,7 @@ def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
     (512, 9728, 2560),  # down projection, long K
     (512, 2560, 16384), # FP8 / FP4: 256-token x 128-row tiles
     (2048, 1024, 16384),  # F16: 256 x 256 tiles with direct-to-LDS loads
+    (4096, 1024, 4096),   # F16: 128 x 128 tiles, two stages of register prefetch
     (47, 9728, 2560),   # three token tiles, activations staged per K slice, slices reduced in order
 ])
 def test_matmul_random_within_bound(dev, fmt, T, K, N):
