@@ -18,6 +18,7 @@
 // Summation order differs from the reference's sequential dot (and the reference's own GPU shaders
 // differ from its CPU loop), so results agree to f32 rounding of the sum, not bit for bit.
 #include <algorithm>
+#include <atomic>
 
 #include "internal.h"
 
@@ -25,6 +26,18 @@ namespace neko_hip {
 namespace {
 
 constexpr int kBlockK = 32;  // quant.h kQuantBlock
+
+// Kernels taking more than 64 KB of dynamic LDS must be allowed it per device (hipFuncSetAttribute on
+// the context's device, which enter() made current); `done` records which devices have been, one bit
+// per device id, safely across host threads.
+int allow_lds(neko_hip_ctx* ctx, const void* kernel, size_t bytes, std::atomic<uint64_t>& done) {
+    const uint64_t bit = uint64_t(1) << (ctx->device & 63);
+    if (done.load(std::memory_order_acquire) & bit) return NEKO_OK;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return fail(ctx, NEKO_ERR_HIP, "matmul: hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done.fetch_or(bit, std::memory_order_release);
+    return NEKO_OK;
+}
 
 struct MmArgs {
     const void* x;
@@ -372,6 +385,9 @@ __global__ __launch_bounds__(64 * max_waves(FMT, TT)) void mm_tile_kernel(MmArgs
 #define NEKO_TUNE_MM_GEMM3 1
 #endif
 constexpr bool kGemm3 = NEKO_TUNE_MM_GEMM3;
+#ifndef NEKO_TUNE_MM_G3_GM
+#define NEKO_TUNE_MM_G3_GM 8
+#endif
 constexpr int kG3BM = 256, kG3BN = 256, kG3Threads = 512;
 
 struct Gemm3Lds {
@@ -392,7 +408,7 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int t
     uint32_t b = blockIdx.x;
     const uint32_t nb = gridDim.x;
     if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
-    constexpr int GM = 8;
+    constexpr int GM = NEKO_TUNE_MM_G3_GM;
     const int group = static_cast<int>(b) / (GM * tiles_n);
     const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
     const int in_group = static_cast<int>(b) - group * GM * tiles_n;
@@ -478,13 +494,8 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int t
 template <typename TY>
 int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) {
     constexpr size_t lds = sizeof(Gemm3Lds);
-    static bool attr_set = false;  // dynamic LDS above 64 KB is enabled once per instantiation
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mm_gemm3_kernel<TY>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (e != hipSuccess) return fail(ctx, NEKO_ERR_HIP, "matmul: hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> allowed{0};
+    if (int rc = allow_lds(ctx, reinterpret_cast<const void*>(&mm_gemm3_kernel<TY>), lds, allowed)) return rc;
     hipLaunchKernelGGL((mm_gemm3_kernel<TY>), grid, dim3(kG3Threads), lds, ctx->stream, a, tm, tn);
     return NEKO_OK;
 }
@@ -1484,13 +1495,8 @@ __global__ __launch_bounds__(C::threads, 2) void mm_gemm2_kernel(MmArgs a, int t
 template <int FMT, typename TY, class C>
 int launch_gemm2(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn, int slices, float* partial) {
     constexpr size_t lds = sizeof(Gemm2Lds<C>);
-    static bool attr_set = false;  // dynamic LDS above 64 KB is enabled once per instantiation
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&mm_gemm2_kernel<FMT, TY, C>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (e != hipSuccess) return fail(ctx, NEKO_ERR_HIP, "matmul: hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> allowed{0};
+    if (int rc = allow_lds(ctx, reinterpret_cast<const void*>(&mm_gemm2_kernel<FMT, TY, C>), lds, allowed)) return rc;
     hipLaunchKernelGGL((mm_gemm2_kernel<FMT, TY, C>), grid, dim3(C::threads), lds, ctx->stream, a, tm, tn, slices, partial);
     return NEKO_OK;
 }

@@ -4,6 +4,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <unordered_map>
 
 #include "internal.h"
@@ -48,10 +49,11 @@ FastDiv make_fast_div(uint32_t d) {
 }
 
 int resident_blocks_per_cu(const void* kernel, int block, size_t lds_bytes) {
+    // Keyed by kernel, block size and LDS (every device here is the same gfx950 part).
     static std::mutex mu;
-    static std::map<std::pair<const void*, size_t>, int> cache;
+    static std::map<std::tuple<const void*, int, size_t>, int> cache;
     std::lock_guard<std::mutex> lk(mu);
-    const auto key = std::make_pair(kernel, lds_bytes);
+    const auto key = std::make_tuple(kernel, block, lds_bytes);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int n = 0;
