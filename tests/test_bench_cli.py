@@ -1,0 +1,28 @@
+"""bench.py's command line without a GPU: it parses, lists its workloads, and refuses more than one GPU
+before touching a device (the driver's contract: N > 1 exits with a message)."""
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                          timeout=300, cwd=ROOT)
+
+
+def test_help_lists_every_workload():
+    r = _run("--help")
+    assert r.returncode == 0, r.stderr
+    text = " ".join(r.stdout.split())
+    for w in ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
+              "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode16_matmul",
+              "qwen3_4b_prefill_matmul"):
+        assert w in text, w
+
+
+def test_more_than_one_gpu_is_refused():
+    r = _run("--gpus", "2")
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
