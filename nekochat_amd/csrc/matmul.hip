@@ -502,7 +502,7 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
 
 // ---------------------------------------------------------------- mid-size T: activations shared in LDS
 //
-// 5 <= T < 48 (FP4; FP8 above 8 tokens; F16 above 16), second form: each wave of a 4-wave workgroup
+// 5 <= T < 48 (FP4; FP8 above 8 tokens; F16 from 9 to 32), second form: each wave of a 4-wave workgroup
 // owns its own 16-row tile, and the workgroup stages its token chunk's activations for one slice of
 // K in LDS once, with coalesced loads (FP4 blocks pre-permuted to the MFMA k order), so every wave
 // reads its A fragments from LDS. (Re-reading them from L1 per wave and group, 16 token rows per instruction, left the L1 tag
@@ -517,9 +517,24 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
 #ifndef NEKO_TUNE_MM_T2_LDS
 #define NEKO_TUNE_MM_T2_LDS 65536
 #endif
+#ifndef NEKO_TUNE_MM_T2_MIN_F16
+#define NEKO_TUNE_MM_T2_MIN_F16 8
+#endif
+#ifndef NEKO_TUNE_MM_T2_MIN_FP8
+#define NEKO_TUNE_MM_T2_MIN_FP8 8
+#endif
+#ifndef NEKO_TUNE_MM_T2_MAX_T
+#define NEKO_TUNE_MM_T2_MAX_T 48
+#endif
+#ifndef NEKO_TUNE_MM_T2_FILL
+#define NEKO_TUNE_MM_T2_FILL 4
+#endif
 constexpr bool kTile2 = NEKO_TUNE_MM_TILE2;
 constexpr int kT2Waves = 4;
 constexpr int kT2Lds = NEKO_TUNE_MM_T2_LDS;  // LDS per workgroup (two per CU at 64 KB)
+constexpr int64_t kT2MaxT = NEKO_TUNE_MM_T2_MAX_T;  // exclusive; at most 65 (four 16-token tiles)
+static_assert(kT2MaxT <= 65, "the shared-activation kernel holds at most 64 tokens");
+constexpr int kT2Fill = NEKO_TUNE_MM_T2_FILL; // K slices until the grid holds this many workgroups per CU
 
 
 // Halves per staged token row for nb blocks: 32 nb plus 8 of padding (16-byte bank groups differ
@@ -868,6 +883,9 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
 #ifndef NEKO_TUNE_MM_GEMM_MIN_T
 #define NEKO_TUNE_MM_GEMM_MIN_T 48
 #endif
+#ifndef NEKO_TUNE_MM_GEMM_MIN_T_F16
+#define NEKO_TUNE_MM_GEMM_MIN_T_F16 33
+#endif
 #ifndef NEKO_TUNE_MM_GEMM_MF
 #define NEKO_TUNE_MM_GEMM_MF 4
 #endif
@@ -880,7 +898,10 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
 #ifndef NEKO_TUNE_MM_GEMM_WN
 #define NEKO_TUNE_MM_GEMM_WN 2
 #endif
-constexpr int64_t kGemmMinT = NEKO_TUNE_MM_GEMM_MIN_T;  // smallest T taking the GEMM path
+// Smallest T taking the GEMM path: from 33 tokens for F16 rows, 48 for FP8 / FP4 (measured on the
+// Qwen3-4B projections: below these the shared-activation kernel's three token tiles are faster).
+constexpr int64_t kGemmMinT = NEKO_TUNE_MM_GEMM_MIN_T;
+constexpr int64_t kGemmMinTF16 = NEKO_TUNE_MM_GEMM_MIN_T_F16;
 constexpr int kGemmMF = NEKO_TUNE_MM_GEMM_MF, kGemmNF = NEKO_TUNE_MM_GEMM_NF;  // 16 x 16 fragments per wave
 constexpr int kGemmWM = NEKO_TUNE_MM_GEMM_WM, kGemmWN = NEKO_TUNE_MM_GEMM_WN;  // waves per workgroup
 constexpr int kGemmThreads = 64 * kGemmWM * kGemmWN;
@@ -1170,22 +1191,31 @@ __global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int 
     }
 }
 
+// The sum over slices of partial[slice][t][n .. n + width), added in slice order. Eight slices'
+// loads are in flight per round (one memory round trip for up to eight slices): indices past the
+// last slice re-read it and are not added.
+template <typename V>
+__device__ __forceinline__ V sum_slices(const float* partial, int64_t total, int64_t i, int slices) {
+    V v = *reinterpret_cast<const V*>(partial + i);
+    for (int s0 = 0; s0 < slices; s0 += 8) {
+        V p[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            p[q] = *reinterpret_cast<const V*>(partial + static_cast<int64_t>(min(s0 + q, slices - 1)) * total + i);
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (s0 + q > 0 && s0 + q < slices) v += p[q];
+    }
+    return v;
+}
+
 // y = epilogue(sum over slices of partial[slice][t][n]), slices added in order.
 template <typename TY>
 __global__ __launch_bounds__(256) void mm_splitk_reduce(MmArgs a, const float* partial, int slices) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= a.T * static_cast<int64_t>(a.N)) return;
     const int64_t total = a.T * static_cast<int64_t>(a.N);
-    float v = partial[i];
-    int sl = 1;
-    for (; sl + 4 <= slices; sl += 4) {  // four slices' loads in flight, added in slice order
-        float p[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) p[q] = partial[static_cast<int64_t>(sl + q) * total + i];
-#pragma unroll
-        for (int q = 0; q < 4; q++) v += p[q];
-    }
-    for (; sl < slices; sl++) v += partial[static_cast<int64_t>(sl) * total + i];
+    if (i >= total) return;
+    const float v = sum_slices<float>(partial, total, i, slices);
     const int64_t t = i / a.N, n = i - t * a.N;
     epilogue<TY>(a, t, n, v);
 }
@@ -1196,17 +1226,7 @@ __global__ __launch_bounds__(256) void mm_splitk_reduce4(MmArgs a, const float* 
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
     const int64_t total = a.T * static_cast<int64_t>(a.N);
     if (i >= total) return;
-    // Loads four slices at a time (one memory round trip each), added in slice order.
-    float4v v = *reinterpret_cast<const float4v*>(partial + i);
-    int sl = 1;
-    for (; sl + 4 <= slices; sl += 4) {
-        float4v p[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) p[q] = *reinterpret_cast<const float4v*>(partial + static_cast<int64_t>(sl + q) * total + i);
-#pragma unroll
-        for (int q = 0; q < 4; q++) v += p[q];
-    }
-    for (; sl < slices; sl++) v += *reinterpret_cast<const float4v*>(partial + static_cast<int64_t>(sl) * total + i);
+    const float4v v = sum_slices<float4v>(partial, total, i, slices);
     const int64_t t = i / a.N, n = i - t * a.N;
 #pragma unroll
     for (int e = 0; e < 4; e++) epilogue<TY>(a, t, n + e, v[e]);
@@ -1633,7 +1653,11 @@ int launch_tile2_tt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, 
     switch (tt) {
         case 1: return launch_tile2<FMT, 1>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
         case 2: return launch_tile2<FMT, 2>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
-        default: return launch_tile2<FMT, 3>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
+        default:  // tt 3, or 4 where the kernel takes more than 48 tokens
+            if constexpr (kT2MaxT > 49) {
+                if (tt == 4) return launch_tile2<FMT, 4>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
+            }
+            return launch_tile2<FMT, 3>(ctx, a, y_dtype, grid, lds, slice_blocks, partial);
     }
 }
 
@@ -1721,7 +1745,7 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
             default: return launch_gemv_nt<2>(ctx, a, y_dtype, grid, kw, gemv_nt);
         }
     }
-    if (fast && T >= kGemmMinT) {
+    if (fast && T >= (fmt == NEKO_FMT_F16 ? kGemmMinTF16 : kGemmMinT)) {
         const bool v2 = kGemmV2 && K % kG2BK == 0;
         // F16: 256 x 256 tiles with direct-to-LDS loads when they give every CU at least two (with
         // fewer, the partial last round of one-per-CU workgroups cost more than the wider tiles save:
@@ -1777,20 +1801,23 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         if (slices > 1) return launch_splitk_reduce(ctx, a, y_dtype, partial, slices, what);
         return NEKO_OK;
     }
-    // The shared-activation kernel where it measured faster: FP4 at every T, FP8 above 8 tokens, F16
-    // above 16 (below that the per-wave kernel's single launch wins over the slices' reduction).
-    const bool tile2 = kTile2 && T < 48 && (fmt == NEKO_FMT_FP4 || (fmt == NEKO_FMT_FP8 && T > 8) || T > 16);
+    // The shared-activation kernel where it measured faster: FP4 at every T, FP8 and F16 above 8
+    // tokens (below that the per-wave kernel's single launch wins over the slices' reduction; F16
+    // takes the GEMM from 33).
+    const bool tile2 = kTile2 && T < kT2MaxT &&
+                       (fmt == NEKO_FMT_FP4 || (fmt == NEKO_FMT_FP8 && T > NEKO_TUNE_MM_T2_MIN_FP8) ||
+                        (fmt == NEKO_FMT_F16 && T > NEKO_TUNE_MM_T2_MIN_F16));
     if (fast && tile2) {
-        const int tt = static_cast<int>((T + 15) / 16);  // 1..3: one chunk of 16 tt tokens
+        const int tt = static_cast<int>((T + 15) / 16);  // 1..4: one chunk of 16 tt tokens
         const int64_t tiles = (N + 16 * kT2Waves - 1) / (16 * kT2Waves);
         const int nblk = static_cast<int>(K / kBlockK);
         const size_t stage = static_cast<size_t>(kT2Waves) * stage_bytes(fmt);
         // The largest slice of K whose staged activations fit beside the staging tiles; then more
-        // slices (halving) until the grid holds about two workgroups per CU, each slice at least 8
+        // slices (halving) until the grid holds about kT2Fill workgroups per CU, each slice at least 8
         // blocks long.
         const int cap = static_cast<int>(((kT2Lds - stage) / (32 * tt) - 8) / 32);
         int slices = (nblk + cap - 1) / cap;
-        while (tiles * slices < 2 * ctx->cu_count && nblk / (2 * slices) >= 8) slices *= 2;
+        while (tiles * slices < kT2Fill * ctx->cu_count && nblk / (2 * slices) >= 8) slices *= 2;
         int slice_blocks = (nblk + slices - 1) / slices;
         slice_blocks = std::min(cap, (slice_blocks + kGroup - 1) / kGroup * kGroup);  // whole groups where possible
         slices = (nblk + slice_blocks - 1) / slice_blocks;
