@@ -65,7 +65,9 @@ const char* neko_hip_last_error(const neko_hip_ctx* ctx);
 int neko_hip_device_name(neko_hip_ctx* ctx, char* buf, size_t buf_bytes);
 size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx);
 /* Routes subsequent work to a hipStream_t on the same device (e.g. a framework's current stream);
- * NULL selects the device's null stream, the default. The caller keeps ownership of the stream. */
+ * NULL selects the device's null stream, the default. The caller keeps ownership of the stream.
+ * On a change the new stream is first made to wait (on the device) for the work already issued on
+ * the previous one, so the context's ops stay ordered across the switch. */
 int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream);
 void* neko_hip_get_stream(const neko_hip_ctx* ctx);
 

@@ -22,6 +22,7 @@ struct neko_hip_ctx {
     std::unordered_set<void*> allocs;
     void* workspace = nullptr;  // device scratch for split reductions, grown on demand
     size_t workspace_bytes = 0;
+    hipEvent_t switch_event = nullptr;  // orders a newly routed stream after the previous one
 };
 
 namespace neko_hip {

@@ -127,6 +127,7 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (void* p : ctx->allocs) (void)hipFree(p);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     delete ctx;
     return rc;
 }
@@ -143,7 +144,16 @@ size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx) { return ctx ? ctx->ma
 
 int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream) {
     NEKO_ENTER(ctx);
-    ctx->stream = static_cast<hipStream_t>(hip_stream);
+    const hipStream_t next = static_cast<hipStream_t>(hip_stream);
+    if (next == ctx->stream) return NEKO_OK;
+    // The new stream waits for the work already issued on the old one (on the device, not the
+    // host): the context's calls share its split-K workspace, which that work may still be using.
+    if (!ctx->switch_event)
+        if (int rc = check(ctx, hipEventCreateWithFlags(&ctx->switch_event, hipEventDisableTiming), "hipEventCreateWithFlags"))
+            return rc;
+    if (int rc = check(ctx, hipEventRecord(ctx->switch_event, ctx->stream), "hipEventRecord")) return rc;
+    if (int rc = check(ctx, hipStreamWaitEvent(next, ctx->switch_event, 0), "hipStreamWaitEvent")) return rc;
+    ctx->stream = next;
     return NEKO_OK;
 }
 

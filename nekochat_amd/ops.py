@@ -127,7 +127,7 @@ _recording = threading.local()
 def _issue(ctx: Context, fn, *args):
     rec = getattr(_recording, "rec", None)
     if rec is not None:  # being prepared: remember the call instead of issuing it
-        rec.append((fn, args))
+        rec.append((ctx, fn, args))
         return
     ctx.check(fn(*args))
 
@@ -143,10 +143,13 @@ def prepare(op, *args, **kwargs):
         _recording.rec = None
     if len(rec) != 1:
         raise NekoError(f"prepare: {getattr(op, '__name__', op)} issued {len(rec)} calls; expected one")
-    fn, cargs = rec[0]
-    handle = cargs[0]
+    ctx, fn, cargs = rec[0]
+    handle, stream = cargs[0], ctx._bound
 
     def run():
+        if ctx._bound != stream:  # another op routed the context elsewhere meanwhile
+            ctx.check(lib.neko_hip_set_stream(handle, stream or None))
+            ctx._bound = stream
         rc = fn(*cargs)
         if rc != NEKO_OK:
             raise NekoError(lib.neko_hip_last_error(handle).decode(), rc)

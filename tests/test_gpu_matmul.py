@@ -85,6 +85,32 @@ def test_matmul_split_k_integer_bitexact(dev, fmt):
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+def test_matmul_split_k_across_stream_switch(dev):
+    """Split-K calls share the context's f32 workspace. Calls issued alternately on two torch
+    streams (each switch re-routes the context; the later shapes grow the workspace) stay ordered:
+    every output equals the exact integer product."""
+    _case("matmul split-K across stream switches")
+    rng = np.random.default_rng(900)
+    cases = []
+    for T, K, N in ((16, 4096, 2560), (16, 2560, 6144), (40, 9728, 2560)):  # all split K
+        tab, w = M.integer_table(ops.FMT_FP4, N, K, rng)
+        x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+        exact = x.astype(np.float64) @ w.astype(np.float64).T
+        assert np.abs(exact).max() < 2 ** 24
+        cases.append((torch.from_numpy(x.astype(np.float16)).to(dev), torch.from_numpy(tab).to(dev), K,
+                      exact.astype(np.float32)))
+    torch.cuda.synchronize()
+    streams = (torch.cuda.Stream(dev), torch.cuda.Stream(dev))
+    outs = []
+    for rep in range(2):
+        for i, (xd, td, K, _) in enumerate(cases):
+            with torch.cuda.stream(streams[(i + rep) % 2]):
+                outs.append((i, ops.matmul(xd, td, ops.FMT_FP4, K)))
+    torch.cuda.synchronize()
+    for i, y in outs:
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), cases[i][3].view(np.uint32)), i
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
     (2000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both

@@ -68,6 +68,30 @@ def test_rmsnorm_strided_inplace_and_edges(dev):
     assert ops.rms_norm(empty, w, 1e-6).shape == (0, C)
 
 
+def test_prepared_call_keeps_its_stream(dev):
+    """ops.prepare replays one C call on the torch stream current at preparation, also after another
+    op has routed the thread's context to a different stream; its output equals a direct call's."""
+    _case("prepared rms_norm replay after a stream switch")
+    x, w = _f16((64, 1024), 11, dev), _w(1024, 12, dev)
+    want = ops.rms_norm(x, w, 1e-6)
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    out = torch.empty_like(x)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        run, res = ops.prepare(ops.rms_norm, x, w, 1e-6, out=out)
+    assert res is out
+    with torch.cuda.stream(s2):
+        ops.rms_norm(_f16((8, 1024), 13, dev), w, 1e-6)  # routes the context to s2
+    ctx = ops.context(dev.index if dev.index is not None else 0)
+    assert ctx._bound == s2.cuda_stream
+    out.zero_()
+    torch.cuda.synchronize()
+    run()
+    assert ctx._bound == s1.cuda_stream
+    s1.synchronize()
+    assert torch.equal(out, want)
+
+
 def test_rmsnorm_f32(dev):
     _case("rmsnorm f32")
     T, C = 17, 2560
