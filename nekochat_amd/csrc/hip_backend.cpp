@@ -115,6 +115,20 @@ private:
         return b->dev;
     }
 
+    // Byte counts for the bounds checks, failing rather than wrapping (grid sizes are 32-bit and the
+    // parameters 31-bit, so their products can pass 64 bits).
+    static uint64_t mul(uint64_t a, uint64_t b, uint64_t c = 1) {
+        uint64_t ab = 0, abc = 0;
+        if (__builtin_mul_overflow(a, b, &ab) || __builtin_mul_overflow(ab, c, &abc))
+            fail("HIP: dispatch size overflows 64 bits");
+        return abc;
+    }
+    static uint64_t add(uint64_t a, uint64_t b) {
+        uint64_t r = 0;
+        if (__builtin_add_overflow(a, b, &r)) fail("HIP: dispatch size overflows 64 bits");
+        return r;
+    }
+
     static void positive(int64_t v, const char* what) {
         if (v < 0) fail(std::string("HIP ") + what + ": negative parameter");
     }
@@ -130,9 +144,9 @@ private:
         const int fmt = (flags & 2) ? NEKO_FMT_FP8 : (flags & 4) ? NEKO_FMT_FP4 : NEKO_FMT_F16;
         // The F16 table is indexed row * C halves; quantized tables by row * rowWords words (embed.comp:23-36).
         const int64_t rowBytes = fmt == NEKO_FMT_F16 ? 2 * C : 4 * rowWords;
-        void* tokens = need(b, 0, uint64_t(T) * 4, "Embed");
-        void* table = need(b, 1, uint64_t(rows) * uint64_t(rowBytes), "Embed");
-        void* out = need(b, 3, uint64_t(T) * uint64_t(C) * 4, "Embed");
+        void* tokens = need(b, 0, mul(T, 4), "Embed");
+        void* table = need(b, 1, mul(rows, rowBytes), "Embed");
+        void* out = need(b, 3, mul(T, C, 4), "Embed");
         const uint16_t* wpe = nullptr;
         int64_t wpeRows = 0;
         if (flags & 1) {
@@ -151,13 +165,13 @@ private:
         positive(C, "LayerNorm");
         positive(rowOffset, "LayerNorm");
         if (rows == 0 || C == 0) return;
-        auto* x = static_cast<const float*>(need(b, 0, uint64_t(rowOffset + rows) * uint64_t(C) * 4, "LayerNorm"));
-        void* y = need(b, 1, uint64_t(rows) * uint64_t(C) * 4, "LayerNorm");
-        auto* g = static_cast<const float*>(need(b, 2, uint64_t(C) * 4, "LayerNorm"));
+        auto* x = static_cast<const float*>(need(b, 0, mul(rowOffset + rows, C, 4), "LayerNorm"));
+        void* y = need(b, 1, mul(rows, C, 4), "LayerNorm");
+        auto* g = static_cast<const float*>(need(b, 2, mul(C, 4), "LayerNorm"));
         if (rms) {
             check(neko_hip_rmsnorm(ctx_, x + rowOffset * C, C, y, C, g, rows, C, eps, NEKO_DT_F32));
         } else {
-            auto* beta = static_cast<const float*>(need(b, 3, uint64_t(C) * 4, "LayerNorm"));
+            auto* beta = static_cast<const float*>(need(b, 3, mul(C, 4), "LayerNorm"));
             check(neko_hip_layernorm(ctx_, x + rowOffset * C, C, y, C, g, beta, rows, C, eps, NEKO_DT_F32));
         }
     }
@@ -173,7 +187,7 @@ private:
         if (hd <= 0 || hd % 2 != 0 || hd > 512) fail("HIP Rope: head dim must be even and <= 512");
         if (T == 0 || gx == 0) return;
         if (stride < int64_t(gx) * hd) fail("HIP Rope: qkv stride shorter than the heads it covers");
-        void* qkv = need(b, 0, (uint64_t(T - 1) * uint64_t(stride) + uint64_t(gx) * uint64_t(hd)) * 4, "Rope");
+        void* qkv = need(b, 0, mul(add(mul(T - 1, stride), mul(gx, hd)), 4), "Rope");
         const float* wn = norm ? static_cast<const float*>(need(b, 1, uint64_t(2 * hd) * 4, "Rope")) : nullptr;
         HipBuffer* cs = as(b[2], "Rope");
         const int64_t nPos = int64_t(cs->size / (uint64_t(hd) * 4));
@@ -187,8 +201,8 @@ private:
         positive(T, "SiluMul");
         positive(I, "SiluMul");
         if (T == 0 || I == 0) return;
-        void* h = need(b, 0, uint64_t(T) * uint64_t(2 * I) * 4, "SiluMul");
-        void* g = need(b, 1, uint64_t(T) * uint64_t(I) * 4, "SiluMul");
+        void* h = need(b, 0, mul(T, 2 * I, 4), "SiluMul");
+        void* g = need(b, 1, mul(T, I, 4), "SiluMul");
         check(neko_hip_swiglu(ctx_, h, 2 * I, g, I, T, I, NEKO_DT_F32));
     }
 
@@ -199,9 +213,9 @@ private:
         if (groups <= 0 || D % groups != 0) fail("HIP GatedRmsNorm: groups must divide D");
         if (zStride < D) fail("HIP GatedRmsNorm: z stride shorter than D");
         if (rows == 0 || D == 0) return;
-        void* y = need(b, 0, uint64_t(rows) * uint64_t(D) * 4, "GatedRmsNorm");
-        void* z = need(b, 1, (uint64_t(rows - 1) * uint64_t(zStride) + uint64_t(D)) * 4, "GatedRmsNorm");
-        auto* w = static_cast<const float*>(need(b, 2, uint64_t(D) * 4, "GatedRmsNorm"));
+        void* y = need(b, 0, mul(rows, D, 4), "GatedRmsNorm");
+        void* z = need(b, 1, mul(add(mul(rows - 1, zStride), D), 4), "GatedRmsNorm");
+        auto* w = static_cast<const float*>(need(b, 2, mul(D, 4), "GatedRmsNorm"));
         check(neko_hip_gated_rmsnorm(ctx_, y, D, z, zStride, y, D, w, rows, D, int(groups), eps, NEKO_DT_F32));
     }
 
@@ -209,8 +223,8 @@ private:
         const int64_t n = pa[0];
         positive(n, "Gelu");
         if (n == 0) return;
-        void* x = need(b, 0, uint64_t(n) * 4, "Gelu");
-        void* y = need(b, 1, uint64_t(n) * 4, "Gelu");
+        void* x = need(b, 0, mul(n, 4), "Gelu");
+        void* y = need(b, 1, mul(n, 4), "Gelu");
         check(neko_hip_gelu_tanh(ctx_, x, y, n, NEKO_DT_F32));
     }
 
@@ -224,9 +238,9 @@ private:
         positive(vOff, "KvStore");
         if (T == 0 || W == 0) return;
         if (stride < kOff + W || stride < vOff + W) fail("HIP KvStore: k/v columns exceed the qkv row stride");
-        void* qkv = need(b, 0, (uint64_t(T - 1) * uint64_t(stride) + uint64_t(std::max(kOff, vOff) + W)) * 4, "KvStore");
-        auto* kc = static_cast<uint16_t*>(need(b, 1, uint64_t(pos0 + T) * uint64_t(W) * 2, "KvStore"));
-        auto* vc = static_cast<uint16_t*>(need(b, 2, uint64_t(pos0 + T) * uint64_t(W) * 2, "KvStore"));
+        void* qkv = need(b, 0, mul(add(mul(T - 1, stride), std::max(kOff, vOff) + W), 4), "KvStore");
+        auto* kc = static_cast<uint16_t*>(need(b, 1, mul(pos0 + T, W, 2), "KvStore"));
+        auto* vc = static_cast<uint16_t*>(need(b, 2, mul(pos0 + T, W, 2), "KvStore"));
         check(neko_hip_store_kv(ctx_, qkv, stride, kOff, vOff, T, W, pos0, nullptr, kc, vc, pos0 + T, NEKO_DT_F32));
     }
 
@@ -236,10 +250,10 @@ private:
         const float eps = bitsFloat(pa[1]);
         positive(C, "AddRmsNorm");
         if (rows == 0 || C == 0) return;
-        void* x = need(b, 0, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
-        void* d = need(b, 1, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
-        void* xn = need(b, 2, uint64_t(rows) * uint64_t(C) * 4, "AddRmsNorm");
-        auto* w = static_cast<const float*>(need(b, 3, uint64_t(C) * 4, "AddRmsNorm"));
+        void* x = need(b, 0, mul(rows, C, 4), "AddRmsNorm");
+        void* d = need(b, 1, mul(rows, C, 4), "AddRmsNorm");
+        void* xn = need(b, 2, mul(rows, C, 4), "AddRmsNorm");
+        auto* w = static_cast<const float*>(need(b, 3, mul(C, 4), "AddRmsNorm"));
         check(neko_hip_add_rmsnorm(ctx_, x, C, d, C, xn, C, w, rows, C, eps, NEKO_DT_F32));
     }
 
@@ -258,10 +272,10 @@ private:
         if (T == 0 || rows == 0) return;
         if (nOff + rows > N) fail(std::string("HIP ") + what + ": output columns exceed the row stride of y");
         const uint64_t rb = neko_quant_row_bytes(fmt, K);
-        auto* x = static_cast<char*>(need(b, 0, uint64_t(row0 + T) * uint64_t(K) * 4, what)) + row0 * K * 4;
-        void* w = need(b, 1, uint64_t(rows) * rb, what);
-        const float* bias = (flags & 4) ? static_cast<const float*>(need(b, 2, uint64_t(rows) * 4, what)) : nullptr;
-        auto* y = static_cast<char*>(need(b, 3, (uint64_t(T - 1) * uint64_t(N) + uint64_t(nOff + rows)) * 4, what)) + nOff * 4;
+        auto* x = static_cast<char*>(need(b, 0, mul(row0 + T, K, 4), what)) + row0 * K * 4;
+        void* w = need(b, 1, mul(rows, rb), what);
+        const float* bias = (flags & 4) ? static_cast<const float*>(need(b, 2, mul(rows, 4), what)) : nullptr;
+        auto* y = static_cast<char*>(need(b, 3, mul(add(mul(T - 1, N), nOff + rows), 4), what)) + nOff * 4;
         check(neko_hip_matmul(ctx_, x, K, T, K, w, int64_t(rb), fmt, rows, bias, y, N, flags & 3, NEKO_DT_F32,
                               NEKO_DT_F32));
     }

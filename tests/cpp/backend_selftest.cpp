@@ -320,12 +320,20 @@ struct Harness {
     void outOfRange() {  // a dispatch reading past a buffer throws instead of faulting
         Buffer* small = be.create(16);
         Buffer* g = be.create(96 * 4);
+        bool threw = false;
         try {
             run(Kernel::LayerNorm, {small, small, g, g}, {96, floatBits(1e-5f), 0, 0}, 3, 1);
         } catch (const NekoError&) {
-            return;
+            threw = true;
         }
-        throw Failure{"out-of-range LayerNorm dispatch did not throw"};
+        if (!threw) throw Failure{"out-of-range LayerNorm dispatch did not throw"};
+        threw = false;
+        try {  // byte counts past 64 bits (2^32 - 1 rows of 2^31 - 1 floats) throw rather than wrap
+            run(Kernel::LayerNorm, {small, small, g, g}, {0x7fffffff, floatBits(1e-5f), 1, 0}, 0xffffffffu, 1);
+        } catch (const NekoError&) {
+            threw = true;
+        }
+        if (!threw) throw Failure{"oversized LayerNorm dispatch did not throw"};
     }
 };
 
