@@ -502,7 +502,7 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
 
 // ---------------------------------------------------------------- mid-size T: activations shared in LDS
 //
-// 5 <= T < 48 (FP4; FP8 above 8 tokens; F16 from 9 to 32), second form: each wave of a 4-wave workgroup
+// 3 <= T < 48 (FP4; FP8 above 8 tokens; F16 from 9 to 32), second form: each wave of a 4-wave workgroup
 // owns its own 16-row tile, and the workgroup stages its token chunk's activations for one slice of
 // K in LDS once, with coalesced loads (FP4 blocks pre-permuted to the MFMA k order), so every wave
 // reads its A fragments from LDS. (Re-reading them from L1 per wave and group, 16 token rows per instruction, left the L1 tag
@@ -745,12 +745,15 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
 }
 
 #ifndef NEKO_TUNE_MM_GEMV_MAX_T
-#define NEKO_TUNE_MM_GEMV_MAX_T 4
+#define NEKO_TUNE_MM_GEMV_MAX_T 2
 #endif
 #ifndef NEKO_TUNE_MM_GEMV_WAVE_TARGET
 #define NEKO_TUNE_MM_GEMV_WAVE_TARGET 8192
 #endif
-constexpr int64_t kGemvMaxT = NEKO_TUNE_MM_GEMV_MAX_T;  // largest T taking the GEMV path
+// Largest T taking the GEMV path: 2 (measured on the Qwen3-4B projections: at 3 and 4 tokens the
+// MFMA tile kernels take 14% less time over the four projections, at 2 the GEMV 11% less).
+constexpr int64_t kGemvMaxT = NEKO_TUNE_MM_GEMV_MAX_T;
+static_assert(kGemvMaxT >= 1 && kGemvMaxT <= 4, "the GEMV holds 1, 2 or 4 tokens per pass");
 constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
 constexpr int kGemvRows = 4;    // weight rows per wave: 16 lanes each
 constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw slices of K
@@ -1608,8 +1611,11 @@ template <int FMT>
 int launch_gemv_nt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int kw, int nt) {
     switch (nt) {
         case 1: return launch_gemv<FMT, 1>(ctx, a, y_dtype, grid, kw);
-        case 2: return launch_gemv<FMT, 2>(ctx, a, y_dtype, grid, kw);
-        default: return launch_gemv<FMT, 4>(ctx, a, y_dtype, grid, kw);
+        default:  // 2, or 4 where the GEMV takes more than two tokens
+            if constexpr (kGemvMaxT > 2) {
+                if (nt == 4) return launch_gemv<FMT, 4>(ctx, a, y_dtype, grid, kw);
+            }
+            return launch_gemv<FMT, 2>(ctx, a, y_dtype, grid, kw);
     }
 }
 

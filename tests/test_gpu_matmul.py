@@ -152,7 +152,8 @@ def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
     (3, 32, 40),        # one block
     (200, 768, 96),     # GPT-2 width, several token chunks
     (2, 4096, 2560),    # two-token decode
-    (4, 9728, 64),      # four tokens whose activations exceed one LDS stage: two token chunks
+    (2, 20480, 64),     # two tokens whose activations exceed the GEMV's LDS stage: two token chunks
+    (4, 9728, 64),      # four tokens, long K: MFMA tiles
     (4, 768, 3072),     # GPT-2 MLP, four tokens
     (256, 2560, 6144),  # prefill chunk: GEMM tiles
     (300, 1024, 700),   # partial token and row tiles
