@@ -504,7 +504,7 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
 
 // ---------------------------------------------------------------- mid-size T: activations shared in LDS
 //
-// 3 <= T < 48 (FP4; FP8 above 8 tokens; F16 from 9 to 32), second form: each wave of a 4-wave workgroup
+// FP4 at 5 <= T < 48, FP8 at 13 <= T < 48, F16 at 17 <= T < 33: second form: each wave of a 4-wave workgroup
 // owns its own 16-row tile, and the workgroup stages its token chunk's activations for one slice of
 // K in LDS once, with coalesced loads (FP4 blocks pre-permuted to the MFMA k order), so every wave
 // reads its A fragments from LDS. (Re-reading them from L1 per wave and group, 16 token rows per instruction, left the L1 tag
@@ -520,10 +520,13 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
 #define NEKO_TUNE_MM_T2_LDS 65536
 #endif
 #ifndef NEKO_TUNE_MM_T2_MIN_F16
-#define NEKO_TUNE_MM_T2_MIN_F16 8
+#define NEKO_TUNE_MM_T2_MIN_F16 16
 #endif
 #ifndef NEKO_TUNE_MM_T2_MIN_FP8
-#define NEKO_TUNE_MM_T2_MIN_FP8 8
+#define NEKO_TUNE_MM_T2_MIN_FP8 12
+#endif
+#ifndef NEKO_TUNE_MM_T2_MIN_FP4
+#define NEKO_TUNE_MM_T2_MIN_FP4 4
 #endif
 #ifndef NEKO_TUNE_MM_T2_MAX_T
 #define NEKO_TUNE_MM_T2_MAX_T 48
@@ -1809,11 +1812,11 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         if (slices > 1) return launch_splitk_reduce(ctx, a, y_dtype, partial, slices, what);
         return NEKO_OK;
     }
-    // The shared-activation kernel where it measured faster: FP4 at every T, FP8 and F16 above 8
-    // tokens (below that the per-wave kernel's single launch wins over the slices' reduction; F16
-    // takes the GEMM from 33).
+    // The shared-activation kernel where it measured faster than the per-wave kernel (whose single
+    // launch needs no reduction of K slices): FP4 above 4 tokens, FP8 above 12, F16 above 16 (and
+    // below 33, where F16 takes the GEMM).
     const bool tile2 = kTile2 && T < kT2MaxT &&
-                       (fmt == NEKO_FMT_FP4 || (fmt == NEKO_FMT_FP8 && T > NEKO_TUNE_MM_T2_MIN_FP8) ||
+                       ((fmt == NEKO_FMT_FP4 && T > NEKO_TUNE_MM_T2_MIN_FP4) || (fmt == NEKO_FMT_FP8 && T > NEKO_TUNE_MM_T2_MIN_FP8) ||
                         (fmt == NEKO_FMT_F16 && T > NEKO_TUNE_MM_T2_MIN_F16));
     if (fast && tile2) {
         const int tt = static_cast<int>((T + 15) / 16);  // 1..4: one chunk of 16 tt tokens

@@ -120,7 +120,7 @@ def test_matmul_split_k_across_stream_switch(dev):
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
     (20, 4096, 100),    # 5 <= T < 48: activations staged per K slice, several slices reduced in order
     (47, 2080, 300),    # three token tiles, K slices ending in a partial group
-    (12, 2560, 700),    # 9-16 tokens (all formats staged per K slice), several slices
+    (12, 2560, 700),    # 12 tokens: F16 / FP8 per-wave tiles, FP4 staged per K slice (several slices)
 ])
 def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
     """Integer-valued weights and activations through each MFMA tiling: every partial sum is exact,
@@ -147,7 +147,7 @@ def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
     (1, 2560, 6144),    # Qwen3-4B decode: q/k/v projection
     (1, 9728, 2560),    # Qwen3-4B decode: down projection
     (8, 2560, 19456),   # Qwen3-4B batch-8 decode: gate/up projection
-    (16, 2560, 6144),   # Qwen3-4B batch-16 decode: q/k/v projection, activations staged per K slice
+    (16, 2560, 6144),   # Qwen3-4B batch-16 decode: q/k/v projection
     (33, 4096, 2560),   # o projection, three token tiles
     (3, 32, 40),        # one block
     (200, 768, 96),     # GPT-2 width, several token chunks
