@@ -39,7 +39,8 @@ def _bound_check(got, exact, mag, K, what):
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 16, 17, 64, 100, 128, 300])
 def test_matmul_integer_rows_bitexact(dev, fmt, T):
     """K = 320 (ten 32-blocks: two 4-block groups and a 2-block tail), N = 37 (a partial row tile).
-    T <= 4: the decode path; 5..127: the MFMA tiles; >= 128: the GEMM (300: a partial token tile)."""
+    T <= 2: the GEMV; 3..47: the MFMA tile kernels (F16: up to 32); above: the GEMM (300: a partial
+    token tile)."""
     _case(f"matmul integer fmt={fmt} T={T}")
     rng = np.random.default_rng(100 + 10 * fmt + T)
     K, N = 320, 37
@@ -118,7 +119,7 @@ def test_matmul_split_k_across_stream_switch(dev):
     (4000, 320, 4100),  # F16: 128 x 128 tiles (too few 256 x 256 tiles for two per CU), partial in both
     (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
-    (20, 4096, 100),    # 5 <= T < 48: activations staged per K slice, several slices reduced in order
+    (20, 4096, 100),    # 20 tokens: activations staged per K slice, several slices reduced in order
     (47, 2080, 300),    # three token tiles, K slices ending in a partial group
     (12, 2560, 700),    # 12 tokens: F16 / FP8 per-wave tiles, FP4 staged per K slice (several slices)
 ])
