@@ -193,7 +193,10 @@ int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t col
  *          shaders' nOffset) are a pointer offset into y.
  * The dot products are summed in f32 (f16 activations and weight codes exactly, each 32-block scaled
  * by its f16 scale) in a different order from the reference's sequential loop: results agree to f32
- * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows. */
+ * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows.
+ * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown) by the
+ * first call that needs more, kept until neko_hip_destroy; make one uncaptured call at the largest
+ * shape before capturing calls in a HIP graph. */
 #define NEKO_MM_GELU 1
 #define NEKO_MM_ACCUMULATE 2
 int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
