@@ -262,7 +262,7 @@ __device__ __forceinline__ void mm_step(float4v (&acc)[TT], MmStage<FMT>& st, co
 
 // Waves per workgroup the kernel is compiled for: more than one token tile needs more than 128
 // VGPRs, which allows at most 8 waves.
-__host__ __device__ constexpr int max_waves(int fmt, int tt) { return tt == 1 ? 16 : 8; }
+__host__ __device__ constexpr int max_waves(int /*fmt*/, int tt) { return tt == 1 ? 16 : 8; }
 
 // Dynamic LDS of a workgroup: the waves' staging tiles and, with more than one wave, the partial
 // tiles of the K split.
