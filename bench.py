@@ -734,16 +734,17 @@ def all_configs(args):
     return out
 
 
-def cpu_baseline(cfg, rows=256, reps=5):
+def cpu_baseline(cfg, rows=None, reps=5):
     """The reference's CPU path for the layer's four ops (its compiled cpu::rmsNorm, the Qwen3 q/k loop
     of rmsNorm + rope, cpu::siluMul on f32 activations, as its CPU forward pass holds them) on one
-    pinned core over `rows` tokens of the same workload, scaled to the full layer; the oracle's f32
-    restatement when oracle/_ref is not built."""
+    pinned core over `rows` tokens of the same workload (default: all of them, ~0.2 s per layer),
+    scaled to the full layer; the oracle's f32 restatement when oracle/_ref is not built."""
     import numpy as np
 
     from nekochat_amd import workloads as wl
     from oracle import oracle as O
 
+    rows = cfg.T if rows is None else rows
     x = _f32((rows, cfg.C), 0.0, 1.0, 1)
     w = wl.weight_f32(cfg.C, 1.0, 0.05, 2, "cpu").numpy()
     qkv = _f32((rows, cfg.qkv_stride), 0.0, 1.0, 4)
@@ -790,8 +791,9 @@ def cpu_baseline(cfg, rows=256, reps=5):
         "value": round(total_bytes / layer_s / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
         "us_per_layer": round(layer_s * 1e6, 1),
         "per_op_us": {k: round(v * 1e6, 1) for k, v in t.items()},
-        "sample": f"{rows} of {cfg.T} tokens per op (median of {reps}), scaled to the full layer; "
-                  f"1 pinned core of {os.cpu_count()}; g++ -O3 portable x86-64 build; f32 activations",
+        "sample": (f"the full {cfg.T}-token layer" if rows == cfg.T else f"{rows} of {cfg.T} tokens, scaled to the full layer")
+                  + f" per op (median of {reps}); 1 pinned core of {os.cpu_count()}; g++ -O3 portable x86-64 build; "
+                  "f32 activations",
     }
 
 
