@@ -197,6 +197,7 @@ GPT2_CHAIN = Gpt2Chain()
 QUANT_GATHER = QuantGather()
 GRANITE_NORMS = GraniteNorms()
 QWEN3_DECODE_MATMUL = Qwen3DecodeMatmul()
+QWEN3_DECODE4_MATMUL = Qwen3DecodeMatmul(T=4)  # one decode step of 4 sequences
 QWEN3_DECODE16_MATMUL = Qwen3DecodeMatmul(T=16)  # one decode step of 16 sequences
 QWEN3_PREFILL_MATMUL = Qwen3PrefillMatmul()
 
