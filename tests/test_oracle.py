@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import mm_tables as M
-from conftest import f32_line
+from conftest import f16_line, f32_line
 from oracle import oracle as O
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
@@ -422,6 +422,78 @@ def test_gelu_silu_textbook():
     sil = np.array([O.lib().oracle_silu(v) for v in xs])
     np.testing.assert_allclose(sil, (xl / (1 + np.exp(-xl))).astype(np.float64), rtol=1e-6, atol=1e-30)
     assert np.all(got[xs > 6] == xs[xs > 6])  # tanh saturates to 1 in float: gelu(x) = x
+
+
+def _gated_textbook(y, z, w, groups, eps, mistake=None):
+    """granite_model.cpp:21,278-287 from the formulas, in long double: g = y * z / (1 + e^-z), then for
+    each of `groups` slices of D / groups channels, g * w[slice] / sqrt(mean(g^2) + eps).
+    `mistake` builds a plausible wrong composition instead: "silu_y" (silu applied to y, not z),
+    "unsliced" (every group takes the first slice of w), "norm_before_gate" (norm y, then gate),
+    "gate_f16" (the gate rounded to fp16 before the norm)."""
+    yl, zl = _ld(y), _ld(z)
+    if mistake == "silu_y":
+        g = yl / (1 + np.exp(-yl)) * zl
+    elif mistake == "norm_before_gate":
+        g = yl
+    else:
+        g = yl * (zl / (1 + np.exp(-zl)))
+    if mistake == "gate_f16":
+        g = _ld(g.astype(np.float64).astype(np.float16))
+    D = g.shape[1]
+    GS = D // groups
+    out = np.empty_like(g)
+    for k in range(groups):
+        s = slice(k * GS, (k + 1) * GS)
+        wk = _ld(w[:GS] if mistake == "unsliced" else w[s])
+        gk = g[:, s]
+        out[:, s] = gk / np.sqrt((gk * gk).mean(1, keepdims=True) + _ld(np.float32(eps))) * wk
+    if mistake == "norm_before_gate":
+        out = out * (zl / (1 + np.exp(-zl)))
+    return out
+
+
+@pytest.mark.parametrize("groups", [1, 3, 4])
+def test_gated_rmsnorm_textbook(groups):
+    """Pins the gate composition of the Granite gated norm independently of any restatement of it:
+    which operand takes silu, the f32 gate kept unrounded before the norm, and each group normed
+    with its own slice of the weights. Every listed mistake falls outside the tolerance."""
+    rng = np.random.default_rng(20 + groups)
+    rows, D, eps = 12, 768, 1e-5
+    GS = D // groups
+    y = (rng.standard_normal((rows, D)) * 2).astype(np.float16).astype(np.float32)
+    zfull = (rng.standard_normal((rows, D + 64)) * 3 - 0.5).astype(np.float16).astype(np.float32)
+    z = zfull[:, 16:16 + D]  # a column slice of a wider row, as the gate columns of in_proj are
+    # Distinct weights per group, so a wrong slice changes every group after the first.
+    w = np.concatenate([(1 + 0.4 * k + 0.05 * rng.standard_normal(GS)) for k in range(groups)]).astype(np.float32)
+
+    # f32 activations: the reference's own type. Error budget: expf, the quotient, the product, the
+    # float scale and two float multiplies, each within an ulp or so.
+    got = y.copy()
+    zp = ctypes.c_void_p(zfull.ctypes.data + 16 * 4)
+    O.lib().oracle_gated_rmsnorm(P(got), zp, D + 64, P(w), rows, D, groups, eps)
+
+    def within(out):
+        ref = out.astype(np.float64)
+        return np.all(np.abs(got.astype(np.float64) - ref) <= 2e-6 * np.abs(ref) + 1e-7)
+
+    assert within(_gated_textbook(y, z, w, groups, eps))
+    wrong = ["silu_y", "norm_before_gate", "gate_f16"] + (["unsliced"] if groups > 1 else [])
+    for m in wrong:
+        assert not within(_gated_textbook(y, z, w, groups, eps, mistake=m)), m
+
+    # fp16 I/O: within 1 fp16 ulp of the long-double value rounded to fp16; the coarse mistakes are
+    # far outside 2 ulp.
+    y16 = y.astype(np.float16).view(np.uint16)
+    z16 = np.ascontiguousarray(z).astype(np.float16).view(np.uint16)
+    got16 = O.gated_rmsnorm_f16(y16, z16, w, groups, eps)
+
+    def ulps(out):
+        want = out.astype(np.float64).astype(np.float16).view(np.uint16)
+        return np.abs(f16_line(got16) - f16_line(want))
+
+    assert ulps(_gated_textbook(y, z, w, groups, eps)).max() <= 1
+    for m in ["silu_y", "norm_before_gate"] + (["unsliced"] if groups > 1 else []):
+        assert ulps(_gated_textbook(y, z, w, groups, eps, mistake=m)).max() > 2, m
 
 
 def test_rope_identities():
