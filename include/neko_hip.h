@@ -67,7 +67,8 @@ size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx);
 /* Routes subsequent work to a hipStream_t on the same device (e.g. a framework's current stream);
  * NULL selects the device's null stream, the default. The caller keeps ownership of the stream.
  * On a change the new stream is first made to wait (on the device) for the work already issued on
- * the previous one, so the context's ops stay ordered across the switch. */
+ * the previous one, so the context's ops stay ordered across the switch -- except when either stream
+ * is under graph capture, where the caller orders the graph's launches. */
 int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream);
 void* neko_hip_get_stream(const neko_hip_ctx* ctx);
 
@@ -83,20 +84,23 @@ int neko_hip_synchronize(neko_hip_ctx* ctx);
 /* ---------------------------------------------------------------- row norms */
 
 /* LayerNorm over rows of C: y = (x - mean) * rstd * gamma + beta, two-pass mean / variance in
- * double (cpu_ops.cpp:483-500; GPU form layernorm.comp flags = 0). x and y may alias. */
+ * double (cpu_ops.cpp:483-500; GPU form layernorm.comp flags = 0). x and y are either the same rows
+ * (same pointer and stride: in place) or disjoint; any other overlap is rejected (NEKO_ERR_INVALID). */
 int neko_hip_layernorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y, int64_t y_stride,
                        const float* gamma, const float* beta, int64_t rows, int64_t C, float eps, int dtype);
 
-/* RMSNorm over rows of C: y = x * float(1/sqrt(sum(x^2)/C + eps)) * w; x and y may alias
- * (cpu_ops.cpp:502-511, cpu_ops.h:27; GPU form layernorm.comp flags = 1). Also the Qwen3 q/k head
- * norm when called on heads as rows (qwen3_model.cpp:250-251). */
+/* RMSNorm over rows of C: y = x * float(1/sqrt(sum(x^2)/C + eps)) * w (cpu_ops.cpp:502-511; GPU form
+ * layernorm.comp flags = 1). x and y are the same rows (same pointer and stride: in place, which
+ * cpu_ops.h:27 allows) or disjoint; other overlaps are rejected. Also the Qwen3 q/k head norm when
+ * called on heads as rows (qwen3_model.cpp:250-251). */
 int neko_hip_rmsnorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y, int64_t y_stride, const float* w,
                      int64_t rows, int64_t C, float eps, int dtype);
 
 /* Granite-4.0-H Mamba2 output gate + group RMSNorm: g = y * silu(z), then RMSNorm of each group of
  * D/groups channels with its slice of w, written to out (granite_model.cpp:278-287, which gates and
- * norms y in place; out may alias y). z rows have stride z_stride (the gate columns of the in_proj
- * row, granite_model.h:86-88). D % groups == 0. */
+ * norms y in place). out is either y itself (same pointer and stride) or disjoint from it, and never
+ * overlaps z. z rows have stride z_stride (the gate columns of the in_proj row,
+ * granite_model.h:86-88). D % groups == 0. */
 int neko_hip_gated_rmsnorm(neko_hip_ctx* ctx, const void* y, int64_t y_stride, const void* z, int64_t z_stride,
                            void* out, int64_t out_stride, const float* w, int64_t rows, int64_t D, int groups,
                            float eps, int dtype);
@@ -139,19 +143,22 @@ int neko_hip_store_kv(neko_hip_ctx* ctx, const void* qkv, int64_t row_stride, in
  * written back to x), then xn[t] = RMSNorm(x[t]) with weights w -- the reference's matmul epilogue
  * with kAccumulate (cpu_ops.cpp:123, dst = dst + v) followed by the next op's cpu::rmsNorm
  * (qwen3_model.cpp:264, cpu_ops.cpp:502-511), with the add moved out of the GEMM so the residual row
- * is read once for both. xn may not alias x or delta. */
+ * is read once for both. xn may not overlap x or delta; delta is either x itself (same pointer and
+ * stride) or disjoint from it. */
 int neko_hip_add_rmsnorm(neko_hip_ctx* ctx, void* x, int64_t x_stride, const void* delta, int64_t delta_stride, void* xn,
                          int64_t xn_stride, const float* w, int64_t rows, int64_t C, float eps, int dtype);
 
 /* ---------------------------------------------------------------- activations */
 
 /* SwiGLU: out[t][i] = gate / (1 + exp(-gate)) * up with gate = h[t][i], up = h[t][I + i]
- * (cpu_ops.cpp:526-533, silu_mul.comp). h rows hold gate then up (stride h_stride >= 2*I). */
+ * (cpu_ops.cpp:526-533, silu_mul.comp). h rows hold gate then up (stride h_stride >= 2*I). out is
+ * disjoint from h, or overwrites its gate halves (out == h, out_stride == h_stride). */
 int neko_hip_swiglu(neko_hip_ctx* ctx, const void* h, int64_t h_stride, void* out, int64_t out_stride, int64_t rows,
                     int64_t I, int dtype);
 
 /* GELU, tanh form: y = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))) over n contiguous elements
- * (cpu_ops.cpp:20-23; the matmul epilogue of matmul.comp:16-19). x and y may alias. */
+ * (cpu_ops.cpp:20-23; the matmul epilogue of matmul.comp:16-19). x and y are the same array or
+ * disjoint. */
 int neko_hip_gelu_tanh(neko_hip_ctx* ctx, const void* x, void* y, int64_t n, int dtype);
 
 /* ---------------------------------------------------------------- embedding gather */
@@ -195,8 +202,9 @@ int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t col
  * by its f16 scale) in a different order from the reference's sequential loop: results agree to f32
  * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows.
  * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown) by the
- * first call that needs more, kept until neko_hip_destroy; make one uncaptured call at the largest
- * shape before capturing calls in a HIP graph. */
+ * first call that needs more; outgrown buffers are kept too (graphs captured earlier still point at
+ * them), all until neko_hip_destroy. A call that would grow it while the context's stream is under
+ * graph capture fails with NEKO_ERR_INVALID: make one uncaptured call at the largest shape first. */
 #define NEKO_MM_GELU 1
 #define NEKO_MM_ACCUMULATE 2
 int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,

@@ -13,8 +13,35 @@
 namespace neko_hip {
 namespace {
 
-// SwiGLU element: silu(gate) * up in float (silu_fast, device.h).
-__device__ __forceinline__ float swiglu_ref(float gate, float up) { return silu_fast(gate) * up; }
+// SwiGLU element: silu(gate) * up in float. SiLU form (knob): 0 libm expf and IEEE division,
+// 1 silu_fast, 2 silu_lite, 3 silu_newton (device.h).
+#ifndef NEKO_TUNE_SWIGLU_SILU
+#define NEKO_TUNE_SWIGLU_SILU 1
+#endif
+__device__ __forceinline__ float swiglu_ref(float gate, float up) {
+    if constexpr (NEKO_TUNE_SWIGLU_SILU == 0) return gate / (1.0f + expf(-gate)) * up;
+    else if constexpr (NEKO_TUNE_SWIGLU_SILU == 1) return silu_fast(gate) * up;
+    else if constexpr (NEKO_TUNE_SWIGLU_SILU == 2) return silu_lite(gate) * up;
+    else return silu_newton(gate) * up;
+}
+
+// SwiGLU loads non-temporal (1) or plain (0); stores non-temporal (1) or plain (0).
+#ifndef NEKO_TUNE_SWIGLU_NT_LOAD
+#define NEKO_TUNE_SWIGLU_NT_LOAD 1
+#endif
+#ifndef NEKO_TUNE_SWIGLU_NT_STORE
+#define NEKO_TUNE_SWIGLU_NT_STORE 0
+#endif
+template <typename V>
+__device__ __forceinline__ V swiglu_load(const V* p) {
+    if constexpr (NEKO_TUNE_SWIGLU_NT_LOAD) return load_nt(p);
+    else return *p;
+}
+template <typename V>
+__device__ __forceinline__ void swiglu_store(V* p, V v) {
+    if constexpr (NEKO_TUNE_SWIGLU_NT_STORE) store_nt(p, v);
+    else *p = v;
+}
 
 // GELU: gelu_ref (device.h).
 
@@ -58,8 +85,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
             src[k] = row * a.hs + col;
             dst[k] = row * a.os + col;
             const T* hp = static_cast<const T*>(a.h) + src[k];
-            g[k] = load_nt(reinterpret_cast<const VT*>(hp));
-            u[k] = load_nt(reinterpret_cast<const VT*>(hp + a.I));
+            g[k] = swiglu_load(reinterpret_cast<const VT*>(hp));
+            u[k] = swiglu_load(reinterpret_cast<const VT*>(hp + a.I));
         }
     }
 #pragma unroll
@@ -71,7 +98,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
             const float v = swiglu_ref(to_f32(lane_elem<VT, T, N>(g[k], e)), to_f32(lane_elem<VT, T, N>(u[k], e)));
             set_elem<VT, T, N>(o, e, from_f32<T>(v));
         }
-        *reinterpret_cast<VT*>(static_cast<T*>(a.out) + dst[k]) = o;
+        swiglu_store(reinterpret_cast<VT*>(static_cast<T*>(a.out) + dst[k]), o);
     }
 }
 
@@ -163,6 +190,13 @@ int neko_hip_swiglu(neko_hip_ctx* ctx, const void* h, int64_t h_stride, void* ou
     NEKO_REQUIRE(ctx, h && out, "%s: null pointer", what);
     NEKO_REQUIRE(ctx, h_stride >= 2 * I && out_stride >= I, "%s: strides (%lld, %lld) too small for I=%lld", what,
                  (long long)h_stride, (long long)out_stride, (long long)I);
+    // out over the gate halves of h (same pointer and stride: each chunk is rewritten by the thread
+    // that read it) or disjoint from h.
+    const size_t esz = dtype_size(dtype);
+    const size_t sh = rows_span(rows, 2 * I, h_stride, esz), so = rows_span(rows, I, out_stride, esz);
+    NEKO_REQUIRE(ctx, sh && so, "%s: rows span more than 2^62 bytes", what);
+    NEKO_REQUIRE(ctx, (out == h && out_stride == h_stride) || !overlaps(h, sh, out, so),
+                 "%s: out overlaps h without being its gate halves (same pointer and stride)", what);
     return dtype == NEKO_DT_F16 ? swiglu_typed<half_t>(ctx, h, h_stride, out, out_stride, rows, I)
                                 : swiglu_typed<float>(ctx, h, h_stride, out, out_stride, rows, I);
 }
@@ -174,6 +208,9 @@ int neko_hip_gelu_tanh(neko_hip_ctx* ctx, const void* x, void* y, int64_t n, int
     NEKO_REQUIRE(ctx, n >= 0, "%s: negative size", what);
     if (n == 0) return NEKO_OK;
     NEKO_REQUIRE(ctx, x && y, "%s: null pointer", what);
+    NEKO_REQUIRE(ctx, n <= (int64_t(1) << 60), "%s: too many elements", what);
+    const size_t bytes = static_cast<size_t>(n) * dtype_size(dtype);
+    NEKO_REQUIRE(ctx, x == y || !overlaps(x, bytes, y, bytes), "%s: x and y overlap without being the same array", what);
     return dtype == NEKO_DT_F16 ? gelu_typed<half_t>(ctx, x, y, n) : gelu_typed<float>(ctx, x, y, n);
 }
 

@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <string>
 #include <unordered_set>
+#include <vector>
 
 #include "../../include/neko_hip.h"
 #include "device.h"
@@ -22,6 +23,7 @@ struct neko_hip_ctx {
     std::unordered_set<void*> allocs;
     void* workspace = nullptr;  // device scratch for split reductions, grown on demand
     size_t workspace_bytes = 0;
+    std::vector<void*> retired;  // outgrown workspaces, kept until destroy (captured graphs may use them)
     hipEvent_t switch_event = nullptr;  // orders a newly routed stream after the previous one
 };
 
@@ -39,9 +41,12 @@ int after_launch(neko_hip_ctx* ctx, const char* what);
 
 FastDiv make_fast_div(uint32_t d);
 
-// The context's device workspace, at least `bytes` long (grown on demand: growing waits for the
-// context's stream, since queued work may still read the old one). Shared by every op on ctx.
+// The context's device workspace, at least `bytes` long, shared by every op on ctx. Grown on
+// demand; an outgrown buffer stays allocated until neko_hip_destroy, since queued work and captured
+// graphs may still use it. Growing while ctx's stream is under graph capture fails (NEKO_ERR_INVALID).
 int workspace(neko_hip_ctx* ctx, size_t bytes, void** out);
+// Whether `stream` is under graph capture.
+int capturing(neko_hip_ctx* ctx, hipStream_t stream, bool* yes);
 
 // Workgroups of `block` threads of `kernel` that fit on one CU at once (cached per kernel), and the
 // grid of a persistent kernel: that many per CU, or fewer when there is less work.
@@ -55,6 +60,27 @@ int launch_store_kv(neko_hip_ctx* ctx, const char* what, const void* qkv, int64_
                     uint16_t* v_cache, int64_t cache_rows, int dtype);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Byte ranges [a, a + an) and [b, b + bn) share a byte.
+inline bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return an && bn && pa < pb + bn && pb < pa + an;
+}
+// Bytes from the first element of `rows` rows of `width` elements, `stride` elements apart, to the
+// end of the last; 0 when that does not fit in 62 bits (callers reject it).
+inline size_t rows_span(int64_t rows, int64_t width, int64_t stride, size_t esz) {
+    if (rows <= 0 || width <= 0) return 0;
+    if (stride > 0 && rows - 1 > ((int64_t(1) << 62) - width) / stride) return 0;
+    return static_cast<size_t>((rows - 1) * stride + width) * esz;
+}
+// An op that reads rows at `in` and writes rows at `out` (same shape) is well defined when the two
+// are the same rows -- same address and stride, each row rewritten in place by the code that read
+// it -- or share no byte. Any other overlap would let one row's store land on a row another wave
+// is still reading.
+inline bool same_or_disjoint(const void* in, int64_t in_stride, const void* out, int64_t out_stride, size_t span_in,
+                             size_t span_out) {
+    return (in == out && in_stride == out_stride) || !overlaps(in, span_in, out, span_out);
+}
 inline size_t dtype_size(int dtype) { return dtype == NEKO_DT_F16 ? 2 : 4; }
 inline bool valid_dtype(int dtype) { return dtype == NEKO_DT_F16 || dtype == NEKO_DT_F32; }
 

@@ -131,7 +131,12 @@ extern "C" int neko_hip_store_kv(neko_hip_ctx* ctx, const void* qkv, int64_t row
     NEKO_REQUIRE(ctx, row_stride >= k_off + width && row_stride >= v_off + width,
                  "%s: k/v columns [%lld, +%lld) / [%lld, +%lld) exceed the row stride %lld", what, (long long)k_off,
                  (long long)width, (long long)v_off, (long long)width, (long long)row_stride);
-    NEKO_REQUIRE(ctx, cache_rows <= INT64_MAX / width, "%s: cache too large", what);
+    NEKO_REQUIRE(ctx, cache_rows <= (int64_t(1) << 60) / width, "%s: cache too large", what);
+    const size_t sq = rows_span(rows, (k_off > v_off ? k_off : v_off) + width, row_stride, dtype_size(dtype));
+    const size_t sc = static_cast<size_t>(cache_rows * width) * 2;
+    NEKO_REQUIRE(ctx, sq != 0, "%s: qkv rows span more than 2^62 bytes", what);
+    NEKO_REQUIRE(ctx, !overlaps(k_cache, sc, v_cache, sc) && !overlaps(qkv, sq, k_cache, sc) && !overlaps(qkv, sq, v_cache, sc),
+                 "%s: the caches may not overlap each other or qkv", what);
     return launch_store_kv(ctx, what, qkv, row_stride, k_off, v_off, rows, width, pos0, positions, k_cache, v_cache,
                            cache_rows, dtype);
 }

@@ -1689,11 +1689,6 @@ int launch_splitk_reduce(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const 
     return after_launch(ctx, what);
 }
 
-bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
-    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
-    return an && bn && pa < pb + bn && pb < pa + an;
-}
-
 }  // namespace
 }  // namespace neko_hip
 

@@ -32,6 +32,11 @@
 #ifndef NEKO_TUNE_NORM_FULLGRID
 #define NEKO_TUNE_NORM_FULLGRID 0
 #endif
+// 1: size a persistent grid so every wave gets the same number of rows (ceil(rows / resident
+// waves) each), instead of filling every resident slot and leaving a partial last round.
+#ifndef NEKO_TUNE_NORM_BALANCE
+#define NEKO_TUNE_NORM_BALANCE 0
+#endif
 // Where the one-wave-per-row kernel keeps the norm weights: 0 in every lane's registers, 1 in one
 // LDS copy per workgroup (frees CH * 8 VGPRs per lane for occupancy). Per norm kind.
 #ifndef NEKO_TUNE_NORM_WLDS_RMS
@@ -151,6 +156,16 @@ struct RowRegs {
     V z[CH];
 };
 
+// Row loads: non-temporal (1) or plain (0).
+#ifndef NEKO_TUNE_NORM_NT_LOAD
+#define NEKO_TUNE_NORM_NT_LOAD 1
+#endif
+template <typename V>
+__device__ __forceinline__ V load_row_chunk(const V* p) {
+    if constexpr (NEKO_TUNE_NORM_NT_LOAD) return load_nt(p);
+    else return *p;
+}
+
 template <Norm K, typename T, int CH, int NT>
 __device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K, T>& p, int tid, int nch) {
     typedef typename Chunk16<T>::V V;
@@ -161,8 +176,8 @@ __device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K,
         rr.x[k] = V{};
         rr.z[k] = V{};
         if (j < nch) {
-            rr.x[k] = load_nt(reinterpret_cast<const V*>(p.x + j * N));
-            if constexpr (has_z(K)) rr.z[k] = load_nt(reinterpret_cast<const V*>(p.z + j * N));
+            rr.x[k] = load_row_chunk(reinterpret_cast<const V*>(p.x + j * N));
+            if constexpr (has_z(K)) rr.z[k] = load_row_chunk(reinterpret_cast<const V*>(p.z + j * N));
         }
     }
 }
@@ -401,8 +416,8 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
                 store_out<K>(reinterpret_cast<V*>(pc.y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
                 if constexpr (K == Norm::AddRms) store_out<K>(reinterpret_cast<V*>(const_cast<T*>(pc.x) + j * N), cur.x[k]);
                 if (more) {
-                    cur.x[k] = load_nt(reinterpret_cast<const V*>(pn.x + j * N));
-                    if constexpr (has_z(K)) cur.z[k] = load_nt(reinterpret_cast<const V*>(pn.z + j * N));
+                    cur.x[k] = load_row_chunk(reinterpret_cast<const V*>(pn.x + j * N));
+                    if constexpr (has_z(K)) cur.z[k] = load_row_chunk(reinterpret_cast<const V*>(pn.z + j * N));
                 }
             }
         } else {
@@ -601,6 +616,10 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         // rows must see one group index, so the wave count is then a multiple of groups.
         const int64_t need = (a.rows + 3) / 4;
         blocks = NEKO_TUNE_NORM_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need, wl ? lds : 0);
+        if (NEKO_TUNE_NORM_BALANCE && blocks < need) {
+            const int64_t per = (a.rows + 4 * blocks - 1) / (4 * blocks);  // rows per wave
+            blocks = ((a.rows + per - 1) / per + 3) / 4;
+        }
         if (blocks < need) {
             const int64_t m = a.groups / gcd64(a.groups, 4);
             blocks = blocks / m * m;
@@ -618,7 +637,22 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
 
 int check_rows(neko_hip_ctx* ctx, const char* what, int64_t rows, int64_t C, int64_t stride, const char* name) {
     NEKO_REQUIRE(ctx, stride >= C, "%s: %s stride %lld < row width %lld", what, name, (long long)stride, (long long)C);
-    (void)rows;
+    NEKO_REQUIRE(ctx, rows_span(rows, C, stride, 4) != 0, "%s: %s rows span more than 2^62 bytes", what, name);
+    return NEKO_OK;
+}
+
+// Rows read at `in` and written at `out`: the same rows (in place) or disjoint (allow_same = false:
+// disjoint only). Persistent waves load a later row while storing the current one, so any partial
+// overlap would race.
+int check_alias(neko_hip_ctx* ctx, const char* what, const void* in, int64_t in_stride, const char* in_name, const void* out,
+                int64_t out_stride, const char* out_name, int64_t rows, int64_t C, int dtype, bool allow_same = true) {
+    const size_t esz = dtype_size(dtype);
+    const size_t si = rows_span(rows, C, in_stride, esz), so = rows_span(rows, C, out_stride, esz);
+    if (allow_same)
+        NEKO_REQUIRE(ctx, same_or_disjoint(in, in_stride, out, out_stride, si, so),
+                     "%s: %s and %s overlap without being the same rows (same pointer and stride)", what, in_name, out_name);
+    else
+        NEKO_REQUIRE(ctx, !overlaps(in, si, out, so), "%s: %s may not overlap %s", what, out_name, in_name);
     return NEKO_OK;
 }
 
@@ -640,6 +674,7 @@ int neko_hip_layernorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void*
     NEKO_REQUIRE(ctx, x && y && gamma && beta, "%s: null pointer", what);
     if (int rc = check_rows(ctx, what, rows, C, x_stride, "x")) return rc;
     if (int rc = check_rows(ctx, what, rows, C, y_stride, "y")) return rc;
+    if (int rc = check_alias(ctx, what, x, x_stride, "x", y, y_stride, "y", rows, C, dtype)) return rc;
     NormArgs a{x, x_stride, nullptr, 0, y, y_stride, gamma, beta, rows, static_cast<int>(C), 1, eps};
     return launch_norm(ctx, Norm::Layer, a, dtype, what);
 }
@@ -655,6 +690,7 @@ int neko_hip_rmsnorm(neko_hip_ctx* ctx, const void* x, int64_t x_stride, void* y
     NEKO_REQUIRE(ctx, x && y && w, "%s: null pointer", what);
     if (int rc = check_rows(ctx, what, rows, C, x_stride, "x")) return rc;
     if (int rc = check_rows(ctx, what, rows, C, y_stride, "y")) return rc;
+    if (int rc = check_alias(ctx, what, x, x_stride, "x", y, y_stride, "y", rows, C, dtype)) return rc;
     NormArgs a{x, x_stride, nullptr, 0, y, y_stride, w, nullptr, rows, static_cast<int>(C), 1, eps};
     return launch_norm(ctx, Norm::Rms, a, dtype, what);
 }
@@ -668,10 +704,12 @@ int neko_hip_add_rmsnorm(neko_hip_ctx* ctx, void* x, int64_t x_stride, const voi
                  (long long)C);
     if (rows == 0) return NEKO_OK;
     NEKO_REQUIRE(ctx, x && delta && xn && w, "%s: null pointer", what);
-    NEKO_REQUIRE(ctx, xn != x && xn != delta, "%s: xn may not alias x or delta", what);
     if (int rc = check_rows(ctx, what, rows, C, x_stride, "x")) return rc;
     if (int rc = check_rows(ctx, what, rows, C, delta_stride, "delta")) return rc;
     if (int rc = check_rows(ctx, what, rows, C, xn_stride, "xn")) return rc;
+    if (int rc = check_alias(ctx, what, x, x_stride, "x", xn, xn_stride, "xn", rows, C, dtype, false)) return rc;
+    if (int rc = check_alias(ctx, what, delta, delta_stride, "delta", xn, xn_stride, "xn", rows, C, dtype, false)) return rc;
+    if (int rc = check_alias(ctx, what, delta, delta_stride, "delta", x, x_stride, "x", rows, C, dtype)) return rc;
     NormArgs a{x, x_stride, delta, delta_stride, xn, xn_stride, w, nullptr, rows, static_cast<int>(C), 1, eps};
     return launch_norm(ctx, Norm::AddRms, a, dtype, what);
 }
@@ -688,6 +726,8 @@ int neko_hip_gated_rmsnorm(neko_hip_ctx* ctx, const void* y, int64_t y_stride, c
     if (int rc = check_rows(ctx, what, rows, D, y_stride, "y")) return rc;
     if (int rc = check_rows(ctx, what, rows, D, z_stride, "z")) return rc;
     if (int rc = check_rows(ctx, what, rows, D, out_stride, "out")) return rc;
+    if (int rc = check_alias(ctx, what, y, y_stride, "y", out, out_stride, "out", rows, D, dtype)) return rc;
+    if (int rc = check_alias(ctx, what, z, z_stride, "z", out, out_stride, "out", rows, D, dtype, false)) return rc;
     NEKO_REQUIRE(ctx, rows <= INT64_MAX / groups, "%s: too many rows", what);
     NormArgs a{y, y_stride, z, z_stride, out, out_stride, w, nullptr, rows * groups, static_cast<int>(D / groups), groups, eps};
     return launch_norm(ctx, Norm::Gated, a, dtype, what);

@@ -5,6 +5,9 @@
 namespace neko_hip {
 namespace {
 
+// 1 / hd when hd is a power of two (the scale then multiplies by it, exactly), else 0 (divide).
+double inv_pow2(int hd) { return hd > 0 && (hd & (hd - 1)) == 0 ? 1.0 / hd : 0.0; }
+
 // Shape and pointer checks shared by both entry points; *skip when there is nothing to do.
 int qk_check(neko_hip_ctx* ctx, const char* what, const QkArgs& a, int dtype, bool* skip) {
     *skip = false;
@@ -51,9 +54,14 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
     }
     if (!with_kv) a.k_cache = a.v_cache = nullptr;
     if (k) {
-        // Persistent waves: as many workgroups as stay resident together.
+        // Persistent waves: as many workgroups as stay resident together, trimmed so that every wave
+        // gets the same number of rows (ceil(rows / resident waves)) and no partial last round is left.
         const int64_t need = (a.rows + 3) / 4;
-        const int64_t blocks = NEKO_TUNE_QK_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        int64_t blocks = NEKO_TUNE_QK_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        if (blocks < need) {
+            const int64_t per = (a.rows + 4 * blocks - 1) / (4 * blocks);
+            blocks = ((a.rows + per - 1) / per + 3) / 4;
+        }
         hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a);
         *fused = with_kv;
         return after_launch(ctx, what);
@@ -83,7 +91,7 @@ extern "C" int neko_hip_qk_norm_rope(neko_hip_ctx* ctx, void* qkv, int64_t row_s
                                      int64_t n_pos, float eps, int dtype) {
     const char* what = "neko_hip_qk_norm_rope";
     NEKO_ENTER(ctx);
-    const QkArgs a{qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps, nullptr, nullptr};
+    const QkArgs a{qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps, nullptr, nullptr, inv_pow2(hd)};
     bool skip, fused;
     if (int rc = qk_check(ctx, what, a, dtype, &skip)) return rc;
     if (skip) return NEKO_OK;
@@ -96,7 +104,7 @@ extern "C" int neko_hip_qk_norm_rope_kv(neko_hip_ctx* ctx, void* qkv, int64_t ro
                                         int dtype) {
     const char* what = "neko_hip_qk_norm_rope_kv";
     NEKO_ENTER(ctx);
-    const QkArgs a{qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps, k_cache, v_cache};
+    const QkArgs a{qkv, row_stride, rows, n_q, n_kv, hd, pos0, positions, wqk, cs, n_pos, eps, k_cache, v_cache, inv_pow2(hd)};
     bool skip, fused;
     if (int rc = qk_check(ctx, what, a, dtype, &skip)) return rc;
     if (skip) return NEKO_OK;
@@ -106,7 +114,12 @@ extern "C" int neko_hip_qk_norm_rope_kv(neko_hip_ctx* ctx, void* qkv, int64_t ro
     const int64_t kvw = static_cast<int64_t>(n_kv) * hd;
     NEKO_REQUIRE(ctx, row_stride >= static_cast<int64_t>(n_q) * hd + 2 * kvw, "%s: row stride %lld holds no v heads", what,
                  (long long)row_stride);
-    NEKO_REQUIRE(ctx, cache_rows <= INT64_MAX / kvw, "%s: cache too large", what);
+    NEKO_REQUIRE(ctx, cache_rows <= (int64_t(1) << 60) / kvw, "%s: cache too large", what);
+    const size_t sq = rows_span(rows, static_cast<int64_t>(n_q) * hd + 2 * kvw, row_stride, dtype_size(dtype));
+    const size_t sc = static_cast<size_t>(cache_rows * kvw) * 2;
+    NEKO_REQUIRE(ctx, sq != 0, "%s: qkv rows span more than 2^62 bytes", what);
+    NEKO_REQUIRE(ctx, !overlaps(k_cache, sc, v_cache, sc) && !overlaps(qkv, sq, k_cache, sc) && !overlaps(qkv, sq, v_cache, sc),
+                 "%s: the caches may not overlap each other or qkv", what);
     if (int rc = qk_launch(ctx, what, a, dtype, true, &fused)) return rc;
     if (fused) return NEKO_OK;
     // No fused kernel for this shape: the same result from the two ops in order. Rows outside the

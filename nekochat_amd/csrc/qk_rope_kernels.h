@@ -28,9 +28,10 @@
 #ifndef NEKO_TUNE_QK_MAXV
 #define NEKO_TUNE_QK_MAXV 8
 #endif
-// Minimum waves per SIMD the rolling kernel is compiled for (caps its VGPRs at 512 / waves).
+// Waves per SIMD the rolling kernel is compiled for (caps its VGPRs at 512 / waves) when a token's
+// data registers leave room for it; tokens that hold more take 3.
 #ifndef NEKO_TUNE_QK_WAVES
-#define NEKO_TUNE_QK_WAVES 3
+#define NEKO_TUNE_QK_WAVES 4
 #endif
 
 namespace neko_hip {
@@ -50,6 +51,7 @@ struct QkArgs {
     float eps;
     uint16_t* k_cache;  // [>= n_pos][n_kv * hd] f16, or null (no KV store)
     uint16_t* v_cache;
+    double inv_hd;  // 1 / hd when hd is a power of two (exact), else 0
 };
 
 // V values of type T as f16 at p: bit copies for f16, one RNE rounding each for f32.
@@ -69,10 +71,11 @@ __device__ __forceinline__ void store_f16(uint16_t* p, const typename VecOf<T, V
 }
 
 // The head's norm scale float(1 / sqrt(ss / hd + eps)) (cpu_ops.cpp:508 with C = hd). ss / hd is
-// the exact product with 1/hd when hd is a power of two (every Qwen3 head size); the reciprocal
-// square root comes from rsqrt_to_float (device.h) or, with the knob off, the libm-style expression.
+// the exact product with 1/hd when hd is a power of two (every Qwen3 head size; the host passes it);
+// the reciprocal square root comes from rsqrt_to_float (device.h) or, with the knob off, the
+// libm-style expression.
 __device__ __forceinline__ float head_scale(const QkArgs& a, double ss) {
-    const double m = (a.hd & (a.hd - 1)) == 0 ? ss * (1.0 / a.hd) : ss / a.hd;
+    const double m = a.inv_hd != 0.0 ? ss * a.inv_hd : ss / a.hd;
     if constexpr (NEKO_TUNE_QK_RSQ) return rsqrt_to_float(m + static_cast<double>(a.eps));
     else return static_cast<float>(1.0 / sqrt(m + static_cast<double>(a.eps)));
 }
@@ -99,6 +102,16 @@ __device__ __forceinline__ VT qk_load(const VT* p) {
 __device__ __forceinline__ bool row_position(const QkArgs& a, int64_t t, int64_t& pos) {
     pos = a.positions ? static_cast<int64_t>(a.positions[t]) : a.pos0 + t;
     return pos >= 0 && pos < a.n_pos;
+}
+
+// The same for a row index every lane of the wave shares. The positions are read through the constant
+// address space (they do not change during the kernel), so a uniform index becomes a scalar load,
+// counted apart from the vector loads: waiting for a position then never waits for row data.
+typedef const int32_t __attribute__((address_space(4)))* ConstI32Ptr;
+__device__ __forceinline__ bool row_position_uniform(const QkArgs& a, int64_t t, int64_t& pos) {
+    const int64_t p = a.positions ? static_cast<int64_t>(((ConstI32Ptr)a.positions)[t]) : a.pos0 + t;
+    pos = p;
+    return p >= 0 && p < a.n_pos;
 }
 
 // One token's q/k heads held by one wave: U passes of 64/L heads, each lane V elements of the first
@@ -208,16 +221,28 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
 // that pass of the wave's next token. A whole token of loads is therefore always in flight behind
 // the token being computed, with one token's worth of data registers, and because every load is
 // issued after the stores it follows, waiting for it never waits on later stores. The norm weights
-// are staged in LDS once per workgroup and read per pass; the cos/sin row of the next token is
-// loaded one token ahead.
+// are staged in LDS once per workgroup. The cos/sin row of the wave's next token is loaded with one
+// coalesced load spread over the lanes (8 bytes each at hd 128) and staged in the wave's own LDS
+// double buffer, from which every pass reads its (c, s) pairs: holding the rows in registers instead
+// (each lane its hd/2-pair slice, twice) is what kept this kernel at 3 waves per SIMD.
+// Waves per SIMD: the knob's 4 where the token's data registers leave room -- at most 40 of them
+// (32 with the KV store, whose cache addressing needs more), found to compile without spills -- else 3.
+template <typename T, int V, int U, bool KV>
+constexpr int qk_waves() {
+    return 2 * U * V * static_cast<int>(sizeof(T)) <= (KV ? 128 : 160) ? NEKO_TUNE_QK_WAVES : 3;
+}
+
 template <typename T, int L, int V, int U, bool KV>
-__global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(QkArgs a) {
+__global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_kernel(QkArgs a) {
     constexpr int HPW = kWave / L;  // heads per wave pass
+    constexpr int HD = 2 * L * V;   // the head size (a power of two): offsets and 1/HD are constants
+    constexpr int PL = (L * V + 63) / 64;  // (cos, sin) pairs each lane stages per row
     typedef typename VecOf<T, V>::V VT;
     __shared__ float wsh[2 * 512];
+    __shared__ __align__(16) float csl[4][2][HD];
     const bool norm = a.wqk != nullptr;
     if (norm)
-        for (int i = threadIdx.x; i < 2 * a.hd; i += 256) wsh[i] = a.wqk[i];
+        for (int i = threadIdx.x; i < 2 * HD; i += 256) wsh[i] = a.wqk[i];
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
@@ -225,31 +250,30 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
     const int hl = lane % L;
     const int hs = lane / L;
-    const int half = a.hd / 2;
+    constexpr int half = HD / 2;
     const int i0 = hl * V;
     const int nqk = a.n_q + a.n_kv;
     const int nh = KV ? nqk + a.n_kv : nqk;  // with the KV store, the v heads ride along as extra passes
-    const int64_t kvw = static_cast<int64_t>(a.n_kv) * a.hd;
+    const int64_t kvw = static_cast<int64_t>(a.n_kv) * HD;
+    float* const cb = &csl[wave][0][0];
     auto next_valid = [&](int64_t t, int64_t& pos) -> int64_t {
         for (; t < a.rows; t += nw)
-            if (row_position(a, t, pos)) return t;
+            if (row_position_uniform(a, t, pos)) return t;
         return a.rows;
     };
-    auto load_cs = [&](int64_t pos, float (&c)[V], float (&s)[V]) {
-        const float* csr = a.cs + pos * a.hd + 2 * i0;
+    // Pairs lane, lane + 64, ... of the row at `pos`: loaded into r, then stored to buffer b.
+    auto cs_load = [&](int64_t pos, float2v (&r)[PL]) {
 #pragma unroll
-        for (int e = 0; e < V; e += 2) {
-            if constexpr (V == 1) {
-                const float2v v = *reinterpret_cast<const float2v*>(csr);
-                c[0] = v[0];
-                s[0] = v[1];
-            } else {
-                const float4v v = *reinterpret_cast<const float4v*>(csr + 2 * e);
-                c[e] = v[0];
-                s[e] = v[1];
-                c[e + 1] = v[2];
-                s[e + 1] = v[3];
-            }
+        for (int k = 0; k < PL; k++) {
+            const int p = lane + 64 * k;
+            if (p < L * V) r[k] = *reinterpret_cast<const float2v*>(a.cs + pos * HD + 2 * p);
+        }
+    };
+    auto cs_store = [&](int b, const float2v (&r)[PL]) {
+#pragma unroll
+        for (int k = 0; k < PL; k++) {
+            const int p = lane + 64 * k;
+            if (p < L * V) *reinterpret_cast<float2v*>(cb + b * HD + 2 * p) = r[k];
         }
     };
 
@@ -257,9 +281,9 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
     int64_t t = next_valid(static_cast<int64_t>(blockIdx.x) * 4 + wave, pos);
     if (t >= a.rows) return;
 
+    // The first token's data loads go out before its cos/sin row is loaded and staged: that staging
+    // waits for the row, and the vector memory counter completes in order.
     VT A[U], B[U];
-    float cc[V], sn[V];
-    load_cs(pos, cc, sn);
     {
         const T* row = static_cast<const T*>(a.qkv) + t * a.stride;
 #pragma unroll
@@ -268,17 +292,22 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
             A[u] = VT{};
             B[u] = VT{};
             if (head < nh) {
-                A[u] = qk_load(reinterpret_cast<const VT*>(row + head * a.hd + i0));
-                B[u] = qk_load(reinterpret_cast<const VT*>(row + head * a.hd + half + i0));
+                A[u] = qk_load(reinterpret_cast<const VT*>(row + head * HD + i0));
+                B[u] = qk_load(reinterpret_cast<const VT*>(row + head * HD + half + i0));
             }
         }
+        float2v r[PL];
+        cs_load(pos, r);
+        cs_store(0, r);
     }
+    int buf = 0;
     while (t < a.rows) {
         int64_t npos;
         const int64_t tn = next_valid(t + nw, npos);
         const bool more = tn < a.rows;
-        float ncc[V], nsn[V];
-        if (more) load_cs(npos, ncc, nsn);
+        float2v ncs[PL];
+        if (more) cs_load(npos, ncs);
+        const float* cr = cb + buf * HD + 2 * i0;  // this lane's V (cos, sin) pairs
         T* row = static_cast<T*>(a.qkv) + t * a.stride;
         const T* nrow = static_cast<const T*>(a.qkv) + (more ? tn : t) * a.stride;
 #pragma unroll
@@ -304,8 +333,9 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
                     ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
                 }
                 ss = group_sum_f64<L>(ss);
-                const float r = head_scale(a, ss);
-                const float* w = wsh + (head < a.n_q ? 0 : a.hd) + i0;
+                const float r = NEKO_TUNE_QK_RSQ ? rsqrt_to_float(ss * (1.0 / HD) + static_cast<double>(a.eps))
+                                                 : head_scale(a, ss);
+                const float* w = wsh + (head < a.n_q ? 0 : HD) + i0;
 #pragma unroll
                 for (int e = 0; e < V; e++) {
                     fa[e] = fa[e] * r * w[e];
@@ -315,8 +345,18 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
             VT oa, ob;
 #pragma unroll
             for (int e = 0; e < V; e++) {
-                const float x0 = fa[e] * cc[e] - fb[e] * sn[e];
-                const float x1 = fa[e] * sn[e] + fb[e] * cc[e];
+                float c, s;
+                if constexpr (V == 1) {
+                    const float2v v = *reinterpret_cast<const float2v*>(cr);
+                    c = v[0];
+                    s = v[1];
+                } else {
+                    const float4v v = *reinterpret_cast<const float4v*>(cr + 2 * (e & ~1));
+                    c = v[2 * (e & 1)];
+                    s = v[2 * (e & 1) + 1];
+                }
+                const float x0 = fa[e] * c - fb[e] * s;
+                const float x1 = fa[e] * s + fb[e] * c;
                 if constexpr (V == 1) {
                     oa = from_f32<T>(x0);
                     ob = from_f32<T>(x1);
@@ -326,7 +366,7 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
                 }
             }
             if (head < nh) {
-                T* hp = row + head * a.hd + i0;
+                T* hp = row + head * HD + i0;
                 if (!KV || head < nqk) {
                     qk_store(reinterpret_cast<VT*>(hp), oa);
                     qk_store(reinterpret_cast<VT*>(hp + half), ob);
@@ -335,25 +375,24 @@ __global__ __launch_bounds__(256, NEKO_TUNE_QK_WAVES) void qk_rope_roll_kernel(Q
                     if (head >= a.n_q) {  // rotated k heads and untouched v heads go to the caches
                         const bool is_v = head >= nqk;
                         uint16_t* cp = (is_v ? a.v_cache : a.k_cache) + pos * kvw +
-                                       static_cast<int64_t>(head - (is_v ? nqk : a.n_q)) * a.hd + i0;
+                                       static_cast<int64_t>(head - (is_v ? nqk : a.n_q)) * HD + i0;
                         store_f16<T, V>(cp, is_v ? A[u] : oa);
                         store_f16<T, V>(cp + half, is_v ? B[u] : ob);
                     }
                 }
                 if (more) {
-                    A[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * a.hd + i0));
-                    B[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * a.hd + half + i0));
+                    A[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * HD + i0));
+                    B[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * HD + half + i0));
                 }
             }
         }
+        // The next token's row goes to the other buffer; this wave's own LDS operations run in order,
+        // so the next iteration's reads see it.
         if (more) {
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                cc[e] = ncc[e];
-                sn[e] = nsn[e];
-            }
+            cs_store(buf ^ 1, ncs);
             pos = npos;
         }
+        buf ^= 1;
         t = tn;
     }
 }
@@ -472,11 +511,14 @@ QkKernel pick_lv(int L, int V, int nh) {
     if constexpr (KV) {
         return V == Chunk16<T>::N ? pick_l<T, Chunk16<T>::N, true>(L, nh) : nullptr;
     } else {
+        // Lane vectors are at most 16 bytes (the launcher's limit): 8 halves or 4 floats.
         switch (V) {
             case 1: return pick_l<T, 1, false>(L, nh);
             case 2: return pick_l<T, 2, false>(L, nh);
             case 4: return pick_l<T, 4, false>(L, nh);
-            case 8: return pick_l<T, 8, false>(L, nh);
+            case 8:
+                if constexpr (sizeof(T) == 2) return pick_l<T, 8, false>(L, nh);
+                return nullptr;
         }
         return nullptr;
     }

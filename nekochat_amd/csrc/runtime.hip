@@ -71,16 +71,35 @@ int64_t persistent_grid(neko_hip_ctx* ctx, const void* kernel, int block, int64_
     return work_blocks < cap ? work_blocks : cap;
 }
 
+int capturing(neko_hip_ctx* ctx, hipStream_t stream, bool* yes) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &st);
+    if (e == hipErrorStreamCaptureImplicit) {
+        // The null stream, queried while another stream captures in global mode: it may not be used
+        // either, which is what the callers need to know.
+        (void)hipGetLastError();
+        *yes = true;
+        return NEKO_OK;
+    }
+    if (int rc = check(ctx, e, "hipStreamIsCapturing")) return rc;
+    *yes = st != hipStreamCaptureStatusNone;
+    return NEKO_OK;
+}
+
 int workspace(neko_hip_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->workspace_bytes) {
-        if (ctx->workspace) {
-            if (int rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return rc;
-            (void)hipFree(ctx->workspace);
-            ctx->workspace = nullptr;
-            ctx->workspace_bytes = 0;
-        }
+        // Growing allocates, which a stream under graph capture cannot record.
+        bool cap = false;
+        if (int rc = capturing(ctx, ctx->stream, &cap)) return rc;
+        if (cap)
+            return fail(ctx, NEKO_ERR_INVALID,
+                        "split-K workspace must grow to %zu bytes (holds %zu) while the stream is being captured: make "
+                        "one uncaptured call at the largest shape first",
+                        bytes, ctx->workspace_bytes);
         void* p = nullptr;
         if (int rc = check(ctx, hipMalloc(&p, bytes), "hipMalloc (workspace)")) return rc;
+        // The old buffer is retired, not freed: queued work and graphs captured earlier still use it.
+        if (ctx->workspace) ctx->retired.push_back(ctx->workspace);
         ctx->workspace = p;
         ctx->workspace_bytes = bytes;
     }
@@ -127,6 +146,7 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (void* p : ctx->allocs) (void)hipFree(p);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     delete ctx;
     return rc;
@@ -148,6 +168,16 @@ int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream) {
     if (next == ctx->stream) return NEKO_OK;
     // The new stream waits for the work already issued on the old one (on the device, not the
     // host): the context's calls share its split-K workspace, which that work may still be using.
+    // Not when either stream is under graph capture: a capture cannot wait on work outside it, and
+    // when its graph runs is up to the caller, who orders its launches.
+    bool cap = false;
+    if (int rc = capturing(ctx, next, &cap)) return rc;
+    if (!cap)
+        if (int rc = capturing(ctx, ctx->stream, &cap)) return rc;
+    if (cap) {
+        ctx->stream = next;
+        return NEKO_OK;
+    }
     if (!ctx->switch_event)
         if (int rc = check(ctx, hipEventCreateWithFlags(&ctx->switch_event, hipEventDisableTiming), "hipEventCreateWithFlags"))
             return rc;

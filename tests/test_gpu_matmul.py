@@ -69,21 +69,80 @@ def test_matmul_integer_rows_bitexact(dev, fmt, T):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_matmul_split_k_integer_bitexact(dev, fmt):
+@pytest.mark.parametrize("K", [2048, 2080])
+def test_matmul_split_k_integer_bitexact(dev, fmt, K):
     """A long K over few output tiles (T = 130, N = 37: two tiles) runs as K slices whose partial
-    sums are reduced afterwards; with integer values every partial is exact, so the result is."""
-    _case(f"matmul split-K integer fmt={fmt}")
-    rng = np.random.default_rng(400 + fmt)
-    T, K, N = 130, 2048, 37
+    sums are reduced afterwards; with integer values every partial is exact, so the result is.
+    K = 2048 takes the 64-deep GEMM (K % 64 == 0), K = 2080 the 32-deep one (K % 64 == 32): two
+    tiles x 8 slices each, then the ordered reduction, with and without accumulation."""
+    rng = np.random.default_rng(400 + fmt + K)
+    T, N = 130, 37
     tab, w = M.integer_table(fmt, N, K, rng)
     x = rng.integers(-4, 5, (T, K)).astype(np.float32)
     bias = rng.integers(-50, 51, N).astype(np.float32)
     y0 = rng.standard_normal((T, N)).astype(np.float32)
-    out = torch.from_numpy(y0).to(dev)
-    ops.matmul(torch.from_numpy(x).to(dev).half(), torch.from_numpy(tab).to(dev), fmt, K,
-               bias=torch.from_numpy(bias).to(dev), out=out, flags=ops.MM_ACCUMULATE)
-    want = O.matmul(fmt, x, tab, K, bias, y0, ops.MM_ACCUMULATE)
-    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    for flags in (0, ops.MM_ACCUMULATE):
+        _case(f"matmul split-K integer fmt={fmt} K={K} flags={flags}")
+        out = torch.from_numpy(y0).to(dev)
+        ops.matmul(torch.from_numpy(x).to(dev).half(), torch.from_numpy(tab).to(dev), fmt, K,
+                   bias=torch.from_numpy(bias).to(dev), out=out, flags=flags)
+        want = O.matmul(fmt, x, tab, K, bias, y0, flags)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), flags
+
+
+def test_matmul_split_k_graph_replays(dev):
+    """A split-K matmul captured in a HIP graph (after one uncaptured call at its shape, so the
+    context's workspace is already large enough) replays bit-identically to an uncaptured call, on
+    fresh inputs each replay with eager work and synchronisations in between."""
+    _case("matmul split-K graph capture + 3 replays")
+    rng = np.random.default_rng(950)
+    fmt, T, K, N = ops.FMT_FP4, 16, 2560, 6144
+    tab, _ = M.integer_table(fmt, N, K, rng)
+    td = torch.from_numpy(tab).to(dev)
+    xd = torch.from_numpy(rng.integers(-4, 5, (T, K)).astype(np.float32)).to(dev).half()
+    out_g = torch.zeros((T, N), dtype=torch.float32, device=dev)
+    ops.matmul(xd, td, fmt, K, out=out_g)  # warm-up: sizes the workspace outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.matmul(xd, td, fmt, K, out=out_g)
+    for i in range(3):
+        xd.copy_(torch.from_numpy(rng.integers(-4, 5, (T, K)).astype(np.float32)).half())
+        g.replay()
+        torch.cuda.synchronize()
+        eager = ops.matmul(xd, td, fmt, K)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g.view(torch.int32), eager.view(torch.int32)), f"replay {i}"
+
+
+def test_matmul_workspace_growth_refused_under_capture(dev):
+    """A fresh context has no workspace: a split-K call captured into a graph would have to allocate
+    it, and fails with NEKO_ERR_INVALID instead (naming the way out) without breaking the capture."""
+    _case("matmul workspace growth under capture")
+    from nekochat_amd._lib import NEKO_ERR_INVALID, lib
+    ctx = ops.Context(dev.index)
+    rng = np.random.default_rng(951)
+    fmt, T, K, N = ops.FMT_FP4, 16, 2560, 6144
+    tab, _ = M.integer_table(fmt, N, K, rng)
+    td = torch.from_numpy(tab).to(dev)
+    xd = torch.from_numpy(rng.integers(-4, 5, (T, K)).astype(np.float32)).to(dev).half()
+    out = torch.zeros((T, N), dtype=torch.float32, device=dev)
+    side = torch.zeros(4, device=dev)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream().cuda_stream
+        assert lib.neko_hip_set_stream(ctx.handle, s) == 0
+        rc = lib.neko_hip_matmul(ctx.handle, xd.data_ptr(), K, T, K, td.data_ptr(), td.shape[1], fmt, N, None,
+                                 out.data_ptr(), N, 0, ops.DT_F16, ops.DT_F32)
+        side.add_(1.0)
+    msg = lib.neko_hip_last_error(ctx.handle).decode()
+    assert rc == NEKO_ERR_INVALID and "captured" in msg, (rc, msg)
+    g.replay()
+    torch.cuda.synchronize()
+    assert bool((side == 1.0).all()) and bool((out == 0).all())
+    assert lib.neko_hip_set_stream(ctx.handle, None) == 0
+    ctx.close()
 
 
 def test_matmul_split_k_across_stream_switch(dev):

@@ -420,6 +420,38 @@ def test_add_rmsnorm_rejects_aliasing(dev):
     x = _f16((4, 256), 68, dev)
     with pytest.raises(NekoError):
         ops.add_rms_norm(x, x.clone(), _w(256, 69, dev), 1e-6, out=x)
+    buf = _f16((5, 256), 75, dev)
+    with pytest.raises(NekoError):  # xn one row past x: the rows overlap
+        ops.add_rms_norm(buf[:4], x.clone(), _w(256, 69, dev), 1e-6, out=buf[1:])
+
+
+def test_partial_overlaps_rejected(dev):
+    """Outputs are the input rows themselves (same address and stride) or disjoint from them: the
+    persistent waves load later rows while storing earlier ones, so any other overlap would race.
+    Each rejected call leaves its buffers untouched; the exact in-place forms still run."""
+    _case("partial overlaps rejected")
+    buf = _f16((9, 512), 70, dev)
+    before = to_bits(buf).copy()
+    w = _w(256, 71, dev)
+    x = buf[:8, :256]
+    z = _f16((8, 256), 72, dev)
+    bad = [
+        lambda: ops.rms_norm(x, w, 1e-6, out=buf[1:9, :256]),  # one row down
+        lambda: ops.rms_norm(x, w, 1e-6, out=buf[:8, 8:264]),  # eight columns right
+        lambda: ops.layer_norm(x, w, w, 1e-5, out=buf[1:9, :256]),
+        lambda: ops.gated_rms_norm(x, z, w, 1, 1e-5, out=buf[1:9, :256]),
+        lambda: ops.gated_rms_norm(x, z, w, 1, 1e-5, out=z),  # out over the gate operand
+        lambda: ops.silu_mul(buf[:8], out=buf[:8, 256:]),  # out over the up halves
+        lambda: ops.gelu(buf.view(-1)[:4000], out=buf.view(-1)[8:4008]),
+    ]
+    for i, call in enumerate(bad):
+        with pytest.raises(NekoError):
+            call()
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(buf), before)
+    want = O.swiglu_f16(to_bits(buf[:8]))
+    ops.silu_mul(buf[:8], out=buf[:8, :256])  # over the gate halves: each chunk rewritten by its reader
+    assert_f16_close(to_bits(buf[:8, :256]), want, what="swiglu over its gate halves")
 
 
 # ------------------------------------------------------------------ SwiGLU / GELU
