@@ -54,7 +54,7 @@ def parse():
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
                         "qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul, "
-                        "qwen3_4b_prefill_matmul)")
+                        "qwen3_4b_prefill_matmul, stream_floor)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -522,7 +522,7 @@ def all_configs(args):
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
-              "qwen3_4b_decode16_matmul", "qwen3_4b_prefill_matmul")
+              "qwen3_4b_decode16_matmul", "qwen3_4b_prefill_matmul", "stream_floor")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -579,6 +579,10 @@ def all_configs(args):
         }, {"rmsnorm": wl.bytes_rmsnorm(c2.T, c2.C), "qk_norm_rope": wl.bytes_qk_rope(c2.T, c2.n_q, c2.n_kv, c2.hd),
             "swiglu": wl.bytes_swiglu(c2.T, c2.I)},
             "Qwen3-0.6B decode: 64 rows, RMSNorm 1024, q/k RoPE 16q+8kv x 128 at random positions, SwiGLU I=3072")
+
+    # The streaming floor: kernels that only move bytes, timed exactly as the ops are.
+    if want("stream_floor"):
+        out["stream_floor"] = stream_floor(args, flush, time_ops)
 
     # Qwen3-4B prefill (the headline layer)
     if want("qwen3_4b_prefill"):
@@ -738,6 +742,118 @@ def all_configs(args):
     return out
 
 
+def _fit(points):
+    """Least-squares time = fixed + bytes / rate over (bytes, us) points: (fixed us, rate GB/s)."""
+    n = len(points)
+    mx = sum(b for b, _ in points) / n
+    my = sum(t for _, t in points) / n
+    sxx = sum((b - mx) ** 2 for b, _ in points)
+    slope = sum((b - mx) * (t - my) for b, t in points) / sxx  # us per byte
+    return round(my - slope * mx, 3), round(1e-3 / slope, 1)
+
+
+def stream_floor(args, flush, time_ops):
+    """What moving the ops' bytes costs with nothing else to do, timed like the ops (same flush and
+    events): an empty kernel; 16-byte-per-lane copies with the byte patterns of the Qwen3-4B prefill
+    ops (RMSNorm: read 42 MB / write 42 MB; q/k RoPE: 84 / 84; SwiGLU: two 159 MB streams in, one
+    out), and the same bytes in SwiGLU's and the q/k RoPE's own row layouts; a read-only sweep; and
+    the RMSNorm at 4096-32768 rows of 2560 beside copies of the same bytes, with the straight-line
+    fits time = fixed + bytes / rate of both."""
+    import ctypes
+
+    import torch
+
+    from nekochat_amd import ops
+    from nekochat_amd import workloads as wl
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "nekochat_amd", "libneko_floor.so"))
+    for name, args_ in (("neko_floor_empty", [ctypes.c_int, ctypes.c_void_p]),
+                        ("neko_floor_copy", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+                        ("neko_floor_copy2", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                              ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+                        ("neko_floor_read", [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
+                        ("neko_floor_rows2", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                              ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+                        ("neko_floor_inplace", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p])):
+        getattr(lib, name).argtypes = args_
+        getattr(lib, name).restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream or None)
+
+    def checked(fn, *a):
+        def call():
+            rc = fn(*a, stream)
+            if rc != 0:
+                raise RuntimeError(f"{fn.__name__}: HIP error {rc}")
+        return call
+
+    cfg = wl.QWEN3_PREFILL
+    big = 2 * cfg.T * cfg.I * 2  # bytes of the SwiGLU input rows, the largest stream
+    # Random bits in every source (and in the in-place buffer): with constant or zero data the copies
+    # run measurably faster than they do on activations, so they would understate the floor.
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(12345)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (big // 4,), dtype=torch.int32, device=dev, generator=gen)
+    dst = torch.randint(-2 ** 31, 2 ** 31 - 1, (big // 4,), dtype=torch.int32, device=dev, generator=gen)
+    sink = torch.zeros(1024, dtype=torch.float32, device=dev)
+    a_ptr, d_ptr = src.data_ptr(), dst.data_ptr()
+    calls, nbytes = {}, {}
+    calls["empty_1wg"], nbytes["empty_1wg"] = checked(lib.neko_floor_empty, 1), 0
+    calls["empty_8192wg"], nbytes["empty_8192wg"] = checked(lib.neko_floor_empty, 8192), 0
+    half = cfg.T * cfg.C * 2
+    patterns = {"rmsnorm": half, "qk_norm_rope": 2 * cfg.T * (cfg.n_q + cfg.n_kv) * cfg.hd}
+    for label, each in patterns.items():  # read `each` bytes, write `each` bytes
+        for items in (1, 4):
+            for ntl, nts in ((1, 1), (1, 0), (0, 0)):
+                name = f"copy_{label}_i{items}_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
+                calls[name] = checked(lib.neko_floor_copy, a_ptr, d_ptr, each, items, ntl, nts)
+                nbytes[name] = 2 * each
+    gi = cfg.T * cfg.I * 2  # SwiGLU: gate and up streams of T x I halves in, T x I out
+    for ntl, nts in ((1, 1), (1, 0), (0, 0)):
+        name = f"copy2_swiglu_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
+        calls[name] = checked(lib.neko_floor_copy2, a_ptr, a_ptr + gi, d_ptr, gi, ntl, nts)
+        nbytes[name] = 3 * gi
+    # The same bytes in the ops' own layouts: SwiGLU's gate and up halves of one [T, 2I] row into a
+    # [T, I] row; the q/k RoPE's in-place rewrite of the first (n_q + n_kv) hd halves of each qkv row.
+    for ntl, nts in ((1, 0), (1, 1), (0, 0)):
+        name = f"rows2_swiglu_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
+        calls[name] = checked(lib.neko_floor_rows2, a_ptr, 2 * gi // cfg.T, d_ptr, gi // cfg.T, cfg.T, gi // cfg.T, ntl, nts)
+        nbytes[name] = 3 * gi
+    # The same SwiGLU-layout stream over constant input (every output line zero): how much cheaper
+    # uniform data is, the reason the sources above are random.
+    ones = torch.ones(big // 4, dtype=torch.float32, device=dev)
+    calls["rows2_swiglu_ntpl_constdata"] = checked(lib.neko_floor_rows2, ones.data_ptr(), 2 * gi // cfg.T, d_ptr,
+                                                   gi // cfg.T, cfg.T, gi // cfg.T, 1, 0)
+    nbytes["rows2_swiglu_ntpl_constdata"] = 3 * gi
+    qk_w = (cfg.n_q + cfg.n_kv) * cfg.hd * 2
+    for ntl, nts in ((0, 0), (1, 0), (1, 1), (0, 1)):
+        name = f"inplace_qk_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
+        calls[name] = checked(lib.neko_floor_inplace, d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, ntl, nts)
+        nbytes[name] = 2 * cfg.T * qk_w
+    calls["read_rmsnorm_in"], nbytes["read_rmsnorm_in"] = checked(lib.neko_floor_read, a_ptr, half, sink.data_ptr()), half
+    # RMSNorm [rows, 2560] at four row counts, and copies of the same bytes.
+    w = wl.weight_f32(cfg.C, 1.0, 0.05, 2, dev)
+    sweep = (4096, 8192, 16384, 32768)
+    for rows in sweep:
+        x = wl.normal_f16((rows, cfg.C), 0.0, 1.0, 1, dev)
+        y = torch.empty_like(x)
+        calls[f"rmsnorm_rows{rows}"] = ops.prepare(ops.rms_norm, x, w, cfg.eps, out=y)[0]
+        nbytes[f"rmsnorm_rows{rows}"] = wl.bytes_rmsnorm(rows, cfg.C)
+        calls[f"copy_rows{rows}"] = checked(lib.neko_floor_copy, a_ptr, d_ptr, rows * cfg.C * 2, 1, 1, 1)
+        nbytes[f"copy_rows{rows}"] = 2 * rows * cfg.C * 2
+    timer = HipTimer(torch.cuda.current_stream().cuda_stream)
+    per_op, _ = time_ops(calls, nbytes, list(calls), args.steps, args.warmup, flush, timer)
+    torch.cuda.synchronize()
+    fits = {kind: _fit([(nbytes[f"{kind}_rows{r}"], per_op[f"{kind}_rows{r}"]["us"]) for r in sweep])
+            for kind in ("rmsnorm", "copy")}
+    return {"workload": "streaming floor: empty kernels, 16-byte copies with the Qwen3-4B prefill ops' byte patterns, "
+                        "RMSNorm rows sweep at hidden 2560 beside copies of the same bytes",
+            "ops": per_op,
+            "fit_us_plus_bytes_per_rate": {k: {"fixed_us": v[0], "GBps": v[1]} for k, v in fits.items()}}
+
+
 def cpu_baseline(cfg, rows=None, reps=5):
     """The reference's CPU path for the layer's four ops (its compiled cpu::rmsNorm, the Qwen3 q/k loop
     of rmsNorm + rope, cpu::siluMul on f32 activations, as its CPU forward pass holds them) on one
@@ -801,13 +917,36 @@ def cpu_baseline(cfg, rows=None, reps=5):
     }
 
 
+# The dominant kernel's sources: its file, the device helpers it uses, and the build flags.
+TRAFFIC_SOURCES = ("nekochat_amd/csrc/act.hip", "nekochat_amd/csrc/device.h", "nekochat_amd/csrc/Makefile")
+
+
+def sources_sha256(paths=TRAFFIC_SOURCES) -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in paths:
+        h.update(rel.encode() + b"\0")
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def traffic_from_profiles():
-    """Per-launch HBM bytes of the dominant kernel measured by rocprofv3 --pmc (profiles/), if recorded."""
+    """(bytes, note): the dominant kernel's per-launch HBM bytes from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (profiles/), when those counters were taken on the kernel sources this build compiles (the
+    profile records their sha256); otherwise (None, why)."""
     path = os.path.join(ROOT, "profiles", "swiglu_qwen3_4b_prefill_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, "no counter profile recorded"
     with open(path) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        rec = json.load(f)
+    have = sources_sha256(rec.get("sources", TRAFFIC_SOURCES))
+    if rec.get("sources_sha256") != have:
+        return None, (f"counter profile taken on other {rec.get('kernel', 'kernel')} sources (sha256 "
+                      f"{str(rec.get('sources_sha256'))[:12]} vs {have[:12]} now): not quoted")
+    return rec["traffic_bytes_per_launch"], (f"rocprofv3 FETCH_SIZE + WRITE_SIZE of {rec['kernel']}, calibrated on "
+                                             f"a device copy; sources sha256 {have[:12]} = this build's")
 
 
 def main():
@@ -857,9 +996,10 @@ def main():
     if not args.only or args.only == DOMINANT:
         d = per_op[DOMINANT]
         achieved = d["bytes"] / (d["mean_us"] * 1e-6) / 1e9
+        traffic, note = traffic_from_profiles()
         line["roofline"] = {"bound": "hbm", "kernel": DOMINANT, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                            "traffic": traffic_from_profiles()}
+                            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                            "traffic_source": note}
     if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(line), flush=True)

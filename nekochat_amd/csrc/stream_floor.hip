@@ -1,0 +1,202 @@
+// Streaming-floor kernels for measurement (libneko_floor.so, loaded by bench.py only; not part of the
+// C ABI in include/neko_hip.h). They move bytes and do nothing else, so their times under the same
+// events and cache flush as the layer ops give the practical floor an op of the same byte pattern can
+// reach on this GPU: an empty kernel (launch and completion cost), a 16-byte-per-lane copy (read n,
+// write n), a two-input stream (read 2n, write n: SwiGLU's byte counts), the same with SwiGLU's row
+// layout (both inputs halves of one row), an in-place read-and-write-back of the first part of each
+// row (the q/k RoPE's layout), and a read-only sweep.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ u32x4 ld(const u32x4* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT>
+__device__ __forceinline__ void st(u32x4* p, u32x4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
+__global__ void empty_kernel() {}
+
+// Chunk i = (block * ITEMS + k) * 256 + thread: each load instruction of a wave covers 1 KB of
+// contiguous bytes; all ITEMS loads are issued before the first store.
+template <int ITEMS, bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * ITEMS + threadIdx.x;
+    u32x4 v[ITEMS];
+#pragma unroll
+    for (int k = 0; k < ITEMS; k++) {
+        const int64_t i = base + k * 256;
+        v[k] = i < n ? ld<NTL>(src + i) : u32x4{};
+    }
+#pragma unroll
+    for (int k = 0; k < ITEMS; k++) {
+        const int64_t i = base + k * 256;
+        if (i < n) st<NTS>(dst + i, v[k]);
+    }
+}
+
+// dst[i] = a[i] ^ b[i]: two read streams, one write stream.
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void copy2_kernel(const u32x4* __restrict__ a, const u32x4* __restrict__ b,
+                                                    u32x4* __restrict__ dst, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) st<NTS>(dst + i, ld<NTL>(a + i) ^ ld<NTL>(b + i));
+}
+
+// Reads every chunk; a lane stores only if its xor equals a value the data never produces in practice,
+// which keeps the loads without writing.
+template <int ITEMS>
+__global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ src, int64_t n, u32x4* sink) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * ITEMS + threadIdx.x;
+    u32x4 acc{};
+#pragma unroll
+    for (int k = 0; k < ITEMS; k++) {
+        const int64_t i = base + k * 256;
+        if (i < n) acc ^= ld<true>(src + i);
+    }
+    if (acc.x == 0x9E3779B9u && acc.y == 0x7F4A7C15u) sink[threadIdx.x] = acc;
+}
+
+// SwiGLU's layout without its arithmetic: rows of h hold two halves of `cpr` chunks; out[r][c] =
+// h[r][c] ^ h[r][cpr + c], the flattened (row, chunk) index split with a division by cpr.
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void rows2_kernel(const u32x4* __restrict__ h, int64_t hs, u32x4* __restrict__ out,
+                                                    int64_t os, uint32_t cpr, uint32_t items) {
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= items) return;
+    const uint32_t row = idx / cpr, col = idx - row * cpr;
+    const u32x4* hp = h + row * hs + col;
+    st<NTS>(out + row * os + col, ld<NTL>(hp) ^ ld<NTL>(hp + cpr));
+}
+
+// The q/k RoPE's layout without its arithmetic: the first `cpr` chunks of each row (stride `stride`
+// chunks) are read and written back in place, xored with `key` (0 at run time, unknown to the
+// compiler, so every store is kept).
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void inplace_kernel(u32x4* buf, int64_t stride, uint32_t cpr, uint32_t items, uint32_t key) {
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= items) return;
+    const uint32_t row = idx / cpr, col = idx - row * cpr;
+    u32x4* p = buf + row * stride + col;
+    st<NTS>(p, ld<NTL>(p) ^ key);
+}
+
+bool ok16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int ITEMS>
+hipError_t launch_copy(const u32x4* s, u32x4* d, int64_t n, int ntl, int nts, hipStream_t st) {
+    const int64_t blocks = (n + 256 * ITEMS - 1) / (256 * ITEMS);
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>(blocks)), b(256);
+    if (ntl && nts) hipLaunchKernelGGL((copy_kernel<ITEMS, true, true>), g, b, 0, st, s, d, n);
+    else if (ntl) hipLaunchKernelGGL((copy_kernel<ITEMS, true, false>), g, b, 0, st, s, d, n);
+    else if (nts) hipLaunchKernelGGL((copy_kernel<ITEMS, false, true>), g, b, 0, st, s, d, n);
+    else hipLaunchKernelGGL((copy_kernel<ITEMS, false, false>), g, b, 0, st, s, d, n);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+// Empty kernel over `blocks` workgroups of 256 threads.
+int neko_floor_empty(int blocks, void* stream) {
+    if (blocks < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(empty_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream));
+    return hipGetLastError();
+}
+
+// dst[0, bytes) = src[0, bytes); bytes % 16 == 0, 16-byte aligned, disjoint. items: 16-byte chunks
+// per lane (1, 2, 4 or 8); nt_load / nt_store: non-temporal loads / stores.
+int neko_floor_copy(const void* src, void* dst, size_t bytes, int items, int nt_load, int nt_store, void* stream) {
+    if (!ok16(src) || !ok16(dst) || bytes % 16) return hipErrorInvalidValue;
+    const auto* s = static_cast<const u32x4*>(src);
+    auto* d = static_cast<u32x4*>(dst);
+    const int64_t n = static_cast<int64_t>(bytes / 16);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (items) {
+        case 1: return launch_copy<1>(s, d, n, nt_load, nt_store, st);
+        case 2: return launch_copy<2>(s, d, n, nt_load, nt_store, st);
+        case 4: return launch_copy<4>(s, d, n, nt_load, nt_store, st);
+        case 8: return launch_copy<8>(s, d, n, nt_load, nt_store, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+// dst[0, out_bytes) = a ^ b over the same range: reads 2 * out_bytes, writes out_bytes.
+int neko_floor_copy2(const void* a, const void* b, void* dst, size_t out_bytes, int nt_load, int nt_store, void* stream) {
+    if (!ok16(a) || !ok16(b) || !ok16(dst) || out_bytes % 16) return hipErrorInvalidValue;
+    const int64_t n = static_cast<int64_t>(out_bytes / 16);
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>(blocks)), bl(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* pa = static_cast<const u32x4*>(a);
+    const auto* pb = static_cast<const u32x4*>(b);
+    auto* d = static_cast<u32x4*>(dst);
+    if (nt_load && nt_store) hipLaunchKernelGGL((copy2_kernel<true, true>), g, bl, 0, st, pa, pb, d, n);
+    else if (nt_load) hipLaunchKernelGGL((copy2_kernel<true, false>), g, bl, 0, st, pa, pb, d, n);
+    else if (nt_store) hipLaunchKernelGGL((copy2_kernel<false, true>), g, bl, 0, st, pa, pb, d, n);
+    else hipLaunchKernelGGL((copy2_kernel<false, false>), g, bl, 0, st, pa, pb, d, n);
+    return hipGetLastError();
+}
+
+// out[r][0, half) = h[r][0, half) ^ h[r][half, 2 half) for rows of h_stride / out_stride bytes;
+// half, the strides and the pointers multiples of 16 bytes; rows * half / 16 < 2^32.
+int neko_floor_rows2(const void* h, int64_t h_stride, void* out, int64_t out_stride, int64_t rows, int64_t half, int nt_load,
+                     int nt_store, void* stream) {
+    if (!ok16(h) || !ok16(out) || half % 16 || h_stride % 16 || out_stride % 16 || half <= 0 || rows <= 0)
+        return hipErrorInvalidValue;
+    const int64_t cpr = half / 16, items = rows * cpr;
+    if (items >= (int64_t(1) << 32) - 256) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>((items + 255) / 256)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* hp = static_cast<const u32x4*>(h);
+    auto* op = static_cast<u32x4*>(out);
+    const int64_t hs = h_stride / 16, os = out_stride / 16;
+    const uint32_t c = static_cast<uint32_t>(cpr), n = static_cast<uint32_t>(items);
+    if (nt_load && nt_store) hipLaunchKernelGGL((rows2_kernel<true, true>), g, b, 0, st, hp, hs, op, os, c, n);
+    else if (nt_load) hipLaunchKernelGGL((rows2_kernel<true, false>), g, b, 0, st, hp, hs, op, os, c, n);
+    else if (nt_store) hipLaunchKernelGGL((rows2_kernel<false, true>), g, b, 0, st, hp, hs, op, os, c, n);
+    else hipLaunchKernelGGL((rows2_kernel<false, false>), g, b, 0, st, hp, hs, op, os, c, n);
+    return hipGetLastError();
+}
+
+// buf[r][0, width) read and written back unchanged, in place, for rows of `stride` bytes; width,
+// stride and buf multiples of 16 bytes; rows * width / 16 < 2^32.
+int neko_floor_inplace(void* buf, int64_t stride, int64_t rows, int64_t width, int nt_load, int nt_store, void* stream) {
+    if (!ok16(buf) || width % 16 || stride % 16 || width <= 0 || rows <= 0 || stride < width) return hipErrorInvalidValue;
+    const int64_t cpr = width / 16, items = rows * cpr;
+    if (items >= (int64_t(1) << 32) - 256) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>((items + 255) / 256)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    auto* p = static_cast<u32x4*>(buf);
+    const int64_t s = stride / 16;
+    const uint32_t c = static_cast<uint32_t>(cpr), n = static_cast<uint32_t>(items);
+    if (nt_load && nt_store) hipLaunchKernelGGL((inplace_kernel<true, true>), g, b, 0, st, p, s, c, n, 0u);
+    else if (nt_load) hipLaunchKernelGGL((inplace_kernel<true, false>), g, b, 0, st, p, s, c, n, 0u);
+    else if (nt_store) hipLaunchKernelGGL((inplace_kernel<false, true>), g, b, 0, st, p, s, c, n, 0u);
+    else hipLaunchKernelGGL((inplace_kernel<false, false>), g, b, 0, st, p, s, c, n, 0u);
+    return hipGetLastError();
+}
+
+// Reads src[0, bytes) (non-temporal, 4 chunks per lane); sink: 4 KB of device memory (256 chunks).
+int neko_floor_read(const void* src, size_t bytes, void* sink, void* stream) {
+    if (!ok16(src) || !ok16(sink) || bytes % 16) return hipErrorInvalidValue;
+    const int64_t n = static_cast<int64_t>(bytes / 16);
+    const int64_t blocks = (n + 1023) / 1024;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((read_kernel<4>), dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4*>(src), n, static_cast<u32x4*>(sink));
+    return hipGetLastError();
+}
+
+}  // extern "C"
