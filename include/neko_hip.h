@@ -204,12 +204,26 @@ int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t col
  * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown) by the
  * first call that needs more; outgrown buffers are kept too (graphs captured earlier still point at
  * them), all until neko_hip_destroy. A call that would grow it while the context's stream is under
- * graph capture fails with NEKO_ERR_INVALID: make one uncaptured call at the largest shape first. */
+ * graph capture fails with NEKO_ERR_INVALID: make one uncaptured call at the largest shape first, or
+ * capture neko_hip_matmul_noalloc. */
 #define NEKO_MM_GELU 1
 #define NEKO_MM_ACCUMULATE 2
 int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
                     int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags,
                     int x_dtype, int y_dtype);
+
+/* neko_hip_matmul without any allocation: the same kernels, the same split of K and bit-identical
+ * results, but split-K partial sums go to a fixed 32 MiB array in device memory (one per GPU, held
+ * from the library's first use on that GPU until the process ends) instead of the context's
+ * workspace. No counterpart in the reference: this is for callers that cannot allocate -- code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc. A shape whose split needs more
+ * than 32 MiB of partial sums (none of the Qwen3-0.6B/4B layer projections at any token count; an
+ * FP8/FP4 vocabulary-sized product at 13-47 tokens does) returns NEKO_ERR_UNSUPPORTED before anything
+ * is launched. Every call on one GPU shares that array: calls that may overlap in time on one GPU
+ * (other streams, other contexts or threads) race and must be ordered by the caller. */
+int neko_hip_matmul_noalloc(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
+                            int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride,
+                            int flags, int x_dtype, int y_dtype);
 
 /* ---------------------------------------------------------------- host-side codecs */
 

@@ -25,6 +25,7 @@ struct neko_hip_ctx {
     size_t workspace_bytes = 0;
     std::vector<void*> retired;  // outgrown workspaces, kept until destroy (captured graphs may use them)
     hipEvent_t switch_event = nullptr;  // orders a newly routed stream after the previous one
+    void* scratch = nullptr;  // device address of the matmul's fixed split-K scratch on this device
 };
 
 namespace neko_hip {
@@ -45,6 +46,9 @@ FastDiv make_fast_div(uint32_t d);
 // demand; an outgrown buffer stays allocated until neko_hip_destroy, since queued work and captured
 // graphs may still use it. Growing while ctx's stream is under graph capture fails (NEKO_ERR_INVALID).
 int workspace(neko_hip_ctx* ctx, size_t bytes, void** out);
+// Looks up (once per device, with that device current) and records in ctx the device address of
+// the fixed split-K scratch array that neko_hip_matmul_noalloc uses (matmul.hip).
+int matmul_scratch_setup(neko_hip_ctx* ctx);
 // Whether `stream` is under graph capture.
 int capturing(neko_hip_ctx* ctx, hipStream_t stream, bool* yes);
 

@@ -19,6 +19,8 @@
 // differ from its CPU loop), so results agree to f32 rounding of the sum, not bit for bit.
 #include <algorithm>
 #include <atomic>
+#include <map>
+#include <mutex>
 
 #include "internal.h"
 
@@ -1689,15 +1691,40 @@ int launch_splitk_reduce(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const 
     return after_launch(ctx, what);
 }
 
-}  // namespace
-}  // namespace neko_hip
+// Split-K partial sums of neko_hip_matmul_noalloc: a fixed array in device memory, so that entry
+// point never allocates. Each device holds its own copy (the runtime places it when the code object
+// loads there) until the process ends. 32 MiB covers every split the planner below makes for the
+// Qwen3-0.6B/4B layer projections at any token count (at most 30 MiB); larger splits are rejected.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-using namespace neko_hip;
+// Device address of `scratch` per device ordinal, looked up once per device by matmul_scratch_setup.
+// On the host, `scratch` names a host-side stand-in, never the device array: only these addresses
+// reach kernels.
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_ptr;
 
-extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
-                               int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride,
-                               int flags, int x_dtype, int y_dtype) {
-    const char* what = "neko_hip_matmul";
+// Where split-K partials go: the context's growable workspace, or (fixed != nullptr) the scratch
+// array, which is never grown.
+int partial_buffer(neko_hip_ctx* ctx, void* fixed, size_t bytes, float** out, const char* what) {
+    if (fixed) {
+        if (bytes > kScratchBytes)
+            return fail(ctx, NEKO_ERR_UNSUPPORTED,
+                        "%s: this shape splits K into %zu bytes of partial sums; the allocation-free entry point "
+                        "holds at most %zu (call neko_hip_matmul instead)",
+                        what, bytes, kScratchBytes);
+        *out = static_cast<float*>(fixed);
+        return NEKO_OK;
+    }
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, bytes, &ws)) return rc;
+    *out = static_cast<float*>(ws);
+    return NEKO_OK;
+}
+
+int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w, int64_t row_bytes,
+                int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int x_dtype, int y_dtype,
+                void* fixed, const char* what) {
     NEKO_ENTER(ctx);
     NEKO_REQUIRE(ctx, valid_dtype(x_dtype) && valid_dtype(y_dtype), "%s: bad dtype x=%d y=%d", what, x_dtype, y_dtype);
     NEKO_REQUIRE(ctx, fmt == NEKO_FMT_F16 || fmt == NEKO_FMT_FP8 || fmt == NEKO_FMT_FP4, "%s: bad weight format %d", what,
@@ -1784,11 +1811,9 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         while (slices < 16 && tiles * slices * 2 <= 2 * ctx->cu_count && nk / (2 * slices) >= 8) slices *= 2;
         NEKO_REQUIRE(ctx, tiles * slices <= 0x7fffffff, "%s: too many output tiles", what);
         float* partial = nullptr;
-        if (slices > 1) {
-            void* ws = nullptr;
-            if (int rc = workspace(ctx, static_cast<size_t>(slices) * T * N * sizeof(float), &ws)) return rc;
-            partial = static_cast<float*>(ws);
-        }
+        if (slices > 1)
+            if (int rc = partial_buffer(ctx, fixed, static_cast<size_t>(slices) * T * N * sizeof(float), &partial, what))
+                return rc;
         const dim3 grid(static_cast<uint32_t>(tiles * slices));
         const int tm = static_cast<int>(tiles_m), tn = static_cast<int>(tiles_n);
         if (v2) {
@@ -1829,11 +1854,9 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         slices = (nblk + slice_blocks - 1) / slice_blocks;
         NEKO_REQUIRE(ctx, tiles <= 0x7fffffff && slices <= 65535, "%s: grid too large", what);
         float* partial = nullptr;
-        if (slices > 1) {
-            void* ws = nullptr;
-            if (int rc = workspace(ctx, static_cast<size_t>(slices) * T * N * sizeof(float), &ws)) return rc;
-            partial = static_cast<float*>(ws);
-        }
+        if (slices > 1)
+            if (int rc = partial_buffer(ctx, fixed, static_cast<size_t>(slices) * T * N * sizeof(float), &partial, what))
+                return rc;
         const size_t lds = static_cast<size_t>(16 * tt) * (32 * slice_blocks + 8) * 2 + stage;
         const dim3 grid(static_cast<uint32_t>(tiles), 1u, static_cast<uint32_t>(slices));
         int rc;
@@ -1878,4 +1901,39 @@ extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_strid
         else hipLaunchKernelGGL((mm_generic_kernel<float, float>), grid, dim3(64), 0, ctx->stream, a);
     }
     return after_launch(ctx, what);
+}
+
+}  // namespace
+
+int matmul_scratch_setup(neko_hip_ctx* ctx) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_ptr.find(ctx->device);
+    if (it == g_scratch_ptr.end()) {
+        void* ptr = nullptr;
+        if (int rc = check(ctx, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (matmul scratch)"))
+            return rc;
+        it = g_scratch_ptr.emplace(ctx->device, ptr).first;
+    }
+    ctx->scratch = it->second;
+    return NEKO_OK;
+}
+
+}  // namespace neko_hip
+
+using namespace neko_hip;
+
+extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
+                               int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride,
+                               int flags, int x_dtype, int y_dtype) {
+    return matmul_impl(ctx, x, x_stride, T, K, w, row_bytes, fmt, N, bias, y, y_stride, flags, x_dtype, y_dtype, nullptr,
+                       "neko_hip_matmul");
+}
+
+extern "C" int neko_hip_matmul_noalloc(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K,
+                                       const void* w, int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y,
+                                       int64_t y_stride, int flags, int x_dtype, int y_dtype) {
+    const char* what = "neko_hip_matmul_noalloc";
+    NEKO_REQUIRE(ctx, ctx && ctx->scratch, "%s: null context, or its device's scratch address was not set up", what);
+    return matmul_impl(ctx, x, x_stride, T, K, w, row_bytes, fmt, N, bias, y, y_stride, flags, x_dtype, y_dtype,
+                       ctx->scratch, what);
 }

@@ -94,7 +94,7 @@ int workspace(neko_hip_ctx* ctx, size_t bytes, void** out) {
         if (cap)
             return fail(ctx, NEKO_ERR_INVALID,
                         "split-K workspace must grow to %zu bytes (holds %zu) while the stream is being captured: make "
-                        "one uncaptured call at the largest shape first",
+                        "one uncaptured call at the largest shape first, or capture neko_hip_matmul_noalloc",
                         bytes, ctx->workspace_bytes);
         void* p = nullptr;
         if (int rc = check(ctx, hipMalloc(&p, bytes), "hipMalloc (workspace)")) return rc;
@@ -136,6 +136,11 @@ int neko_hip_create(int device, neko_hip_ctx** out) {
     ctx->max_alloc = prop.totalGlobalMem;
     ctx->name = prop.name;
     ctx->stream = nullptr;  // the device's null stream until the caller routes work elsewhere
+    if (matmul_scratch_setup(ctx) != NEKO_OK) {
+        const std::string msg = "neko_hip_create: " + ctx->err;
+        delete ctx;
+        return fail(nullptr, NEKO_ERR_HIP, "%s", msg.c_str());
+    }
     *out = ctx;
     return NEKO_OK;
 }
