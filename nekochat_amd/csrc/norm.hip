@@ -9,6 +9,9 @@
 // which holds two operands per row, reads its weights from one LDS copy per workgroup and runs
 // without the second row buffer, trading per-wave prefetch for three times the resident waves; the
 // residual add + RMSNorm streams x and delta, writes the sum back over x and the norm to xn.
+// With many rows per resident wave (3 or more), RMSNorm and LayerNorm instead cover every row with
+// its own wave over the whole grid, which the dispatcher keeps full (plain loads and stores, no
+// prefetch): a persistent grid's partial last rounds then cost more than its prefetch saves.
 // Rows wider than one wave's registers use four waves per row. Sums are accumulated in double, like
 // the reference, and reduced across the wave with DPP and v_readlane (LDS only joins the partial
 // sums of multi-wave rows). The norm scale is
@@ -36,6 +39,11 @@
 // waves) each), instead of filling every resident slot and leaving a partial last round.
 #ifndef NEKO_TUNE_NORM_BALANCE
 #define NEKO_TUNE_NORM_BALANCE 0
+#endif
+// RMSNorm / LayerNorm take the one-row-per-wave grid from this many rows per resident persistent
+// wave on.
+#ifndef NEKO_TUNE_NORM_ROW_RATIO
+#define NEKO_TUNE_NORM_ROW_RATIO 3
 #endif
 // Where the one-wave-per-row kernel keeps the norm weights: 0 in every lane's registers, 1 in one
 // LDS copy per workgroup (frees CH * 8 VGPRs per lane for occupancy). Per norm kind.
@@ -118,9 +126,11 @@ constexpr int prefetch_mode(Norm k) {
 #ifndef NEKO_TUNE_GATED_NT_STORE
 #define NEKO_TUNE_GATED_NT_STORE 0
 #endif
-template <Norm K, typename V>
+// PLAIN: the one-row-per-wave kernel, whose plain loads and stores measured faster than the
+// non-temporal ones there.
+template <Norm K, bool PLAIN = false, typename V>
 __device__ __forceinline__ void store_out(V* p, V v) {
-    if constexpr (K == Norm::Gated ? NEKO_TUNE_GATED_NT_STORE : NEKO_TUNE_NORM_NT_STORE) store_nt(p, v);
+    if constexpr (!PLAIN && (K == Norm::Gated ? NEKO_TUNE_GATED_NT_STORE : NEKO_TUNE_NORM_NT_STORE)) store_nt(p, v);
     else *p = v;
 }
 
@@ -160,13 +170,13 @@ struct RowRegs {
 #ifndef NEKO_TUNE_NORM_NT_LOAD
 #define NEKO_TUNE_NORM_NT_LOAD 1
 #endif
-template <typename V>
+template <bool PLAIN = false, typename V>
 __device__ __forceinline__ V load_row_chunk(const V* p) {
-    if constexpr (NEKO_TUNE_NORM_NT_LOAD) return load_nt(p);
+    if constexpr (!PLAIN && NEKO_TUNE_NORM_NT_LOAD) return load_nt(p);
     else return *p;
 }
 
-template <Norm K, typename T, int CH, int NT>
+template <Norm K, typename T, int CH, int NT, bool PLAIN = false>
 __device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K, T>& p, int tid, int nch) {
     typedef typename Chunk16<T>::V V;
     constexpr int N = Chunk16<T>::N;
@@ -176,8 +186,8 @@ __device__ __forceinline__ void load_row(RowRegs<K, T, CH>& rr, const RowPtrs<K,
         rr.x[k] = V{};
         rr.z[k] = V{};
         if (j < nch) {
-            rr.x[k] = load_row_chunk(reinterpret_cast<const V*>(p.x + j * N));
-            if constexpr (has_z(K)) rr.z[k] = load_row_chunk(reinterpret_cast<const V*>(p.z + j * N));
+            rr.x[k] = load_row_chunk<PLAIN>(reinterpret_cast<const V*>(p.x + j * N));
+            if constexpr (has_z(K)) rr.z[k] = load_row_chunk<PLAIN>(reinterpret_cast<const V*>(p.z + j * N));
         }
     }
 }
@@ -195,7 +205,7 @@ __device__ __forceinline__ void add_residual(RowRegs<K, T, CH>& rr) {
 }
 
 // AddRms: writes the updated residual chunks back over x.
-template <Norm K, typename T, int CH, int NT>
+template <Norm K, typename T, int CH, int NT, bool PLAIN = false>
 __device__ __forceinline__ void store_residual(const RowRegs<K, T, CH>& rr, const RowPtrs<K, T>& p, int tid, int nch) {
     if constexpr (K == Norm::AddRms) {
         typedef typename Chunk16<T>::V V;
@@ -203,7 +213,7 @@ __device__ __forceinline__ void store_residual(const RowRegs<K, T, CH>& rr, cons
 #pragma unroll
         for (int k = 0; k < CH; k++) {
             const int j = k * NT + tid;
-            if (j < nch) store_out<K>(reinterpret_cast<V*>(const_cast<T*>(p.x) + j * N), rr.x[k]);
+            if (j < nch) store_out<K, PLAIN>(reinterpret_cast<V*>(const_cast<T*>(p.x) + j * N), rr.x[k]);
         }
     }
 }
@@ -341,7 +351,7 @@ __device__ __forceinline__ typename Chunk16<T>::V out_chunk(const F& f, int k, f
     return out;
 }
 
-template <Norm K, typename T, int CH, int NT, typename F, typename W>
+template <Norm K, typename T, int CH, int NT, bool PLAIN = false, typename F, typename W>
 __device__ __forceinline__ void store_row(T* y, const F& f, float scale, float mean_f, const W& wt, int tid, int nch) {
     typedef typename Chunk16<T>::V V;
     constexpr int N = Chunk16<T>::N;
@@ -349,7 +359,7 @@ __device__ __forceinline__ void store_row(T* y, const F& f, float scale, float m
     for (int k = 0; k < CH; k++) {
         const int j = k * NT + tid;
         if (j >= nch) continue;
-        store_out<K>(reinterpret_cast<V*>(y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
+        store_out<K, PLAIN>(reinterpret_cast<V*>(y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
     }
 }
 
@@ -357,8 +367,9 @@ __device__ __forceinline__ void store_row(T* y, const F& f, float scale, float m
 // keeps the weights in registers (or its workgroup's LDS copy) across rows and loads the next row
 // while it normalises this one. Every row of a wave shares one group index (the host makes nw a
 // multiple of groups, or gives each wave at most one row). With WL the dynamic LDS holds the
-// groups * C weights (then C betas for LayerNorm).
-template <Norm K, typename T, int CH, bool WL, int PF = prefetch_mode(K)>
+// groups * C weights (then C betas for LayerNorm). ROW: the grid covers every row, one per wave,
+// with plain loads and stores and no prefetch registers (the form for many rows per resident wave).
+template <Norm K, typename T, int CH, bool WL, bool ROW = false, int PF = ROW ? 0 : prefetch_mode(K)>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     constexpr int N = Chunk16<T>::N;
     const int lane = threadIdx.x & 63;
@@ -387,10 +398,10 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     }
 
     RowRegs<K, T, CH> cur, nxt;
-    load_row<K, T, CH, kWave>(cur, p0, lane, nch);
+    load_row<K, T, CH, kWave, ROW>(cur, p0, lane, nch);
     for (; r < a.rows; r += nw) {
         const bool more = r + nw < a.rows;
-        if (PF == 1 && more) load_row<K, T, CH, kWave>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
+        if (PF == 1 && more) load_row<K, T, CH, kWave, ROW>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
         add_residual(cur);
         RowVals<K, T, CH> f;
         f.init(cur);
@@ -413,19 +424,20 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
             for (int k = 0; k < CH; k++) {
                 const int j = k * kWave + lane;
                 if (j >= nch) continue;
-                store_out<K>(reinterpret_cast<V*>(pc.y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
-                if constexpr (K == Norm::AddRms) store_out<K>(reinterpret_cast<V*>(const_cast<T*>(pc.x) + j * N), cur.x[k]);
+                store_out<K, ROW>(reinterpret_cast<V*>(pc.y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
+                if constexpr (K == Norm::AddRms)
+                    store_out<K, ROW>(reinterpret_cast<V*>(const_cast<T*>(pc.x) + j * N), cur.x[k]);
                 if (more) {
-                    cur.x[k] = load_row_chunk(reinterpret_cast<const V*>(pn.x + j * N));
-                    if constexpr (has_z(K)) cur.z[k] = load_row_chunk(reinterpret_cast<const V*>(pn.z + j * N));
+                    cur.x[k] = load_row_chunk<ROW>(reinterpret_cast<const V*>(pn.x + j * N));
+                    if constexpr (has_z(K)) cur.z[k] = load_row_chunk<ROW>(reinterpret_cast<const V*>(pn.z + j * N));
                 }
             }
         } else {
             const RowPtrs<K, T> pc = row_ptrs<K, T>(a, r);
-            store_row<K, T, CH, kWave>(pc.y, f, scale, mean_f, wt, lane, nch);
-            store_residual<K, T, CH, kWave>(cur, pc, lane, nch);
+            store_row<K, T, CH, kWave, ROW>(pc.y, f, scale, mean_f, wt, lane, nch);
+            store_residual<K, T, CH, kWave, ROW>(cur, pc, lane, nch);
             if (PF == 1 && more) cur = nxt;
-            else if (more) load_row<K, T, CH, kWave>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
+            else if (more) load_row<K, T, CH, kWave, ROW>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
         }
     }
 }
@@ -534,16 +546,16 @@ __global__ __launch_bounds__(256) void norm_rows_generic(NormArgs a) {
 // ------------------------------------------------------------------ dispatch
 typedef void (*NormKernel)(NormArgs);
 
-template <Norm K, typename T, bool WL>
+template <Norm K, typename T, bool WL, bool ROW>
 NormKernel pick_wave(int CH) {
     switch (CH) {
-        case 1: return norm_wave_kernel<K, T, 1, WL>;
-        case 2: return norm_wave_kernel<K, T, 2, WL>;
-        case 3: return norm_wave_kernel<K, T, 3, WL>;
-        case 4: return norm_wave_kernel<K, T, 4, WL>;
-        case 5: return norm_wave_kernel<K, T, 5, WL>;
-        case 6: return norm_wave_kernel<K, T, 6, WL>;
-        case 8: return norm_wave_kernel<K, T, 8, WL>;
+        case 1: return norm_wave_kernel<K, T, 1, WL, ROW>;
+        case 2: return norm_wave_kernel<K, T, 2, WL, ROW>;
+        case 3: return norm_wave_kernel<K, T, 3, WL, ROW>;
+        case 4: return norm_wave_kernel<K, T, 4, WL, ROW>;
+        case 5: return norm_wave_kernel<K, T, 5, WL, ROW>;
+        case 6: return norm_wave_kernel<K, T, 6, WL, ROW>;
+        case 8: return norm_wave_kernel<K, T, 8, WL, ROW>;
     }
     return nullptr;
 }
@@ -557,13 +569,19 @@ NormKernel pick_wide(int CH) {
     return nullptr;
 }
 
+// The one-row-per-wave form exists for the plain norms (RMSNorm, LayerNorm) with weights in
+// registers; the gated and residual norms measured no gain from it.
+constexpr bool has_row_form(Norm k) { return k == Norm::Rms || k == Norm::Layer; }
+
 template <Norm K>
-NormKernel pick(int dtype, int W, int CH, bool wl) {
+NormKernel pick(int dtype, int W, int CH, bool wl, bool row = false) {
     const bool h = dtype == NEKO_DT_F16;
     if (W == 0) return h ? norm_rows_generic<K, half_t> : norm_rows_generic<K, float>;
     if (W == 1) {
-        if (wl) return h ? pick_wave<K, half_t, true>(CH) : pick_wave<K, float, true>(CH);
-        return h ? pick_wave<K, half_t, false>(CH) : pick_wave<K, float, false>(CH);
+        if constexpr (has_row_form(K))
+            if (row && !wl) return h ? pick_wave<K, half_t, false, true>(CH) : pick_wave<K, float, false, true>(CH);
+        if (wl) return h ? pick_wave<K, half_t, true, false>(CH) : pick_wave<K, float, true, false>(CH);
+        return h ? pick_wave<K, half_t, false, false>(CH) : pick_wave<K, float, false, false>(CH);
     }
     return h ? pick_wide<K, half_t>(CH) : pick_wide<K, float>(CH);
 }
@@ -611,6 +629,28 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
     }
     if (!k) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: no kernel for C=%d", what, a.C);
     int64_t blocks;
+    if (W == 1 && has_row_form(kind) && !wl && !NEKO_TUNE_NORM_FULLGRID) {
+        // Many rows per resident wave: one row per wave over the whole grid, which the dispatcher keeps
+        // full, instead of persistent waves (measured at 2560 and 1536 halves: 16384 and 32768 rows
+        // 7-12% faster, 8192 rows of 2560 -- 2.7 per resident wave -- 5% slower).
+        const int64_t resident = static_cast<int64_t>(ctx->cu_count > 0 ? ctx->cu_count : 256) * 4 *
+                                 resident_blocks_per_cu(reinterpret_cast<const void*>(k), 256, 0);
+        if (a.rows >= NEKO_TUNE_NORM_ROW_RATIO * resident) {
+            NormKernel kr = nullptr;
+            switch (kind) {
+                case Norm::Rms: kr = pick<Norm::Rms>(dtype, W, CH, wl, true); break;
+                case Norm::Layer: kr = pick<Norm::Layer>(dtype, W, CH, wl, true); break;
+                default: break;
+            }
+            if (kr) {
+                const int64_t rblocks = (a.rows + 3) / 4;
+                if (rblocks > 0x7fffffff)
+                    return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: %lld rows exceed one launch", what, (long long)a.rows);
+                hipLaunchKernelGGL(kr, dim3(static_cast<uint32_t>(rblocks)), dim3(256), 0, ctx->stream, a);
+                return after_launch(ctx, what);
+            }
+        }
+    }
     if (W == 1) {
         // Persistent waves: as many workgroups as stay resident together. A wave that handles several
         // rows must see one group index, so the wave count is then a multiple of groups.

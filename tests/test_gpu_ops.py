@@ -34,7 +34,8 @@ def _w(n, stream, dev, mean=1.0, std=0.05):
 @pytest.mark.parametrize("T,C,eps", [
     (64, 1024, 1e-6),      # Qwen3-0.6B decode
     (8192, 2560, 1e-6),    # Qwen3-4B prefill
-    (16384, 1536, 1e-5),   # Granite pre-norm
+    (16384, 1536, 1e-5),   # Granite pre-norm: one row per wave over the whole grid
+    (32768, 2560, 1e-6),   # one row per wave (more than 3 rows per resident persistent wave)
     (3, 96, 1e-6),         # reference self-test width
     (5, 4104, 1e-6),       # four waves per row
     (7, 100, 1e-6),        # width not a multiple of 8: fallback kernel
@@ -92,9 +93,11 @@ def test_prepared_call_keeps_its_stream(dev):
     assert torch.equal(out, want)
 
 
-def test_rmsnorm_f32(dev):
-    _case("rmsnorm f32")
-    T, C = 17, 2560
+@pytest.mark.parametrize("T", [17, 40000])
+def test_rmsnorm_f32(dev, T):
+    """17 rows: the persistent kernel; 40000 rows of 1024 floats: the one-row-per-wave grid."""
+    _case(f"rmsnorm f32 T={T}")
+    C = 2560 if T == 17 else 1024
     x = _f16((T, C), 5, dev).float() * 20
     w = _w(C, 6, dev)
     y = ops.rms_norm(x, w, 1e-6)
@@ -105,7 +108,8 @@ def test_rmsnorm_f32(dev):
 
 # ------------------------------------------------------------------ LayerNorm
 
-@pytest.mark.parametrize("T,C,shift", [(128, 768, 0.0), (64, 1024, 100.0), (3, 96, 0.0), (9, 770, 3.0), (4, 2560, 0.0)])
+@pytest.mark.parametrize("T,C,shift", [(128, 768, 0.0), (64, 1024, 100.0), (3, 96, 0.0), (9, 770, 3.0), (4, 2560, 0.0),
+                                       (40000, 768, 1.0)])  # the last: one row per wave over the grid
 def test_layernorm_f16(dev, T, C, shift):
     _case(f"layernorm f16 T={T} C={C} shift={shift}")
     x = _f16((T, C), 7, dev, mean=shift)
