@@ -58,6 +58,28 @@ __device__ __forceinline__ void store_nt(V* p, V v) {
     __builtin_nontemporal_store(v, p);
 }
 
+// ---------------------------------------------------------------- range-checked buffer access
+// A raw buffer resource over [p, p + bytes) (stride 0; gfx9 descriptor word 3). Loads through it past
+// `bytes` return zeros and stores past it are dropped by the hardware, so a wave can move a row whose
+// tail covers only some lanes without a per-lane branch. That matters for the memory counter: the
+// compiler's s_waitcnt placement can only count loads that every path issues, so a load under a
+// branch in a loop makes the next wait drain every outstanding load and store (prefetch included).
+typedef __amdgpu_buffer_rsrc_t BufRes;
+__device__ __forceinline__ BufRes buf_res(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+// 16 bytes at byte offset `off`; NT sets the non-temporal cache policy (aux bit 1 on gfx94x/gfx950).
+template <bool NT, typename V>
+__device__ __forceinline__ V buf_load16(BufRes r, uint32_t off) {
+    static_assert(sizeof(V) == 16, "16-byte vector");
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT ? 2 : 0));
+}
+template <bool NT, typename V>
+__device__ __forceinline__ void buf_store16(BufRes r, uint32_t off, V v) {
+    static_assert(sizeof(V) == 16, "16-byte vector");
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4v, v), r, off, 0, NT ? 2 : 0);
+}
+
 // silu(g) = g / (1 + exp(-g)) in float, the reference's formula (cpu_ops.cpp:526-533,
 // granite_model.cpp:21), with a cheaper evaluation than libm expf + IEEE division (those cost ~33
 // VALU ops per element and left streaming kernels VALU-bound on MI355X; this form takes ~17):

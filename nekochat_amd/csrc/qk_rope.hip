@@ -1,5 +1,7 @@
 // Qwen3 attention prologue: argument checks, launch and the C entry points of the q/k RMSNorm +
 // NeoX RoPE kernels (qk_rope_kernels.h), with and without the fused KV-cache store.
+#include <algorithm>
+
 #include "qk_rope_kernels.h"
 
 namespace neko_hip {
@@ -56,15 +58,27 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
     if (k) {
         // Persistent waves: as many workgroups as stay resident together, trimmed so that every wave
         // gets the same number of rows (ceil(rows / resident waves)) and no partial last round is left.
+        // A wave takes at most kQkMaxTokensPerWave rows (the roll kernel holds one position per lane),
+        // so larger row counts go in several launches.
         const int64_t need = (a.rows + 3) / 4;
         int64_t blocks = NEKO_TUNE_QK_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        const int64_t chunk = std::min<int64_t>(a.rows, 4 * blocks * kQkMaxTokensPerWave);
         if (blocks < need) {
-            const int64_t per = (a.rows + 4 * blocks - 1) / (4 * blocks);
-            blocks = ((a.rows + per - 1) / per + 3) / 4;
+            const int64_t per = (chunk + 4 * blocks - 1) / (4 * blocks);
+            blocks = ((chunk + per - 1) / per + 3) / 4;
         }
-        hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, ctx->stream, a);
+        for (int64_t r0 = 0; r0 < a.rows; r0 += chunk) {
+            QkArgs s = a;
+            s.rows = std::min(chunk, a.rows - r0);
+            s.qkv = static_cast<char*>(a.qkv) + r0 * a.stride * static_cast<int64_t>(esz);
+            if (a.positions) s.positions = a.positions + r0;
+            else s.pos0 = a.pos0 + r0;
+            const int64_t b = std::min<int64_t>(blocks, (s.rows + 3) / 4);
+            hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(b)), dim3(256), 0, ctx->stream, s);
+            if (int rc = after_launch(ctx, what)) return rc;
+        }
         *fused = with_kv;
-        return after_launch(ctx, what);
+        return NEKO_OK;
     }
     NEKO_REQUIRE(ctx, a.rows <= 65535 * 64LL, "%s: %lld rows exceed the fallback grid", what, (long long)a.rows);
     QkKernel g = dtype == NEKO_DT_F16 ? qk_rope_generic<half_t> : qk_rope_generic<float>;

@@ -33,6 +33,11 @@
 #ifndef NEKO_TUNE_QK_WAVES
 #define NEKO_TUNE_QK_WAVES 4
 #endif
+// 1: a wave loads its first token's cos/sin row before that token's row data (waiting for the
+// position first); 0: after it (measured 0.8 us faster at the Qwen3-4B prefill shape).
+#ifndef NEKO_TUNE_QK_CS_FIRST
+#define NEKO_TUNE_QK_CS_FIRST 0
+#endif
 
 namespace neko_hip {
 
@@ -70,6 +75,41 @@ __device__ __forceinline__ void store_f16(uint16_t* p, const typename VecOf<T, V
     }
 }
 
+// A lane vector (V elements of T, 2..16 bytes) through a range-checked buffer resource.
+template <bool NT, typename VT>
+__device__ __forceinline__ VT buf_load16v(BufRes r, uint32_t off) {
+    constexpr int aux = NT ? 2 : 0;
+    if constexpr (sizeof(VT) == 16) return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, aux));
+    else if constexpr (sizeof(VT) == 8) return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, aux));
+    else if constexpr (sizeof(VT) == 4) return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, aux));
+    else return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, aux));
+}
+template <bool NT, typename VT>
+__device__ __forceinline__ void buf_store16v(BufRes r, uint32_t off, VT v) {
+    constexpr int aux = NT ? 2 : 0;
+    if constexpr (sizeof(VT) == 16) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4v, v), r, off, 0, aux);
+    else if constexpr (sizeof(VT) == 8) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uint2v, v), r, off, 0, aux);
+    else if constexpr (sizeof(VT) == 4) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, aux);
+    else __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), r, off, 0, aux);
+}
+
+// V values of type T as f16 through a buffer resource: bit copies for f16, one RNE rounding each
+// for f32.
+template <typename T, int V>
+__device__ __forceinline__ void store_f16_buf(BufRes r, uint32_t off, const typename VecOf<T, V>::V& v) {
+    typedef typename VecOf<half_t, V>::V VH;
+    if constexpr (sizeof(T) == 2) {
+        buf_store16v<false>(r, off, __builtin_bit_cast(VH, v));
+    } else {
+        VH h;
+        if constexpr (V == 1) h = static_cast<half_t>(v);
+        else
+#pragma unroll
+            for (int e = 0; e < V; e++) h[e] = static_cast<half_t>(v[e]);
+        buf_store16v<false>(r, off, h);
+    }
+}
+
 // The head's norm scale float(1 / sqrt(ss / hd + eps)) (cpu_ops.cpp:508 with C = hd). ss / hd is
 // the exact product with 1/hd when hd is a power of two (every Qwen3 head size; the host passes it);
 // the reciprocal square root comes from rsqrt_to_float (device.h) or, with the knob off, the
@@ -102,16 +142,6 @@ __device__ __forceinline__ VT qk_load(const VT* p) {
 __device__ __forceinline__ bool row_position(const QkArgs& a, int64_t t, int64_t& pos) {
     pos = a.positions ? static_cast<int64_t>(a.positions[t]) : a.pos0 + t;
     return pos >= 0 && pos < a.n_pos;
-}
-
-// The same for a row index every lane of the wave shares. The positions are read through the constant
-// address space (they do not change during the kernel), so a uniform index becomes a scalar load,
-// counted apart from the vector loads: waiting for a position then never waits for row data.
-typedef const int32_t __attribute__((address_space(4)))* ConstI32Ptr;
-__device__ __forceinline__ bool row_position_uniform(const QkArgs& a, int64_t t, int64_t& pos) {
-    const int64_t p = a.positions ? static_cast<int64_t>(((ConstI32Ptr)a.positions)[t]) : a.pos0 + t;
-    pos = p;
-    return p >= 0 && p < a.n_pos;
 }
 
 // One token's q/k heads held by one wave: U passes of 64/L heads, each lane V elements of the first
@@ -220,11 +250,19 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
 // registers; as each pass of token t is normalised, rotated and stored, the same registers receive
 // that pass of the wave's next token. A whole token of loads is therefore always in flight behind
 // the token being computed, with one token's worth of data registers, and because every load is
-// issued after the stores it follows, waiting for it never waits on later stores. The norm weights
-// are staged in LDS once per workgroup. The cos/sin row of the wave's next token is loaded with one
-// coalesced load spread over the lanes (8 bytes each at hd 128) and staged in the wave's own LDS
-// double buffer, from which every pass reads its (c, s) pairs: holding the rows in registers instead
-// (each lane its hd/2-pair slice, twice) is what kept this kernel at 3 waves per SIMD.
+// issued after the stores it follows, waiting for it never waits on later stores.
+// Wave w takes tokens w, w + nw, ... (nw waves in the grid; at most 64 each, which the host
+// guarantees). Everything a token needs besides its row is fetched ahead of it: the positions of all
+// of the wave's tokens in one vector load at the start (lane k holds token k's), and the cos/sin row
+// of the next token, loaded with one coalesced load spread over the lanes (8 bytes each at hd 128)
+// and staged in the wave's own LDS double buffer, from which every pass reads its (c, s) pairs. The
+// norm weights are staged once per wave in its own LDS copy, so no wave waits on a barrier before its
+// first row loads go out. Row data moves through range-checked buffer resources (device.h): lanes past
+// the last head load zeros and their stores are dropped, so no load or store is under a per-lane
+// branch, and the first and the last token of a wave are peeled, so the loop issues every load
+// unconditionally -- together these keep the compiler's memory-counter waits at "this pass's data"
+// rather than "everything outstanding". A token whose position lies outside the table is written
+// back unchanged (and not stored to the caches).
 // Waves per SIMD: the knob's 4 where the token's data registers leave room -- at most 40 of them
 // (32 with the KV store, whose cache addressing needs more), found to compile without spills -- else 3.
 template <typename T, int V, int U, bool KV>
@@ -232,22 +270,25 @@ constexpr int qk_waves() {
     return 2 * U * V * static_cast<int>(sizeof(T)) <= (KV ? 128 : 160) ? NEKO_TUNE_QK_WAVES : 3;
 }
 
+// Tokens one wave of qk_rope_roll_kernel may take (one position per lane).
+constexpr int kQkMaxTokensPerWave = 64;
+
 template <typename T, int L, int V, int U, bool KV>
 __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_kernel(QkArgs a) {
     constexpr int HPW = kWave / L;  // heads per wave pass
     constexpr int HD = 2 * L * V;   // the head size (a power of two): offsets and 1/HD are constants
     constexpr int PL = (L * V + 63) / 64;  // (cos, sin) pairs each lane stages per row
+    constexpr int WQ = 2 * HD > 256 ? 2 * HD : 256;  // floats of a wave's weight copy (64 lanes x 4 at least)
     typedef typename VecOf<T, V>::V VT;
-    __shared__ float wsh[2 * 512];
+    __shared__ __align__(16) float wsh[4][WQ];
     __shared__ __align__(16) float csl[4][2][HD];
-    const bool norm = a.wqk != nullptr;
-    if (norm)
-        for (int i = threadIdx.x; i < 2 * HD; i += 256) wsh[i] = a.wqk[i];
-    __syncthreads();
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, kept in SGPRs
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    if (t0 >= a.rows) return;  // wave-uniform
+    const int ntok = static_cast<int>((a.rows - 1 - t0) / nw) + 1;
     const int hl = lane % L;
     const int hs = lane / L;
     constexpr int half = HD / 2;
@@ -255,21 +296,48 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     const int nqk = a.n_q + a.n_kv;
     const int nh = KV ? nqk + a.n_kv : nqk;  // with the KV store, the v heads ride along as extra passes
     const int64_t kvw = static_cast<int64_t>(a.n_kv) * HD;
+    // Byte extents: the heads a wave loads (v included with the KV store) and the ones it writes back.
+    const uint32_t load_bytes = static_cast<uint32_t>(nh) * HD * sizeof(T);
+    const uint32_t store_bytes = static_cast<uint32_t>(nqk) * HD * sizeof(T);
+    const uint32_t cache_bytes = static_cast<uint32_t>(kvw) * 2u;
+    const bool norm = a.wqk != nullptr;
     float* const cb = &csl[wave][0][0];
-    auto next_valid = [&](int64_t t, int64_t& pos) -> int64_t {
-        for (; t < a.rows; t += nw)
-            if (row_position_uniform(a, t, pos)) return t;
-        return a.rows;
+    const float* const wl = &wsh[wave][0];
+    auto row_of = [&](int64_t t) __attribute__((always_inline)) -> const T* {
+        return static_cast<const T*>(a.qkv) + t * a.stride;
     };
-    // Pairs lane, lane + 64, ... of the row at `pos`: loaded into r, then stored to buffer b.
-    auto cs_load = [&](int64_t pos, float2v (&r)[PL]) {
+    // Byte offsets of this lane's vector of pass u in a row (first half; the partner is half later).
+    auto off = [&](int u) __attribute__((always_inline)) -> uint32_t {
+        return static_cast<uint32_t>((u * HPW + hs) * HD + i0) * sizeof(T);
+    };
+
+    // Issued first: the wave's positions (lane k: token k's), its weight copy, then the first token's
+    // row -- none of them waits for another.
+    int32_t posv = 0;
+    if (a.positions) posv = a.positions[t0 + static_cast<int64_t>(lane < ntok ? lane : ntok - 1) * nw];
+    float4v wv{};
+    if (norm) wv = buf_load16<false, float4v>(buf_res(a.wqk, 2 * HD * 4u), lane * 16u);
+    VT A[U], B[U];
+    auto load_pass = [&](const BufRes& r, int u) __attribute__((always_inline)) {
+        A[u] = buf_load16v<NEKO_TUNE_QK_NT_LOAD, VT>(r, off(u));
+        B[u] = buf_load16v<NEKO_TUNE_QK_NT_LOAD, VT>(r, off(u) + half * sizeof(T));
+    };
+    // Token k's position (wave-uniform) and whether it indexes the table.
+    auto pos_of = [&](int k) __attribute__((always_inline)) -> int64_t {
+        return a.positions ? static_cast<int64_t>(__builtin_amdgcn_readlane(posv, k)) : a.pos0 + t0 + k * nw;
+    };
+    auto in_table = [&](int64_t p) __attribute__((always_inline)) -> bool { return p >= 0 && p < a.n_pos; };
+    // Pairs lane, lane + 64, ... of the row at `pos` (row 0 for a position outside the table): loaded
+    // into r, then stored to buffer b.
+    auto cs_load = [&](int64_t pos, float2v (&r)[PL]) __attribute__((always_inline)) {
+        const float* row = a.cs + (in_table(pos) ? pos : 0) * HD;
 #pragma unroll
         for (int k = 0; k < PL; k++) {
             const int p = lane + 64 * k;
-            if (p < L * V) r[k] = *reinterpret_cast<const float2v*>(a.cs + pos * HD + 2 * p);
+            if (p < L * V) r[k] = *reinterpret_cast<const float2v*>(row + 2 * p);
         }
     };
-    auto cs_store = [&](int b, const float2v (&r)[PL]) {
+    auto cs_store = [&](int b, const float2v (&r)[PL]) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < PL; k++) {
             const int p = lane + 64 * k;
@@ -277,124 +345,129 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
         }
     };
 
-    int64_t pos;
-    int64_t t = next_valid(static_cast<int64_t>(blockIdx.x) * 4 + wave, pos);
-    if (t >= a.rows) return;
-
-    // The first token's data loads go out before its cos/sin row is loaded and staged: that staging
-    // waits for the row, and the vector memory counter completes in order.
-    VT A[U], B[U];
-    {
-        const T* row = static_cast<const T*>(a.qkv) + t * a.stride;
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int head = u * HPW + hs;
-            A[u] = VT{};
-            B[u] = VT{};
-            if (head < nh) {
-                A[u] = qk_load(reinterpret_cast<const VT*>(row + head * HD + i0));
-                B[u] = qk_load(reinterpret_cast<const VT*>(row + head * HD + half + i0));
-            }
-        }
-        float2v r[PL];
-        cs_load(pos, r);
-        cs_store(0, r);
-    }
-    int buf = 0;
-    while (t < a.rows) {
-        int64_t npos;
-        const int64_t tn = next_valid(t + nw, npos);
-        const bool more = tn < a.rows;
-        float2v ncs[PL];
-        if (more) cs_load(npos, ncs);
+    // Normalises, rotates and stores every pass of token k (cos/sin from LDS buffer `buf`); with
+    // `more`, refills each pass's registers with token k + 1's right after its stores.
+    auto step = [&](int k, int buf, bool more) __attribute__((always_inline)) {
+        const int64_t t = t0 + k * nw;
+        const int64_t pos = pos_of(k);
+        const bool valid = in_table(pos);
         const float* cr = cb + buf * HD + 2 * i0;  // this lane's V (cos, sin) pairs
-        T* row = static_cast<T*>(a.qkv) + t * a.stride;
-        const T* nrow = static_cast<const T*>(a.qkv) + (more ? tn : t) * a.stride;
+        const BufRes st = buf_res(row_of(t), store_bytes);
+        const BufRes ld = buf_res(row_of(more ? t + nw : t), load_bytes);
+        // The cache rows of this token's position (only written with the KV store, and only for a
+        // position inside the table: otherwise the resources are empty and every store drops).
+        const int64_t cpos = valid ? pos : 0;
+        const uint32_t cbytes = valid ? cache_bytes : 0u;
+        const BufRes kc = buf_res(KV ? static_cast<const void*>(a.k_cache + cpos * kvw) : a.qkv, cbytes);
+        const BufRes vc = buf_res(KV ? static_cast<const void*>(a.v_cache + cpos * kvw) : a.qkv, cbytes);
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int head = u * HPW + hs;
-            float fa[V], fb[V];
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                if constexpr (V == 1) {
-                    fa[e] = to_f32(A[u]);
-                    fb[e] = to_f32(B[u]);
-                } else {
-                    fa[e] = to_f32(A[u][e]);
-                    fb[e] = to_f32(B[u][e]);
-                }
-            }
-            if (norm) {
-                // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
-                double ss = 0.0;
+            VT oa = A[u], ob = B[u];
+            if (valid) {
+                float fa[V], fb[V];
 #pragma unroll
                 for (int e = 0; e < V; e++) {
-                    ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
-                    ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
-                }
-                ss = group_sum_f64<L>(ss);
-                const float r = NEKO_TUNE_QK_RSQ ? rsqrt_to_float(ss * (1.0 / HD) + static_cast<double>(a.eps))
-                                                 : head_scale(a, ss);
-                const float* w = wsh + (head < a.n_q ? 0 : HD) + i0;
-#pragma unroll
-                for (int e = 0; e < V; e++) {
-                    fa[e] = fa[e] * r * w[e];
-                    fb[e] = fb[e] * r * w[half + e];
-                }
-            }
-            VT oa, ob;
-#pragma unroll
-            for (int e = 0; e < V; e++) {
-                float c, s;
-                if constexpr (V == 1) {
-                    const float2v v = *reinterpret_cast<const float2v*>(cr);
-                    c = v[0];
-                    s = v[1];
-                } else {
-                    const float4v v = *reinterpret_cast<const float4v*>(cr + 2 * (e & ~1));
-                    c = v[2 * (e & 1)];
-                    s = v[2 * (e & 1) + 1];
-                }
-                const float x0 = fa[e] * c - fb[e] * s;
-                const float x1 = fa[e] * s + fb[e] * c;
-                if constexpr (V == 1) {
-                    oa = from_f32<T>(x0);
-                    ob = from_f32<T>(x1);
-                } else {
-                    oa[e] = from_f32<T>(x0);
-                    ob[e] = from_f32<T>(x1);
-                }
-            }
-            if (head < nh) {
-                T* hp = row + head * HD + i0;
-                if (!KV || head < nqk) {
-                    qk_store(reinterpret_cast<VT*>(hp), oa);
-                    qk_store(reinterpret_cast<VT*>(hp + half), ob);
-                }
-                if constexpr (KV) {
-                    if (head >= a.n_q) {  // rotated k heads and untouched v heads go to the caches
-                        const bool is_v = head >= nqk;
-                        uint16_t* cp = (is_v ? a.v_cache : a.k_cache) + pos * kvw +
-                                       static_cast<int64_t>(head - (is_v ? nqk : a.n_q)) * HD + i0;
-                        store_f16<T, V>(cp, is_v ? A[u] : oa);
-                        store_f16<T, V>(cp + half, is_v ? B[u] : ob);
+                    if constexpr (V == 1) {
+                        fa[e] = to_f32(A[u]);
+                        fb[e] = to_f32(B[u]);
+                    } else {
+                        fa[e] = to_f32(A[u][e]);
+                        fb[e] = to_f32(B[u][e]);
                     }
                 }
-                if (more) {
-                    A[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * HD + i0));
-                    B[u] = qk_load(reinterpret_cast<const VT*>(nrow + head * HD + half + i0));
+                if (norm) {
+                    // Squares of f16/f32 values are exact in double, so fma == the reference's mul + add.
+                    double ss = 0.0;
+#pragma unroll
+                    for (int e = 0; e < V; e++) {
+                        ss = __builtin_fma(static_cast<double>(fa[e]), static_cast<double>(fa[e]), ss);
+                        ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
+                    }
+                    ss = group_sum_f64<L>(ss);
+                    const float r = NEKO_TUNE_QK_RSQ ? rsqrt_to_float(ss * (1.0 / HD) + static_cast<double>(a.eps))
+                                                     : head_scale(a, ss);
+                    const float* w = wl + (head < a.n_q ? 0 : HD) + i0;
+#pragma unroll
+                    for (int e = 0; e < V; e++) {
+                        fa[e] = fa[e] * r * w[e];
+                        fb[e] = fb[e] * r * w[half + e];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    float c, s;
+                    if constexpr (V == 1) {
+                        const float2v v = *reinterpret_cast<const float2v*>(cr);
+                        c = v[0];
+                        s = v[1];
+                    } else {
+                        const float4v v = *reinterpret_cast<const float4v*>(cr + 2 * (e & ~1));
+                        c = v[2 * (e & 1)];
+                        s = v[2 * (e & 1) + 1];
+                    }
+                    const float x0 = fa[e] * c - fb[e] * s;
+                    const float x1 = fa[e] * s + fb[e] * c;
+                    if constexpr (V == 1) {
+                        oa = from_f32<T>(x0);
+                        ob = from_f32<T>(x1);
+                    } else {
+                        oa[e] = from_f32<T>(x0);
+                        ob[e] = from_f32<T>(x1);
+                    }
                 }
             }
+            // q and k heads back in place (v heads and lanes past the last head fall outside `st`).
+            buf_store16v<NEKO_TUNE_QK_NT_STORE>(st, off(u), oa);
+            buf_store16v<NEKO_TUNE_QK_NT_STORE>(st, off(u) + half * sizeof(T), ob);
+            if constexpr (KV) {
+                // Rotated k heads to the k cache row, untouched v heads to the v cache row; each
+                // resource's range drops the other heads' stores (their offsets wrap past it).
+                const uint32_t ko = static_cast<uint32_t>((head - a.n_q) * HD + i0) * 2u;
+                const uint32_t vo = static_cast<uint32_t>((head - nqk) * HD + i0) * 2u;
+                store_f16_buf<T, V>(kc, ko, oa);
+                store_f16_buf<T, V>(kc, ko + half * 2u, ob);
+                store_f16_buf<T, V>(vc, vo, A[u]);
+                store_f16_buf<T, V>(vc, vo + half * 2u, B[u]);
+            }
+            if (more) load_pass(ld, u);
         }
-        // The next token's row goes to the other buffer; this wave's own LDS operations run in order,
-        // so the next iteration's reads see it.
-        if (more) {
-            cs_store(buf ^ 1, ncs);
-            pos = npos;
+    };
+
+    // The first token's cos/sin row goes out before its row data when the knob asks for it (the load
+    // then waits for the position, but its staging does not wait for the row data: the memory counter
+    // completes in order).
+    {
+        float2v r[PL];
+        if constexpr (NEKO_TUNE_QK_CS_FIRST) cs_load(pos_of(0), r);
+        const BufRes ld = buf_res(row_of(t0), load_bytes);
+#pragma unroll
+        for (int u = 0; u < U; u++) load_pass(ld, u);
+        if (norm) {
+            *reinterpret_cast<float4v*>(&wsh[wave][lane * 4]) = wv;
+            for (int i = 256 + lane * 4; i < 2 * HD; i += 256)
+                *reinterpret_cast<float4v*>(&wsh[wave][i]) = *reinterpret_cast<const float4v*>(a.wqk + i);
         }
-        buf ^= 1;
-        t = tn;
+        if constexpr (!NEKO_TUNE_QK_CS_FIRST) cs_load(pos_of(0), r);
+        cs_store(0, r);
     }
+    // Token k with a next token: its passes, the refills, and the next cos/sin row staged in the other
+    // LDS buffer (this wave's own LDS operations run in order, so the next step's reads see it).
+    int k = 0;
+    auto advance = [&]() __attribute__((always_inline)) {
+        float2v ncs[PL];
+        cs_load(pos_of(k + 1), ncs);
+        step(k, k & 1, true);
+        cs_store((k & 1) ^ 1, ncs);
+        k++;
+    };
+    // The first step is peeled so that the loop is entered with the memory ops of a step outstanding,
+    // as after each iteration (the compiler's waits then hold for both ways into the loop).
+    if (k + 1 < ntok) {
+        advance();
+        while (k + 1 < ntok) advance();
+    }
+    step(k, k & 1, false);
 }
 
 // Tokens with more heads than U passes: persistent waves, each token in batches of U passes, the norm
@@ -499,7 +572,9 @@ QkKernel pick_l(int L, int nh) {
         case 8: return pick_u<T, 8, V, KV>(passes);
         case 16: return pick_u<T, 16, V, KV>(passes);
         case 32: return pick_u<T, 32, V, KV>(passes);
-        case 64: return pick_u<T, 64, V, KV>(passes);
+        case 64:
+            if constexpr (2 * 64 * V <= 512) return pick_u<T, 64, V, KV>(passes);  // head sizes up to 512
+            return nullptr;
     }
     return nullptr;
 }

@@ -246,6 +246,19 @@ def test_qk_rope_shapes(dev, n_q, n_kv, hd, norm, dtype):
     _qk_case(dev, 37, n_q, n_kv, hd, 512, pos, norm, theta=1e4, dtype=dtype)
 
 
+def test_qk_rope_rows_beyond_one_launch(dev):
+    """More rows than the persistent grid takes in one launch (at most 64 per wave: with the 8192
+    resident waves a one-pass head layout allows, 524288 rows), so the op runs in several launches;
+    some positions fall outside the table."""
+    _case("qk rope 600000 rows (several launches)")
+    T, n_q, n_kv, hd, n_pos = 600000, 1, 1, 64, 4096
+    rng = np.random.default_rng(27)
+    pos = rng.integers(0, n_pos, T).astype(np.int32)
+    pos[rng.integers(0, T, 50)] = -5
+    pos[rng.integers(0, T, 50)] = n_pos
+    _qk_case(dev, T, n_q, n_kv, hd, n_pos, pos, True)
+
+
 def test_qk_rope_pos0_and_out_of_range(dev):
     _case("qk rope pos0 form and out-of-range positions")
     # pos0 + row (the reference's GPU ABI)
