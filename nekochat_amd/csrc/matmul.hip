@@ -55,6 +55,7 @@ struct MmArgs {
     int flags;
     int fmt;
     int blocks_per_wave;  // 32-wide blocks of K per wave, a multiple of kGroup (fast path)
+    int vec_y;            // 1: every run of 4 outputs starting at a multiple of 4 is naturally aligned
 };
 
 constexpr int kGelu = 1, kAccumulate = 2;  // cpu_ops.h MatmulFlags
@@ -66,6 +67,72 @@ __device__ __forceinline__ void epilogue(const MmArgs& a, int64_t t, int64_t n, 
     TY* yp = static_cast<TY*>(a.y) + t * a.ys + n;
     if (a.flags & kAccumulate) v += to_f32(*yp);
     *yp = from_f32<TY>(v);
+}
+
+// The same for outputs n .. n + 3 of row t (n a multiple of 4): one 4-element load and store when
+// all four exist and a.vec_y says they are aligned, else element by element. Rows t >= T are skipped.
+template <typename TY>
+__device__ __forceinline__ void epilogue4(const MmArgs& a, int64_t t, int64_t n, float4v v) {
+    if (t >= a.T) return;
+    if (a.vec_y && n + 4 <= a.N) {
+        typedef typename VecOf<TY, 4>::V V4;
+        if (a.bias) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] += a.bias[n + q];
+        }
+        if (a.flags & kGelu) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = gelu_ref(v[q]);
+        }
+        V4* yp = reinterpret_cast<V4*>(static_cast<TY*>(a.y) + t * a.ys + n);
+        if (a.flags & kAccumulate) {
+            const V4 old = *yp;
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] += to_f32(old[q]);
+        }
+        V4 o;
+#pragma unroll
+        for (int q = 0; q < 4; q++) o[q] = from_f32<TY>(v[q]);
+        *yp = o;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (n + q < a.N) epilogue<TY>(a, t, n + q, v[q]);
+    }
+}
+
+// LDS floats a wave needs to regroup one 32 x 32 accumulator tile (rows padded to 36 floats: 16-byte
+// aligned, and the two row groups one write instruction covers fall on different banks).
+constexpr int kTileLdsRow = 36;
+constexpr int kTileLdsFloats = 32 * kTileLdsRow;
+
+// Stores a wave's TM x TN grid of 32 x 32 v_mfma_f32_32x32x16 accumulator tiles -- lane (l32, h) holds
+// C[8 (e / 4) + 4 h + e % 4][l32] of each -- as 4-output row chunks: each tile is written to the
+// wave's LDS scratch (kTileLdsFloats) and read back so that lane l takes columns 4 (l % 8) .. + 3 of
+// rows l / 8, 8 + l / 8, ...; every store instruction then covers eight whole 128-byte row segments,
+// with a quarter of the instructions of element-wise stores. Tile (i, j) covers rows m_base + 32 i ..
+// and columns n_base + 32 j ...
+template <typename TY, int TM, int TN>
+__device__ __forceinline__ void store_tiles(const MmArgs& a, const float16v (&acc)[TM][TN], float* scratch, int64_t m_base,
+                                            int64_t n_base, int lane) {
+    const int l32 = lane & 31, h = lane >> 5;
+    const int rr = lane >> 3, cc = 4 * (lane & 7);
+    unrolled<TM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        unrolled<TN>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const float16v v = acc[i][j];
+            unrolled<16>([&](auto ec) {
+                constexpr int e = decltype(ec)::value;
+                scratch[(8 * (e >> 2) + 4 * h + (e & 3)) * kTileLdsRow + l32] = v[e];
+            });
+            for (int r = 0; r < 4; r++) {
+                const int row = 8 * r + rr;
+                const float4v o = *reinterpret_cast<const float4v*>(&scratch[row * kTileLdsRow + cc]);
+                epilogue4<TY>(a, m_base + i * 32 + row, n_base + j * 32 + cc, o);
+            }
+        });
+    });
 }
 
 // ---------------------------------------------------------------- fast path: MFMA tiles
@@ -401,6 +468,8 @@ struct Gemm3Lds {
 
 __device__ __forceinline__ int g3_slot(int row, int c) { return c ^ ((row >> 1) & 7); }
 
+static_assert(sizeof(Gemm3Lds) >= (kG3Threads / 64) * kTileLdsFloats * sizeof(float), "epilogue scratch");
+
 template <typename TY>
 __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int tiles_m, int tiles_n) {
     extern __shared__ __align__(16) uint8_t g3_lds[];
@@ -477,22 +546,10 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int t
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next stage have landed
         __syncthreads();                // and every wave's; this stage's reads are done
     }
-    // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile. (Indices
-    // fixed at compile time: with f16 output a rolled loop here sent acc to scratch memory.)
-    unrolled<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const int64_t n = n0 + wn * 64 + j * 32 + l32;
-        if (n >= a.N) return;
-        unrolled<TM>([&](auto ic) {
-            constexpr int i = decltype(ic)::value;
-            const float16v v = acc[i][j];
-            unrolled<16>([&](auto ec) {
-                constexpr int e = decltype(ec)::value;
-                const int64_t t = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (t < a.T) epilogue<TY>(a, t, n, v[e]);
-            });
-        });
-    });
+    // The operand buffers are free once every wave is past its last stage: each wave regroups its
+    // tiles through its own slice of them.
+    __syncthreads();
+    store_tiles<TY, TM, TN>(a, acc, reinterpret_cast<float*>(g3_lds) + wave * kTileLdsFloats, m0 + wm * 128, n0 + wn * 64, lane);
 }
 
 template <typename TY>
@@ -1446,6 +1503,7 @@ __device__ __forceinline__ void gemm2_step(Gemm2Acc<C>& acc, const Gemm2Lds<C>& 
 // Grid and split of K as mm_gemm_kernel (tiles of BM x BN), in stages of 64.
 template <int FMT, typename TY, class C>
 __global__ __launch_bounds__(C::threads, 2) void mm_gemm2_kernel(MmArgs a, int tiles_m, int tiles_n, int slices, float* partial) {
+    static_assert(sizeof(Gemm2Lds<C>) >= (C::threads / 64) * kTileLdsFloats * sizeof(float), "epilogue scratch");
     extern __shared__ __align__(16) uint8_t g2_lds[];
     Gemm2Lds<C>& L = *reinterpret_cast<Gemm2Lds<C>*>(g2_lds);
     const int tid = static_cast<int>(threadIdx.x);
@@ -1503,6 +1561,13 @@ __global__ __launch_bounds__(C::threads, 2) void mm_gemm2_kernel(MmArgs a, int t
         }
     }
     // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
+    if (!partial) {
+        // The operand buffers are free once every wave is past its last stage.
+        __syncthreads();
+        store_tiles<TY, C::TM, C::TN>(a, acc.v, reinterpret_cast<float*>(g2_lds) + wave * kTileLdsFloats,
+                                      m0 + wm * 32 * C::TM, n0 + wn * 32 * C::TN, lane);
+        return;
+    }
     const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int j = 0; j < C::TN; j++) {
@@ -1514,9 +1579,7 @@ __global__ __launch_bounds__(C::threads, 2) void mm_gemm2_kernel(MmArgs a, int t
             unrolled<16>([&](auto ec) {
                 constexpr int e = decltype(ec)::value;
                 const int64_t t = m0 + wm * 32 * C::TM + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (t >= a.T) return;
-                if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = v[e];
-                else epilogue<TY>(a, t, n, v[e]);
+                if (t < a.T) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = v[e];
             });
         }
     }
@@ -1749,7 +1812,7 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                  "%s: y may not overlap x or the weights", what);
 
     MmArgs a{x, x_stride, T, static_cast<const uint8_t*>(w), row_bytes, static_cast<int>(K), static_cast<int>(N), bias,
-             y, y_stride, flags, fmt, 0};
+             y, y_stride, flags, fmt, 0, aligned(y, 4 * dtype_size(y_dtype)) && y_stride % 4 == 0};
     const bool fast = x_dtype == NEKO_DT_F16 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 8 == 0 &&
                       aligned(w, 16) && row_bytes % 16 == 0;
     // Decode-sized T: the GEMV path, NT tokens per pass with their activations staged in 64 KB of LDS.
