@@ -561,6 +561,180 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
     return NEKO_OK;
 }
 
+// ---------------------------------------------------------------- prefill GEMM, FP8 / FP4, direct-to-LDS loads
+//
+// The F16 kernel's tiling and pipeline (256 x 256 tiles, eight waves of 128 x 64, K staged 64 at a time
+// in double-buffered LDS filled by global_load_lds) for code rows: the activations land in LDS exactly
+// as there; the stage's raw codes land chunk-major -- 16-byte chunk c of row r at (c * 256 + r) * 16, so
+// the 32 rows a read serves are contiguous and conflict-free -- and each row's two f16 block scales as
+// one dword. Every wave decodes its own B fragments from the codes (FP8 by the bit trick, FP4 by
+// v_cvt_scalef32_pk_f16_fp4; exact f16 values), sums each 32-wide block with two MFMAs from zero and
+// adds it into the accumulators scaled by the block's f32 scale (one fma per output per block), as the
+// register-staged kernel does.
+#ifndef NEKO_TUNE_MM_GEMM3Q
+#define NEKO_TUNE_MM_GEMM3Q 1
+#endif
+constexpr bool kGemm3q = NEKO_TUNE_MM_GEMM3Q;
+
+template <int FMT>
+struct Gemm3qLds {
+    static constexpr int KC = FMT == 1 ? 4 : 2;  // 16-byte code chunks per row and stage
+    half_t a[2][kG3BM * 64];
+    uint8_t b[2][KC * kG3BN * 16];
+    uint32_t s[2][kG3BN];
+};
+
+// FP4 byte SEL of word q -> its two weights as f16 (low nibble first); SEL must be a literal.
+#define NEKO_FP4_PAIR3(q, SEL) __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4((q), 1.0f, SEL))
+
+// The two B operands (k 0..15 and 16..31 of block bb, this lane's 8 of each) of row r.
+template <int FMT>
+__device__ __forceinline__ void g3q_read_b(const uint8_t* lb, int bb, int r, int h, half8 (&B)[2]) {
+    if constexpr (FMT == 1) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint2v w = *reinterpret_cast<const uint2v*>(lb + ((2 * bb + q) * kG3BN + r) * 16 + 8 * h);
+            uint4v o;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                o[2 * i] = fp8_pair_bits(__builtin_amdgcn_perm(0u, w[i], 0x0C010C00u));
+                o[2 * i + 1] = fp8_pair_bits(__builtin_amdgcn_perm(0u, w[i], 0x0C030C02u));
+            }
+            B[q] = __builtin_bit_cast(half8, o);
+        }
+    } else {
+        // Bytes 8 h .. 8 h + 7 of the block: weights 8 h + j (low nibbles) and 16 + 8 h + j (high).
+        const uint2v w = *reinterpret_cast<const uint2v*>(lb + (bb * kG3BN + r) * 16 + 8 * h);
+        uint32_t pr[8];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            pr[4 * i] = NEKO_FP4_PAIR3(w[i], 0);
+            pr[4 * i + 1] = NEKO_FP4_PAIR3(w[i], 1);
+            pr[4 * i + 2] = NEKO_FP4_PAIR3(w[i], 2);
+            pr[4 * i + 3] = NEKO_FP4_PAIR3(w[i], 3);
+        }
+        uint4v lo, hi;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            lo[j] = __builtin_amdgcn_perm(pr[2 * j + 1], pr[2 * j], 0x05040100u);
+            hi[j] = __builtin_amdgcn_perm(pr[2 * j + 1], pr[2 * j], 0x07060302u);
+        }
+        B[0] = __builtin_bit_cast(half8, lo);
+        B[1] = __builtin_bit_cast(half8, hi);
+    }
+}
+#undef NEKO_FP4_PAIR3
+
+template <int FMT, typename TY>
+__global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3q_kernel(MmArgs a, int tiles_m, int tiles_n) {
+    typedef Gemm3qLds<FMT> Lds;
+    constexpr int KC = Lds::KC, NB = KC / 2;  // B load instructions per lane and stage
+    static_assert(sizeof(Lds) >= (kG3Threads / 64) * kTileLdsFloats * sizeof(float), "epilogue scratch");
+    extern __shared__ __align__(16) uint8_t g3_lds[];
+    Lds& L = *reinterpret_cast<Lds*>(g3_lds);
+    constexpr int TM = 4, TN = 2;
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 1, wn = wave >> 1;
+
+    uint32_t b = blockIdx.x;
+    const uint32_t nb = gridDim.x;
+    if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
+    constexpr int GM = NEKO_TUNE_MM_G3_GM;
+    const int group = static_cast<int>(b) / (GM * tiles_n);
+    const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
+    const int in_group = static_cast<int>(b) - group * GM * tiles_n;
+    const int64_t m0 = static_cast<int64_t>(first_m + in_group % gm) * kG3BM;
+    const int64_t n0 = static_cast<int64_t>(in_group / gm) * kG3BN;
+    const int64_t lastN = static_cast<int64_t>(a.N) - 1;
+
+    // Activations: as mm_gemm3_kernel (rows (4 wave + i) * 8 + lane / 8, swizzled chunk slots).
+    const half_t* xa[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (wave * 4 + i) * 8 + (lane >> 3), c = g3_slot(row, lane & 7);
+        xa[i] = static_cast<const half_t*>(a.x) + min(m0 + row, a.T - 1) * a.xs + 8 * c;
+    }
+    // Codes: this lane's chunk p = (wave NB + i) 64 + lane of the stage, chunk p / 256 of row p % 256.
+    const uint8_t* wb[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int p = (wave * NB + i) * 64 + lane, c = p / kG3BN, r = p % kG3BN;
+        wb[i] = a.w + min(n0 + r, lastN) * a.rb + 16 * c;
+    }
+    // Scales: waves 0-3, lane l: row 64 wave + l.
+    const uint8_t* ws = a.w + min(n0 + 64 * (wave & 3) + lane, lastN) * a.rb + (FMT == 1 ? a.K : a.K / 2);
+    auto issue = [&](int k0, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r0 = (wave * 4 + i) * 8;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(xa[i] + k0),
+                                             (__attribute__((address_space(3))) void*)(&L.a[buf][r0 * 64]), 16, 0, 0);
+        }
+        const int kb = FMT == 1 ? k0 : k0 / 2;  // code bytes before the stage
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(wb[i] + kb),
+                                             (__attribute__((address_space(3))) void*)(&L.b[buf][(wave * NB + i) * 64 * 16]), 16, 0, 0);
+        if (wave < 4)
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(ws + 2 * (k0 / kBlockK)),
+                                             (__attribute__((address_space(3))) void*)(&L.s[buf][64 * wave]), 4, 0, 0);
+    };
+
+    float16v acc[TM][TN] = {};
+    const int l32 = lane & 31, h = lane >> 5;
+    const int nk = a.K / 64;
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int s = 0; s < nk; s++) {
+        const int buf = s & 1;
+        if (s + 1 < nk) issue((s + 1) * 64, buf ^ 1);  // that buffer's last readers passed the barrier
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            half8 B[TN][2];
+            float sc[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int r = wn * 64 + j * 32 + l32;
+                g3q_read_b<FMT>(L.b[buf], bb, r, h, B[j]);
+                const half2v s2 = __builtin_bit_cast(half2v, L.s[buf][r]);
+                sc[j] = static_cast<float>(s2[bb]) * block_scale_factor<FMT>();
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int r = wm * 128 + i * 32 + l32;
+                half8 A[2];
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+                    A[q] = *reinterpret_cast<const half8*>(&L.a[buf][r * 64 + 8 * g3_slot(r, 4 * bb + 2 * q + h)]);
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    float16v blk = {};
+                    blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[j][0], blk, 0, 0, 0);
+                    blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[j][1], blk, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[i][j][e] = __builtin_fmaf(sc[j], blk[e], acc[i][j][e]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of the next stage have landed
+        __syncthreads();                // and every wave's; this stage's reads are done
+    }
+    // The operand buffers are free once every wave is past its last stage: each wave regroups its
+    // tiles through its own slice of them.
+    __syncthreads();
+    store_tiles<TY, TM, TN>(a, acc, reinterpret_cast<float*>(g3_lds) + wave * kTileLdsFloats, m0 + wm * 128, n0 + wn * 64, lane);
+}
+
+template <int FMT, typename TY>
+int launch_gemm3q(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) {
+    constexpr size_t lds = sizeof(Gemm3qLds<FMT>);
+    static std::atomic<uint64_t> allowed{0};
+    if (int rc = allow_lds(ctx, reinterpret_cast<const void*>(&mm_gemm3q_kernel<FMT, TY>), lds, allowed)) return rc;
+    hipLaunchKernelGGL((mm_gemm3q_kernel<FMT, TY>), grid, dim3(kG3Threads), lds, ctx->stream, a, tm, tn);
+    return NEKO_OK;
+}
+
 // ---------------------------------------------------------------- mid-size T: activations shared in LDS
 //
 // FP4 at 5 <= T < 48, FP8 at 13 <= T < 48, F16 at 17 <= T < 33: second form: each wave of a 4-wave workgroup
@@ -1853,6 +2027,16 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
             const int tm = static_cast<int>(g3_m), tn = static_cast<int>(g3_n);
             const int rc = y_dtype == NEKO_DT_F16 ? launch_gemm3<half_t>(ctx, grid, a, tm, tn)
                                                   : launch_gemm3<float>(ctx, grid, a, tm, tn);
+            if (rc) return rc;
+            return after_launch(ctx, what);
+        }
+        if (v2 && kGemm3q && fmt != NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
+            NEKO_REQUIRE(ctx, g3_m * g3_n <= 0x7fffffff, "%s: too many output tiles", what);
+            const dim3 grid(static_cast<uint32_t>(g3_m * g3_n));
+            const int tm = static_cast<int>(g3_m), tn = static_cast<int>(g3_n);
+            const bool h = y_dtype == NEKO_DT_F16;
+            const int rc = fmt == NEKO_FMT_FP8 ? (h ? launch_gemm3q<1, half_t>(ctx, grid, a, tm, tn) : launch_gemm3q<1, float>(ctx, grid, a, tm, tn))
+                                               : (h ? launch_gemm3q<2, half_t>(ctx, grid, a, tm, tn) : launch_gemm3q<2, float>(ctx, grid, a, tm, tn));
             if (rc) return rc;
             return after_launch(ctx, what);
         }

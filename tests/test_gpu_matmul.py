@@ -174,7 +174,7 @@ def test_matmul_split_k_across_stream_switch(dev):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
     (2000, 320, 8200),  # FP8 / FP4: 256-token x 128-row tiles (enough to fill the GPU), partial in both
-    (4000, 320, 8200),  # F16: 256 x 256 tiles, direct-to-LDS loads (two per CU), partial in both
+    (4000, 320, 8200),  # 256 x 256 tiles, direct-to-LDS loads (two per CU; FP8 / FP4 decoded per wave), partial in both
     (4000, 320, 4100),  # F16: 128 x 128 tiles (too few 256 x 256 tiles for two per CU), partial in both
     (300, 352, 37),     # K % 64 == 32: the 32-wide staged kernel
     (200, 320, 37),     # 128 x 128 tiles in 64-wide stages
@@ -219,7 +219,7 @@ def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
     (300, 1024, 700),   # partial token and row tiles
     (512, 9728, 2560),  # down projection, long K
     (512, 2560, 16384), # FP8 / FP4: 256-token x 128-row tiles
-    (2048, 1024, 16384),  # F16: 256 x 256 tiles with direct-to-LDS loads
+    (2048, 1024, 16384),  # 256 x 256 tiles with direct-to-LDS loads (FP8 / FP4: codes and scales too)
     (4096, 1024, 4096),   # F16: 128 x 128 tiles, two stages of register prefetch
     (47, 9728, 2560),   # three token tiles, activations staged per K slice, slices reduced in order
 ])
