@@ -69,18 +69,26 @@ __device__ __forceinline__ void epilogue(const MmArgs& a, int64_t t, int64_t n, 
     *yp = from_f32<TY>(v);
 }
 
-// The same for outputs n .. n + 3 of row t (n a multiple of 4): one 4-element load and store when
-// all four exist and a.vec_y says they are aligned, else element by element. Rows t >= T are skipped.
-template <typename TY>
-__device__ __forceinline__ void epilogue4(const MmArgs& a, int64_t t, int64_t n, float4v v) {
+// LDS floats a wave needs to regroup one 32 x 32 accumulator tile (rows padded to 36 floats: 16-byte
+// aligned, and the two row groups one write instruction covers fall on different banks).
+constexpr int kTileLdsRow = 36;
+constexpr int kTileLdsFloats = 32 * kTileLdsRow;
+
+// Outputs n .. n + 3 of row t from a regrouped tile row in LDS (`src` holds their four values), GELU
+// applied or not at compile time: one 4-element load and store when all four exist and a.vec_y says
+// they are aligned, else element by element in a loop that stays rolled (the rare tail / unaligned
+// case; rereading LDS keeps it one copy). Rows t >= T are skipped.
+template <typename TY, bool GELU>
+__device__ __forceinline__ void epilogue4_lds(const MmArgs& a, int64_t t, int64_t n, const float* src) {
     if (t >= a.T) return;
     if (a.vec_y && n + 4 <= a.N) {
         typedef typename VecOf<TY, 4>::V V4;
+        float4v v = *reinterpret_cast<const float4v*>(src);
         if (a.bias) {
 #pragma unroll
             for (int q = 0; q < 4; q++) v[q] += a.bias[n + q];
         }
-        if (a.flags & kGelu) {
+        if constexpr (GELU) {
 #pragma unroll
             for (int q = 0; q < 4; q++) v[q] = gelu_ref(v[q]);
         }
@@ -95,26 +103,21 @@ __device__ __forceinline__ void epilogue4(const MmArgs& a, int64_t t, int64_t n,
         for (int q = 0; q < 4; q++) o[q] = from_f32<TY>(v[q]);
         *yp = o;
     } else {
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (n + q < a.N) epilogue<TY>(a, t, n + q, v[q]);
+#pragma unroll 1
+        for (int q = 0; q < 4 && n + q < a.N; q++) {
+            float v = src[q];
+            if (a.bias) v += a.bias[n + q];
+            if constexpr (GELU) v = gelu_ref(v);
+            TY* yp = static_cast<TY*>(a.y) + t * a.ys + n + q;
+            if (a.flags & kAccumulate) v += to_f32(*yp);
+            *yp = from_f32<TY>(v);
+        }
     }
 }
 
-// LDS floats a wave needs to regroup one 32 x 32 accumulator tile (rows padded to 36 floats: 16-byte
-// aligned, and the two row groups one write instruction covers fall on different banks).
-constexpr int kTileLdsRow = 36;
-constexpr int kTileLdsFloats = 32 * kTileLdsRow;
-
-// Stores a wave's TM x TN grid of 32 x 32 v_mfma_f32_32x32x16 accumulator tiles -- lane (l32, h) holds
-// C[8 (e / 4) + 4 h + e % 4][l32] of each -- as 4-output row chunks: each tile is written to the
-// wave's LDS scratch (kTileLdsFloats) and read back so that lane l takes columns 4 (l % 8) .. + 3 of
-// rows l / 8, 8 + l / 8, ...; every store instruction then covers eight whole 128-byte row segments,
-// with a quarter of the instructions of element-wise stores. Tile (i, j) covers rows m_base + 32 i ..
-// and columns n_base + 32 j ...
-template <typename TY, int TM, int TN>
-__device__ __forceinline__ void store_tiles(const MmArgs& a, const float16v (&acc)[TM][TN], float* scratch, int64_t m_base,
-                                            int64_t n_base, int lane) {
+template <typename TY, int TM, int TN, bool GELU>
+__device__ __forceinline__ void store_tiles_as(const MmArgs& a, const float16v (&acc)[TM][TN], float* scratch, int64_t m_base,
+                                               int64_t n_base, int lane) {
     const int l32 = lane & 31, h = lane >> 5;
     const int rr = lane >> 3, cc = 4 * (lane & 7);
     unrolled<TM>([&](auto ic) {
@@ -126,13 +129,36 @@ __device__ __forceinline__ void store_tiles(const MmArgs& a, const float16v (&ac
                 constexpr int e = decltype(ec)::value;
                 scratch[(8 * (e >> 2) + 4 * h + (e & 3)) * kTileLdsRow + l32] = v[e];
             });
-            for (int r = 0; r < 4; r++) {
-                const int row = 8 * r + rr;
-                const float4v o = *reinterpret_cast<const float4v*>(&scratch[row * kTileLdsRow + cc]);
-                epilogue4<TY>(a, m_base + i * 32 + row, n_base + j * 32 + cc, o);
+            if constexpr (GELU) {
+#pragma unroll 1
+                for (int r = 0; r < 4; r++) {
+                    const int row = 8 * r + rr;
+                    epilogue4_lds<TY, true>(a, m_base + i * 32 + row, n_base + j * 32 + cc, &scratch[row * kTileLdsRow + cc]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = 8 * r + rr;
+                    epilogue4_lds<TY, false>(a, m_base + i * 32 + row, n_base + j * 32 + cc, &scratch[row * kTileLdsRow + cc]);
+                }
             }
         });
     });
+}
+
+// Stores a wave's TM x TN grid of 32 x 32 v_mfma_f32_32x32x16 accumulator tiles -- lane (l32, h) holds
+// C[8 (e / 4) + 4 h + e % 4][l32] of each -- as 4-output row chunks: each tile is written to the
+// wave's LDS scratch (kTileLdsFloats) and read back so that lane l takes columns 4 (l % 8) .. + 3 of
+// rows l / 8, 8 + l / 8, ...; every store instruction then covers eight whole 128-byte row segments,
+// with a quarter of the instructions of element-wise stores. Tile (i, j) covers rows m_base + 32 i ..
+// and columns n_base + 32 j ... The GELU epilogue is a separate instantiation chosen once per call:
+// inlined into every tile's rows it made the kernel's code several hundred KB, which the instruction
+// cache then streamed through on every tile's epilogue.
+template <typename TY, int TM, int TN>
+__device__ __forceinline__ void store_tiles(const MmArgs& a, const float16v (&acc)[TM][TN], float* scratch, int64_t m_base,
+                                            int64_t n_base, int lane) {
+    if (a.flags & kGelu) store_tiles_as<TY, TM, TN, true>(a, acc, scratch, m_base, n_base, lane);
+    else store_tiles_as<TY, TM, TN, false>(a, acc, scratch, m_base, n_base, lane);
 }
 
 // ---------------------------------------------------------------- fast path: MFMA tiles
