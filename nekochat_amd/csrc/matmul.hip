@@ -724,7 +724,9 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3q_kernel(MmArgs a, int 
                 const int r = wn * 64 + j * 32 + l32;
                 g3q_read_b<FMT>(L.b[buf], bb, r, h, B[j]);
                 const half2v s2 = __builtin_bit_cast(half2v, L.s[buf][r]);
-                sc[j] = static_cast<float>(s2[bb]) * block_scale_factor<FMT>();
+                // FP8 codes decode to value / 2^8; FP4 always goes through the hardware conversion
+                // here (exact values), whatever the other kernels' decode knob says.
+                sc[j] = static_cast<float>(s2[bb]) * (FMT == 1 ? 256.0f : 1.0f);
             }
 #pragma unroll
             for (int i = 0; i < TM; i++) {

@@ -204,6 +204,47 @@ def test_matmul_gemm_tilings_integer_bitexact(dev, fmt, T, K, N):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T,K,N", [
+    (4096, 64, 8192),   # 256 x 256 tiles (two per CU), direct-to-LDS loads
+    (4096, 64, 4100),   # F16: 128 x 128 tiles; FP8 / FP4: 256-token x 128-row tiles; a 4-column last tile
+])
+def test_matmul_gemm_epilogue_variants(dev, fmt, T, K, N):
+    """The GEMM kernels' regrouped epilogue in each of its forms, on integer-valued data (the sums are
+    exact): bias + GELU (the separately instantiated GELU epilogue; checked on a random sample of
+    outputs against the oracle's GELU of the same exact argument, within 2 f32 ulp), f16 output (one
+    rounding of the exact value, every output), and an output slice that starts one float into each row
+    with an odd row stride (no 4-wide stores: the element-wise tail path), accumulated into, with the
+    columns either side left untouched."""
+    _case(f"matmul GEMM epilogues fmt={fmt} T={T} K={K} N={N}")
+    rng = np.random.default_rng(700 + fmt + N)
+    tab, w = M.integer_table(fmt, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T + bias
+    assert np.abs(exact).max() < 2 ** 24
+    e32 = exact.astype(np.float32)
+    xd, td, bd = (torch.from_numpy(v).to(dev) for v in (x.astype(np.float16), tab, bias))
+
+    got = ops.matmul(xd, td, fmt, K, bias=bd, flags=ops.MM_GELU).cpu().numpy()
+    idx = rng.integers(0, T * N, 200_000)
+    idx = np.concatenate([idx, np.arange(T * N - N, T * N)])  # and the whole last row
+    want = np.array([O.lib().oracle_gelu(float(v)) for v in e32.ravel()[idx]], np.float32)
+    d = np.abs(got.ravel()[idx].view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert d.max() <= 2, int(d.max())
+
+    got16 = ops.matmul(xd, td, fmt, K, bias=bd, out_dtype=torch.float16).cpu().numpy()
+    assert np.array_equal(got16.view(np.uint16), O.f32_to_f16(e32))
+
+    base = rng.standard_normal((T, N + 3)).astype(np.float32)
+    buf = torch.from_numpy(base).to(dev)
+    ops.matmul(xd, td, fmt, K, bias=bd, out=buf[:, 1:1 + N], flags=ops.MM_ACCUMULATE)
+    res = buf.cpu().numpy()
+    want = (base[:, 1:1 + N].astype(np.float64) + exact).astype(np.float32)
+    assert np.array_equal(res[:, 1:1 + N].view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(res[:, :1], base[:, :1]) and np.array_equal(res[:, 1 + N:], base[:, 1 + N:])
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,K,N", [
     (1, 2560, 6144),    # Qwen3-4B decode: q/k/v projection
     (1, 9728, 2560),    # Qwen3-4B decode: down projection
     (8, 2560, 19456),   # Qwen3-4B batch-8 decode: gate/up projection
