@@ -776,7 +776,9 @@ def stream_floor(args, flush, time_ops):
                         ("neko_floor_rows2", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                               ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
                         ("neko_floor_inplace", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p])):
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+                        ("neko_floor_inplace_rows", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p])):
         getattr(lib, name).argtypes = args_
         getattr(lib, name).restype = ctypes.c_int
     dev = torch.device("cuda:0")
@@ -832,6 +834,24 @@ def stream_floor(args, flush, time_ops):
         name = f"inplace_qk_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
         calls[name] = checked(lib.neko_floor_inplace, d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, ntl, nts)
         nbytes[name] = 2 * cfg.T * qk_w
+    # The op itself on the headline's inputs, and the same rewrite of its own qkv buffer in the q/k
+    # kernel's schedule: whole rows per wave, wave w taking rows w, w + nw, ..., at the kernel's
+    # occupancy of four waves per SIMD (its load policy first), all timed in the same rounds.
+    qk_in = wl.qwen3_prefill_inputs(cfg, dev)
+    calls["qk_norm_rope_op"] = ops.prepare(ops.qk_norm_rope, qk_in["qkv"], cfg.n_q, cfg.n_kv, cfg.hd, qk_in["cs"], cfg.eps,
+                                           wqk=qk_in["wqk"], positions=qk_in["positions"])[0]
+    nbytes["qk_norm_rope_op"] = wl.bytes_qk_rope(cfg.T, cfg.n_q, cfg.n_kv, cfg.hd)
+    waves = 16 * torch.cuda.get_device_properties(dev).multi_processor_count
+    for ntl, nts in ((1, 0), (0, 0)):
+        name = f"inplace_qk_rows_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
+        calls[name] = checked(lib.neko_floor_inplace_rows, qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T, qk_w,
+                              waves, ntl, nts)
+        nbytes[name] = 2 * cfg.T * qk_w
+    # (and the flat rewrite on that buffer too: the same bytes have timed differently on different
+    # allocations, so the op is compared with floors over its own buffer)
+    calls["inplace_qk_plpl_opbuf"] = checked(lib.neko_floor_inplace, qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T,
+                                             qk_w, 0, 0)
+    nbytes["inplace_qk_plpl_opbuf"] = 2 * cfg.T * qk_w
     calls["read_rmsnorm_in"], nbytes["read_rmsnorm_in"] = checked(lib.neko_floor_read, a_ptr, half, sink.data_ptr()), half
     # RMSNorm [rows, 2560] at four row counts, and copies of the same bytes.
     w = wl.weight_f32(cfg.C, 1.0, 0.05, 2, dev)

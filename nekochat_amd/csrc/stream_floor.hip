@@ -4,7 +4,7 @@
 // reach on this GPU: an empty kernel (launch and completion cost), a 16-byte-per-lane copy (read n,
 // write n), a two-input stream (read 2n, write n: SwiGLU's byte counts), the same with SwiGLU's row
 // layout (both inputs halves of one row), an in-place read-and-write-back of the first part of each
-// row (the q/k RoPE's layout), and a read-only sweep.
+// row (the q/k RoPE's layout; flat, and in that kernel's per-wave token order), and a read-only sweep.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -87,6 +87,34 @@ __global__ __launch_bounds__(256) void inplace_kernel(u32x4* buf, int64_t stride
     const uint32_t row = idx / cpr, col = idx - row * cpr;
     u32x4* p = buf + row * stride + col;
     st<NTS>(p, ld<NTL>(p) ^ key);
+}
+
+// The same bytes in the q/k RoPE kernel's schedule: wave w of nw rewrites rows w, w + nw, ... (the
+// first 64 * CPL chunks of each, in place, xored with `key`), holding one row in registers and
+// refilling each chunk with the wave's next row right after storing it; the last row is peeled so no
+// load is under a branch.
+template <int CPL, bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void inplace_rows_kernel(u32x4* buf, int64_t stride, int64_t rows, uint32_t key) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (t >= rows) return;
+    u32x4 r[CPL];
+    const u32x4* p0 = buf + t * stride + lane;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) r[j] = ld<NTL>(p0 + 64 * j);
+    for (; t + nw < rows; t += nw) {
+        u32x4* q = buf + t * stride + lane;
+        const u32x4* nx = buf + (t + nw) * stride + lane;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            st<NTS>(q + 64 * j, r[j] ^ key);
+            r[j] = ld<NTL>(nx + 64 * j);
+        }
+    }
+    u32x4* q = buf + t * stride + lane;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) st<NTS>(q + 64 * j, r[j] ^ key);
 }
 
 bool ok16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -185,6 +213,26 @@ int neko_floor_inplace(void* buf, int64_t stride, int64_t rows, int64_t width, i
     else if (nt_load) hipLaunchKernelGGL((inplace_kernel<true, false>), g, b, 0, st, p, s, c, n, 0u);
     else if (nt_store) hipLaunchKernelGGL((inplace_kernel<false, true>), g, b, 0, st, p, s, c, n, 0u);
     else hipLaunchKernelGGL((inplace_kernel<false, false>), g, b, 0, st, p, s, c, n, 0u);
+    return hipGetLastError();
+}
+
+// buf[r][0, width) read and written back unchanged, in place, by `waves` waves in the q/k RoPE
+// kernel's token order (wave w: rows w, w + waves', ... with waves' = waves rounded up to 4); width
+// must be 10240 bytes (640 chunks: 32 + 8 heads of 128 halves), stride a multiple of 16 bytes.
+int neko_floor_inplace_rows(void* buf, int64_t stride, int64_t rows, int64_t width, int waves, int nt_load, int nt_store,
+                            void* stream) {
+    constexpr int kCpl = 10;
+    if (!ok16(buf) || width != 64 * 16 * kCpl || stride % 16 || stride < width || rows <= 0 || waves <= 0)
+        return hipErrorInvalidValue;
+    const int64_t w = waves < rows ? waves : rows;
+    const dim3 g(static_cast<uint32_t>((w + 3) / 4)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    auto* p = static_cast<u32x4*>(buf);
+    const int64_t s = stride / 16;
+    if (nt_load && nt_store) hipLaunchKernelGGL((inplace_rows_kernel<kCpl, true, true>), g, b, 0, st, p, s, rows, 0u);
+    else if (nt_load) hipLaunchKernelGGL((inplace_rows_kernel<kCpl, true, false>), g, b, 0, st, p, s, rows, 0u);
+    else if (nt_store) hipLaunchKernelGGL((inplace_rows_kernel<kCpl, false, true>), g, b, 0, st, p, s, rows, 0u);
+    else hipLaunchKernelGGL((inplace_rows_kernel<kCpl, false, false>), g, b, 0, st, p, s, rows, 0u);
     return hipGetLastError();
 }
 
