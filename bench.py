@@ -825,9 +825,12 @@ def stream_floor(args, flush, time_ops):
         nbytes[name] = 3 * gi
     # The same SwiGLU-layout stream over constant input (every output line zero): how much cheaper
     # uniform data is, the reason the sources above are random.
+    # Its output goes to a buffer of its own: written into the shared destination, it left constant data
+    # there that the in-place floors after it then rewrote faster than random bits.
     ones = torch.ones(big // 4, dtype=torch.float32, device=dev)
-    calls["rows2_swiglu_ntpl_constdata"] = checked(lib.neko_floor_rows2, ones.data_ptr(), 2 * gi // cfg.T, d_ptr,
-                                                   gi // cfg.T, cfg.T, gi // cfg.T, 1, 0)
+    const_out = torch.empty(gi // 4, dtype=torch.int32, device=dev)
+    calls["rows2_swiglu_ntpl_constdata"] = checked(lib.neko_floor_rows2, ones.data_ptr(), 2 * gi // cfg.T,
+                                                   const_out.data_ptr(), gi // cfg.T, cfg.T, gi // cfg.T, 1, 0)
     nbytes["rows2_swiglu_ntpl_constdata"] = 3 * gi
     qk_w = (cfg.n_q + cfg.n_kv) * cfg.hd * 2
     for ntl, nts in ((0, 0), (1, 0), (1, 1), (0, 1)):
@@ -847,8 +850,7 @@ def stream_floor(args, flush, time_ops):
         calls[name] = checked(lib.neko_floor_inplace_rows, qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T, qk_w,
                               waves, ntl, nts)
         nbytes[name] = 2 * cfg.T * qk_w
-    # (and the flat rewrite on that buffer too: the same bytes have timed differently on different
-    # allocations, so the op is compared with floors over its own buffer)
+    # (and the flat rewrite over that buffer too)
     calls["inplace_qk_plpl_opbuf"] = checked(lib.neko_floor_inplace, qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T,
                                              qk_w, 0, 0)
     nbytes["inplace_qk_plpl_opbuf"] = 2 * cfg.T * qk_w
