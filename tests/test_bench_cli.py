@@ -26,3 +26,16 @@ def test_more_than_one_gpu_is_refused():
     r = _run("--gpus", "2")
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_floor_library_exports_what_bench_binds():
+    """The streaming-floor kernels bench.py times beside the ops: every neko_floor_* function it binds is
+    exported by the built libneko_floor.so (loaded without touching a device)."""
+    import ctypes
+    import re
+
+    names = sorted(set(re.findall(r'"(neko_floor_[a-z0-9_]+)"', open(os.path.join(ROOT, "bench.py")).read())))
+    assert "neko_floor_inplace_rows" in names and len(names) >= 6
+    lib = ctypes.CDLL(os.path.join(ROOT, "nekochat_amd", "libneko_floor.so"))
+    for n in names:
+        assert hasattr(lib, n), f"bench.py binds {n}, which libneko_floor.so does not export"
