@@ -807,26 +807,29 @@ constexpr int kT2Fill = NEKO_TUNE_MM_T2_FILL; // K slices until the grid holds t
 // between the 16 token rows a ds_read_b128 pass serves: the row stride over 16 is odd).
 __host__ __device__ constexpr int t2_row(int nb) { return 32 * nb + 8; }
 
-template <int TT>
-__host__ __device__ constexpr size_t t2_acts_bytes(int nb) { return static_cast<size_t>(16 * TT) * t2_row(nb) * 2; }
+// Bytes of the staged activations: `rows` token rows (the chunk's tokens, at most 16 TT) of nb blocks.
+__host__ __device__ constexpr size_t t2_acts_bytes(int rows, int nb) { return static_cast<size_t>(rows) * t2_row(nb) * 2; }
 
+// xoff[tt]: halves from the staged activations to this lane's token row of tile tt. Token rows past
+// the chunk's last token read that token's row (a broadcast, no extra bank traffic); their MFMA
+// output rows are never stored.
 template <int FMT, int TT>
-__device__ __forceinline__ void t2_load_acts(half8 (&A)[kGroup][TT], const half_t* xl, int xr_stride, int b0, int n, int g) {
+__device__ __forceinline__ void t2_load_acts(half8 (&A)[kGroup][TT], const half_t* xl, const int (&xoff)[TT], int b0, int g) {
 #pragma unroll
     for (int j = 0; j < kGroup; j++)
 #pragma unroll
         for (int tt = 0; tt < TT; tt++)
-            A[j][tt] = *reinterpret_cast<const half8*>(xl + (tt * 16 + n) * xr_stride + (b0 + j) * kBlockK + 8 * g);
+            A[j][tt] = *reinterpret_cast<const half8*>(xl + xoff[tt] + (b0 + j) * kBlockK + 8 * g);
 }
 
 // One group, as mm_step, with the next group's activation fragments read from LDS.
 template <int FMT, int TT>
 __device__ __forceinline__ void t2_step(float4v (&acc)[TT], MmStage<FMT>& st, const half8 (&A)[kGroup][TT],
                                         half8 (&A_next)[kGroup][TT], const uint8_t* const (&prow)[pieces(FMT)],
-                                        int col16, const uint8_t* wrow, int soff, const half_t* xl, int xr_stride,
+                                        int col16, const uint8_t* wrow, int soff, const half_t* xl, const int (&xoff)[TT],
                                         int g, int n, uint8_t* tile, const int (&slot)[pieces(FMT)], int b_acts_rel,
                                         int b_stage) {
-    t2_load_acts<FMT, TT>(A_next, xl, xr_stride, b_acts_rel, n, g);
+    t2_load_acts<FMT, TT>(A_next, xl, xoff, b_acts_rel, g);
     wave_sync_lds();  // the previous group's operand reads are done
 #pragma unroll
     for (int q = 0; q < pieces(FMT); q++) *reinterpret_cast<uint4v*>(tile + slot[q]) = st.w[q];
@@ -846,8 +849,8 @@ __device__ __forceinline__ void t2_step(float4v (&acc)[TT], MmStage<FMT>& st, co
 }
 
 // Grid: x = groups of 4 row tiles (64 rows), y = chunks of 16 TT tokens, z = K slices of
-// `slice_blocks` blocks. Dynamic LDS: the staged activations (16 TT rows of t2_row(slice_blocks)
-// halves), then one weight staging tile per wave.
+// `slice_blocks` blocks. Dynamic LDS: the staged activations (one row of t2_row(slice_blocks) halves
+// per token of the chunk, at most 16 TT), then one weight staging tile per wave.
 template <int FMT, int TT, typename TY>
 __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int slice_blocks, float* partial,
                                                                   FastDiv div_full, FastDiv div_last) {
@@ -862,8 +865,12 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
     const int kb0 = static_cast<int>(blockIdx.z) * slice_blocks;
     const int nb = min(nblk - kb0, slice_blocks);  // > 0: the host sizes the slices
     const int xr_stride = t2_row(slice_blocks);
+    const int rows = static_cast<int>(min<int64_t>(16 * TT, a.T - t_base));  // tokens of this chunk
     half_t* xl = reinterpret_cast<half_t*>(lds);
-    uint8_t* tile = lds + t2_acts_bytes<TT>(slice_blocks) + wave * stage_bytes(FMT);
+    uint8_t* tile = lds + t2_acts_bytes(rows, slice_blocks) + wave * stage_bytes(FMT);
+    int xoff[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) xoff[tt] = min(tt * 16 + n, rows - 1) * xr_stride;
 
     const int64_t last = a.N - 1;
     const uint8_t* wrow = a.w + min(row0 + n, last) * a.rb;
@@ -890,7 +897,7 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
     // Eight chunks per thread are requested before any is stored (one memory round trip per batch;
     // chunk indices past the end re-read the last chunk and are not stored).
     constexpr int kBatch = 8, kThreads = 64 * kT2Waves;
-    const int chunks = 16 * TT * nb * 4;
+    const int chunks = rows * nb * 4;
     const FastDiv per_row = nb == slice_blocks ? div_full : div_last;  // chunk -> token: by nb * 4
     for (int c0 = tid; c0 < chunks; c0 += kThreads * kBatch) {
         uint4v v[kBatch];
@@ -898,7 +905,7 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
         for (int u = 0; u < kBatch; u++) {
             const int c = min(c0 + kThreads * u, chunks - 1);
             const int t = static_cast<int>(fast_div(static_cast<uint32_t>(c), per_row)), q = c - t * (nb * 4);
-            const int64_t tok = min(t_base + t, a.T - 1);  // rows past T read the last token, never stored
+            const int64_t tok = t_base + t;  // t < rows
             v[u] = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + tok * a.xs + kb0 * kBlockK + 8 * q);
         }
 #pragma unroll
@@ -926,12 +933,12 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
     for (int tt = 0; tt < TT; tt++) acc[tt] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
     if (nfull > 0) {
         half8 A0[G][TT], A1[G][TT];
-        t2_load_acts<FMT, TT>(A0, xl, xr_stride, 0, n, g);
+        t2_load_acts<FMT, TT>(A0, xl, xoff, 0, g);
         for (int i = 0;; i += 2) {
-            t2_step<FMT, TT>(acc, st0, A0, A1, prow, col16, wrow, soff, xl, xr_stride, g, n, tile, slot,
+            t2_step<FMT, TT>(acc, st0, A0, A1, prow, col16, wrow, soff, xl, xoff, g, n, tile, slot,
                              min(i + 1, lastg) * G, kb0 + min(i + 2, lastg) * G);
             if (i + 1 >= nfull) break;
-            t2_step<FMT, TT>(acc, st1, A1, A0, prow, col16, wrow, soff, xl, xr_stride, g, n, tile, slot,
+            t2_step<FMT, TT>(acc, st1, A1, A0, prow, col16, wrow, soff, xl, xoff, g, n, tile, slot,
                              min(i + 2, lastg) * G, kb0 + min(i + 3, lastg) * G);
             if (i + 2 >= nfull) break;
         }
@@ -940,7 +947,7 @@ __global__ __launch_bounds__(64 * kT2Waves) void mm_tile2_kernel(MmArgs a, int s
         half8 A[TT];
 #pragma unroll
         for (int tt = 0; tt < TT; tt++)
-            A[tt] = *reinterpret_cast<const half8*>(xl + (tt * 16 + n) * xr_stride + b * kBlockK + 8 * g);
+            A[tt] = *reinterpret_cast<const half8*>(xl + xoff[tt] + b * kBlockK + 8 * g);
         const half8 B = decode_b<FMT>(load_b_raw<FMT>(wrow, kb0 + b, g));
         float s = 0.0f;
         if constexpr (FMT != 0)
@@ -2115,13 +2122,14 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                         (fmt == NEKO_FMT_F16 && T > NEKO_TUNE_MM_T2_MIN_F16));
     if (fast && tile2) {
         const int tt = static_cast<int>((T + 15) / 16);  // 1..4: one chunk of 16 tt tokens
+        const int rows = static_cast<int>(T);           // token rows staged (the kernel's `rows`)
         const int64_t tiles = (N + 16 * kT2Waves - 1) / (16 * kT2Waves);
         const int nblk = static_cast<int>(K / kBlockK);
         const size_t stage = static_cast<size_t>(kT2Waves) * stage_bytes(fmt);
         // The largest slice of K whose staged activations fit beside the staging tiles; then more
         // slices (halving) until the grid holds about kT2Fill workgroups per CU, each slice at least 8
         // blocks long.
-        const int cap = static_cast<int>(((kT2Lds - stage) / (32 * tt) - 8) / 32);
+        const int cap = static_cast<int>(((kT2Lds - stage) / (2 * rows) - 8) / 32);
         int slices = (nblk + cap - 1) / cap;
         while (tiles * slices < kT2Fill * ctx->cu_count && nblk / (2 * slices) >= 8) slices *= 2;
         int slice_blocks = (nblk + slices - 1) / slices;
@@ -2132,7 +2140,7 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
         if (slices > 1)
             if (int rc = partial_buffer(ctx, fixed, static_cast<size_t>(slices) * T * N * sizeof(float), &partial, what))
                 return rc;
-        const size_t lds = static_cast<size_t>(16 * tt) * (32 * slice_blocks + 8) * 2 + stage;
+        const size_t lds = t2_acts_bytes(rows, slice_blocks) + stage;
         const dim3 grid(static_cast<uint32_t>(tiles), 1u, static_cast<uint32_t>(slices));
         int rc;
         switch (fmt) {
