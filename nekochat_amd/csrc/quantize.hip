@@ -3,17 +3,21 @@
 //
 // One thread per 32-weight block, all of a block's arithmetic in that thread in the reference's order
 // (the FP4 least-squares sums are sequential float additions, so splitting a block across lanes would
-// change their rounding); FP8 waves load their 64 blocks coalesced and hand them out through LDS. Divisions are IEEE (correctly rounded, hipcc's default), products are not
-// contracted (-ffp-contract=off), nearbyint is v_rndne_f32 and halfBits is one RNE v_cvt_f16_f32
-// (subnormals kept). Consecutive threads take consecutive blocks of a row, so the code stores (16 or
-// 32 bytes per thread) and the f16 scales are contiguous across the wave; the thread of a row's last
-// block zero-fills the row's padding, as the reference's zero-initialised buffer leaves it.
+// change their rounding); a wave loads its 64 blocks coalesced and hands them out through LDS.
+// Divisions are IEEE (correctly rounded, hipcc's default), products are not contracted
+// (-ffp-contract=off) and halfBits is one RNE f32 -> f16 conversion (subnormals kept). The FP4 fits'
+// nearest-E2M1 rounding and the FP8 codes use the hardware's E2M1 / E4M3 conversions, with the
+// corrections that make them equal the reference's arithmetic on every input (below). Consecutive
+// threads take consecutive blocks of a row, so the code stores (16 or 32 bytes per thread) and the
+// f16 scales are contiguous across the wave; the thread of a row's last block zero-fills the row's
+// padding, as the reference's zero-initialised buffer leaves it.
 #include "internal.h"
 
 namespace neko_hip {
 namespace {
 
 constexpr int kBlock = 32;  // quant.h:17 kQuantBlock
+typedef short short2v __attribute__((ext_vector_type(2)));
 
 // halfBits: one RNE conversion of f as computed (f16_rne keeps a preceding multiply out of the
 // conversion, so -0 products stay -0).
@@ -22,14 +26,18 @@ __device__ __forceinline__ float half_value(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(h)));
 }
 
-// quant.cpp:43-49: the f16 pattern of y/256, rounded to nearest even over its 7 low bits, clamped to
-// 0x7E (448; 0x7F would decode as 480).
-__device__ __forceinline__ uint32_t encode_fp8(float y) {
-    const uint32_t h = half_bits(y * (1.0f / 256.0f));
-    const uint32_t mag = h & 0x7FFFu;
-    uint32_t c = (mag + 0x3Fu + ((mag >> 7) & 1u)) >> 7;
-    if (c > 0x7Eu) c = 0x7Eu;
-    return c | ((h >> 8) & 0x80u);
+// quant.cpp:43-49 for four values, packed little-endian: the f16 pattern of y/256, rounded to nearest
+// even over its 7 low bits, clamped to 0x7E (448; 0x7F would decode as 480). Those bits are the E4M3 code of 256 x f16(y/256):
+// the hardware conversion of f16 to E4M3 with scale 1/256 (round to nearest even) gives the same byte
+// for every f16 whose magnitude times 256 stays below 452 (measured over all 65536 patterns on
+// gfx950); past that it returns the NaN code where the reference clamps to 448, so y is clamped to
+// +-448 first (its codes there are 0x7E / 0xFE either way). f16(y/256) is the reference's own
+// rounding, kept as a separate step: the double rounding is part of its result.
+__device__ __forceinline__ uint32_t encode_fp8x4(float y0, float y1, float y2, float y3) {
+    const auto h = [](float y) { return f16_rne(__builtin_amdgcn_fmed3f(y, -448.0f, 448.0f) * (1.0f / 256.0f)); };
+    const short2v lo = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(short2v{0, 0}, half2v{h(y0), h(y1)}, 1.0f / 256.0f, false);
+    const short2v both = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(lo, half2v{h(y2), h(y3)}, 1.0f / 256.0f, true);
+    return __builtin_bit_cast(uint32_t, both);
 }
 
 // quant.cpp:57-61: threshold ladder over |y|; a zero magnitude keeps no sign.
@@ -39,11 +47,18 @@ __device__ __forceinline__ uint32_t encode_fp4(float y) {
     return c == 0 ? 0u : (c | (y < 0.0f ? 8u : 0u));
 }
 
-// quant.cpp:93-97: nearest E2M1 magnitude of a >= 0.
-__device__ __forceinline__ float fp4_round(float a) {
-    if (a < 1.75f) return __builtin_rintf(a * 2.0f) * 0.5f;
-    if (a < 3.5f) return __builtin_rintf(a);
-    return a < 5.0f ? 4.0f : 6.0f;
+// quant.cpp:93-97: nearest E2M1 magnitude of a >= 0, for two values at once. The hardware E2M1
+// conversion (round to nearest even; NaN and values past 6 give 6) returns the reference's
+// threshold ladder's value for every non-negative f32 but 5.0, the one tie the ladder rounds up (to 6)
+// where nearest-even rounds down (to 4): measured over all 2^31 patterns on gfx950. One conversion
+// each way for the pair, and the 5.0 case set explicitly, in place of the ladder's two roundings and
+// three selects per value.
+__device__ __forceinline__ float2v fp4_round2(float a0, float a1) {
+    const uint32_t code = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, a0, a1, 1.0f, 0);
+    float2v r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(code, 1.0f, 0);
+    r.x = a0 == 5.0f ? 6.0f : r.x;
+    r.y = a1 == 5.0f ? 6.0f : r.y;
+    return r;
 }
 
 struct Fit {
@@ -55,12 +70,15 @@ __device__ __forceinline__ Fit fit_fp4(const float (&ax)[kBlock], float s) {
     Fit f{0.0f, 0.0f, 0.0f};
     const float inv = 1.0f / s;
 #pragma unroll
-    for (int i = 0; i < kBlock; i++) {
-        const float r = fp4_round(ax[i] * inv);
-        const float d = ax[i] - r * s;
-        f.err = f.err + d * d;
-        f.xr = f.xr + ax[i] * r;
-        f.rr = f.rr + r * r;
+    for (int i = 0; i < kBlock; i += 2) {
+        const float2v r = fp4_round2(ax[i] * inv, ax[i + 1] * inv);
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float d = ax[i + e] - r[e] * s;
+            f.err = f.err + d * d;
+            f.xr = f.xr + ax[i + e] * r[e];
+            f.rr = f.rr + r[e] * r[e];
+        }
     }
     return f;
 }
@@ -108,26 +126,6 @@ struct QuantArgs {
     FastDiv nb;        // blocks per row
 };
 
-// One block read by its own thread (8 x 16 bytes; used where occupancy matters more than coalescing).
-template <typename TI>
-__device__ __forceinline__ void load_block(const TI* p, float (&x)[kBlock]) {
-    if constexpr (sizeof(TI) == 4) {
-#pragma unroll
-        for (int q = 0; q < kBlock / 4; q++) {
-            const float4v v = load_nt(reinterpret_cast<const float4v*>(p) + q);
-#pragma unroll
-            for (int e = 0; e < 4; e++) x[4 * q + e] = v[e];
-        }
-    } else {
-#pragma unroll
-        for (int q = 0; q < kBlock / 8; q++) {
-            const half8 v = load_nt(reinterpret_cast<const half8*>(p) + q);
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[8 * q + e] = static_cast<float>(v[e]);
-        }
-    }
-}
-
 // A wave's 64 consecutive blocks go through LDS: the lanes load them as consecutive 16-byte chunks
 // (coalesced, whatever the row boundaries), store them with one pad word per 32 (block b starts at
 // word 33 b), and each lane then reads its own block, lanes b and b+1 landing in adjacent banks.
@@ -166,25 +164,22 @@ __device__ __forceinline__ void stage_blocks(const QuantArgs& a, uint32_t wave_b
     for (int i = 0; i < kBlock; i++) x[i] = lds[lane * kStride + i];
 }
 
-// FMT 1: FP8 (quant.cpp:81-90), 2: FP4 (quant.cpp:167-178).
-// FP8 (light arithmetic, bound by the loads) stages its blocks through LDS; FP4 (bound by its scale
-// search's VALU work) reads them directly and keeps the occupancy the LDS would cost.
+// FMT 1: FP8 (quant.cpp:81-90), 2: FP4 (quant.cpp:167-178). Both stage their blocks through LDS:
+// with each lane loading its own block's 128 bytes directly, FP4 ran 13% slower over a 65536 x 2048
+// f32 table despite the occupancy the LDS costs (6 -> 4 waves per SIMD).
 template <int FMT, typename TI>
 __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
-    constexpr bool kStage = FMT == 1;
-    __shared__ float lds[kStage ? 4 : 1][kStage ? kWave * kStride : 1];
+    __shared__ float lds[4][kWave * kStride];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const uint32_t wave_block0 = blockIdx.x * 256u + static_cast<uint32_t>(wave) * kWave;
     if (wave_block0 >= a.items) return;  // wave-uniform
     float x[kBlock];
-    if constexpr (kStage) stage_blocks<TI>(a, wave_block0, lds[wave], lane, x);
+    stage_blocks<TI>(a, wave_block0, lds[wave], lane, x);
     const uint32_t idx = wave_block0 + static_cast<uint32_t>(lane);
     if (idx >= a.items) return;
     const uint32_t r = fast_div(idx, a.nb);
     const uint32_t b = idx - r * a.nb.d;
-    if constexpr (!kStage)
-        load_block(static_cast<const TI*>(a.src) + static_cast<int64_t>(r) * a.src_stride + static_cast<int64_t>(b) * kBlock, x);
     uint8_t* row = a.dst + static_cast<int64_t>(r) * a.row_bytes;
     if constexpr (FMT == 1) {
         const float amax = block_amax(x);
@@ -193,12 +188,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
         const float inv = sv > 0.0f ? 1.0f / sv : 0.0f;
         uint4v codes[2];
 #pragma unroll
-        for (int w = 0; w < 8; w++) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) word |= encode_fp8(x[4 * w + e] * inv) << (8 * e);
-            codes[w / 4][w % 4] = word;
-        }
+        for (int w = 0; w < 8; w++)
+            codes[w / 4][w % 4] = encode_fp8x4(x[4 * w] * inv, x[4 * w + 1] * inv, x[4 * w + 2] * inv, x[4 * w + 3] * inv);
         uint4v* out = reinterpret_cast<uint4v*>(row + static_cast<int64_t>(b) * kBlock);
         out[0] = codes[0];
         out[1] = codes[1];

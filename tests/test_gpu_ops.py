@@ -695,6 +695,56 @@ def test_quantize_gpu_bitexact(dev, fmt, src_dtype):
         assert np.array_equal(host, want)
 
 
+def _quant_edges():
+    """Blocks aimed at the encoders' rounding edges. FP4: blocks whose amax is 6, so the first fit's
+    scale is exactly 1 and it rounds the raw magnitudes -- every tie of the E2M1 ladder (0.25 ... 5.0,
+    5.0 the one the reference rounds up where nearest-even rounds down) and its f32 neighbours, alone
+    and repeated so that the refit's scale depends on them. FP8: blocks whose f16 scale is a subnormal
+    rounded well below amax/448, so the scaled weights reach past 448 (the codes clamp to 0x7E)."""
+    f = np.float32
+    ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], f)
+    near = np.concatenate([ties, np.nextafter(ties, f(0)), np.nextafter(ties, f(10))])
+    rows = []
+    rng = np.random.default_rng(17)
+    for k in range(30):
+        blk = np.resize(near[rng.permutation(near.size)], 32).astype(f)
+        blk[k % 32] = 6.0
+        if k % 3 == 1:
+            blk[:24] = 5.0
+            blk[24] = 6.0
+        if k % 3 == 2:
+            blk[1::2] *= -1
+        rows.append(blk)
+    for m in (1.1, 1.4, 1.49, 2.3, 2.6, 3.3, 5.5, 9.7, 17.3, 33.1):
+        amax = f(448.0 * m * 2.0 ** -24)
+        blk = (rng.uniform(-1, 1, 32) * amax).astype(f)
+        blk[3] = amax
+        blk[7] = -amax
+        blk[11] = f(0.97) * amax
+        rows.append(blk)
+    return np.concatenate(rows).reshape(-1, 256)  # 40 blocks: 5 rows of 8
+
+
+@pytest.mark.parametrize("fmt", [ops.FMT_FP8, ops.FMT_FP4])
+def test_quantize_gpu_rounding_edges(dev, fmt):
+    """The hardware E2M1 / E4M3 conversions, with their corrections, give the oracle's bytes at the
+    encoders' rounding edges (the oracle is the reference's own arithmetic, pinned bit-exact to the
+    compiled quantizeMatrix)."""
+    _case(f"quantize rounding edges fmt={fmt}")
+    x = _quant_edges()
+    got, used = ops.quantize(torch.from_numpy(x).to(dev), fmt)
+    assert used == fmt
+    want = O.quantize_rows(fmt, x)
+    assert np.array_equal(got.cpu().numpy(), want)
+    # the edges are reached: FP4's first fits run at scale 1 (amax 6), FP8 scaled weights pass 448
+    if fmt == ops.FMT_FP4:
+        assert (np.abs(x.reshape(-1, 32)[:30]).max(axis=1) == 6.0).all()
+    else:
+        s = want[:, 256:].view(np.float16).astype(np.float32)
+        y = np.abs(x.reshape(-1, 8, 32)) / np.where(s > 0, s, np.inf)[:, :, None]
+        assert (y.max(axis=2) > 452).sum() >= 5
+
+
 def test_quantize_gpu_shapes(dev):
     _case("quantize: cols % 32 != 0 stores F16, strided source, then the gather reads the table back")
     x = _quant_source(40, 100, 91)
