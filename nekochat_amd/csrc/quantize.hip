@@ -40,11 +40,27 @@ __device__ __forceinline__ uint32_t encode_fp8x4(float y0, float y1, float y2, f
     return __builtin_bit_cast(uint32_t, both);
 }
 
-// quant.cpp:57-61: threshold ladder over |y|; a zero magnitude keeps no sign.
-__device__ __forceinline__ uint32_t encode_fp4(float y) {
+// quant.cpp:57-61 encodes |y| by a threshold ladder: the nearest E2M1 magnitude with every tie
+// (0.25, 0.75, ..., 5.0) rounded down, the sign kept only on a nonzero magnitude, and NaN as 0. The
+// hardware conversion (round to nearest even) differs only at the ties it rounds up -- 0.75, 1.75,
+// 3.5 -- and in the sign of a zero magnitude, so those inputs are replaced first (a tie by a value
+// below it, |y| <= 0.25 or NaN by +0); with that, code = ladder for every f32 pattern (measured over
+// all 2^32 on gfx950). Returns the input to hand the conversion.
+__device__ __forceinline__ float fp4_encode_input(float y) {
     const float a = fabsf(y);
-    const uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
-    return c == 0 ? 0u : (c | (y < 0.0f ? 8u : 0u));
+    const bool tie_up = a == 0.75f || a == 1.75f || a == 3.5f;
+    return !(a > 0.25f) ? 0.0f : (tie_up ? y * 0.9f : y);
+}
+
+// Word w of a block's codes: byte e holds code(x[4w + e] * inv) in its low nibble and
+// code(x[16 + 4w + e] * inv) in its high nibble (quant.cpp:167-178).
+__device__ __forceinline__ uint32_t encode_fp4_word(const float (&x)[kBlock], int w, float inv) {
+    const auto in = [&](int j) { return fp4_encode_input(x[j] * inv); };
+    const int j = 4 * w;
+    uint32_t word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, in(j), in(j + 16), 1.0f, 0);
+    word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, in(j + 1), in(j + 17), 1.0f, 1);
+    word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, in(j + 2), in(j + 18), 1.0f, 2);
+    return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, in(j + 3), in(j + 19), 1.0f, 3);
 }
 
 // quant.cpp:93-97: nearest E2M1 magnitude of a >= 0, for two values at once. The hardware E2M1
@@ -199,15 +215,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
         const float inv = s ? 1.0f / half_value(s) : 0.0f;
         uint4v codes;
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int j = 4 * w + e;
-                word |= (encode_fp4(x[j] * inv) | (encode_fp4(x[16 + j] * inv) << 4)) << (8 * e);
-            }
-            codes[w] = word;
-        }
+        for (int w = 0; w < 4; w++) codes[w] = encode_fp4_word(x, w, inv);
         *reinterpret_cast<uint4v*>(row + static_cast<int64_t>(b) * (kBlock / 2)) = codes;
         reinterpret_cast<uint16_t*>(row + a.cols / 2)[b] = static_cast<uint16_t>(s);
     }
