@@ -696,11 +696,12 @@ def test_quantize_gpu_bitexact(dev, fmt, src_dtype):
 
 
 def _quant_edges():
-    """Blocks aimed at the encoders' rounding edges. FP4: blocks whose amax is 6, so the first fit's
-    scale is exactly 1 and it rounds the raw magnitudes -- every tie of the E2M1 ladder (0.25 ... 5.0,
-    5.0 the one the reference rounds up where nearest-even rounds down) and its f32 neighbours, alone
-    and repeated so that the refit's scale depends on them. FP8: blocks whose f16 scale is a subnormal
-    rounded well below amax/448, so the scaled weights reach past 448 (the codes clamp to 0x7E)."""
+    """Blocks aimed at the encoders' rounding edges. FP4 fits: blocks whose amax is 6, so the first
+    fit's scale is exactly 1 and it rounds the raw magnitudes -- every tie of the E2M1 ladder (0.25 ...
+    5.0, 5.0 the one the reference rounds up where nearest-even rounds down) and its f32 neighbours,
+    alone and repeated so that the refit's scale depends on them. FP8: blocks whose f16 scale is a
+    subnormal rounded well below amax/448, so the scaled weights reach past 448 (the codes clamp to
+    0x7E). FP4 codes: blocks whose final scale is 1 with exact ties in them (below)."""
     f = np.float32
     ties = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], f)
     near = np.concatenate([ties, np.nextafter(ties, f(0)), np.nextafter(ties, f(10))])
@@ -722,7 +723,16 @@ def _quant_edges():
         blk[7] = -amax
         blk[11] = f(0.97) * amax
         rows.append(blk)
-    return np.concatenate(rows).reshape(-1, 256)  # 40 blocks: 5 rows of 8
+    # FP4 encoder ties: 0.75 / 1.75 / 3.5 (which nearest-even rounds up and the reference down), each
+    # balanced by ties the fits round down (1.25, 2.5), among exact grid values and small magnitudes of
+    # either sign (codes with no sign): the least-squares refit returns exactly 1, so the encoder sees
+    # the ties exactly.
+    for k in range(8):
+        tie = np.array([0.75, 1.25, 1.75, 1.25, 1.25, 3.5, 2.5, 2.5], f) * rng.choice([-1, 1], 8).astype(f)
+        small = np.array([-0.1, -0.25, 0.25, -0.0, 0.2, -0.24], f)
+        grid = rng.choice(np.array([0.5, 1, 1.5, 2, 3, 4, 6, -0.5, -1, -2, -6], f), 17).astype(f)
+        rows.append(np.concatenate([[f(6.0)], tie, small, grid]).astype(f)[rng.permutation(32)])
+    return np.concatenate(rows).reshape(-1, 256)  # 48 blocks: 6 rows of 8
 
 
 @pytest.mark.parametrize("fmt", [ops.FMT_FP8, ops.FMT_FP4])
@@ -739,6 +749,7 @@ def test_quantize_gpu_rounding_edges(dev, fmt):
     # the edges are reached: FP4's first fits run at scale 1 (amax 6), FP8 scaled weights pass 448
     if fmt == ops.FMT_FP4:
         assert (np.abs(x.reshape(-1, 32)[:30]).max(axis=1) == 6.0).all()
+        assert (want[:, 128:].view(np.uint16).reshape(-1)[40:] == 0x3C00).all()  # the tie blocks: scale 1
     else:
         s = want[:, 256:].view(np.float16).astype(np.float32)
         y = np.abs(x.reshape(-1, 8, 32)) / np.where(s > 0, s, np.inf)[:, :, None]
