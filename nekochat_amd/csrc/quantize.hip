@@ -11,6 +11,8 @@
 // threads take consecutive blocks of a row, so the code stores (16 or 32 bytes per thread) and the
 // f16 scales are contiguous across the wave; the thread of a row's last block zero-fills the row's
 // padding, as the reference's zero-initialised buffer leaves it.
+#include <algorithm>
+
 #include "internal.h"
 #include "quant_codes.h"
 
@@ -102,37 +104,57 @@ struct QuantArgs {
     FastDiv nb;        // blocks per row
 };
 
-// A wave's 64 consecutive blocks go through LDS: the lanes load them as consecutive 16-byte chunks
-// (coalesced, whatever the row boundaries), store them with one pad word per 32 (block b starts at
-// word 33 b), and each lane then reads its own block, lanes b and b+1 landing in adjacent banks.
+// A wave takes spans of 64 consecutive blocks. They go through LDS: the lanes load a span as
+// consecutive 16-byte chunks (coalesced, whatever the row boundaries), store them with one pad word
+// per 32 (block b starts at word 33 b), and each lane then reads its own block, lanes b and b+1
+// landing in adjacent banks.
 constexpr int kStride = kBlock + 1;
 
 template <typename TI>
-__device__ __forceinline__ void stage_blocks(const QuantArgs& a, uint32_t wave_block0, float* lds, int lane,
-                                             float (&x)[kBlock]) {
-    constexpr int EPC = 16 / sizeof(TI);     // elements per 16-byte chunk
-    constexpr int CPB = kBlock / EPC;        // chunks per block
+struct Span {
+    static constexpr int EPC = 16 / sizeof(TI);  // elements per 16-byte chunk
+    static constexpr int CPB = kBlock / EPC;     // chunks per block
+    uint4v c[CPB];                               // this lane's chunks m = lane + 64 k
+};
+
+// Requests the span of blocks [block0, block0 + 64). Chunks of blocks past the last re-read the last
+// block (never encoded): the loads are branch-free, so the compiler's waits for them stay partial.
+template <typename TI>
+__device__ __forceinline__ void load_span(const QuantArgs& a, uint32_t block0, int lane, Span<TI>& sp) {
 #pragma unroll
-    for (int k = 0; k < CPB; k++) {
-        const uint32_t m = static_cast<uint32_t>(lane) + kWave * k;  // chunk index within the wave's span
-        const uint32_t blk = wave_block0 + m / CPB;
-        if (blk >= a.items) continue;
+    for (int k = 0; k < Span<TI>::CPB; k++) {
+        const uint32_t m = static_cast<uint32_t>(lane) + kWave * k;
+        const uint32_t blk = min(block0 + m / Span<TI>::CPB, a.items - 1);
         const uint32_t r = fast_div(blk, a.nb);
-        const int64_t col = static_cast<int64_t>(blk - r * a.nb.d) * kBlock + (m % CPB) * EPC;
+        const int64_t col = static_cast<int64_t>(blk - r * a.nb.d) * kBlock + (m % Span<TI>::CPB) * Span<TI>::EPC;
         const TI* p = static_cast<const TI*>(a.src) + static_cast<int64_t>(r) * a.src_stride + col;
-        float* d = lds + (m / CPB) * kStride + (m % CPB) * EPC;
+        if constexpr (sizeof(TI) == 4) sp.c[k] = __builtin_bit_cast(uint4v, load_nt(reinterpret_cast<const float4v*>(p)));
+        else sp.c[k] = __builtin_bit_cast(uint4v, load_nt(reinterpret_cast<const half8*>(p)));
+    }
+}
+
+// Hands a loaded span out: each lane gets its own block's 32 values in x.
+template <typename TI>
+__device__ __forceinline__ void unstage_span(const Span<TI>& sp, float* lds, int lane, float (&x)[kBlock]) {
+    // Only this wave's lanes use these words and the wave runs in lockstep, so wave-local fences (not
+    // workgroup barriers) order the previous span's reads, these stores and the reads below.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int k = 0; k < Span<TI>::CPB; k++) {
+        const uint32_t m = static_cast<uint32_t>(lane) + kWave * k;
+        float* d = lds + (m / Span<TI>::CPB) * kStride + (m % Span<TI>::CPB) * Span<TI>::EPC;
         if constexpr (sizeof(TI) == 4) {
-            const float4v v = load_nt(reinterpret_cast<const float4v*>(p));
+            const float4v v = __builtin_bit_cast(float4v, sp.c[k]);
 #pragma unroll
             for (int e = 0; e < 4; e++) d[e] = v[e];
         } else {
-            const half8 v = load_nt(reinterpret_cast<const half8*>(p));
+            const half8 v = __builtin_bit_cast(half8, sp.c[k]);
 #pragma unroll
             for (int e = 0; e < 8; e++) d[e] = static_cast<float>(v[e]);
         }
     }
-    // Only this wave's lanes wrote these words; the wave runs in lockstep, so a wave-local fence
-    // (not a workgroup barrier) orders the stores before the reads.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -140,20 +162,10 @@ __device__ __forceinline__ void stage_blocks(const QuantArgs& a, uint32_t wave_b
     for (int i = 0; i < kBlock; i++) x[i] = lds[lane * kStride + i];
 }
 
-// FMT 1: FP8 (quant.cpp:81-90), 2: FP4 (quant.cpp:167-178). Both stage their blocks through LDS:
-// with each lane loading its own block's 128 bytes directly, FP4 ran 13% slower over a 65536 x 2048
-// f32 table despite the occupancy the LDS costs (6 -> 4 waves per SIMD).
-template <int FMT, typename TI>
-__global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
-    __shared__ float lds[4][kWave * kStride];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const uint32_t wave_block0 = blockIdx.x * 256u + static_cast<uint32_t>(wave) * kWave;
-    if (wave_block0 >= a.items) return;  // wave-uniform
-    float x[kBlock];
-    stage_blocks<TI>(a, wave_block0, lds[wave], lane, x);
-    const uint32_t idx = wave_block0 + static_cast<uint32_t>(lane);
-    if (idx >= a.items) return;
+// Block idx's codes and scale, and the row's padding from the thread of its last block.
+// FMT 1: FP8 (quant.cpp:81-90), 2: FP4 (quant.cpp:167-178).
+template <int FMT>
+__device__ __forceinline__ void encode_block(const QuantArgs& a, uint32_t idx, const float (&x)[kBlock]) {
     const uint32_t r = fast_div(idx, a.nb);
     const uint32_t b = idx - r * a.nb.d;
     uint8_t* row = a.dst + static_cast<int64_t>(r) * a.row_bytes;
@@ -181,6 +193,32 @@ __global__ __launch_bounds__(256) void quantize_kernel(QuantArgs a) {
     }
     if (b == a.nb.d - 1)
         for (int64_t i = a.pad_from; i < a.row_bytes; i++) row[i] = 0;
+}
+
+// Persistent waves, each over spans w, w + (waves in the grid), ...: the next span's loads are in
+// flight while this one is encoded. Both formats stage through LDS: with each lane loading its own
+// block's 128 bytes directly, FP4 had fetched 24% extra and ran 13% slower, despite the occupancy the
+// LDS costs (4 waves per SIMD).
+template <int FMT, typename TI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void quantize_kernel(QuantArgs a, uint32_t spans) {
+    __shared__ float lds[4][kWave * kStride];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const uint32_t step = gridDim.x * 4u;
+    uint32_t sp = blockIdx.x * 4u + static_cast<uint32_t>(wave);
+    if (sp >= spans) return;  // wave-uniform
+    Span<TI> raw;
+    load_span<TI>(a, sp * kWave, lane, raw);
+    for (;;) {  // wave-uniform trip count
+        float x[kBlock];
+        unstage_span<TI>(raw, lds[wave], lane, x);
+        const uint32_t next = sp + step;
+        load_span<TI>(a, min(next, spans - 1) * kWave, lane, raw);  // past the end: re-read, unused
+        const uint32_t idx = sp * kWave + static_cast<uint32_t>(lane);
+        if (idx < a.items) encode_block<FMT>(a, idx, x);
+        if (next >= spans) break;
+        sp = next;
+    }
 }
 
 // F16 rows (quant.cpp:180-186 rowToHalf): 8 elements per thread, flattened (row, chunk) space.
@@ -250,9 +288,14 @@ int launch_typed(neko_hip_ctx* ctx, const char* what, int fmt, int64_t rows, int
         QuantArgs a{static_cast<const TI*>(src) + r0 * src_stride, src_stride, dst + r0 * row_bytes, row_bytes, cols,
                     fmt == NEKO_FMT_FP8 ? cols + 2 * nb : cols / 2 + 2 * nb, static_cast<uint32_t>(n * nb),
                     make_fast_div(static_cast<uint32_t>(nb))};
-        const uint32_t blocks = (a.items + 255u) / 256u;
-        if (fmt == NEKO_FMT_FP8) hipLaunchKernelGGL((quantize_kernel<1, TI>), dim3(blocks), dim3(256), 0, ctx->stream, a);
-        else hipLaunchKernelGGL((quantize_kernel<2, TI>), dim3(blocks), dim3(256), 0, ctx->stream, a);
+        if (a.items == 0) continue;
+        // One workgroup per LDS slot of the chip (four fit a CU), each wave looping over spans.
+        const uint32_t spans = (a.items + kWave - 1) / kWave;
+        const uint32_t blocks = std::min<uint32_t>((spans + 3u) / 4u, static_cast<uint32_t>(4 * std::max(1, ctx->cu_count)));
+        if (fmt == NEKO_FMT_FP8)
+            hipLaunchKernelGGL((quantize_kernel<1, TI>), dim3(blocks), dim3(256), 0, ctx->stream, a, spans);
+        else
+            hipLaunchKernelGGL((quantize_kernel<2, TI>), dim3(blocks), dim3(256), 0, ctx->stream, a, spans);
         if (int rc = after_launch(ctx, what)) return rc;
     }
     return NEKO_OK;
