@@ -2,7 +2,7 @@
  * CPU oracle for the fused layer ops: a plain-C restatement of the reference's own arithmetic.
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product (nekochat_amd/, include/) links, loads or calls
- * this code. It is used by tests/ (as the checker), by __graft_entry__.smoke() (as the checker) and
+ * this code. It is used by tests/ and by __graft_entry__.smoke() (for the expected results) and
  * by bench.py's cpu_baseline leg (as the timed CPU path). The GPU path never routes through it.
  *
  * Every function cites the reference file:line it restates (paths relative to the reference's

@@ -2,7 +2,7 @@
 reference CPU ops (oracle/_ref/libneko_ref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
-as the checker or the timed CPU baseline -- never by the product package.
+as the expected results or the timed CPU baseline -- never by the product package.
 
 Arrays: fp16 data travels as numpy uint16 bit patterns (so NaN payloads and -0 survive), f32 as float32.
 Every wrapper allocates its outputs and returns them; inputs are never modified unless the name says
