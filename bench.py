@@ -956,8 +956,8 @@ def sources_sha256(paths=TRAFFIC_SOURCES) -> str:
 
 def traffic_from_profiles():
     """(bytes, note): the dominant kernel's per-launch HBM bytes from rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (profiles/), when those counters were taken on the kernel sources this build compiles (the
-    profile records their sha256); otherwise (None, why)."""
+    (profiles/), when those counters were taken on the kernel sources as they are now (the profile
+    records their sha256); otherwise (None, why)."""
     path = os.path.join(ROOT, "profiles", "swiglu_qwen3_4b_prefill_traffic.json")
     if not os.path.exists(path):
         return None, "no counter profile recorded"
@@ -968,13 +968,13 @@ def traffic_from_profiles():
         return None, (f"counter profile taken on other {rec.get('kernel', 'kernel')} sources (sha256 "
                       f"{str(rec.get('sources_sha256'))[:12]} vs {have[:12]} now): not quoted")
     return rec["traffic_bytes_per_launch"], (f"rocprofv3 FETCH_SIZE + WRITE_SIZE of {rec['kernel']}, calibrated on "
-                                             f"a device copy; sources sha256 {have[:12]} = this build's")
+                                             f"a device copy; sources sha256 {have[:12]} = the current sources'")
 
 
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU; the ops are per-row and shard by tokens with no "
+        print("bench.py: measures one GPU; the ops are per-row and shard by tokens with no "
               "communication, so N > 1 is not run here.", file=sys.stderr)
         sys.exit(2)
     if args.all:

@@ -41,7 +41,7 @@ extern "C" {
 #define NEKO_ERR_INVALID (-1)     /* bad argument: null pointer, size, stride, alignment or format */
 #define NEKO_ERR_HIP (-2)         /* a HIP runtime call or kernel launch failed */
 #define NEKO_ERR_NO_DEVICE (-3)   /* no usable gfx950 device */
-#define NEKO_ERR_UNSUPPORTED (-4) /* valid request this build does not implement */
+#define NEKO_ERR_UNSUPPORTED (-4) /* valid request this library does not implement */
 
 typedef enum { NEKO_DT_F32 = 0, NEKO_DT_F16 = 1 } neko_dtype;
 

@@ -127,7 +127,7 @@ int neko_hip_create(int device, neko_hip_ctx** out) {
     if (hipGetDeviceProperties(&prop, device) != hipSuccess)
         return fail(nullptr, NEKO_ERR_HIP, "neko_hip_create: hipGetDeviceProperties failed");
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
-        return fail(nullptr, NEKO_ERR_NO_DEVICE, "neko_hip_create: device %d is %s; this build targets gfx950", device,
+        return fail(nullptr, NEKO_ERR_NO_DEVICE, "neko_hip_create: device %d is %s; this library is built for gfx950", device,
                     prop.gcnArchName);
     if (hipSetDevice(device) != hipSuccess) return fail(nullptr, NEKO_ERR_HIP, "neko_hip_create: hipSetDevice failed");
     auto* ctx = new neko_hip_ctx;

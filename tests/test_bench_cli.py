@@ -1,5 +1,5 @@
 """bench.py's command line without a GPU: it parses, lists its workloads, and refuses more than one GPU
-before touching a device (the driver's contract: N > 1 exits with a message)."""
+before touching a device (N > 1 exits with a message)."""
 import os
 import subprocess
 import sys
