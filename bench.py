@@ -53,7 +53,7 @@ def parse():
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
-                        "qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul, "
+                        "qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul, qwen3_4b_decode24_matmul, "
                         "qwen3_4b_prefill_matmul, stream_floor)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
@@ -451,7 +451,7 @@ def add_cpu_jobs(leg, want):
         leg.add("granite_4.0h_norms", "gated_rmsnorm", gated, c.T / n, s + ": y *= silu(z), then rmsNorm per group")
         leg.add("granite_4.0h_norms", "swiglu", swiglu_job(n, c.I, 56), c.T / n, s)
 
-    def matmul_jobs(label, c):  # qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul
+    def matmul_jobs(label, c):  # qwen3_4b_decode_matmul and its 4-, 16- and 24-sequence forms
         n = 256
 
         def mm(fmt, N, K):
@@ -502,6 +502,7 @@ def add_cpu_jobs(leg, want):
             ("qwen3_4b_decode_matmul", lambda: matmul_jobs("qwen3_4b_decode_matmul", wl.QWEN3_DECODE_MATMUL)),
             ("qwen3_4b_decode4_matmul", lambda: matmul_jobs("qwen3_4b_decode4_matmul", wl.QWEN3_DECODE4_MATMUL)),
             ("qwen3_4b_decode16_matmul", lambda: matmul_jobs("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL)),
+            ("qwen3_4b_decode24_matmul", lambda: matmul_jobs("qwen3_4b_decode24_matmul", wl.QWEN3_DECODE24_MATMUL)),
             ("qwen3_4b_prefill_matmul", prefill_matmul_jobs),
     ):
         if want(label):
@@ -522,7 +523,7 @@ def all_configs(args):
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
-              "qwen3_4b_decode16_matmul", "qwen3_4b_prefill_matmul", "stream_floor")
+              "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_prefill_matmul", "stream_floor")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -678,11 +679,12 @@ def all_configs(args):
 
     # Qwen3-4B decode step (T = 1): the four weight matmuls in each weight format, f16 activations,
     # f32 outputs; bytes = the weight rows once + activations + outputs.
-    # Qwen3-4B decode steps of 1, 4 and 16 sequences: the layer's four weight matmuls, weight-bandwidth
-    # bound.
+    # Qwen3-4B decode steps of 1, 4, 16 and 24 sequences: the layer's four weight matmuls,
+    # weight-bandwidth bound.
     for label8, c8 in (("qwen3_4b_decode_matmul", wl.QWEN3_DECODE_MATMUL),
                        ("qwen3_4b_decode4_matmul", wl.QWEN3_DECODE4_MATMUL),
-                       ("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL)):
+                       ("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL),
+                       ("qwen3_4b_decode24_matmul", wl.QWEN3_DECODE24_MATMUL)):
         if not want(label8):
             continue
         calls8, bytes8 = {}, {}

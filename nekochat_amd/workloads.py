@@ -199,6 +199,7 @@ GRANITE_NORMS = GraniteNorms()
 QWEN3_DECODE_MATMUL = Qwen3DecodeMatmul()
 QWEN3_DECODE4_MATMUL = Qwen3DecodeMatmul(T=4)  # one decode step of 4 sequences
 QWEN3_DECODE16_MATMUL = Qwen3DecodeMatmul(T=16)  # one decode step of 16 sequences
+QWEN3_DECODE24_MATMUL = Qwen3DecodeMatmul(T=24)  # one decode step of 24 sequences
 QWEN3_PREFILL_MATMUL = Qwen3PrefillMatmul()
 
 
