@@ -200,7 +200,9 @@ int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t col
  *          shaders' nOffset) are a pointer offset into y.
  * The dot products are summed in f32 (f16 activations and weight codes exactly, each 32-block scaled
  * by its f16 scale) in a different order from the reference's sequential loop: results agree to f32
- * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows.
+ * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows (the
+ * MFMA kernels); f32 activations with aligned rows take a VALU kernel at any T (near the weight-read
+ * time at one token, about 3x the f16 time at 4-16 tokens), other shapes a generic kernel.
  * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown) by the
  * first call that needs more; outgrown buffers are kept too (graphs captured earlier still point at
  * them), all until neko_hip_destroy. A call that would grow it while the context's stream is under

@@ -981,14 +981,14 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // Two weights as f16 (exact values / 2^8 for FP8, the values for FP4) paired with the activation
-// pair at the same positions of the staged x block; dot of one 32-wide block against token t.
-template <int FMT>
-__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const half_t* xb) {
-    const uint4v* xv = reinterpret_cast<const uint4v*>(xb);
+// pair at the same positions of the staged x block; dot of one 32-wide block against token t. f16
+// activations: one fdot2 per pair; f32 activations (the reference's own type): one fma per weight,
+// the f16 weight widened exactly.
+template <int FMT, typename TX>
+__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const TX* xb) {
     float d = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {  // 4 x 8 activations
-        const uint4v xc = xv[c];
         uint32_t wp[4];
         if constexpr (FMT == 0) {
 #pragma unroll
@@ -1008,10 +1008,22 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
             wp[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2));
             wp[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3));
         }
+        if constexpr (sizeof(TX) == 2) {
+            const uint4v xc = reinterpret_cast<const uint4v*>(xb)[c];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t xw = xc[i];
-            d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wp[i]), __builtin_bit_cast(half2v, xw), d, false);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t xw = xc[i];
+                d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wp[i]), __builtin_bit_cast(half2v, xw), d, false);
+            }
+        } else {
+            const float4v x0 = reinterpret_cast<const float4v*>(xb)[2 * c], x1 = reinterpret_cast<const float4v*>(xb)[2 * c + 1];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const half2v w2 = __builtin_bit_cast(half2v, wp[i]);
+                const float xa = i < 2 ? x0[2 * i] : x1[2 * i - 4], xb2 = i < 2 ? x0[2 * i + 1] : x1[2 * i - 3];
+                d = __builtin_fmaf(xa, static_cast<float>(w2[0]), d);
+                d = __builtin_fmaf(xb2, static_cast<float>(w2[1]), d);
+            }
         }
     }
     return d;
@@ -1028,6 +1040,10 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
 constexpr int64_t kGemvMaxT = NEKO_TUNE_MM_GEMV_MAX_T;
 static_assert(kGemvMaxT >= 1 && kGemvMaxT <= 4, "the GEMV holds 1, 2 or 4 tokens per pass");
 constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
+// f32 activations (the reference's own type, as its ComputeBackend passes them) take the GEMV at any
+// T its grid holds: the MFMA kernels read f16 activations, and the GEMV's NT-token passes beat the
+// generic kernel's per-element loads at every T measured (4-5x at 1 token, ~3x at 4-16).
+constexpr int64_t kGemv32MaxT = 65535;
 constexpr int kGemvRows = 4;    // weight rows per wave: 16 lanes each
 constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw slices of K
 #ifndef NEKO_TUNE_MM_GEMV_BATCH
@@ -1036,14 +1052,15 @@ constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw
 constexpr int kGemvBatch = NEKO_TUNE_MM_GEMV_BATCH;  // 32-wide blocks per lane whose weights are requested together
 
 // Grid: x = workgroups of 4 * 8 / kw weight rows, y = chunks of NT tokens. Wave w works on row
-// group w / kw and K slice w % kw (a.blocks_per_wave blocks). Dynamic LDS: the chunk's activations as f16 [NT][K] (FP4: each 32-block
+// group w / kw and K slice w % kw (a.blocks_per_wave blocks). Dynamic LDS: the chunk's activations as TX [NT][K] (FP4: each 32-block
 // stored as (x_j, x_16+j) pairs), then 8 * 4 * NT partial sums.
-template <int FMT, int NT, typename TY>
+template <int FMT, int NT, typename TY, typename TX>
 __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int kw) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int NW = FMT == 0 ? 4 : FMT == 1 ? 2 : 1;  // 16-byte weight loads per block
     constexpr int U = kGemvBatch;
-    half_t* xs = reinterpret_cast<half_t*>(lds);
+    constexpr int EPC = 16 / static_cast<int>(sizeof(TX));  // activations per 16-byte piece
+    TX* xs = reinterpret_cast<TX*>(lds);
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int rg = wave / kw, ks = wave - rg * kw;  // row group, K slice
@@ -1086,23 +1103,25 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
         if (j0 == 0) {
             // Stage x rows t0 .. t0 + NT - 1 (rows past T are zero) in 16-byte pieces, while the
             // first weights are in flight.
-            const int kc = K / 8;
+            const int kc = K / EPC;
             for (int i = static_cast<int>(threadIdx.x); i < NT * kc; i += static_cast<int>(blockDim.x)) {
                 const int t = i / kc, c = i - t * kc;
                 uint4v v = {0u, 0u, 0u, 0u};
-                if (t < nt) v = *reinterpret_cast<const uint4v*>(static_cast<const half_t*>(a.x) + (t0 + t) * a.xs + 8 * c);
-                half_t* dst = xs + static_cast<int64_t>(t) * K;
+                if (t < nt) v = *reinterpret_cast<const uint4v*>(static_cast<const TX*>(a.x) + (t0 + t) * a.xs + EPC * c);
+                TX* dst = xs + static_cast<int64_t>(t) * K;
                 if constexpr (FMT == 2) {
-                    // Piece c of a block holds k = 8 (c & 3) .. + 7: to 2 k (k < 16) or 2 (k - 16) + 1.
-                    const int kb = 8 * (c & 3), base = (c >> 2) * 32;
-                    const half8 h = __builtin_bit_cast(half8, v);
+                    // Piece c holds k = kb .. kb + EPC - 1 of its block: to 2 k (k < 16) or 2 (k - 16) + 1.
+                    const int kb = (EPC * c) % kBlockK, base = (EPC * c) / kBlockK * kBlockK;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
+                    for (int e = 0; e < EPC; e++) {
                         const int k = kb + e;
-                        dst[base + (k < 16 ? 2 * k : 2 * (k - 16) + 1)] = h[e];
+                        TX val;
+                        if constexpr (sizeof(TX) == 2) val = __builtin_bit_cast(half8, v)[e];
+                        else val = __builtin_bit_cast(float4v, v)[e];
+                        dst[base + (k < 16 ? 2 * k : 2 * (k - 16) + 1)] = val;
                     }
                 } else {
-                    *reinterpret_cast<uint4v*>(dst + 8 * c) = v;
+                    *reinterpret_cast<uint4v*>(dst + EPC * c) = v;
                 }
             }
             __syncthreads();
@@ -1112,7 +1131,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
             if (j0 + u >= steps) break;  // wave-uniform
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                const float d = block_dot<FMT>(q[u], xs + static_cast<int64_t>(t) * K + bl[u] * kBlockK);
+                const float d = block_dot<FMT, TX>(q[u], xs + static_cast<int64_t>(t) * K + bl[u] * kBlockK);
                 const float v = FMT == 0 ? d : d * sc[u];
                 acc[t] += valid[u] ? v : 0.0f;
             }
@@ -1122,7 +1141,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
     for (int t = 0; t < NT; t++) acc[t] = row16_sum(acc[t]);
 
     if (kw > 1) {
-        float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(NT) * K * sizeof(half_t));
+        float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(NT) * K * sizeof(TX));
         if (sl == 0) {
 #pragma unroll
             for (int t = 0; t < NT; t++) red[(wave * kGemvRows + r) * NT + t] = acc[t];
@@ -1144,8 +1163,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
     epilogue<TY>(a, t0 + sl, row, v);
 }
 
-__host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt) {
-    return static_cast<size_t>(nt) * K * 2 + static_cast<size_t>(kGemvWaves) * kGemvRows * nt * 4;
+__host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt, int x_bytes = 2) {
+    return static_cast<size_t>(nt) * K * x_bytes + static_cast<size_t>(kGemvWaves) * kGemvRows * nt * 4;
 }
 
 // ---------------------------------------------------------------- prefill path: MFMA GEMM
@@ -1876,25 +1895,32 @@ __global__ __launch_bounds__(64) void mm_generic_kernel(MmArgs a) {
 
 // ---------------------------------------------------------------- launch
 
-template <int FMT, int NT>
+template <int FMT, int NT, typename TX>
 int launch_gemv(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int kw) {
-    const size_t lds = gemv_lds_bytes(a.K, NT);
+    const size_t lds = gemv_lds_bytes(a.K, NT, static_cast<int>(sizeof(TX)));
     if (y_dtype == NEKO_DT_F16)
-        hipLaunchKernelGGL((mm_gemv_kernel<FMT, NT, half_t>), grid, dim3(64 * kGemvWaves), lds, ctx->stream, a, kw);
+        hipLaunchKernelGGL((mm_gemv_kernel<FMT, NT, half_t, TX>), grid, dim3(64 * kGemvWaves), lds, ctx->stream, a, kw);
     else
-        hipLaunchKernelGGL((mm_gemv_kernel<FMT, NT, float>), grid, dim3(64 * kGemvWaves), lds, ctx->stream, a, kw);
+        hipLaunchKernelGGL((mm_gemv_kernel<FMT, NT, float, TX>), grid, dim3(64 * kGemvWaves), lds, ctx->stream, a, kw);
     return after_launch(ctx, "neko_hip_matmul");
 }
 
 template <int FMT>
-int launch_gemv_nt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int kw, int nt) {
+int launch_gemv_nt(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, dim3 grid, int kw, int nt, bool x_f32) {
+    if (x_f32) {  // f32 activations: 1, 2 or 4 tokens per pass
+        switch (nt) {
+            case 1: return launch_gemv<FMT, 1, float>(ctx, a, y_dtype, grid, kw);
+            case 2: return launch_gemv<FMT, 2, float>(ctx, a, y_dtype, grid, kw);
+            default: return launch_gemv<FMT, 4, float>(ctx, a, y_dtype, grid, kw);
+        }
+    }
     switch (nt) {
-        case 1: return launch_gemv<FMT, 1>(ctx, a, y_dtype, grid, kw);
+        case 1: return launch_gemv<FMT, 1, half_t>(ctx, a, y_dtype, grid, kw);
         default:  // 2, or 4 where the GEMV takes more than two tokens
             if constexpr (kGemvMaxT > 2) {
-                if (nt == 4) return launch_gemv<FMT, 4>(ctx, a, y_dtype, grid, kw);
+                if (nt == 4) return launch_gemv<FMT, 4, half_t>(ctx, a, y_dtype, grid, kw);
             }
-            return launch_gemv<FMT, 2>(ctx, a, y_dtype, grid, kw);
+            return launch_gemv<FMT, 2, half_t>(ctx, a, y_dtype, grid, kw);
     }
 }
 
@@ -2024,12 +2050,15 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
              y, y_stride, flags, fmt, 0, aligned(y, 4 * dtype_size(y_dtype)) && y_stride % 4 == 0};
     const bool fast = x_dtype == NEKO_DT_F16 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 8 == 0 &&
                       aligned(w, 16) && row_bytes % 16 == 0;
+    const bool fast32 = x_dtype == NEKO_DT_F32 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 4 == 0 &&
+                        aligned(w, 16) && row_bytes % 16 == 0;
     // Decode-sized T: the GEMV path, NT tokens per pass with their activations staged in 64 KB of LDS.
     int gemv_nt = 0;
-    if (fast && T <= kGemvMaxT) {
+    if ((fast && T <= kGemvMaxT) || (fast32 && T <= kGemv32MaxT)) {
+        const int xb = fast32 ? 4 : 2;
         int nt = T <= 1 ? 1 : T <= 2 ? 2 : 4;
-        while (nt > 1 && gemv_lds_bytes(static_cast<int>(K), nt) > 65536) nt /= 2;
-        if (gemv_lds_bytes(static_cast<int>(K), nt) <= 65536) gemv_nt = nt;
+        while (nt > 1 && gemv_lds_bytes(static_cast<int>(K), nt, xb) > 65536) nt /= 2;
+        if (gemv_lds_bytes(static_cast<int>(K), nt, xb) <= 65536) gemv_nt = nt;
     }
     if (gemv_nt > 0) {
         // kw waves share 4 rows, splitting K; a workgroup holds 8 / kw such row groups. kw: the
@@ -2045,9 +2074,9 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
         const int64_t rows_per_wg = static_cast<int64_t>(kGemvRows) * (kGemvWaves / kw);
         const dim3 grid(static_cast<uint32_t>((N + rows_per_wg - 1) / rows_per_wg), static_cast<uint32_t>(chunks));
         switch (fmt) {
-            case NEKO_FMT_F16: return launch_gemv_nt<0>(ctx, a, y_dtype, grid, kw, gemv_nt);
-            case NEKO_FMT_FP8: return launch_gemv_nt<1>(ctx, a, y_dtype, grid, kw, gemv_nt);
-            default: return launch_gemv_nt<2>(ctx, a, y_dtype, grid, kw, gemv_nt);
+            case NEKO_FMT_F16: return launch_gemv_nt<0>(ctx, a, y_dtype, grid, kw, gemv_nt, fast32);
+            case NEKO_FMT_FP8: return launch_gemv_nt<1>(ctx, a, y_dtype, grid, kw, gemv_nt, fast32);
+            default: return launch_gemv_nt<2>(ctx, a, y_dtype, grid, kw, gemv_nt, fast32);
         }
     }
     if (fast && T >= (fmt == NEKO_FMT_F16 ? kGemmMinTF16 : kGemmMinT)) {

@@ -282,6 +282,58 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
         assert np.abs(y - want).max() <= float(((2 * K + 65) * U * mag).max())
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9, 33])
+def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
+    """f32 activations -- the reference's own type, as the ComputeBackend adapter passes them -- take
+    the GEMV's f32 form at any T (1, 2 or 4 tokens per pass, several passes past 4): integer-valued
+    data, every flag, bit-identical to the oracle; f16 output one rounding of the exact value."""
+    _case(f"matmul f32 activations integer fmt={fmt} T={T}")
+    rng = np.random.default_rng(900 + 10 * fmt + T)
+    K, N = 320, 37
+    tab, w = M.integer_table(fmt, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    y0 = rng.standard_normal((T, N)).astype(np.float32)
+    xd = torch.from_numpy(x).to(dev)
+    td = torch.from_numpy(tab).to(dev)
+    bd = torch.from_numpy(bias).to(dev)
+    for flags, b in ((0, None), (0, bias), (ops.MM_ACCUMULATE, bias), (ops.MM_GELU, bias)):
+        want = O.matmul(fmt, x, tab, K, b, y0, flags)
+        out = torch.from_numpy(y0).to(dev)
+        ops.matmul(xd, td, fmt, K, bias=None if b is None else bd, out=out, flags=flags)
+        got = out.cpu().numpy()
+        if flags & ops.MM_GELU:
+            d = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+            assert d.max() <= 2, (flags, int(d.max()))
+        else:
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (flags, b is None)
+    out16 = ops.matmul(xd, td, fmt, K, bias=bd, out_dtype=torch.float16)
+    assert np.array_equal(out16.cpu().numpy().view(np.uint16), O.f32_to_f16(O.matmul(fmt, x, tab, K, bias)))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T,K,N", [
+    (1, 2560, 6144),    # Qwen3-4B decode through the adapter: q/k/v
+    (1, 9728, 2560),    # down: one token per pass (39 KB of f32 activations in LDS)
+    (4, 2560, 19456),   # four tokens per pass
+    (17, 4096, 2560),   # five passes, the last one token
+    (2, 20480, 64),     # f32 activations too long for the GEMV's LDS: the generic kernel
+])
+def test_matmul_f32_activations_random_within_bound(dev, fmt, T, K, N):
+    _case(f"matmul f32 activations random fmt={fmt} T={T} K={K} N={N}")
+    rng = np.random.default_rng(11 * T + K + N + fmt)
+    w = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    tab, used = ops.quantize_rows(fmt, w)
+    wd = M.dequant(fmt, tab, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    y = ops.matmul(torch.from_numpy(x).to(dev), torch.from_numpy(tab).to(dev), fmt, K,
+                   bias=torch.from_numpy(bias).to(dev)).cpu().numpy()
+    exact, mag = M.exact_and_bound(x, wd, bias)
+    _bound_check(y, exact, mag, K, f"f32 x fmt={fmt} T={T} K={K} N={N}")
+
+
 def test_matmul_generic_paths(dev):
     """f32 activations, misaligned rows, K not a multiple of 32 (F16 only), f16 output."""
     _case("matmul generic paths")
