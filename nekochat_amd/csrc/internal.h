@@ -21,8 +21,10 @@ struct neko_hip_ctx {
     std::string name;
     std::string err;
     std::unordered_set<void*> allocs;
-    void* workspace = nullptr;  // device scratch for split reductions, grown on demand
-    size_t workspace_bytes = 0;
+    // Device scratch, grown on demand: [0] split-K partial sums, [1] the f32-activation matmul's f16
+    // planes and sums (its GEMMs may split K into [0] meanwhile).
+    void* workspace[2] = {nullptr, nullptr};
+    size_t workspace_bytes[2] = {0, 0};
     std::vector<void*> retired;  // outgrown workspaces, kept until destroy (captured graphs may use them)
     hipEvent_t switch_event = nullptr;  // orders a newly routed stream after the previous one
     void* scratch = nullptr;  // device address of the matmul's fixed split-K scratch on this device
@@ -42,10 +44,11 @@ int after_launch(neko_hip_ctx* ctx, const char* what);
 
 FastDiv make_fast_div(uint32_t d);
 
-// The context's device workspace, at least `bytes` long, shared by every op on ctx. Grown on
-// demand; an outgrown buffer stays allocated until neko_hip_destroy, since queued work and captured
-// graphs may still use it. Growing while ctx's stream is under graph capture fails (NEKO_ERR_INVALID).
-int workspace(neko_hip_ctx* ctx, size_t bytes, void** out);
+// The context's device workspace `slot` (0 or 1), at least `bytes` long, shared by every op on ctx.
+// Grown on demand; an outgrown buffer stays allocated until neko_hip_destroy, since queued work and
+// captured graphs may still use it. Growing while ctx's stream is under graph capture fails
+// (NEKO_ERR_INVALID).
+int workspace(neko_hip_ctx* ctx, size_t bytes, void** out, int slot = 0);
 // Looks up (once per device, with that device current) and records in ctx the device address of
 // the fixed split-K scratch array that neko_hip_matmul_noalloc uses (matmul.hip).
 int matmul_scratch_setup(neko_hip_ctx* ctx);

@@ -1868,6 +1868,65 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
+// ---------------------------------------------------------------- f32 activations on the MFMA kernels
+//
+// Row t of f32 activations becomes two f16 rows, scaled by a power of two s_t that puts the row's
+// largest magnitude in [2^14, 2^15): hi = f16(x s_t), lo = f16(x s_t - hi). hi + lo holds x s_t to
+// within 2^-22 of its magnitude (the largest |x| never overflows f16, values more than 2^28 below it
+// lose bits only beside it), so y = (hi . W + lo . W) / s_t, two f16 matmuls and an exact rescale,
+// stays far inside the f32 summation bound that every matmul path meets.
+constexpr int kSplitThreads = 256;
+
+// One workgroup per row: the row's largest magnitude, then its two planes and 1 / s_t.
+__global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* x, int64_t xs, int K, half_t* hi,
+                                                                   half_t* lo, float* inv_s) {
+    __shared__ float part[kSplitThreads / kWave];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int64_t t = blockIdx.x;
+    const float4v* xr = reinterpret_cast<const float4v*>(x + t * xs);
+    const int K4 = K / 4;
+    float m = 0.0f;
+    for (int i = tid; i < K4; i += kSplitThreads) {
+        const float4v v = xr[i];
+#pragma unroll
+        for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(v[e]));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) part[tid >> 6] = m;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kSplitThreads / kWave; w++) m = fmaxf(m, part[w]);
+    int e = 0;
+    if (m > 0.0f && m <= 3.4028235e38f) (void)frexpf(m, &e);  // m in [2^(e-1), 2^e)
+    const int sh = max(-126, min(126, 15 - e));                  // m * 2^sh in [2^14, 2^15)
+    const float sc = ldexpf(1.0f, sh);
+    if (tid == 0) inv_s[t] = ldexpf(1.0f, -sh);
+    half_t* h = hi + t * K;
+    half_t* l = lo + t * K;
+    for (int i = tid; i < K4; i += kSplitThreads) {
+        const float4v v = xr[i];
+        half4 vh, vl;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; e2++) {
+            const float u = v[e2] * sc;
+            vh[e2] = f16_rne(u);
+            vl[e2] = f16_rne(u - static_cast<float>(vh[e2]));
+        }
+        reinterpret_cast<half4*>(h)[i] = vh;
+        reinterpret_cast<half4*>(l)[i] = vl;
+    }
+}
+
+// y[t][n] = epilogue(sums[t][n] / s_t): the row's scale undone (exact), then bias, GELU, accumulate.
+template <typename TY>
+__global__ __launch_bounds__(256) void combine_rows_kernel(MmArgs a, const float* sums, const float* inv_s) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= a.T * a.N) return;
+    const int64_t t = i / a.N, n = i - t * a.N;
+    epilogue<TY>(a, t, n, sums[i] * inv_s[t]);
+}
+
 // Grid: x = weight rows, y = groups of 4 tokens; one wave each.
 template <typename TX, typename TY>
 __global__ __launch_bounds__(64) void mm_generic_kernel(MmArgs a) {
@@ -2022,6 +2081,49 @@ int partial_buffer(neko_hip_ctx* ctx, void* fixed, size_t bytes, float** out, co
 
 int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w, int64_t row_bytes,
                 int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int x_dtype, int y_dtype,
+                void* fixed, const char* what);
+
+#ifndef NEKO_TUNE_MM_F32_SPLIT_MIN_T
+#define NEKO_TUNE_MM_F32_SPLIT_MIN_T 5
+#endif
+// From this many tokens, f32 activations go through the MFMA kernels as two f16 planes. Measured on
+// the Qwen3-4B projections: at 6 tokens and up the planes win (gate/up 2.1x at 6, 3.7x at 16, 16x
+// at 512 tokens of the down projection); at 3-4 they win for gate/up and lose for the FP4 q/k/v and
+// down, so the f32 GEMV keeps T <= 4.
+constexpr int64_t kF32SplitMinT = NEKO_TUNE_MM_F32_SPLIT_MIN_T;
+
+// f32 activations (16-byte aligned rows, K % 32 == 0) as two f16 planes: both through the f16 paths
+// into f32 sums in workspace slot 1 (any split of K uses slot 0), then rescaled into y with the call's
+// bias / GELU / accumulate.
+int matmul_f32_split(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const char* what) {
+    const int64_t T = a.T, K = a.K, N = a.N;
+    const auto up = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+    const size_t plane = up(static_cast<size_t>(T) * K * 2), sums = up(static_cast<size_t>(T) * N * 4);
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, 2 * plane + sums + up(static_cast<size_t>(T) * 4), &ws, 1)) return rc;
+    uint8_t* base = static_cast<uint8_t*>(ws);
+    half_t* hi = reinterpret_cast<half_t*>(base);
+    half_t* lo = reinterpret_cast<half_t*>(base + plane);
+    float* s = reinterpret_cast<float*>(base + 2 * plane);
+    float* inv = reinterpret_cast<float*>(base + 2 * plane + sums);
+    NEKO_REQUIRE(ctx, T <= 0x7fffffff && T * N / 256 < 0x7fffffff, "%s: T=%lld too large", what, (long long)T);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kSplitThreads), 0, ctx->stream,
+                       static_cast<const float*>(a.x), a.xs, static_cast<int>(K), hi, lo, inv);
+    if (int rc = after_launch(ctx, what)) return rc;
+    if (int rc = matmul_impl(ctx, hi, K, T, K, a.w, a.rb, a.fmt, N, nullptr, s, N, 0, NEKO_DT_F16, NEKO_DT_F32, nullptr,
+                             what))
+        return rc;
+    if (int rc = matmul_impl(ctx, lo, K, T, K, a.w, a.rb, a.fmt, N, nullptr, s, N, kAccumulate, NEKO_DT_F16, NEKO_DT_F32,
+                             nullptr, what))
+        return rc;
+    const dim3 grid(static_cast<uint32_t>((T * N + 255) / 256));
+    if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((combine_rows_kernel<half_t>), grid, dim3(256), 0, ctx->stream, a, s, inv);
+    else hipLaunchKernelGGL((combine_rows_kernel<float>), grid, dim3(256), 0, ctx->stream, a, s, inv);
+    return after_launch(ctx, what);
+}
+
+int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w, int64_t row_bytes,
+                int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int x_dtype, int y_dtype,
                 void* fixed, const char* what) {
     NEKO_ENTER(ctx);
     NEKO_REQUIRE(ctx, valid_dtype(x_dtype) && valid_dtype(y_dtype), "%s: bad dtype x=%d y=%d", what, x_dtype, y_dtype);
@@ -2052,6 +2154,9 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                       aligned(w, 16) && row_bytes % 16 == 0;
     const bool fast32 = x_dtype == NEKO_DT_F32 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 4 == 0 &&
                         aligned(w, 16) && row_bytes % 16 == 0;
+    // f32 activations from kF32SplitMinT tokens: two f16 planes through the MFMA kernels. Below, and
+    // in the allocation-free entry (no workspace), the f32 GEMV.
+    if (fast32 && !fixed && T >= kF32SplitMinT) return matmul_f32_split(ctx, a, y_dtype, what);
     // Decode-sized T: the GEMV path, NT tokens per pass with their activations staged in 64 KB of LDS.
     int gemv_nt = 0;
     if ((fast && T <= kGemvMaxT) || (fast32 && T <= kGemv32MaxT)) {

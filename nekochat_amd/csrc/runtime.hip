@@ -86,24 +86,24 @@ int capturing(neko_hip_ctx* ctx, hipStream_t stream, bool* yes) {
     return NEKO_OK;
 }
 
-int workspace(neko_hip_ctx* ctx, size_t bytes, void** out) {
-    if (bytes > ctx->workspace_bytes) {
+int workspace(neko_hip_ctx* ctx, size_t bytes, void** out, int slot) {
+    if (bytes > ctx->workspace_bytes[slot]) {
         // Growing allocates, which a stream under graph capture cannot record.
         bool cap = false;
         if (int rc = capturing(ctx, ctx->stream, &cap)) return rc;
         if (cap)
             return fail(ctx, NEKO_ERR_INVALID,
-                        "split-K workspace must grow to %zu bytes (holds %zu) while the stream is being captured: make "
+                        "matmul workspace must grow to %zu bytes (holds %zu) while the stream is being captured: make "
                         "one uncaptured call at the largest shape first, or capture neko_hip_matmul_noalloc",
-                        bytes, ctx->workspace_bytes);
+                        bytes, ctx->workspace_bytes[slot]);
         void* p = nullptr;
         if (int rc = check(ctx, hipMalloc(&p, bytes), "hipMalloc (workspace)")) return rc;
         // The old buffer is retired, not freed: queued work and graphs captured earlier still use it.
-        if (ctx->workspace) ctx->retired.push_back(ctx->workspace);
-        ctx->workspace = p;
-        ctx->workspace_bytes = bytes;
+        if (ctx->workspace[slot]) ctx->retired.push_back(ctx->workspace[slot]);
+        ctx->workspace[slot] = p;
+        ctx->workspace_bytes[slot] = bytes;
     }
-    *out = ctx->workspace;
+    *out = ctx->workspace[slot];
     return NEKO_OK;
 }
 
@@ -150,7 +150,8 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     int rc = enter(ctx);
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (void* p : ctx->allocs) (void)hipFree(p);
-    if (ctx->workspace) (void)hipFree(ctx->workspace);
+    for (void* p : ctx->workspace)
+        if (p) (void)hipFree(p);
     for (void* p : ctx->retired) (void)hipFree(p);
     if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     delete ctx;

@@ -285,9 +285,10 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9, 33])
 def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
-    """f32 activations -- the reference's own type, as the ComputeBackend adapter passes them -- take
-    the GEMV's f32 form at any T (1, 2 or 4 tokens per pass, several passes past 4): integer-valued
-    data, every flag, bit-identical to the oracle; f16 output one rounding of the exact value."""
+    """f32 activations -- the reference's own type, as the ComputeBackend adapter passes them: up to 4
+    tokens the GEMV's f32 form, from 5 two f16 planes (each row scaled by a power of two) through the
+    MFMA kernels and an exact rescale. Integer-valued data, every flag, bit-identical to the oracle;
+    f16 output one rounding of the exact value."""
     _case(f"matmul f32 activations integer fmt={fmt} T={T}")
     rng = np.random.default_rng(900 + 10 * fmt + T)
     K, N = 320, 37
@@ -317,8 +318,12 @@ def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
     (1, 2560, 6144),    # Qwen3-4B decode through the adapter: q/k/v
     (1, 9728, 2560),    # down: one token per pass (39 KB of f32 activations in LDS)
     (4, 2560, 19456),   # four tokens per pass
-    (17, 4096, 2560),   # five passes, the last one token
+    (4, 4096, 2560),    # two passes of two tokens (64 KB of LDS holds two f32 rows of 4096)
     (2, 20480, 64),     # f32 activations too long for the GEMV's LDS: the generic kernel
+    (8, 2560, 19456),   # from 5 tokens: two f16 planes through the MFMA tile kernels
+    (64, 2560, 6144),   # ... the GEMM
+    (300, 1024, 700),   # ... partial token and row tiles
+    (512, 9728, 2560),  # ... long K
 ])
 def test_matmul_f32_activations_random_within_bound(dev, fmt, T, K, N):
     _case(f"matmul f32 activations random fmt={fmt} T={T} K={K} N={N}")
@@ -332,6 +337,29 @@ def test_matmul_f32_activations_random_within_bound(dev, fmt, T, K, N):
                    bias=torch.from_numpy(bias).to(dev)).cpu().numpy()
     exact, mag = M.exact_and_bound(x, wd, bias)
     _bound_check(y, exact, mag, K, f"f32 x fmt={fmt} T={T} K={K} N={N}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_matmul_f32_activations_row_magnitudes(dev, fmt):
+    """f32 activation rows far outside f16's range, tiny, zero, and with values 2^30 apart in one row,
+    through the two-plane path (each row scaled by its own power of two): within the bound."""
+    _case(f"matmul f32 activations row magnitudes fmt={fmt}")
+    rng = np.random.default_rng(77 + fmt)
+    T, K, N = 16, 2560, 384
+    w = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    tab, _ = ops.quantize_rows(fmt, w)
+    wd = M.dequant(fmt, tab, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    scale = np.array([1e30, 1e-30, 1e5, 1e-5, 0.0, 7e4, 1.0, 3e-38] + [1.0] * 8, np.float32)
+    x *= scale[:, None]
+    x[8, :K // 2] *= np.float32(2.0 ** -30)  # one row holding values 2^30 apart
+    x[9, 7] = np.float32(6e4)                # one outlier in an ordinary row
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    y = ops.matmul(torch.from_numpy(x).to(dev), torch.from_numpy(tab).to(dev), fmt, K,
+                   bias=torch.from_numpy(bias).to(dev)).cpu().numpy()
+    exact, mag = M.exact_and_bound(x, wd, bias)
+    assert np.isfinite(y).all()
+    _bound_check(y, exact, mag, K, f"f32 row magnitudes fmt={fmt}")
 
 
 def test_matmul_generic_paths(dev):
