@@ -52,6 +52,7 @@ def parse():
                    help="time every configured workload's ops (one JSON line with all of them) instead")
     p.add_argument("--workload", default=None,
                    help="with --all: time only this workload (gpt2_small_chain, qwen3_0.6b_decode, qwen3_4b_prefill, "
+                        "qwen3_4b_prefill_f32, "
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
                         "qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul, qwen3_4b_decode24_matmul, "
                         "qwen3_4b_prefill_matmul, stream_floor)")
@@ -355,15 +356,14 @@ def add_cpu_jobs(leg, want):
                 1, every("all 64 rows: per-token q/k rmsNorm + rope"))
         leg.add("qwen3_0.6b_decode", "swiglu", swiglu_job(c.T, c.I, 6), 1, full)
 
-    def prefill_jobs():  # qwen3_4b_prefill
+    def prefill_jobs(label="qwen3_4b_prefill"):  # qwen3_4b_prefill, qwen3_4b_prefill_f32 (the same f32 CPU ops)
         c, n = wl.QWEN3_PREFILL, 256
         s = rows_of(n, c.T)
         pos = np.arange(n) % c.seq
-        leg.add("qwen3_4b_prefill", "rmsnorm_in", rms_job(n, c.C, c.eps, 1), c.T / n, s)
-        leg.add("qwen3_4b_prefill", "qk_norm_rope", qk_job(n, c.n_q, c.n_kv, c.hd, c.theta, c.seq, pos, c.eps, 4),
-                c.T / n, s)
-        leg.add("qwen3_4b_prefill", "rmsnorm_post", rms_job(n, c.C, c.eps, 1), c.T / n, s)
-        leg.add("qwen3_4b_prefill", "swiglu", swiglu_job(n, c.I, 6), c.T / n, s)
+        leg.add(label, "rmsnorm_in", rms_job(n, c.C, c.eps, 1), c.T / n, s)
+        leg.add(label, "qk_norm_rope", qk_job(n, c.n_q, c.n_kv, c.hd, c.theta, c.seq, pos, c.eps, 4), c.T / n, s)
+        leg.add(label, "rmsnorm_post", rms_job(n, c.C, c.eps, 1), c.T / n, s)
+        leg.add(label, "swiglu", swiglu_job(n, c.I, 6), c.T / n, s)
 
     def gather_jobs():  # quant_gather_qwen3_1.7b
         c, n = wl.QUANT_GATHER, 2048
@@ -495,6 +495,7 @@ def add_cpu_jobs(leg, want):
             ("gpt2_small_chain", gpt2_jobs),
             ("qwen3_0.6b_decode", decode_jobs),
             ("qwen3_4b_prefill", prefill_jobs),
+            ("qwen3_4b_prefill_f32", lambda: prefill_jobs("qwen3_4b_prefill_f32")),
             ("quant_gather_qwen3_1.7b", gather_jobs),
             ("qwen3_4b_fused", fused_jobs),
             ("quantize_qwen3_1.7b_table", quantize_jobs),
@@ -521,7 +522,8 @@ def all_configs(args):
     flush = torch.ones(256 << 20, dtype=torch.float32, device=dev)
     out = {}
 
-    labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
+    labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "qwen3_4b_prefill_f32", "quant_gather_qwen3_1.7b",
+              "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
               "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_prefill_matmul", "stream_floor")
     if args.workload is not None and args.workload not in labels:
@@ -591,6 +593,27 @@ def all_configs(args):
                                                              warmup=args.warmup, no_flush=False))
         out["qwen3_4b_prefill"] = {"workload": "Qwen3-4B prefill layer (headline)", "ops": per_op,
                                    "layer_step_us": round(statistics.median(layer) * 1e3, 3)}
+
+    # The headline layer's four ops on f32 activations, the type the reference's ComputeBackend (and so
+    # the C++ adapter) passes: twice the activation bytes, the same kernels instantiated for f32.
+    if want("qwen3_4b_prefill_f32"):
+        c6 = wl.QWEN3_PREFILL
+        inp = wl.qwen3_prefill_inputs(c6, dev)
+        x6, xp6, qkv6, h6 = (inp[k].float() for k in ("x", "x_post", "qkv", "h"))
+        y6, yp6 = torch.empty_like(x6), torch.empty_like(xp6)
+        o6 = torch.empty((c6.T, c6.I), dtype=torch.float32, device=dev)
+        run("qwen3_4b_prefill_f32", {
+            "rmsnorm_in": ops.prepare(ops.rms_norm, x6, inp["w_in"], c6.eps, out=y6)[0],
+            "qk_norm_rope": ops.prepare(ops.qk_norm_rope, qkv6, c6.n_q, c6.n_kv, c6.hd, inp["cs"], c6.eps,
+                                        wqk=inp["wqk"], positions=inp["positions"])[0],
+            "rmsnorm_post": ops.prepare(ops.rms_norm, xp6, inp["w_post"], c6.eps, out=yp6)[0],
+            "swiglu": ops.prepare(ops.silu_mul, h6, out=o6)[0],
+        }, {"rmsnorm_in": wl.bytes_rmsnorm(c6.T, c6.C, 4), "rmsnorm_post": wl.bytes_rmsnorm(c6.T, c6.C, 4),
+            "qk_norm_rope": wl.bytes_qk_rope(c6.T, c6.n_q, c6.n_kv, c6.hd, e=4),
+            "swiglu": wl.bytes_swiglu(c6.T, c6.I, 4)},
+            "Qwen3-4B prefill layer's non-GEMM ops on f32 activations (the ComputeBackend's type): 2x RMSNorm "
+            "[8192,2560], q/k RMSNorm+NeoX RoPE (32q+8kv x 128), SwiGLU [8192,9728]")
+        del inp, x6, xp6, qkv6, h6, y6, yp6, o6
 
     # Quantised gather: 151936 x 2048 tied table, 16384 Zipf(1.1) ids, FP16 / FP8 / FP4 rows
     if want("quant_gather_qwen3_1.7b"):

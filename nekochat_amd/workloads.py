@@ -53,20 +53,21 @@ def zipf_ids(n: int, vocab: int, s: float, stream: int) -> np.ndarray:
 
 # ------------------------------------------------------------------ byte counts
 
-def bytes_rmsnorm(T: int, C: int) -> int:
-    return 2 * T * C * 2 + C * 4
+def bytes_rmsnorm(T: int, C: int, e: int = 2) -> int:
+    """x read and y written (e-byte activations: 2 for f16, 4 for f32), the f32 weights once."""
+    return 2 * T * C * e + C * 4
 
 
 def bytes_layernorm(T: int, C: int) -> int:
     return 2 * T * C * 2 + 2 * C * 4
 
 
-def bytes_qk_rope(T: int, n_q: int, n_kv: int, hd: int, positions: bool = True) -> int:
-    return 2 * T * (n_q + n_kv) * hd * 2 + (T * 4 if positions else 0) + 2 * hd * 4
+def bytes_qk_rope(T: int, n_q: int, n_kv: int, hd: int, positions: bool = True, e: int = 2) -> int:
+    return 2 * T * (n_q + n_kv) * hd * e + (T * 4 if positions else 0) + 2 * hd * 4
 
 
-def bytes_swiglu(T: int, I: int) -> int:
-    return T * (2 * I * 2 + I * 2)
+def bytes_swiglu(T: int, I: int, e: int = 2) -> int:
+    return T * (2 * I * e + I * e)
 
 
 def bytes_gelu(n: int) -> int:

@@ -16,7 +16,8 @@ def test_help_lists_every_workload():
     r = _run("--help")
     assert r.returncode == 0, r.stderr
     text = " ".join(r.stdout.split())
-    for w in ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "quant_gather_qwen3_1.7b", "qwen3_4b_fused",
+    for w in ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "qwen3_4b_prefill_f32", "quant_gather_qwen3_1.7b",
+              "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
               "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_prefill_matmul"):
         assert w in text, w
