@@ -55,6 +55,7 @@ def parse():
                         "qwen3_4b_prefill_f32, "
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
                         "qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul, qwen3_4b_decode24_matmul, "
+                        "qwen3_4b_decode_matmul_f32, qwen3_4b_decode16_matmul_f32, "
                         "qwen3_4b_prefill_matmul, stream_floor)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
@@ -504,6 +505,9 @@ def add_cpu_jobs(leg, want):
             ("qwen3_4b_decode4_matmul", lambda: matmul_jobs("qwen3_4b_decode4_matmul", wl.QWEN3_DECODE4_MATMUL)),
             ("qwen3_4b_decode16_matmul", lambda: matmul_jobs("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL)),
             ("qwen3_4b_decode24_matmul", lambda: matmul_jobs("qwen3_4b_decode24_matmul", wl.QWEN3_DECODE24_MATMUL)),
+            ("qwen3_4b_decode_matmul_f32", lambda: matmul_jobs("qwen3_4b_decode_matmul_f32", wl.QWEN3_DECODE_MATMUL)),
+            ("qwen3_4b_decode16_matmul_f32",
+             lambda: matmul_jobs("qwen3_4b_decode16_matmul_f32", wl.QWEN3_DECODE16_MATMUL)),
             ("qwen3_4b_prefill_matmul", prefill_matmul_jobs),
     ):
         if want(label):
@@ -525,7 +529,8 @@ def all_configs(args):
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "qwen3_4b_prefill_f32", "quant_gather_qwen3_1.7b",
               "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
-              "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_prefill_matmul", "stream_floor")
+              "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_decode_matmul_f32",
+              "qwen3_4b_decode16_matmul_f32", "qwen3_4b_prefill_matmul", "stream_floor")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -704,27 +709,32 @@ def all_configs(args):
     # f32 outputs; bytes = the weight rows once + activations + outputs.
     # Qwen3-4B decode steps of 1, 4, 16 and 24 sequences: the layer's four weight matmuls,
     # weight-bandwidth bound.
-    for label8, c8 in (("qwen3_4b_decode_matmul", wl.QWEN3_DECODE_MATMUL),
-                       ("qwen3_4b_decode4_matmul", wl.QWEN3_DECODE4_MATMUL),
-                       ("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL),
-                       ("qwen3_4b_decode24_matmul", wl.QWEN3_DECODE24_MATMUL)):
+    # The _f32 forms take f32 activations, the type the reference's ComputeBackend (the adapter) passes.
+    for label8, c8, x32 in (("qwen3_4b_decode_matmul", wl.QWEN3_DECODE_MATMUL, False),
+                            ("qwen3_4b_decode4_matmul", wl.QWEN3_DECODE4_MATMUL, False),
+                            ("qwen3_4b_decode16_matmul", wl.QWEN3_DECODE16_MATMUL, False),
+                            ("qwen3_4b_decode24_matmul", wl.QWEN3_DECODE24_MATMUL, False),
+                            ("qwen3_4b_decode_matmul_f32", wl.QWEN3_DECODE_MATMUL, True),
+                            ("qwen3_4b_decode16_matmul_f32", wl.QWEN3_DECODE16_MATMUL, True)):
         if not want(label8):
             continue
         calls8, bytes8 = {}, {}
         for pname, N, K in c8.projections:
             wsrc = wl.normal_f16((N, K), 0.0, 0.02, 81, dev).float()
             x8 = wl.normal_f16((c8.T, K), 0.0, 1.0, 82, dev)
+            if x32:
+                x8 = x8.float()
             y8 = torch.empty((c8.T, N), dtype=torch.float32, device=dev)
             for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
                 tab8, _ = ops.quantize(wsrc, fmt)
                 name = f"{pname}_{fname}"
                 calls8[name] = ops.prepare(ops.matmul, x8, tab8, fmt, K, out=y8)[0]
                 calls8[name].table = tab8
-                bytes8[name] = wl.bytes_matmul(c8.T, K, N, tab8.shape[1])
+                bytes8[name] = wl.bytes_matmul(c8.T, K, N, tab8.shape[1], x_bytes=4 if x32 else 2)
             del wsrc
         run(label8, calls8, bytes8,
             f"Qwen3-4B decode step, T={c8.T}: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
-            "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs")
+            f"weight matmuls in F16 / FP8 / FP4 rows, {'f32' if x32 else 'f16'} activations, f32 outputs")
         del calls8
 
     # Qwen3-4B prefill (T = 8192): the same four weight matmuls, MFMA-bound; flops = 2 T N K.

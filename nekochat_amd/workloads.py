@@ -92,10 +92,11 @@ def bytes_store_kv(T: int, width: int, positions: bool = True) -> int:
     return 4 * T * width * 2 + (T * 4 if positions else 0)
 
 
-def bytes_matmul(T: int, K: int, N: int, row_bytes: int, y_bytes: int = 4, accumulate: bool = False) -> int:
-    """The weight rows read once, the fp16 activations read, the outputs written (and read when
-    accumulating)."""
-    return N * row_bytes + T * K * 2 + T * N * y_bytes * (2 if accumulate else 1)
+def bytes_matmul(T: int, K: int, N: int, row_bytes: int, y_bytes: int = 4, accumulate: bool = False,
+                 x_bytes: int = 2) -> int:
+    """The weight rows read once, the activations (x_bytes each) read, the outputs written (and read
+    when accumulating)."""
+    return N * row_bytes + T * K * x_bytes + T * N * y_bytes * (2 if accumulate else 1)
 
 
 def bytes_qk_rope_kv(T: int, n_q: int, n_kv: int, hd: int, positions: bool = True) -> int:

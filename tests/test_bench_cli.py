@@ -19,7 +19,8 @@ def test_help_lists_every_workload():
     for w in ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "qwen3_4b_prefill_f32", "quant_gather_qwen3_1.7b",
               "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
-              "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_prefill_matmul"):
+              "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_decode_matmul_f32",
+              "qwen3_4b_decode16_matmul_f32", "qwen3_4b_prefill_matmul"):
         assert w in text, w
 
 
