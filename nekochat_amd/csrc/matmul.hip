@@ -980,12 +980,30 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+#ifndef NEKO_TUNE_MM_GEMV_SWZ
+#define NEKO_TUNE_MM_GEMV_SWZ 1
+#endif
+// The staged f32 activations of one 32-wide block are eight 16-byte chunks, stored with chunk c at
+// chunk position c ^ key(block). The 16 lanes of a weight row read the same chunk of 16 consecutive
+// blocks in one instruction: unswizzled, those addresses are 128 bytes apart and fall on 2 of LDS's
+// sixteen 16-byte bank groups (8-way conflicts); with the key they take all sixteen, for any first
+// block. Measured at 1-4 tokens on the Qwen3-4B projections: 13-34% faster at one token (F16 down
+// 24.3 -> 16.0 us), 2.2x at four (FP4 gate/up 54.6 -> 25.1 us). f16 activations (four chunks, 4-way
+// conflicts) stay unswizzled: there the per-read address arithmetic cost more than the conflicts
+// (0.1-0.8 us slower at one token).
+template <typename TX>
+__device__ __forceinline__ int gemv_swz_key(int blk) {
+    constexpr int CPB = 32 / (16 / static_cast<int>(sizeof(TX)));  // 16-byte chunks per block: 4 or 8
+    if constexpr (!NEKO_TUNE_MM_GEMV_SWZ || sizeof(TX) == 2) return 0;
+    return (blk / (16 / CPB)) & (CPB - 1);
+}
+
 // Two weights as f16 (exact values / 2^8 for FP8, the values for FP4) paired with the activation
 // pair at the same positions of the staged x block; dot of one 32-wide block against token t. f16
 // activations: one fdot2 per pair; f32 activations (the reference's own type): one fma per weight,
-// the f16 weight widened exactly.
+// the f16 weight widened exactly. key: the block's chunk swizzle.
 template <int FMT, typename TX>
-__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const TX* xb) {
+__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const TX* xb, int key) {
     float d = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {  // 4 x 8 activations
@@ -1009,14 +1027,15 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
             wp[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3));
         }
         if constexpr (sizeof(TX) == 2) {
-            const uint4v xc = reinterpret_cast<const uint4v*>(xb)[c];
+            const uint4v xc = reinterpret_cast<const uint4v*>(xb)[c ^ key];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t xw = xc[i];
                 d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wp[i]), __builtin_bit_cast(half2v, xw), d, false);
             }
         } else {
-            const float4v x0 = reinterpret_cast<const float4v*>(xb)[2 * c], x1 = reinterpret_cast<const float4v*>(xb)[2 * c + 1];
+            const float4v x0 = reinterpret_cast<const float4v*>(xb)[(2 * c) ^ key],
+                          x1 = reinterpret_cast<const float4v*>(xb)[(2 * c + 1) ^ key];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const half2v w2 = __builtin_bit_cast(half2v, wp[i]);
@@ -1040,9 +1059,10 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
 constexpr int64_t kGemvMaxT = NEKO_TUNE_MM_GEMV_MAX_T;
 static_assert(kGemvMaxT >= 1 && kGemvMaxT <= 4, "the GEMV holds 1, 2 or 4 tokens per pass");
 constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
-// f32 activations (the reference's own type, as its ComputeBackend passes them) take the GEMV at any
-// T its grid holds: the MFMA kernels read f16 activations, and the GEMV's NT-token passes beat the
-// generic kernel's per-element loads at every T measured (4-5x at 1 token, ~3x at 4-16).
+// f32 activations (the reference's own type, as its ComputeBackend passes them) take the GEMV below
+// the two-plane split's threshold, and at any T its grid holds where the split cannot run (the
+// allocation-free entry): the MFMA kernels read f16 activations, and the GEMV's NT-token passes beat
+// the generic kernel's per-element loads at every T measured (4-5x at 1 token, ~3x at 4-16).
 constexpr int64_t kGemv32MaxT = 65535;
 constexpr int kGemvRows = 4;    // weight rows per wave: 16 lanes each
 constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw slices of K
@@ -1108,6 +1128,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
                 const int t = i / kc, c = i - t * kc;
                 uint4v v = {0u, 0u, 0u, 0u};
                 if (t < nt) v = *reinterpret_cast<const uint4v*>(static_cast<const TX*>(a.x) + (t0 + t) * a.xs + EPC * c);
+                // Chunk j of a block lands in chunk j ^ key: element offset o within the block -> o ^ (key * EPC).
+                const int kswz = gemv_swz_key<TX>((EPC * c) / kBlockK) * EPC;
                 TX* dst = xs + static_cast<int64_t>(t) * K;
                 if constexpr (FMT == 2) {
                     // Piece c holds k = kb .. kb + EPC - 1 of its block: to 2 k (k < 16) or 2 (k - 16) + 1.
@@ -1118,10 +1140,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
                         TX val;
                         if constexpr (sizeof(TX) == 2) val = __builtin_bit_cast(half8, v)[e];
                         else val = __builtin_bit_cast(float4v, v)[e];
-                        dst[base + (k < 16 ? 2 * k : 2 * (k - 16) + 1)] = val;
+                        dst[base + ((k < 16 ? 2 * k : 2 * (k - 16) + 1) ^ kswz)] = val;
                     }
                 } else {
-                    *reinterpret_cast<uint4v*>(dst + EPC * c) = v;
+                    *reinterpret_cast<uint4v*>(dst + ((EPC * c) ^ kswz)) = v;
                 }
             }
             __syncthreads();
@@ -1131,7 +1153,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
             if (j0 + u >= steps) break;  // wave-uniform
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                const float d = block_dot<FMT, TX>(q[u], xs + static_cast<int64_t>(t) * K + bl[u] * kBlockK);
+                const float d = block_dot<FMT, TX>(q[u], xs + static_cast<int64_t>(t) * K + bl[u] * kBlockK,
+                                                   gemv_swz_key<TX>(bl[u]));
                 const float v = FMT == 0 ? d : d * sc[u];
                 acc[t] += valid[u] ? v : 0.0f;
             }
@@ -2084,12 +2107,13 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                 void* fixed, const char* what);
 
 #ifndef NEKO_TUNE_MM_F32_SPLIT_MIN_T
-#define NEKO_TUNE_MM_F32_SPLIT_MIN_T 5
+#define NEKO_TUNE_MM_F32_SPLIT_MIN_T 9
 #endif
 // From this many tokens, f32 activations go through the MFMA kernels as two f16 planes. Measured on
-// the Qwen3-4B projections: at 6 tokens and up the planes win (gate/up 2.1x at 6, 3.7x at 16, 16x
-// at 512 tokens of the down projection); at 3-4 they win for gate/up and lose for the FP4 q/k/v and
-// down, so the f32 GEMV keeps T <= 4.
+// the Qwen3-4B projections: at 3-8 tokens the f32 GEMV is faster in every format but one case (F16
+// down at 6 tokens, 5% slower; FP4 gate/up at 5-8 tokens 30-31 us against 36-38, FP4 down 23-25
+// against 36-37); at 10-16 the planes win for gate/up (16 tokens: 41-53 us against 52-68) and the
+// F16 / FP8 down, the GEMV for q/k/v and the FP4 down; at 512 tokens the planes are 16x faster.
 constexpr int64_t kF32SplitMinT = NEKO_TUNE_MM_F32_SPLIT_MIN_T;
 
 // f32 activations (16-byte aligned rows, K % 32 == 0) as two f16 planes: both through the f16 paths

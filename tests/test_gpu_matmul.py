@@ -283,10 +283,10 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 9, 33])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 9, 33])
 def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
-    """f32 activations -- the reference's own type, as the ComputeBackend adapter passes them: up to 4
-    tokens the GEMV's f32 form, from 5 two f16 planes (each row scaled by a power of two) through the
+    """f32 activations -- the reference's own type, as the ComputeBackend adapter passes them: up to 8
+    tokens the GEMV's f32 form (passes of 1, 2 or 4 tokens), from 9 two f16 planes (each row scaled by a power of two) through the
     MFMA kernels and an exact rescale. Integer-valued data, every flag, bit-identical to the oracle;
     f16 output one rounding of the exact value."""
     _case(f"matmul f32 activations integer fmt={fmt} T={T}")
@@ -320,7 +320,8 @@ def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
     (4, 2560, 19456),   # four tokens per pass
     (4, 4096, 2560),    # two passes of two tokens (64 KB of LDS holds two f32 rows of 4096)
     (2, 20480, 64),     # f32 activations too long for the GEMV's LDS: the generic kernel
-    (8, 2560, 19456),   # from 5 tokens: two f16 planes through the MFMA tile kernels
+    (8, 2560, 19456),   # two passes of four tokens
+    (12, 2560, 19456),  # from 9 tokens: two f16 planes through the MFMA tile kernels
     (64, 2560, 6144),   # ... the GEMM
     (300, 1024, 700),   # ... partial token and row tiles
     (512, 9728, 2560),  # ... long K
