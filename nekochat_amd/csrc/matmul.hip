@@ -980,30 +980,25 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-#ifndef NEKO_TUNE_MM_GEMV_SWZ
-#define NEKO_TUNE_MM_GEMV_SWZ 1
-#endif
-// The staged f32 activations of one 32-wide block are eight 16-byte chunks, stored with chunk c at
-// chunk position c ^ key(block). The 16 lanes of a weight row read the same chunk of 16 consecutive
-// blocks in one instruction: unswizzled, those addresses are 128 bytes apart and fall on 2 of LDS's
-// sixteen 16-byte bank groups (8-way conflicts); with the key they take all sixteen, for any first
-// block. Measured at 1-4 tokens on the Qwen3-4B projections: 13-34% faster at one token (F16 down
-// 24.3 -> 16.0 us), 2.2x at four (FP4 gate/up 54.6 -> 25.1 us). f16 activations (four chunks, 4-way
-// conflicts) stay unswizzled: there the per-read address arithmetic cost more than the conflicts
-// (0.1-0.8 us slower at one token).
-template <typename TX>
-__device__ __forceinline__ int gemv_swz_key(int blk) {
-    constexpr int CPB = 32 / (16 / static_cast<int>(sizeof(TX)));  // 16-byte chunks per block: 4 or 8
-    if constexpr (!NEKO_TUNE_MM_GEMV_SWZ || sizeof(TX) == 2) return 0;
-    return (blk / (16 / CPB)) & (CPB - 1);
+// Staged activation rows: 16 bytes of padding after every 256 bytes of blocks (every 4 f16 / 2 f32
+// blocks). The 16 lanes of a weight row read the same 16-byte chunk of 16 consecutive blocks in one
+// instruction: unpadded, those addresses are 64 / 128 bytes apart and fall on 4 / 2 of LDS's sixteen
+// 16-byte bank groups (4- / 8-way conflicts); padded they take all sixteen, for any first block,
+// and every chunk read keeps a constant offset from its block's address. Measured at 1-4 tokens on
+// the Qwen3-4B projections against unpadded rows: f32 activations 1.2-2.5x faster (FP4 gate/up
+// 19.3 -> 12.2 us at one token, 54.6 -> 22.2 at four), f16 up to 11% (FP4 gate/up at two tokens
+// 14.4 -> 12.8 us; FP8 within 0.3 us either way). An XOR swizzle of the chunks instead (no padding)
+// gained less for f32 and cost time for f16: its per-read address arithmetic.
+__host__ __device__ constexpr int gemv_blk_off(int blk, int x_bytes) {  // element offset of block blk
+    return blk * 32 + (blk >> (x_bytes == 4 ? 1 : 2)) * (16 / x_bytes);
 }
 
 // Two weights as f16 (exact values / 2^8 for FP8, the values for FP4) paired with the activation
 // pair at the same positions of the staged x block; dot of one 32-wide block against token t. f16
 // activations: one fdot2 per pair; f32 activations (the reference's own type): one fma per weight,
-// the f16 weight widened exactly. key: the block's chunk swizzle.
+// the f16 weight widened exactly.
 template <int FMT, typename TX>
-__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const TX* xb, int key) {
+__device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT == 1 ? 2 : 1], const TX* xb) {
     float d = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {  // 4 x 8 activations
@@ -1027,15 +1022,14 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
             wp[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3));
         }
         if constexpr (sizeof(TX) == 2) {
-            const uint4v xc = reinterpret_cast<const uint4v*>(xb)[c ^ key];
+            const uint4v xc = reinterpret_cast<const uint4v*>(xb)[c];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t xw = xc[i];
                 d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, wp[i]), __builtin_bit_cast(half2v, xw), d, false);
             }
         } else {
-            const float4v x0 = reinterpret_cast<const float4v*>(xb)[(2 * c) ^ key],
-                          x1 = reinterpret_cast<const float4v*>(xb)[(2 * c + 1) ^ key];
+            const float4v x0 = reinterpret_cast<const float4v*>(xb)[2 * c], x1 = reinterpret_cast<const float4v*>(xb)[2 * c + 1];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const half2v w2 = __builtin_bit_cast(half2v, wp[i]);
@@ -1062,7 +1056,7 @@ constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
 // f32 activations (the reference's own type, as its ComputeBackend passes them) take the GEMV below
 // the two-plane split's threshold, and at any T its grid holds where the split cannot run (the
 // allocation-free entry): the MFMA kernels read f16 activations, and the GEMV's NT-token passes beat
-// the generic kernel's per-element loads at every T measured (4-5x at 1 token, ~3x at 4-16).
+// the generic kernel's per-element loads at every T measured (4.9-7.4x at one token).
 constexpr int64_t kGemv32MaxT = 65535;
 constexpr int kGemvRows = 4;    // weight rows per wave: 16 lanes each
 constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw slices of K
@@ -1072,7 +1066,7 @@ constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw
 constexpr int kGemvBatch = NEKO_TUNE_MM_GEMV_BATCH;  // 32-wide blocks per lane whose weights are requested together
 
 // Grid: x = workgroups of 4 * 8 / kw weight rows, y = chunks of NT tokens. Wave w works on row
-// group w / kw and K slice w % kw (a.blocks_per_wave blocks). Dynamic LDS: the chunk's activations as TX [NT][K] (FP4: each 32-block
+// group w / kw and K slice w % kw (a.blocks_per_wave blocks). Dynamic LDS: the chunk's activations as TX [NT][xrow], rows padded as above (FP4: each 32-block
 // stored as (x_j, x_16+j) pairs), then 8 * 4 * NT partial sums.
 template <int FMT, int NT, typename TY, typename TX>
 __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int kw) {
@@ -1088,6 +1082,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
     const int64_t t0 = static_cast<int64_t>(blockIdx.y) * NT;
     const int nt = static_cast<int>(min(static_cast<int64_t>(NT), a.T - t0));
     const int K = a.K;
+    const int xrow = gemv_blk_off(K / kBlockK, sizeof(TX));  // staged row, elements
 
     const int64_t row = (static_cast<int64_t>(blockIdx.x) * (kGemvWaves / kw) + rg) * kGemvRows + r;
     const uint8_t* wrow = a.w + min(row, static_cast<int64_t>(a.N) - 1) * a.rb;
@@ -1128,22 +1123,21 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
                 const int t = i / kc, c = i - t * kc;
                 uint4v v = {0u, 0u, 0u, 0u};
                 if (t < nt) v = *reinterpret_cast<const uint4v*>(static_cast<const TX*>(a.x) + (t0 + t) * a.xs + EPC * c);
-                // Chunk j of a block lands in chunk j ^ key: element offset o within the block -> o ^ (key * EPC).
-                const int kswz = gemv_swz_key<TX>((EPC * c) / kBlockK) * EPC;
-                TX* dst = xs + static_cast<int64_t>(t) * K;
+                // Piece c: elements kb .. kb + EPC - 1 of block c * EPC / 32, at that block's padded offset.
+                const int kb = (EPC * c) % kBlockK;
+                TX* dst = xs + static_cast<int64_t>(t) * xrow + gemv_blk_off((EPC * c) / kBlockK, sizeof(TX));
                 if constexpr (FMT == 2) {
-                    // Piece c holds k = kb .. kb + EPC - 1 of its block: to 2 k (k < 16) or 2 (k - 16) + 1.
-                    const int kb = (EPC * c) % kBlockK, base = (EPC * c) / kBlockK * kBlockK;
+                    // Element k of the block to 2 k (k < 16) or 2 (k - 16) + 1.
 #pragma unroll
                     for (int e = 0; e < EPC; e++) {
                         const int k = kb + e;
                         TX val;
                         if constexpr (sizeof(TX) == 2) val = __builtin_bit_cast(half8, v)[e];
                         else val = __builtin_bit_cast(float4v, v)[e];
-                        dst[base + ((k < 16 ? 2 * k : 2 * (k - 16) + 1) ^ kswz)] = val;
+                        dst[k < 16 ? 2 * k : 2 * (k - 16) + 1] = val;
                     }
                 } else {
-                    *reinterpret_cast<uint4v*>(dst + ((EPC * c) ^ kswz)) = v;
+                    *reinterpret_cast<uint4v*>(dst + kb) = v;
                 }
             }
             __syncthreads();
@@ -1153,8 +1147,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
             if (j0 + u >= steps) break;  // wave-uniform
 #pragma unroll
             for (int t = 0; t < NT; t++) {
-                const float d = block_dot<FMT, TX>(q[u], xs + static_cast<int64_t>(t) * K + bl[u] * kBlockK,
-                                                   gemv_swz_key<TX>(bl[u]));
+                const float d = block_dot<FMT, TX>(q[u], xs + static_cast<int64_t>(t) * xrow + gemv_blk_off(bl[u], sizeof(TX)));
                 const float v = FMT == 0 ? d : d * sc[u];
                 acc[t] += valid[u] ? v : 0.0f;
             }
@@ -1164,7 +1157,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
     for (int t = 0; t < NT; t++) acc[t] = row16_sum(acc[t]);
 
     if (kw > 1) {
-        float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(NT) * K * sizeof(TX));
+        float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(NT) * xrow * sizeof(TX));
         if (sl == 0) {
 #pragma unroll
             for (int t = 0; t < NT; t++) red[(wave * kGemvRows + r) * NT + t] = acc[t];
@@ -1187,7 +1180,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void mm_gemv_kernel(MmArgs a, int 
 }
 
 __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt, int x_bytes = 2) {
-    return static_cast<size_t>(nt) * K * x_bytes + static_cast<size_t>(kGemvWaves) * kGemvRows * nt * 4;
+    return static_cast<size_t>(nt) * gemv_blk_off(K / kBlockK, x_bytes) * x_bytes + static_cast<size_t>(kGemvWaves) * kGemvRows * nt * 4;
 }
 
 // ---------------------------------------------------------------- prefill path: MFMA GEMM
