@@ -201,9 +201,9 @@ int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t col
  * The dot products are summed in f32 (f16 activations and weight codes exactly, each 32-block scaled
  * by its f16 scale) in a different order from the reference's sequential loop: results agree to f32
  * rounding of the sum. Fastest with f16 activations, 16-byte aligned x rows and weight rows (the
- * MFMA kernels). f32 activations with aligned rows: up to 8 tokens a VALU kernel (1.0-1.3x the
- * f16 time at one token); from 9, each row split into two f16 planes (scaled by a power of
- * two) for the MFMA kernels, about 2-3x the f16 time, with the call's context workspace holding the
+ * MFMA kernels). f32 activations with aligned rows: up to 8 tokens (16 for weights of at most
+ * 2^24 elements) a VALU kernel (1.0-1.3x the f16 time at one token); beyond, each row split into
+ * two f16 planes (scaled by a power of two) for the MFMA kernels, about 2-3x the f16 time, with the call's context workspace holding the
  * planes and sums. Other shapes take a generic kernel.
  * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown) by the
  * first call that needs more; outgrown buffers are kept too (graphs captured earlier still point at

@@ -2107,7 +2107,15 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
 // down at 6 tokens, 5% slower; FP4 gate/up at 5-8 tokens 30-31 us against 36-38, FP4 down 23-25
 // against 36-37); at 10-16 the planes win for gate/up (16 tokens: 41-53 us against 52-68) and the
 // F16 / FP8 down, the GEMV for q/k/v and the FP4 down; at 512 tokens the planes are 16x faster.
+// Weights of at most kF32SmallNK elements keep the GEMV through 16 tokens: at 10-16 it measured
+// 1.1-2.2x faster than the planes for the Qwen3-4B q/k/v [6144, 2560] and o [2560, 4096] and the
+// Qwen3-0.6B projections (the planes' four launches dominate there).
 constexpr int64_t kF32SplitMinT = NEKO_TUNE_MM_F32_SPLIT_MIN_T;
+#ifndef NEKO_TUNE_MM_F32_SPLIT_MIN_T_SMALL
+#define NEKO_TUNE_MM_F32_SPLIT_MIN_T_SMALL 17
+#endif
+constexpr int64_t kF32SplitMinTSmall = NEKO_TUNE_MM_F32_SPLIT_MIN_T_SMALL;
+constexpr int64_t kF32SmallNK = int64_t{1} << 24;
 
 // f32 activations (16-byte aligned rows, K % 32 == 0) as two f16 planes: both through the f16 paths
 // into f32 sums in workspace slot 1 (any split of K uses slot 0), then rescaled into y with the call's
@@ -2173,7 +2181,8 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                         aligned(w, 16) && row_bytes % 16 == 0;
     // f32 activations from kF32SplitMinT tokens: two f16 planes through the MFMA kernels. Below, and
     // in the allocation-free entry (no workspace), the f32 GEMV.
-    if (fast32 && !fixed && T >= kF32SplitMinT) return matmul_f32_split(ctx, a, y_dtype, what);
+    if (fast32 && !fixed && T >= (N * K <= kF32SmallNK ? kF32SplitMinTSmall : kF32SplitMinT))
+        return matmul_f32_split(ctx, a, y_dtype, what);
     // Decode-sized T: the GEMV path, NT tokens per pass with their activations staged in 64 KB of LDS.
     int gemv_nt = 0;
     if ((fast && T <= kGemvMaxT) || (fast32 && T <= kGemv32MaxT)) {

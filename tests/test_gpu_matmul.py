@@ -283,10 +283,11 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 9, 33])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 9, 16, 17, 33])
 def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
     """f32 activations -- the reference's own type, as the ComputeBackend adapter passes them: up to 8
-    tokens the GEMV's f32 form (passes of 1, 2 or 4 tokens), from 9 two f16 planes (each row scaled by a power of two) through the
+    tokens the GEMV's f32 form (passes of 1, 2 or 4 tokens; up to 16 for weights of at most 2^24
+    elements, as here), from 9 (17) two f16 planes (each row scaled by a power of two) through the
     MFMA kernels and an exact rescale. Integer-valued data, every flag, bit-identical to the oracle;
     f16 output one rounding of the exact value."""
     _case(f"matmul f32 activations integer fmt={fmt} T={T}")
