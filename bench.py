@@ -47,6 +47,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-flush", action="store_true", help="skip the cache flush (cache-warm figures)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-floors", action="store_true", help="skip the per-op floors timed beside the ops")
     p.add_argument("--only", default=None, help="time a single op (for profiling runs)")
     p.add_argument("--all", action="store_true",
                    help="time every configured workload's ops (one JSON line with all of them) instead")
@@ -60,6 +61,11 @@ def parse():
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
+
+
+def progress(msg: str) -> None:
+    """One line on stderr per finished phase, so a long run shows it is moving."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
 
 
 class HipTimer:
@@ -105,21 +111,157 @@ class HipTimer:
         self.events = []
 
 
-def time_ops(calls, op_bytes, names, steps, warmup, flush, timer):
-    """Times each named op: `warmup` untimed rounds, then `steps` rounds, each op after a cache
-    flush (unless flush is None) inside its own event pair. Returns (per-op stats, wall ms/round)."""
+class FloorLib:
+    """The streaming-floor kernels (libneko_floor.so) and the HIP runtime's own device-to-device copies
+    (hipMemcpyAsync, hipMemcpy2DAsync), as zero-argument calls on one stream that raise on error."""
+
+    H2D, D2D = 1, 3
+
+    def __init__(self, stream: int):
+        import ctypes
+
+        c = ctypes
+        self.ct = c
+        lib = c.CDLL(os.path.join(ROOT, "nekochat_amd", "libneko_floor.so"))
+        for name, args_ in (("neko_floor_empty", [c.c_int, c.c_void_p]),
+                            ("neko_floor_copy", [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_int, c.c_int,
+                                                 c.c_void_p]),
+                            ("neko_floor_copy2", [c.c_void_p, c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_int,
+                                                  c.c_void_p]),
+                            ("neko_floor_read", [c.c_void_p, c.c_size_t, c.c_void_p, c.c_void_p]),
+                            ("neko_floor_rows2", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_int64,
+                                                  c.c_int, c.c_int, c.c_void_p]),
+                            ("neko_floor_inplace", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_int,
+                                                    c.c_void_p]),
+                            ("neko_floor_inplace_rows", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_int,
+                                                         c.c_int, c.c_void_p])):
+            getattr(lib, name).argtypes = args_
+            getattr(lib, name).restype = c.c_int
+        self.lib = lib
+        hip = c.CDLL("libamdhip64.so.7")  # the runtime torch already loaded
+        hip.hipMemcpyAsync.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_void_p]
+        hip.hipMemcpyAsync.restype = c.c_int
+        hip.hipMemcpy2DAsync.argtypes = [c.c_void_p, c.c_size_t, c.c_void_p, c.c_size_t, c.c_size_t, c.c_size_t,
+                                         c.c_int, c.c_void_p]
+        hip.hipMemcpy2DAsync.restype = c.c_int
+        self.hip = hip
+        self.stream = c.c_void_p(stream or None)
+
+    def _checked(self, fn, *a):
+        stream = self.stream
+
+        def call():
+            rc = fn(*a, stream)
+            if rc != 0:
+                raise RuntimeError(f"{fn.__name__}: HIP error {rc}")
+        return call
+
+    def __getattr__(self, name):  # floor kernels by their exported name without the prefix
+        fn = getattr(self.lib, "neko_floor_" + name)
+        return lambda *a: self._checked(fn, *a)
+
+    def memcpy(self, dst, src, nbytes):
+        """hipMemcpyAsync device to device."""
+        return self._checked(self.hip.hipMemcpyAsync, dst, src, nbytes, self.D2D)
+
+    def memcpy2d(self, dst, dpitch, src, spitch, width, rows):
+        """hipMemcpy2DAsync device to device: `rows` rows of `width` bytes."""
+        return self._checked(self.hip.hipMemcpy2DAsync, dst, dpitch, src, spitch, width, rows, self.D2D)
+
+
+def headline_floors(cfg, inp, dev, fl):
+    """Floor candidates for each headline op over the op's own byte pattern: the floor kernels (copies
+    in the op's layout) and the runtime's device-to-device copies (hipMemcpyAsync, hipMemcpy2DAsync,
+    torch's copy_). Returns (calls, bytes, {op: [candidate names]}, {op: {candidate: call}} for the
+    layer-floor step, whose two RMSNorm floors use separate buffers so neither finds the other's bytes
+    in a cache)."""
     import torch
+
+    from nekochat_amd import workloads as wl
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(12345)
+
+    def rand_bytes(n):
+        return torch.randint(-2 ** 31, 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device=dev, generator=gen)
+
+    calls, nbytes, groups, layer = {}, {}, {}, {}
+    half = cfg.T * cfg.C * 2  # one [T, C] fp16 row set
+    for op in ("rmsnorm_in", "rmsnorm_post"):
+        src, dst = rand_bytes(half), rand_bytes(half)
+        cand = {
+            "copy_i1_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 1, 1, 1),
+            "copy_i4_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 4, 1, 1),
+            "hipMemcpyAsync": fl.memcpy(dst.data_ptr(), src.data_ptr(), half),
+            "torch_copy_": (lambda d=dst, s=src: d.copy_(s)),
+        }
+        layer[op] = cand
+        if op == "rmsnorm_in":  # both RMSNorms move the same bytes: one set of candidates is timed
+            groups["rmsnorm"] = []
+            for k, v in cand.items():
+                calls[f"rmsnorm:{k}"], nbytes[f"rmsnorm:{k}"] = v, 2 * half
+                groups["rmsnorm"].append(f"rmsnorm:{k}")
+        layer[op]["_keep"] = (src, dst)
+    # q/k RoPE: 10240 of every 12288 bytes of each qkv row read and written back, in place.
+    qk_w = (cfg.n_q + cfg.n_kv) * cfg.hd * 2
+    rs = cfg.qkv_stride * 2
+    qf = inp["qkv"].clone()
+    qf2 = torch.empty_like(qf)
+    waves = 16 * torch.cuda.get_device_properties(dev).multi_processor_count
+    cand = {
+        "inplace_rows_ntpl": fl.inplace_rows(qf.data_ptr(), rs, cfg.T, qk_w, waves, 1, 0),
+        "inplace_plpl": fl.inplace(qf.data_ptr(), rs, cfg.T, qk_w, 0, 0),
+        "hipMemcpy2DAsync": fl.memcpy2d(qf2.data_ptr(), rs, qf.data_ptr(), rs, qk_w, cfg.T),
+    }
+    layer["qk_norm_rope"] = dict(cand, _keep=(qf, qf2))
+    groups["qk_norm_rope"] = []
+    for k, v in cand.items():
+        calls[f"qk_norm_rope:{k}"], nbytes[f"qk_norm_rope:{k}"] = v, 2 * cfg.T * qk_w
+        groups["qk_norm_rope"].append(f"qk_norm_rope:{k}")
+    # SwiGLU: gate and up halves of each [T, 2I] row in, [T, I] out (318 + 159 MB). The runtime's copies
+    # move as many bytes in as out, so theirs is the same total (239 + 239 MB) in a 1:1 mix.
+    gi = cfg.T * cfg.I * 2
+    h = inp["h"]
+    gout = torch.empty((cfg.T, cfg.I), dtype=torch.float16, device=dev)
+    tot = 3 * gi // 2 // 16 * 16
+    s1, d1 = rand_bytes(tot), rand_bytes(tot)
+    cand = {
+        "rows2_ntpl": fl.rows2(h.data_ptr(), 2 * gi // cfg.T, gout.data_ptr(), gi // cfg.T, cfg.T, gi // cfg.T, 1, 0),
+        "copy2_ntpl": fl.copy2(h.data_ptr(), h.data_ptr() + gi, gout.data_ptr(), gi, 1, 0),
+        "hipMemcpyAsync_same_total": fl.memcpy(d1.data_ptr(), s1.data_ptr(), tot),
+    }
+    layer["swiglu"] = dict(cand, _keep=(gout, s1, d1))
+    groups["swiglu"] = []
+    for k, v in cand.items():
+        calls[f"swiglu:{k}"], nbytes[f"swiglu:{k}"] = v, 3 * gi if not k.startswith("hip") else 2 * tot
+        groups["swiglu"].append(f"swiglu:{k}")
+    return calls, nbytes, groups, layer
+
+
+def time_ops(calls, op_bytes, names, steps, warmup, flush, timer, flushes=None, tails=None):
+    """Times each named op: `warmup` untimed rounds, then `steps` rounds, each op after a cache
+    flush (unless flush is None) inside its own event pair. flushes: {name: buffer} replacing the flush
+    buffer for those ops; tails: {name: fn} run after the op inside its event pair. Returns (per-op
+    stats, wall ms/round)."""
+    import torch
+
+    flushes, tails = flushes or {}, tails or {}
 
     def step(record):
         for name in names:
-            if flush is not None:
-                flush.sum()
+            fl = flushes.get(name, flush)
+            if fl is not None:
+                fl.sum()
             if record is None:
                 calls[name]()
+                if name in tails:
+                    tails[name]()
             else:
                 s, e = record[name]
                 timer.record(s)
                 calls[name]()
+                if name in tails:
+                    tails[name]()
                 timer.record(e)
 
     for _ in range(warmup):
@@ -204,11 +346,38 @@ def gpu_bench(args):
     timer = HipTimer(torch.cuda.current_stream().cuda_stream)
     per_op, wall = time_ops(calls, cfg.op_bytes(), names, args.steps, args.warmup,
                             None if args.no_flush else flush, timer)
+    progress("ops timed")
     layer = None
+    floors = None
     if not args.only:
         layer = time_layer(calls, names, args.steps, args.warmup, None if args.no_flush else flush,
                            HipTimer(torch.cuda.current_stream().cuda_stream))
-    return cfg, per_op, wall, layer
+        progress("layer step timed")
+        if not args.no_floors:
+            floors = time_floors(cfg, inp, dev, args, None if args.no_flush else flush)
+            progress("floors timed")
+    return cfg, per_op, wall, layer, floors
+
+
+def time_floors(cfg, inp, dev, args, flush):
+    """Per-op floors measured in the same run as the ops, under the same events and flush: every
+    candidate of headline_floors timed in its own rounds, the fastest per op taken as that op's floor,
+    and the layer-floor step (the four ops' fastest floors back-to-back after one flush, one event
+    pair, as the layer step is timed)."""
+    import torch
+
+    stream = torch.cuda.current_stream().cuda_stream
+    fl = FloorLib(stream)
+    calls, nbytes, groups, layer_cands = headline_floors(cfg, inp, dev, fl)
+    per, _ = time_ops(calls, nbytes, list(calls), args.steps, args.warmup, flush, HipTimer(stream))
+    best = {op: min(names, key=lambda n: per[n]["us"]) for op, names in groups.items()}
+    op_group = {"rmsnorm_in": "rmsnorm", "rmsnorm_post": "rmsnorm", "qk_norm_rope": "qk_norm_rope", "swiglu": "swiglu"}
+    step_calls = {op: layer_cands[op][best[op_group[op]].split(":", 1)[1]] for op in OPS}
+    step = time_layer(step_calls, list(OPS), args.steps, args.warmup, flush, HipTimer(stream))
+    torch.cuda.synchronize()
+    return {"candidates_us": {n: per[n]["us"] for n in calls},
+            "best": {op: {"kind": best[g].split(":", 1)[1], "us": per[best[g]]["us"]} for op, g in op_group.items()},
+            "layer_step_us": round(statistics.median(step) * 1e3, 3)}
 
 
 def _pin_one_core():
@@ -538,6 +707,7 @@ def all_configs(args):
         return args.workload is None or args.workload == label
 
     def run(label, calls, op_bytes, workload, op_flops=None):
+        progress(f"timing {label}")
         timer = HipTimer(torch.cuda.current_stream().cuda_stream)
         per_op, _ = time_ops(calls, op_bytes, list(calls), args.steps, args.warmup, flush, timer)
         for n, f in (op_flops or {}).items():  # MFMA-bound ops: their roofline is the dense f16 peak
@@ -590,6 +760,7 @@ def all_configs(args):
 
     # The streaming floor: kernels that only move bytes, timed exactly as the ops are.
     if want("stream_floor"):
+        progress("timing stream_floor")
         out["stream_floor"] = stream_floor(args, flush, time_ops)
 
     # Qwen3-4B prefill (the headline layer)
@@ -791,40 +962,20 @@ def stream_floor(args, flush, time_ops):
     """What moving the ops' bytes costs with nothing else to do, timed like the ops (same flush and
     events): an empty kernel; 16-byte-per-lane copies with the byte patterns of the Qwen3-4B prefill
     ops (RMSNorm: read 42 MB / write 42 MB; q/k RoPE: 84 / 84; SwiGLU: two 159 MB streams in, one
-    out), and the same bytes in SwiGLU's and the q/k RoPE's own row layouts; a read-only sweep; and
-    the RMSNorm at 4096-32768 rows of 2560 beside copies of the same bytes, with the straight-line
-    fits time = fixed + bytes / rate of both."""
-    import ctypes
-
+    out), and the same bytes in SwiGLU's and the q/k RoPE's own row layouts; the HIP runtime's own
+    device-to-device copies (hipMemcpyAsync, hipMemcpy2DAsync, torch's copy_) of the same bytes; a
+    read-only sweep; the RMSNorm at 4096-32768 rows of 2560 beside copies of the same bytes, with the
+    straight-line fits time = fixed + bytes / rate of both; the RMSNorm and the read sweep after 1, 2
+    and 4 GiB flushes; and each headline op (and its floor) with a 1 GiB read sweep after it inside the
+    event pair, beside the sweep alone -- the difference is the op plus any write-back of its output
+    that the op's own end event does not wait for."""
     import torch
 
     from nekochat_amd import ops
     from nekochat_amd import workloads as wl
 
-    lib = ctypes.CDLL(os.path.join(ROOT, "nekochat_amd", "libneko_floor.so"))
-    for name, args_ in (("neko_floor_empty", [ctypes.c_int, ctypes.c_void_p]),
-                        ("neko_floor_copy", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
-                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
-                        ("neko_floor_copy2", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                              ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
-                        ("neko_floor_read", [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
-                        ("neko_floor_rows2", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
-                                              ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
-                        ("neko_floor_inplace", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
-                        ("neko_floor_inplace_rows", [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-                                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p])):
-        getattr(lib, name).argtypes = args_
-        getattr(lib, name).restype = ctypes.c_int
     dev = torch.device("cuda:0")
-    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream or None)
-
-    def checked(fn, *a):
-        def call():
-            rc = fn(*a, stream)
-            if rc != 0:
-                raise RuntimeError(f"{fn.__name__}: HIP error {rc}")
-        return call
+    fl = FloorLib(torch.cuda.current_stream().cuda_stream)
 
     cfg = wl.QWEN3_PREFILL
     big = 2 * cfg.T * cfg.I * 2  # bytes of the SwiGLU input rows, the largest stream
@@ -837,26 +988,36 @@ def stream_floor(args, flush, time_ops):
     sink = torch.zeros(1024, dtype=torch.float32, device=dev)
     a_ptr, d_ptr = src.data_ptr(), dst.data_ptr()
     calls, nbytes = {}, {}
-    calls["empty_1wg"], nbytes["empty_1wg"] = checked(lib.neko_floor_empty, 1), 0
-    calls["empty_8192wg"], nbytes["empty_8192wg"] = checked(lib.neko_floor_empty, 8192), 0
+    calls["empty_1wg"], nbytes["empty_1wg"] = fl.empty(1), 0
+    calls["empty_8192wg"], nbytes["empty_8192wg"] = fl.empty(8192), 0
     half = cfg.T * cfg.C * 2
     patterns = {"rmsnorm": half, "qk_norm_rope": 2 * cfg.T * (cfg.n_q + cfg.n_kv) * cfg.hd}
     for label, each in patterns.items():  # read `each` bytes, write `each` bytes
         for items in (1, 4):
             for ntl, nts in ((1, 1), (1, 0), (0, 0)):
                 name = f"copy_{label}_i{items}_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
-                calls[name] = checked(lib.neko_floor_copy, a_ptr, d_ptr, each, items, ntl, nts)
+                calls[name] = fl.copy(a_ptr, d_ptr, each, items, ntl, nts)
                 nbytes[name] = 2 * each
+        # the runtime's copy of the same bytes, and torch's copy_ (which calls it)
+        calls[f"hipMemcpyAsync_{label}"], nbytes[f"hipMemcpyAsync_{label}"] = fl.memcpy(d_ptr, a_ptr, each), 2 * each
+        sv, dv = src[:each // 4], dst[:each // 4]
+        calls[f"torch_copy__{label}"], nbytes[f"torch_copy__{label}"] = (lambda d=dv, s=sv: d.copy_(s)), 2 * each
     gi = cfg.T * cfg.I * 2  # SwiGLU: gate and up streams of T x I halves in, T x I out
     for ntl, nts in ((1, 1), (1, 0), (0, 0)):
         name = f"copy2_swiglu_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
-        calls[name] = checked(lib.neko_floor_copy2, a_ptr, a_ptr + gi, d_ptr, gi, ntl, nts)
+        calls[name] = fl.copy2(a_ptr, a_ptr + gi, d_ptr, gi, ntl, nts)
         nbytes[name] = 3 * gi
+    # The runtime's copies cannot read two bytes for each one written: the gate halves of the
+    # [T, 2I] rows copied out (159 + 159 MB, 2D), and a flat copy of the op's total (239 + 239 MB).
+    calls["hipMemcpy2DAsync_swiglu_gate"] = fl.memcpy2d(d_ptr, gi // cfg.T, a_ptr, 2 * gi // cfg.T, gi // cfg.T, cfg.T)
+    nbytes["hipMemcpy2DAsync_swiglu_gate"] = 2 * gi
+    calls["hipMemcpyAsync_swiglu_same_total"] = fl.memcpy(d_ptr, a_ptr, 3 * gi // 2)
+    nbytes["hipMemcpyAsync_swiglu_same_total"] = 3 * gi
     # The same bytes in the ops' own layouts: SwiGLU's gate and up halves of one [T, 2I] row into a
     # [T, I] row; the q/k RoPE's in-place rewrite of the first (n_q + n_kv) hd halves of each qkv row.
     for ntl, nts in ((1, 0), (1, 1), (0, 0)):
         name = f"rows2_swiglu_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
-        calls[name] = checked(lib.neko_floor_rows2, a_ptr, 2 * gi // cfg.T, d_ptr, gi // cfg.T, cfg.T, gi // cfg.T, ntl, nts)
+        calls[name] = fl.rows2(a_ptr, 2 * gi // cfg.T, d_ptr, gi // cfg.T, cfg.T, gi // cfg.T, ntl, nts)
         nbytes[name] = 3 * gi
     # The same SwiGLU-layout stream over constant input (every output line zero): how much cheaper
     # uniform data is, the reason the sources above are random.
@@ -864,13 +1025,13 @@ def stream_floor(args, flush, time_ops):
     # there that the in-place floors after it then rewrote faster than random bits.
     ones = torch.ones(big // 4, dtype=torch.float32, device=dev)
     const_out = torch.empty(gi // 4, dtype=torch.int32, device=dev)
-    calls["rows2_swiglu_ntpl_constdata"] = checked(lib.neko_floor_rows2, ones.data_ptr(), 2 * gi // cfg.T,
-                                                   const_out.data_ptr(), gi // cfg.T, cfg.T, gi // cfg.T, 1, 0)
+    calls["rows2_swiglu_ntpl_constdata"] = fl.rows2(ones.data_ptr(), 2 * gi // cfg.T, const_out.data_ptr(), gi // cfg.T,
+                                                    cfg.T, gi // cfg.T, 1, 0)
     nbytes["rows2_swiglu_ntpl_constdata"] = 3 * gi
     qk_w = (cfg.n_q + cfg.n_kv) * cfg.hd * 2
     for ntl, nts in ((0, 0), (1, 0), (1, 1), (0, 1)):
         name = f"inplace_qk_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
-        calls[name] = checked(lib.neko_floor_inplace, d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, ntl, nts)
+        calls[name] = fl.inplace(d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, ntl, nts)
         nbytes[name] = 2 * cfg.T * qk_w
     # The op itself on the headline's inputs, and the same rewrite of its own qkv buffer in the q/k
     # kernel's schedule: whole rows per wave, wave w taking rows w, w + nw, ..., at the kernel's
@@ -882,33 +1043,85 @@ def stream_floor(args, flush, time_ops):
     waves = 16 * torch.cuda.get_device_properties(dev).multi_processor_count
     for ntl, nts in ((1, 0), (0, 0)):
         name = f"inplace_qk_rows_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
-        calls[name] = checked(lib.neko_floor_inplace_rows, qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T, qk_w,
-                              waves, ntl, nts)
+        calls[name] = fl.inplace_rows(qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T, qk_w, waves, ntl, nts)
         nbytes[name] = 2 * cfg.T * qk_w
-    # (and the flat rewrite over that buffer too)
-    calls["inplace_qk_plpl_opbuf"] = checked(lib.neko_floor_inplace, qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T,
-                                             qk_w, 0, 0)
+    # (and the flat rewrite over that buffer too, and the runtime's 2D copy of those bytes elsewhere)
+    calls["inplace_qk_plpl_opbuf"] = fl.inplace(qk_in["qkv"].data_ptr(), cfg.qkv_stride * 2, cfg.T, qk_w, 0, 0)
     nbytes["inplace_qk_plpl_opbuf"] = 2 * cfg.T * qk_w
-    calls["read_rmsnorm_in"], nbytes["read_rmsnorm_in"] = checked(lib.neko_floor_read, a_ptr, half, sink.data_ptr()), half
+    qk_copy = torch.empty_like(qk_in["qkv"])
+    calls["hipMemcpy2DAsync_qk"] = fl.memcpy2d(qk_copy.data_ptr(), cfg.qkv_stride * 2, qk_in["qkv"].data_ptr(),
+                                               cfg.qkv_stride * 2, qk_w, cfg.T)
+    nbytes["hipMemcpy2DAsync_qk"] = 2 * cfg.T * qk_w
+    calls["read_rmsnorm_in"], nbytes["read_rmsnorm_in"] = fl.read(a_ptr, half, sink.data_ptr()), half
     # RMSNorm [rows, 2560] at four row counts, and copies of the same bytes.
     w = wl.weight_f32(cfg.C, 1.0, 0.05, 2, dev)
     sweep = (4096, 8192, 16384, 32768)
+    norm_io = {}
     for rows in sweep:
         x = wl.normal_f16((rows, cfg.C), 0.0, 1.0, 1, dev)
         y = torch.empty_like(x)
+        norm_io[rows] = (x, y)
         calls[f"rmsnorm_rows{rows}"] = ops.prepare(ops.rms_norm, x, w, cfg.eps, out=y)[0]
         nbytes[f"rmsnorm_rows{rows}"] = wl.bytes_rmsnorm(rows, cfg.C)
-        calls[f"copy_rows{rows}"] = checked(lib.neko_floor_copy, a_ptr, d_ptr, rows * cfg.C * 2, 1, 1, 1)
+        calls[f"copy_rows{rows}"] = fl.copy(a_ptr, d_ptr, rows * cfg.C * 2, 1, 1, 1)
         nbytes[f"copy_rows{rows}"] = 2 * rows * cfg.C * 2
+    # Flush size: the RMSNorm, its copy and the read sweep after 1, 2 and 4 GiB read sweeps (the
+    # default rounds above use 1 GiB).
+    flushes = {}
+    big_flush = {g: torch.ones(g * (256 << 20), dtype=torch.float32, device=dev) for g in (2, 4)}
+    big_flush[1] = flush
+    for g in (1, 2, 4):
+        for base in ("rmsnorm_rows8192", "copy_rows8192", "read_rmsnorm_in"):
+            name = f"{base}_flush{g}gib"
+            calls[name], nbytes[name], flushes[name] = calls[base], nbytes[base], big_flush[g]
+    # Trailing write-back: each headline op (and the floors of its pattern) followed by a 1 GiB read
+    # sweep inside the same event pair, and the sweep alone after the same flush.
+    tails = {}
+    trail = torch.ones(256 << 20, dtype=torch.float32, device=dev)  # not the flush buffer: no hits in it
+
+    def sweep_once():
+        trail.sum()
+
+    h_in = qk_in["h"]
+    g_out = torch.empty((cfg.T, cfg.I), dtype=torch.float16, device=dev)
+    xn = torch.empty_like(qk_in["x"])
+    trailed = {
+        "rmsnorm_op": (ops.prepare(ops.rms_norm, qk_in["x"], qk_in["w_in"], cfg.eps, out=xn)[0],
+                       wl.bytes_rmsnorm(cfg.T, cfg.C)),
+        "copy_rmsnorm_i1_ntnt": (calls["copy_rmsnorm_i1_ntnt"], nbytes["copy_rmsnorm_i1_ntnt"]),
+        "hipMemcpyAsync_rmsnorm": (calls["hipMemcpyAsync_rmsnorm"], nbytes["hipMemcpyAsync_rmsnorm"]),
+        "qk_norm_rope_op": (calls["qk_norm_rope_op"], nbytes["qk_norm_rope_op"]),
+        "inplace_qk_rows_ntpl": (calls["inplace_qk_rows_ntpl"], nbytes["inplace_qk_rows_ntpl"]),
+        "swiglu_op": (ops.prepare(ops.silu_mul, h_in, out=g_out)[0], wl.bytes_swiglu(cfg.T, cfg.I)),
+        "rows2_swiglu_ntpl": (calls["rows2_swiglu_ntpl"], nbytes["rows2_swiglu_ntpl"]),
+    }
+    calls["sweep1gib_alone"], nbytes["sweep1gib_alone"] = sweep_once, 1 << 30
+    for base, (fn, nb) in trailed.items():
+        name = f"{base}+sweep1gib"
+        calls[name], nbytes[name], tails[name] = fn, nb, sweep_once
+        if base not in calls:
+            calls[base], nbytes[base] = fn, nb
     timer = HipTimer(torch.cuda.current_stream().cuda_stream)
-    per_op, _ = time_ops(calls, nbytes, list(calls), args.steps, args.warmup, flush, timer)
+    per_op, _ = time_ops(calls, nbytes, list(calls), args.steps, args.warmup, flush, timer, flushes=flushes,
+                         tails=tails)
     torch.cuda.synchronize()
     fits = {kind: _fit([(nbytes[f"{kind}_rows{r}"], per_op[f"{kind}_rows{r}"]["us"]) for r in sweep])
             for kind in ("rmsnorm", "copy")}
+    alone = per_op["sweep1gib_alone"]["us"]
+    writeback = {base: {"op_us": per_op[base]["us"], "op_plus_sweep_minus_sweep_us": round(per_op[f"{base}+sweep1gib"]["us"] - alone, 3)}
+                 for base in trailed}
+    for v in writeback.values():
+        v["hidden_us"] = round(v["op_plus_sweep_minus_sweep_us"] - v["op_us"], 3)
+    flush_size = {base: {f"{g}GiB": per_op[f"{base}_flush{g}gib"]["us"] for g in (1, 2, 4)}
+                  for base in ("rmsnorm_rows8192", "copy_rows8192", "read_rmsnorm_in")}
+    del big_flush
     return {"workload": "streaming floor: empty kernels, 16-byte copies with the Qwen3-4B prefill ops' byte patterns, "
-                        "RMSNorm rows sweep at hidden 2560 beside copies of the same bytes",
+                        "the runtime's device-to-device copies of the same bytes, RMSNorm rows sweep at hidden 2560 "
+                        "beside copies of the same bytes, flush-size and trailing write-back checks",
             "ops": per_op,
-            "fit_us_plus_bytes_per_rate": {k: {"fixed_us": v[0], "GBps": v[1]} for k, v in fits.items()}}
+            "fit_us_plus_bytes_per_rate": {k: {"fixed_us": v[0], "GBps": v[1]} for k, v in fits.items()},
+            "flush_size_us": flush_size,
+            "trailing_writeback": {"sweep_alone_us": alone, "ops": writeback}}
 
 
 def cpu_baseline(cfg, rows=None, reps=5):
@@ -1016,7 +1229,7 @@ def main():
         print(json.dumps({"metric": METRIC, "unit": "GB/s", "data": "synthetic", "configs": all_configs(args)}),
               flush=True)
         return
-    cfg, per_op, wall, layer = gpu_bench(args)
+    cfg, per_op, wall, layer, floors = gpu_bench(args)
     sum_us = sum(v["us"] for v in per_op.values())
     total_bytes = sum(v["bytes"] for v in per_op.values())
     # The step: the layer's ops back-to-back after one flush, one event pair (median over steps);
@@ -1050,6 +1263,14 @@ def main():
     }
     if layer:
         line["layer_mean_us"] = round(statistics.fmean(layer) * 1e3, 3)
+    if floors:
+        # Each op beside the fastest byte-moving floor of its own pattern, timed in the same run.
+        for op, d in per_op.items():
+            b = floors["best"][op]
+            d["floor_us"], d["floor_kind"] = b["us"], b["kind"]
+            d["over_floor"] = round(d["us"] / b["us"] - 1, 4)
+        line["floors"] = {"candidates_us": floors["candidates_us"], "layer_floor_us": floors["layer_step_us"],
+                          "layer_over_floor": round(total_us / floors["layer_step_us"] - 1, 4)}
     if not args.only or args.only == DOMINANT:
         d = per_op[DOMINANT]
         achieved = d["bytes"] / (d["mean_us"] * 1e-6) / 1e9
