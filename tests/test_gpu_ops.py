@@ -32,10 +32,13 @@ def _w(n, stream, dev, mean=1.0, std=0.05):
 # ------------------------------------------------------------------ RMSNorm
 
 @pytest.mark.parametrize("T,C,eps", [
-    (64, 1024, 1e-6),      # Qwen3-0.6B decode
-    (8192, 2560, 1e-6),    # Qwen3-4B prefill
-    (16384, 1536, 1e-5),   # Granite pre-norm: one row per wave over the whole grid
-    (32768, 2560, 1e-6),   # one row per wave (more than 3 rows per resident persistent wave)
+    (64, 1024, 1e-6),      # Qwen3-0.6B decode (one round, one row per wave)
+    (8192, 2560, 1e-6),    # Qwen3-4B prefill (one round, two rows per wave)
+    (16384, 1536, 1e-5),   # Granite pre-norm (one round, four rows per wave)
+    (12288, 2560, 1e-6),   # one round, three rows per wave
+    (4096, 2560, 1e-6),    # one round, one row of five chunks per lane
+    (8191, 2000, 1e-6),    # two rows per wave, the last wave one short; 250 chunks: lanes past the row end
+    (32768, 2560, 1e-6),   # one row per wave over the whole grid (more than one round's four rows per wave)
     (3, 96, 1e-6),         # reference self-test width
     (5, 4104, 1e-6),       # four waves per row
     (7, 100, 1e-6),        # width not a multiple of 8: fallback kernel
@@ -93,9 +96,10 @@ def test_prepared_call_keeps_its_stream(dev):
     assert torch.equal(out, want)
 
 
-@pytest.mark.parametrize("T", [17, 40000])
+@pytest.mark.parametrize("T", [17, 40000, 8192])
 def test_rmsnorm_f32(dev, T):
-    """17 rows: the persistent kernel; 40000 rows of 1024 floats: the one-row-per-wave grid."""
+    """17 rows of 2560 floats: four waves per row; 40000 rows of 1024 floats: the one-row-per-wave
+    grid; 8192 rows of 1024: one round, two rows per wave."""
     _case(f"rmsnorm f32 T={T}")
     C = 2560 if T == 17 else 1024
     x = _f16((T, C), 5, dev).float() * 20
@@ -109,6 +113,7 @@ def test_rmsnorm_f32(dev, T):
 # ------------------------------------------------------------------ LayerNorm
 
 @pytest.mark.parametrize("T,C,shift", [(128, 768, 0.0), (64, 1024, 100.0), (3, 96, 0.0), (9, 770, 3.0), (4, 2560, 0.0),
+                                       (8192, 768, 2.0), (12287, 512, 0.5),  # one round: two / three rows per wave
                                        (40000, 768, 1.0)])  # the last: one row per wave over the grid
 def test_layernorm_f16(dev, T, C, shift):
     _case(f"layernorm f16 T={T} C={C} shift={shift}")
