@@ -205,9 +205,10 @@ int neko_hip_quantize_rows(neko_hip_ctx* ctx, int fmt, int64_t rows, int64_t col
  * 2^24 elements) a VALU kernel (1.0-1.3x the f16 time at one token); beyond, each row split into
  * two f16 planes (scaled by a power of two) for the MFMA kernels, about 2-3x the f16 time, with the call's context workspace holding the
  * planes and sums. Other shapes take a generic kernel.
- * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown) by the
- * first call that needs more; outgrown buffers are kept too (graphs captured earlier still point at
- * them), all until neko_hip_destroy. A call that would grow it while the context's stream is under
+ * Shapes that split K keep f32 partial sums in a per-context workspace: allocated (or grown, to the
+ * next power of two) by the first call that needs more; outgrown buffers are kept too (graphs
+ * captured earlier still point at them), all until neko_hip_destroy -- together always less than the
+ * live buffer. A call that would grow it while the context's stream is under
  * graph capture fails with NEKO_ERR_INVALID: make one uncaptured call at the largest shape first, or
  * capture neko_hip_matmul_noalloc. */
 #define NEKO_MM_GELU 1
@@ -217,14 +218,18 @@ int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t 
                     int x_dtype, int y_dtype);
 
 /* neko_hip_matmul without any allocation: the same kernels, the same split of K and bit-identical
- * results, but split-K partial sums go to a fixed 32 MiB array in device memory (one per GPU, held
- * from the library's first use on that GPU until the process ends) instead of the context's
- * workspace. No counterpart in the reference: this is for callers that cannot allocate -- code under
- * HIP graph capture, serving loops, harnesses that forbid hipMalloc. A shape whose split needs more
- * than 32 MiB of partial sums (none of the Qwen3-0.6B/4B layer projections at any token count; an
- * FP8/FP4 vocabulary-sized product at 13-47 tokens does) returns NEKO_ERR_UNSUPPORTED before anything
- * is launched. Every call on one GPU shares that array: calls that may overlap in time on one GPU
- * (other streams, other contexts or threads) race and must be ordered by the caller. */
+ * results, but the memory neko_hip_matmul takes from the context's workspace -- split-K partial sums,
+ * and for f32 activations from 9 tokens (17 for weights of at most 2^24 elements) the two f16 planes
+ * and their sums -- comes from a fixed 32 MiB array in device memory (one per GPU, held from the
+ * library's first use on that GPU until the process ends). No counterpart in the reference: this is
+ * for callers that cannot allocate -- code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc. A shape that needs more than the array holds (none of the Qwen3-0.6B/4B layer
+ * projections with f16 activations at any token count; an FP8/FP4 vocabulary-sized product at 13-47
+ * tokens, or f32 activations at prefill sizes, do) returns NEKO_ERR_UNSUPPORTED before anything is
+ * launched. The array belongs to the first context that calls this entry point on its GPU until that
+ * context is destroyed; a call through any other context returns NEKO_ERR_UNSUPPORTED. Calls through
+ * the owning context are ordered on its stream; a caller that replays graphs captured from them on
+ * several streams at once must order those replays itself. */
 int neko_hip_matmul_noalloc(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
                             int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride,
                             int flags, int x_dtype, int y_dtype);

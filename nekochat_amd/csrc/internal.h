@@ -45,13 +45,17 @@ int after_launch(neko_hip_ctx* ctx, const char* what);
 FastDiv make_fast_div(uint32_t d);
 
 // The context's device workspace `slot` (0 or 1), at least `bytes` long, shared by every op on ctx.
-// Grown on demand; an outgrown buffer stays allocated until neko_hip_destroy, since queued work and
-// captured graphs may still use it. Growing while ctx's stream is under graph capture fails
-// (NEKO_ERR_INVALID).
+// Grown on demand to the next power of two; an outgrown buffer stays allocated until
+// neko_hip_destroy, since queued work and captured graphs may still use it -- the doubling keeps all
+// retired buffers of a slot together smaller than its live one. Growing while ctx's stream is under
+// graph capture fails (NEKO_ERR_INVALID).
 int workspace(neko_hip_ctx* ctx, size_t bytes, void** out, int slot = 0);
 // Looks up (once per device, with that device current) and records in ctx the device address of
-// the fixed split-K scratch array that neko_hip_matmul_noalloc uses (matmul.hip).
+// the fixed scratch array that neko_hip_matmul_noalloc uses (matmul.hip).
 int matmul_scratch_setup(neko_hip_ctx* ctx);
+// Gives up ctx's claim on its device's scratch array (taken by its first neko_hip_matmul_noalloc
+// call), once its stream has drained.
+void matmul_scratch_release(const neko_hip_ctx* ctx);
 // Whether `stream` is under graph capture.
 int capturing(neko_hip_ctx* ctx, hipStream_t stream, bool* yes);
 

@@ -1887,13 +1887,15 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 // ---------------------------------------------------------------- f32 activations on the MFMA kernels
 //
 // Row t of f32 activations becomes two f16 rows, scaled by a power of two s_t that puts the row's
-// largest magnitude in [2^14, 2^15): hi = f16(x s_t), lo = f16(x s_t - hi). hi + lo holds x s_t to
-// within 2^-22 of its magnitude (the largest |x| never overflows f16, values more than 2^28 below it
-// lose bits only beside it), so y = (hi . W + lo . W) / s_t, two f16 matmuls and an exact rescale,
-// stays far inside the f32 summation bound that every matmul path meets.
+// largest finite magnitude in [2^14, 2^15): hi = f16(x s_t), lo = f16(x s_t - hi). hi + lo holds x s_t
+// to within 2^-22 of its magnitude (the largest |x| never overflows f16, values more than 2^28 below
+// it lose bits only beside it), so y = (hi . W + lo . W) / s_t, two f16 matmuls and an exact rescale,
+// stays far inside the f32 summation bound that every matmul path meets. An infinite or NaN value
+// keeps its value in hi (inf * s_t = inf) with lo = 0, so its outputs are the +-inf / NaN the f32 dot
+// product gives, and the row's finite values keep their scale.
 constexpr int kSplitThreads = 256;
 
-// One workgroup per row: the row's largest magnitude, then its two planes and 1 / s_t.
+// One workgroup per row: the row's largest finite magnitude, then its two planes and 1 / s_t.
 __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* x, int64_t xs, int K, half_t* hi,
                                                                    half_t* lo, float* inv_s) {
     __shared__ float part[kSplitThreads / kWave];
@@ -1905,7 +1907,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
     for (int i = tid; i < K4; i += kSplitThreads) {
         const float4v v = xr[i];
 #pragma unroll
-        for (int e = 0; e < 4; e++) m = fmaxf(m, fabsf(v[e]));
+        for (int e = 0; e < 4; e++)
+            if (fabsf(v[e]) <= 3.4028235e38f) m = fmaxf(m, fabsf(v[e]));
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -1927,7 +1930,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_rows_kernel(const float* 
         for (int e2 = 0; e2 < 4; e2++) {
             const float u = v[e2] * sc;
             vh[e2] = f16_rne(u);
-            vl[e2] = f16_rne(u - static_cast<float>(vh[e2]));
+            vl[e2] = fabsf(u) <= 3.4028235e38f ? f16_rne(u - static_cast<float>(vh[e2])) : half_t(0.0f);
         }
         reinterpret_cast<half4*>(h)[i] = vh;
         reinterpret_cast<half4*>(l)[i] = vl;
@@ -2064,29 +2067,39 @@ int launch_splitk_reduce(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const 
     return after_launch(ctx, what);
 }
 
-// Split-K partial sums of neko_hip_matmul_noalloc: a fixed array in device memory, so that entry
-// point never allocates. Each device holds its own copy (the runtime places it when the code object
-// loads there) until the process ends. 32 MiB covers every split the planner below makes for the
-// Qwen3-0.6B/4B layer projections at any token count (at most 30 MiB); larger splits are rejected.
+// The scratch memory of neko_hip_matmul_noalloc: split-K partial sums, and for f32 activations the
+// two f16 planes and their sums, in a fixed array in device memory, so that entry point never
+// allocates. Each device holds its own copy (the runtime places it when the code object loads there)
+// until the process ends. 32 MiB covers every split the planner below makes for the Qwen3-0.6B/4B
+// layer projections at any token count with f16 activations (at most 30 MiB); requests beyond it are
+// rejected.
 constexpr size_t kScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-// Device address of `scratch` per device ordinal, looked up once per device by matmul_scratch_setup.
-// On the host, `scratch` names a host-side stand-in, never the device array: only these addresses
-// reach kernels.
+// Device address of `scratch` per device ordinal, looked up once per device by matmul_scratch_setup,
+// and the context that may use it: the first to call neko_hip_matmul_noalloc on the device, until it
+// is destroyed. On the host, `scratch` names a host-side stand-in, never the device array: only these
+// addresses reach kernels.
 std::mutex g_scratch_mu;
 std::map<int, void*> g_scratch_ptr;
+std::map<int, const neko_hip_ctx*> g_scratch_owner;
 
-// Where split-K partials go: the context's growable workspace, or (fixed != nullptr) the scratch
-// array, which is never grown.
-int partial_buffer(neko_hip_ctx* ctx, void* fixed, size_t bytes, float** out, const char* what) {
-    if (fixed) {
-        if (bytes > kScratchBytes)
+// Device memory a call may use instead of the context's workspace: p == nullptr means the workspace
+// (which grows); otherwise `bytes` at p and no more.
+struct Fixed {
+    uint8_t* p = nullptr;
+    size_t bytes = 0;
+};
+
+// Where split-K partials go: the context's growable workspace, or the fixed memory, never grown.
+int partial_buffer(neko_hip_ctx* ctx, const Fixed& fixed, size_t bytes, float** out, const char* what) {
+    if (fixed.p) {
+        if (bytes > fixed.bytes)
             return fail(ctx, NEKO_ERR_UNSUPPORTED,
                         "%s: this shape splits K into %zu bytes of partial sums; the allocation-free entry point "
-                        "holds at most %zu (call neko_hip_matmul instead)",
-                        what, bytes, kScratchBytes);
-        *out = static_cast<float*>(fixed);
+                        "has %zu of its %zu bytes for them (call neko_hip_matmul instead)",
+                        what, bytes, fixed.bytes, kScratchBytes);
+        *out = reinterpret_cast<float*>(fixed.p);
         return NEKO_OK;
     }
     void* ws = nullptr;
@@ -2097,7 +2110,7 @@ int partial_buffer(neko_hip_ctx* ctx, void* fixed, size_t bytes, float** out, co
 
 int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w, int64_t row_bytes,
                 int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int x_dtype, int y_dtype,
-                void* fixed, const char* what);
+                const Fixed& fixed, const char* what);
 
 #ifndef NEKO_TUNE_MM_F32_SPLIT_MIN_T
 #define NEKO_TUNE_MM_F32_SPLIT_MIN_T 9
@@ -2119,14 +2132,29 @@ constexpr int64_t kF32SmallNK = int64_t{1} << 24;
 
 // f32 activations (16-byte aligned rows, K % 32 == 0) as two f16 planes: both through the f16 paths
 // into f32 sums in workspace slot 1 (any split of K uses slot 0), then rescaled into y with the call's
-// bias / GELU / accumulate.
-int matmul_f32_split(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const char* what) {
+// bias / GELU / accumulate. With fixed memory, the planes and sums take its start and any split of K
+// the rest.
+int matmul_f32_split(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const Fixed& fixed, const char* what) {
     const int64_t T = a.T, K = a.K, N = a.N;
     const auto up = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
     const size_t plane = up(static_cast<size_t>(T) * K * 2), sums = up(static_cast<size_t>(T) * N * 4);
-    void* ws = nullptr;
-    if (int rc = workspace(ctx, 2 * plane + sums + up(static_cast<size_t>(T) * 4), &ws, 1)) return rc;
-    uint8_t* base = static_cast<uint8_t*>(ws);
+    const size_t need = 2 * plane + sums + up(static_cast<size_t>(T) * 4);
+    uint8_t* base = nullptr;
+    Fixed rest;
+    if (fixed.p) {
+        if (need > fixed.bytes)
+            return fail(ctx, NEKO_ERR_UNSUPPORTED,
+                        "%s: f32 activations of this shape need %zu bytes for their f16 planes and sums; the "
+                        "allocation-free entry point holds at most %zu (call neko_hip_matmul instead)",
+                        what, need, fixed.bytes);
+        base = fixed.p;
+        rest.p = fixed.p + need;
+        rest.bytes = fixed.bytes - need;
+    } else {
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, need, &ws, 1)) return rc;
+        base = static_cast<uint8_t*>(ws);
+    }
     half_t* hi = reinterpret_cast<half_t*>(base);
     half_t* lo = reinterpret_cast<half_t*>(base + plane);
     float* s = reinterpret_cast<float*>(base + 2 * plane);
@@ -2135,11 +2163,10 @@ int matmul_f32_split(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const char
     hipLaunchKernelGGL(split_rows_kernel, dim3(static_cast<uint32_t>(T)), dim3(kSplitThreads), 0, ctx->stream,
                        static_cast<const float*>(a.x), a.xs, static_cast<int>(K), hi, lo, inv);
     if (int rc = after_launch(ctx, what)) return rc;
-    if (int rc = matmul_impl(ctx, hi, K, T, K, a.w, a.rb, a.fmt, N, nullptr, s, N, 0, NEKO_DT_F16, NEKO_DT_F32, nullptr,
-                             what))
+    if (int rc = matmul_impl(ctx, hi, K, T, K, a.w, a.rb, a.fmt, N, nullptr, s, N, 0, NEKO_DT_F16, NEKO_DT_F32, rest, what))
         return rc;
     if (int rc = matmul_impl(ctx, lo, K, T, K, a.w, a.rb, a.fmt, N, nullptr, s, N, kAccumulate, NEKO_DT_F16, NEKO_DT_F32,
-                             nullptr, what))
+                             rest, what))
         return rc;
     const dim3 grid(static_cast<uint32_t>((T * N + 255) / 256));
     if (y_dtype == NEKO_DT_F16) hipLaunchKernelGGL((combine_rows_kernel<half_t>), grid, dim3(256), 0, ctx->stream, a, s, inv);
@@ -2149,7 +2176,7 @@ int matmul_f32_split(neko_hip_ctx* ctx, const MmArgs& a, int y_dtype, const char
 
 int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w, int64_t row_bytes,
                 int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int x_dtype, int y_dtype,
-                void* fixed, const char* what) {
+                const Fixed& fixed, const char* what) {
     NEKO_ENTER(ctx);
     NEKO_REQUIRE(ctx, valid_dtype(x_dtype) && valid_dtype(y_dtype), "%s: bad dtype x=%d y=%d", what, x_dtype, y_dtype);
     NEKO_REQUIRE(ctx, fmt == NEKO_FMT_F16 || fmt == NEKO_FMT_FP8 || fmt == NEKO_FMT_FP4, "%s: bad weight format %d", what,
@@ -2179,10 +2206,10 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                       aligned(w, 16) && row_bytes % 16 == 0;
     const bool fast32 = x_dtype == NEKO_DT_F32 && K % kBlockK == 0 && aligned(x, 16) && x_stride % 4 == 0 &&
                         aligned(w, 16) && row_bytes % 16 == 0;
-    // f32 activations from kF32SplitMinT tokens: two f16 planes through the MFMA kernels. Below, and
-    // in the allocation-free entry (no workspace), the f32 GEMV.
-    if (fast32 && !fixed && T >= (N * K <= kF32SmallNK ? kF32SplitMinTSmall : kF32SplitMinT))
-        return matmul_f32_split(ctx, a, y_dtype, what);
+    // f32 activations from kF32SplitMinT tokens: two f16 planes through the MFMA kernels; below, the
+    // f32 GEMV.
+    if (fast32 && T >= (N * K <= kF32SmallNK ? kF32SplitMinTSmall : kF32SplitMinT))
+        return matmul_f32_split(ctx, a, y_dtype, fixed, what);
     // Decode-sized T: the GEMV path, NT tokens per pass with their activations staged in 64 KB of LDS.
     int gemv_nt = 0;
     if ((fast && T <= kGemvMaxT) || (fast32 && T <= kGemv32MaxT)) {
@@ -2348,6 +2375,12 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
 
 }  // namespace
 
+void matmul_scratch_release(const neko_hip_ctx* ctx) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_owner.find(ctx->device);
+    if (it != g_scratch_owner.end() && it->second == ctx) g_scratch_owner.erase(it);
+}
+
 int matmul_scratch_setup(neko_hip_ctx* ctx) {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     auto it = g_scratch_ptr.find(ctx->device);
@@ -2368,7 +2401,7 @@ using namespace neko_hip;
 extern "C" int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w,
                                int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride,
                                int flags, int x_dtype, int y_dtype) {
-    return matmul_impl(ctx, x, x_stride, T, K, w, row_bytes, fmt, N, bias, y, y_stride, flags, x_dtype, y_dtype, nullptr,
+    return matmul_impl(ctx, x, x_stride, T, K, w, row_bytes, fmt, N, bias, y, y_stride, flags, x_dtype, y_dtype, Fixed{},
                        "neko_hip_matmul");
 }
 
@@ -2377,6 +2410,21 @@ extern "C" int neko_hip_matmul_noalloc(neko_hip_ctx* ctx, const void* x, int64_t
                                        int64_t y_stride, int flags, int x_dtype, int y_dtype) {
     const char* what = "neko_hip_matmul_noalloc";
     NEKO_REQUIRE(ctx, ctx && ctx->scratch, "%s: null context, or its device's scratch address was not set up", what);
-    return matmul_impl(ctx, x, x_stride, T, K, w, row_bytes, fmt, N, bias, y, y_stride, flags, x_dtype, y_dtype,
-                       ctx->scratch, what);
+    {
+        // One context per device uses the array at a time: calls through one context are ordered on
+        // its stream, calls through two could overlap and overwrite each other's partial sums.
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        auto it = g_scratch_owner.find(ctx->device);
+        if (it == g_scratch_owner.end()) g_scratch_owner.emplace(ctx->device, ctx);
+        else if (it->second != ctx)
+            return fail(ctx, NEKO_ERR_UNSUPPORTED,
+                        "%s: device %d's scratch array belongs to another live context (the first to call this entry "
+                        "point on the device, until it is destroyed); use that context, or neko_hip_matmul",
+                        what, ctx->device);
+    }
+    Fixed fixed;
+    fixed.p = static_cast<uint8_t*>(ctx->scratch);
+    fixed.bytes = kScratchBytes;
+    return matmul_impl(ctx, x, x_stride, T, K, w, row_bytes, fmt, N, bias, y, y_stride, flags, x_dtype, y_dtype, fixed,
+                       what);
 }

@@ -96,12 +96,16 @@ int workspace(neko_hip_ctx* ctx, size_t bytes, void** out, int slot) {
                         "matmul workspace must grow to %zu bytes (holds %zu) while the stream is being captured: make "
                         "one uncaptured call at the largest shape first, or capture neko_hip_matmul_noalloc",
                         bytes, ctx->workspace_bytes[slot]);
+        // The next power of two (at least 1 MiB): the buffers a slot outgrows add up to less than the
+        // one it has, however the requests rise.
+        size_t grown = size_t(1) << 20;
+        while (grown < bytes) grown <<= 1;
         void* p = nullptr;
-        if (int rc = check(ctx, hipMalloc(&p, bytes), "hipMalloc (workspace)")) return rc;
+        if (int rc = check(ctx, hipMalloc(&p, grown), "hipMalloc (workspace)")) return rc;
         // The old buffer is retired, not freed: queued work and graphs captured earlier still use it.
         if (ctx->workspace[slot]) ctx->retired.push_back(ctx->workspace[slot]);
         ctx->workspace[slot] = p;
-        ctx->workspace_bytes[slot] = bytes;
+        ctx->workspace_bytes[slot] = grown;
     }
     *out = ctx->workspace[slot];
     return NEKO_OK;
@@ -149,6 +153,7 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     if (!ctx) return NEKO_OK;
     int rc = enter(ctx);
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    matmul_scratch_release(ctx);
     for (void* p : ctx->allocs) (void)hipFree(p);
     for (void* p : ctx->workspace)
         if (p) (void)hipFree(p);

@@ -342,17 +342,20 @@ def test_matmul_f32_activations_random_within_bound(dev, fmt, T, K, N):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_matmul_f32_activations_row_magnitudes(dev, fmt):
-    """f32 activation rows far outside f16's range, tiny, zero, and with values 2^30 apart in one row,
-    through the two-plane path (each row scaled by its own power of two): within the bound."""
-    _case(f"matmul f32 activations row magnitudes fmt={fmt}")
+@pytest.mark.parametrize("T", [16, 24])
+def test_matmul_f32_activations_row_magnitudes(dev, fmt, T):
+    """f32 activation rows far outside f16's range, tiny, zero, and with values 2^30 apart in one row:
+    T = 24 through the two-plane path (each row scaled by its own power of two, the 3e-38 row at the
+    scale's 2^126 clamp), T = 16 through the f32 GEMV (weights of at most 2^24 elements keep it through
+    16 tokens): within the bound."""
+    _case(f"matmul f32 activations row magnitudes fmt={fmt} T={T}")
     rng = np.random.default_rng(77 + fmt)
-    T, K, N = 16, 2560, 384
+    K, N = 2560, 384
     w = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
     tab, _ = ops.quantize_rows(fmt, w)
     wd = M.dequant(fmt, tab, K)
     x = rng.standard_normal((T, K)).astype(np.float32)
-    scale = np.array([1e30, 1e-30, 1e5, 1e-5, 0.0, 7e4, 1.0, 3e-38] + [1.0] * 8, np.float32)
+    scale = np.array([1e30, 1e-30, 1e5, 1e-5, 0.0, 7e4, 1.0, 3e-38] + [1.0] * (T - 8), np.float32)
     x *= scale[:, None]
     x[8, :K // 2] *= np.float32(2.0 ** -30)  # one row holding values 2^30 apart
     x[9, 7] = np.float32(6e4)                # one outlier in an ordinary row
@@ -362,6 +365,41 @@ def test_matmul_f32_activations_row_magnitudes(dev, fmt):
     exact, mag = M.exact_and_bound(x, wd, bias)
     assert np.isfinite(y).all()
     _bound_check(y, exact, mag, K, f"f32 row magnitudes fmt={fmt}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("T", [4, 24])
+def test_matmul_f32_activations_nonfinite(dev, fmt, T):
+    """f32 activation rows holding one +inf, one -inf or one NaN (T = 4: the f32 GEMV; T = 24: the
+    two-plane split, where such a value must not set its row's scale): every output of those rows is
+    the IEEE value of the float64 product -- +-inf by the sign of the weight, NaN where the weight is
+    zero or the value is NaN -- and every other row stays within the bound."""
+    _case(f"matmul f32 activations non-finite fmt={fmt} T={T}")
+    rng = np.random.default_rng(91 + 7 * fmt + T)
+    K, N = 2560, 384
+    w = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    tab, _ = ops.quantize_rows(fmt, w)
+    wd = M.dequant(fmt, tab, K)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    special = {0: (5, np.inf), 1: (700, -np.inf), 2: (1300, np.nan)}
+    for t, (k, v) in special.items():
+        x[t, k] = v
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    y = ops.matmul(torch.from_numpy(x).to(dev), torch.from_numpy(tab).to(dev), fmt, K,
+                   bias=torch.from_numpy(bias).to(dev)).cpu().numpy()
+    wz = wd.astype(np.float64)
+    for t, (k, v) in special.items():
+        col = wz[:, k]
+        if np.isnan(v):
+            want_inf = np.zeros(N, bool)
+        else:
+            want_inf = col != 0
+            assert np.array_equal(np.sign(y[t][want_inf]), np.sign(v * col[want_inf])), f"row {t}: signs"
+        assert np.array_equal(np.isinf(y[t]), want_inf), f"row {t}: infinities"
+        assert np.array_equal(np.isnan(y[t]), ~want_inf), f"row {t}: NaNs"
+    rest = np.arange(3, T)
+    exact, mag = M.exact_and_bound(x[rest], wd, bias)
+    _bound_check(y[rest], exact, mag, K, f"f32 non-finite rows fmt={fmt} T={T}: the other rows")
 
 
 def test_matmul_generic_paths(dev):
