@@ -122,6 +122,7 @@ class FloorLib:
 
         c = ctypes
         self.ct = c
+        self.bound = set()  # functions whose argument types are declared below
         lib = c.CDLL(os.path.join(ROOT, "nekochat_amd", "libneko_floor.so"))
         for name, args_ in (("neko_floor_empty", [c.c_int, c.c_void_p]),
                             ("neko_floor_copy", [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_int, c.c_int,
@@ -134,9 +135,12 @@ class FloorLib:
                             ("neko_floor_inplace", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_int,
                                                     c.c_void_p]),
                             ("neko_floor_inplace_rows", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_int,
-                                                         c.c_int, c.c_void_p])):
+                                                         c.c_int, c.c_void_p]),
+                            ("neko_floor_rows_up", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_int,
+                                                    c.c_int, c.c_int, c.c_void_p])):
             getattr(lib, name).argtypes = args_
             getattr(lib, name).restype = c.c_int
+            self.bound.add(name)
         self.lib = lib
         hip = c.CDLL("libamdhip64.so.7")  # the runtime torch already loaded
         hip.hipMemcpyAsync.argtypes = [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_void_p]
@@ -157,7 +161,12 @@ class FloorLib:
         return call
 
     def __getattr__(self, name):  # floor kernels by their exported name without the prefix
-        fn = getattr(self.lib, "neko_floor_" + name)
+        full = "neko_floor_" + name
+        if full not in self.__dict__.get("bound", ()):
+            # Without declared argument types ctypes passes Python ints as 32-bit C ints: device
+            # pointers would reach the kernel truncated.
+            raise AttributeError(f"{full}: no argument types declared in FloorLib")
+        fn = getattr(self.lib, full)
         return lambda *a: self._checked(fn, *a)
 
     def memcpy(self, dst, src, nbytes):
@@ -187,14 +196,24 @@ def headline_floors(cfg, inp, dev, fl):
 
     calls, nbytes, groups, layer = {}, {}, {}, {}
     half = cfg.T * cfg.C * 2  # one [T, C] fp16 row set
+    # the one-round row kernels' shape: every row of a wave requested before any store (at four waves
+    # per SIMD: ceil(T / (16 CUs)) rows per wave), with and without a barrier between reads and writes
+    r_up = -(-cfg.T // (16 * torch.cuda.get_device_properties(dev).multi_processor_count))
+    row_b = cfg.C * 2
     for op in ("rmsnorm_in", "rmsnorm_post"):
         src, dst = rand_bytes(half), rand_bytes(half)
         cand = {
             "copy_i1_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 1, 1, 1),
             "copy_i4_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 4, 1, 1),
+            "copy_i1_plpl": fl.copy(src.data_ptr(), dst.data_ptr(), half, 1, 0, 0),
+            "copy_i4_plpl": fl.copy(src.data_ptr(), dst.data_ptr(), half, 4, 0, 0),
             "hipMemcpyAsync": fl.memcpy(dst.data_ptr(), src.data_ptr(), half),
             "torch_copy_": (lambda d=dst, s=src: d.copy_(s)),
         }
+        if r_up <= 3 and row_b % 1024 == 0 and row_b // 1024 in (5, 10):
+            for sync in (0, 1):
+                cand[f"rows_up_r{r_up}{'_sync' if sync else ''}"] = fl.rows_up(
+                    src.data_ptr(), row_b, dst.data_ptr(), row_b, cfg.T, r_up, row_b // 1024, sync)
         layer[op] = cand
         if op == "rmsnorm_in":  # both RMSNorms move the same bytes: one set of candidates is timed
             groups["rmsnorm"] = []
@@ -1028,7 +1047,17 @@ def stream_floor(args, flush, time_ops):
     calls["rows2_swiglu_ntpl_constdata"] = fl.rows2(ones.data_ptr(), 2 * gi // cfg.T, const_out.data_ptr(), gi // cfg.T,
                                                     cfg.T, gi // cfg.T, 1, 0)
     nbytes["rows2_swiglu_ntpl_constdata"] = 3 * gi
+    # The one-round shape (every row of a wave loaded before its stores; two rows per wave at 8192
+    # rows), with and without a workgroup barrier between the reads and the writes: the RMSNorm's bytes
+    # copied, the q/k rows rewritten in place.
     qk_w = (cfg.n_q + cfg.n_kv) * cfg.hd * 2
+    for sync in (0, 1):
+        tag = "_sync" if sync else ""
+        calls[f"rows_up_rmsnorm_r2{tag}"] = fl.rows_up(a_ptr, cfg.C * 2, d_ptr, cfg.C * 2, cfg.T, 2, cfg.C * 2 // 1024, sync)
+        nbytes[f"rows_up_rmsnorm_r2{tag}"] = 2 * half
+        calls[f"rows_up_qk_inplace_r2{tag}"] = fl.rows_up(d_ptr, cfg.qkv_stride * 2, d_ptr, cfg.qkv_stride * 2, cfg.T, 2,
+                                                          qk_w // 1024, sync)
+        nbytes[f"rows_up_qk_inplace_r2{tag}"] = 2 * cfg.T * qk_w
     for ntl, nts in ((0, 0), (1, 0), (1, 1), (0, 1)):
         name = f"inplace_qk_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
         calls[name] = fl.inplace(d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, ntl, nts)

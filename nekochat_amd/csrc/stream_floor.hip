@@ -4,7 +4,8 @@
 // reach on this GPU: an empty kernel (launch and completion cost), a 16-byte-per-lane copy (read n,
 // write n), a two-input stream (read 2n, write n: SwiGLU's byte counts), the same with SwiGLU's row
 // layout (both inputs halves of one row), an in-place read-and-write-back of the first part of each
-// row (the q/k RoPE's layout; flat, and in that kernel's per-wave token order), and a read-only sweep.
+// row (the q/k RoPE's layout; flat, and in that kernel's per-wave token order), rows moved in the
+// one-round row kernels' shape (every row of a wave loaded before any store), and a read-only sweep.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -115,6 +116,37 @@ __global__ __launch_bounds__(256) void inplace_rows_kernel(u32x4* buf, int64_t s
     u32x4* q = buf + t * stride + lane;
 #pragma unroll
     for (int j = 0; j < CPL; j++) st<NTS>(q + 64 * j, r[j] ^ key);
+}
+
+// Rows moved in the shape of the one-round row kernels: wave w of nw takes rows w, w + nw, ...,
+// (R of them, nw * R >= rows), issues every load of all R rows before its first store, then stores
+// them; each row is CPL 16-byte chunks per lane (64 * CPL chunks), read at `src` and written at `dst`
+// (the same pointer and stride for an in-place rewrite), xored with `key`. SYNC: a workgroup barrier
+// between the loads and the stores (the workgroup's reads all land before any of its writes, as in
+// the row kernels that stage their weights behind a barrier).
+template <int R, int CPL, bool SYNC>
+__global__ __launch_bounds__(256) void rows_up_kernel(const u32x4* src, int64_t ss, u32x4* dst, int64_t ds, int64_t rows,
+                                                      uint32_t key) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    u32x4 v[R][CPL];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int64_t row = w + r * nw;
+        const u32x4* p = src + (row < rows ? row : 0) * ss + lane;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) v[r][j] = __builtin_nontemporal_load(p + 64 * j);
+    }
+    if constexpr (SYNC) __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int64_t row = w + r * nw;
+        if (row >= rows) break;
+        u32x4* p = dst + row * ds + lane;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) __builtin_nontemporal_store(v[r][j] ^ key, p + 64 * j);
+    }
 }
 
 bool ok16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -233,6 +265,35 @@ int neko_floor_inplace_rows(void* buf, int64_t stride, int64_t rows, int64_t wid
     else if (nt_load) hipLaunchKernelGGL((inplace_rows_kernel<kCpl, true, false>), g, b, 0, st, p, s, rows, 0u);
     else if (nt_store) hipLaunchKernelGGL((inplace_rows_kernel<kCpl, false, true>), g, b, 0, st, p, s, rows, 0u);
     else hipLaunchKernelGGL((inplace_rows_kernel<kCpl, false, false>), g, b, 0, st, p, s, rows, 0u);
+    return hipGetLastError();
+}
+
+// `rows` rows of 64 * cpl 16-byte chunks copied from src (row stride s_stride bytes) to dst (d_stride)
+// by ceil(rows / r) waves, each loading its r rows (rows w, w + nw, ...) before storing them (sync:
+// with a workgroup barrier between); src == dst with equal strides rewrites in place. (r, cpl) in
+// {1, 2, 3} x {5, 10}; strides multiples of 16.
+int neko_floor_rows_up(const void* src, int64_t s_stride, void* dst, int64_t d_stride, int64_t rows, int r, int cpl,
+                       int sync, void* stream) {
+    if (!ok16(src) || !ok16(dst) || s_stride % 16 || d_stride % 16 || rows <= 0 || r < 1 || r > 3 ||
+        (cpl != 5 && cpl != 10) || s_stride < 1024 * cpl || d_stride < 1024 * cpl)
+        return hipErrorInvalidValue;
+    const int64_t waves = (rows + r - 1) / r;
+    const dim3 g(static_cast<uint32_t>((waves + 3) / 4)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* sp = static_cast<const u32x4*>(src);
+    auto* dp = static_cast<u32x4*>(dst);
+    const int64_t ss = s_stride / 16, dsd = d_stride / 16;
+    // The grid holds ceil(waves / 4) * 4 waves; the kernel's nw is that count, so rows w + k nw with
+    // k < r cover every row exactly once.
+    const int64_t nw = static_cast<int64_t>(g.x) * 4;
+    if (nw * r < rows) return hipErrorInvalidValue;
+#define NEKO_ROWS_UP(R, C)                                                                                       \
+    if (r == R && cpl == C) {                                                                                    \
+        if (sync) hipLaunchKernelGGL((rows_up_kernel<R, C, true>), g, b, 0, st, sp, ss, dp, dsd, rows, 0u);       \
+        else hipLaunchKernelGGL((rows_up_kernel<R, C, false>), g, b, 0, st, sp, ss, dp, dsd, rows, 0u);          \
+    }
+    NEKO_ROWS_UP(1, 5) NEKO_ROWS_UP(2, 5) NEKO_ROWS_UP(3, 5) NEKO_ROWS_UP(1, 10) NEKO_ROWS_UP(2, 10) NEKO_ROWS_UP(3, 10)
+#undef NEKO_ROWS_UP
     return hipGetLastError();
 }
 

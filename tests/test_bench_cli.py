@@ -41,3 +41,31 @@ def test_floor_library_exports_what_bench_binds():
     lib = ctypes.CDLL(os.path.join(ROOT, "nekochat_amd", "libneko_floor.so"))
     for n in names:
         assert hasattr(lib, n), f"bench.py binds {n}, which libneko_floor.so does not export"
+
+
+def test_floor_calls_declare_their_argument_types():
+    """bench.FloorLib hands out only floor functions whose ctypes argument types it declares (without
+    them, 64-bit device pointers would be passed as truncated 32-bit ints), and declares one for every
+    function the floor library exports. Checked without a device: the library loads on the CPU."""
+    import ctypes
+    import re
+    import subprocess as sp
+
+    sys.path.insert(0, ROOT)
+    import bench
+
+    fl = bench.FloorLib.__new__(bench.FloorLib)
+    bench.FloorLib.__init__(fl, 0)
+    out = sp.run(["nm", "-D", "--defined-only", os.path.join(ROOT, "nekochat_amd", "libneko_floor.so")],
+                 capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\b(neko_floor_[a-z0-9_]+)\b", out))
+    assert exported and exported == fl.bound, (exported, fl.bound)
+    for name in fl.bound:
+        assert getattr(fl.lib, name).argtypes, name
+    try:
+        fl.not_a_function
+    except AttributeError:
+        pass
+    else:
+        raise AssertionError("FloorLib returned a function without declared argument types")
+    del ctypes
