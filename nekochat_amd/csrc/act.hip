@@ -13,34 +13,18 @@
 namespace neko_hip {
 namespace {
 
-// SwiGLU element: silu(gate) * up in float. SiLU form (knob): 0 libm expf and IEEE division,
-// 1 silu_fast, 2 silu_lite, 3 silu_newton (device.h).
-#ifndef NEKO_TUNE_SWIGLU_SILU
-#define NEKO_TUNE_SWIGLU_SILU 1
-#endif
-__device__ __forceinline__ float swiglu_ref(float gate, float up) {
-    if constexpr (NEKO_TUNE_SWIGLU_SILU == 0) return gate / (1.0f + expf(-gate)) * up;
-    else if constexpr (NEKO_TUNE_SWIGLU_SILU == 1) return silu_fast(gate) * up;
-    else if constexpr (NEKO_TUNE_SWIGLU_SILU == 2) return silu_lite(gate) * up;
-    else return silu_newton(gate) * up;
-}
+// SwiGLU element: silu(gate) * up in float, the SiLU from silu_fast (device.h): the libm form (expf
+// and an IEEE division) made the stream VALU-bound (94% VALUBusy).
+__device__ __forceinline__ float swiglu_ref(float gate, float up) { return silu_fast(gate) * up; }
 
-// SwiGLU loads non-temporal (1) or plain (0); stores non-temporal (1) or plain (0).
-#ifndef NEKO_TUNE_SWIGLU_NT_LOAD
-#define NEKO_TUNE_SWIGLU_NT_LOAD 1
-#endif
-#ifndef NEKO_TUNE_SWIGLU_NT_STORE
-#define NEKO_TUNE_SWIGLU_NT_STORE 0
-#endif
+// SwiGLU loads are non-temporal (measured faster), stores plain.
 template <typename V>
 __device__ __forceinline__ V swiglu_load(const V* p) {
-    if constexpr (NEKO_TUNE_SWIGLU_NT_LOAD) return load_nt(p);
-    else return *p;
+    return load_nt(p);
 }
 template <typename V>
 __device__ __forceinline__ void swiglu_store(V* p, V v) {
-    if constexpr (NEKO_TUNE_SWIGLU_NT_STORE) store_nt(p, v);
-    else *p = v;
+    *p = v;
 }
 
 // GELU: gelu_ref (device.h).

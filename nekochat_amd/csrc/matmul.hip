@@ -167,10 +167,6 @@ __device__ __forceinline__ void store_tiles(const MmArgs& a, const float16v (&ac
 // FP8: codes g*8 .. g*8+7 of the block (8 bytes). FP4: bytes g*4 .. g*4+3 of the 16-byte block, low
 // nibbles (k = g*4 + i) then high nibbles (k = 16 + g*4 + i). F16: halves g*8 .. g*8+7. Loaded raw
 // (so a group can be fetched ahead) and decoded to exact f16 values just before its MFMA.
-#ifndef NEKO_TUNE_MM_FP4_CVT
-#define NEKO_TUNE_MM_FP4_CVT 1
-#endif
-constexpr bool kFp4Cvt = NEKO_TUNE_MM_FP4_CVT;
 
 template <int FMT>
 struct BRaw {
@@ -203,7 +199,7 @@ __device__ __forceinline__ half8 decode_b(typename BRaw<FMT>::T q) {
         h[2] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q[1], 0x0C010C00u));
         h[3] = fp8_pair_bits(__builtin_amdgcn_perm(0u, q[1], 0x0C030C02u));
         return __builtin_bit_cast(half8, h);
-    } else if constexpr (kFp4Cvt) {
+    } else {
         // gfx950's E2M1 -> f16 conversion (scale 1: the code values themselves, exact, -0 for code 8):
         // byte i -> [low nibble, high nibble]; regrouped into the low nibbles of bytes 0..3 then the
         // high nibbles.
@@ -216,14 +212,6 @@ __device__ __forceinline__ half8 decode_b(typename BRaw<FMT>::T q) {
         h[1] = __builtin_amdgcn_perm(c[3], c[2], 0x05040100u);
         h[2] = __builtin_amdgcn_perm(c[1], c[0], 0x07060302u);
         h[3] = __builtin_amdgcn_perm(c[3], c[2], 0x07060302u);
-        return __builtin_bit_cast(half8, h);
-    } else {
-        const uint32_t hi = q >> 4;
-        uint4v h;
-        h[0] = fp4_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C010C00u));
-        h[1] = fp4_pair_bits(__builtin_amdgcn_perm(0u, q, 0x0C030C02u));
-        h[2] = fp4_pair_bits(__builtin_amdgcn_perm(0u, hi, 0x0C010C00u));
-        h[3] = fp4_pair_bits(__builtin_amdgcn_perm(0u, hi, 0x0C030C02u));
         return __builtin_bit_cast(half8, h);
     }
 }
@@ -240,11 +228,11 @@ __device__ __forceinline__ half8 load_a(const half_t* xr, int b, int g) {
     }
 }
 
-// What the block sum is multiplied by besides the f16 scale: decoded FP8 codes are value / 2^8, FP4
-// codes value / 2^14 with the bit-pattern decode and the value itself with the hardware conversion.
+// What the block sum is multiplied by besides the f16 scale: decoded FP8 codes are value / 2^8; FP4
+// codes, from the hardware conversion, the values themselves.
 template <int FMT>
 __device__ __forceinline__ float block_scale_factor() {
-    return FMT == 1 ? 256.0f : (kFp4Cvt ? 1.0f : 16384.0f);
+    return FMT == 1 ? 256.0f : 1.0f;
 }
 
 // One 32-wide block: acc[tt] += scale * (x-tile . codes) (FP8/FP4) or acc[tt] += x-tile . w (F16).
@@ -262,12 +250,6 @@ __device__ __forceinline__ void mma_block(float4v (&acc)[TT], const half8 (&A)[T
     }
 }
 
-#ifndef NEKO_TUNE_MM_WAVE_TARGET
-#define NEKO_TUNE_MM_WAVE_TARGET 1024
-#endif
-#ifndef NEKO_TUNE_MM_MAXW
-#define NEKO_TUNE_MM_MAXW 16
-#endif
 // Weights travel in groups of four 32-wide blocks of each of the tile's 16 rows (256 / 128 / 64
 // contiguous bytes per row for F16 / FP8 / FP4): lanes load a group coalesced, 16 bytes each along
 // the rows, write it to the wave's LDS tile and read their MFMA operands back from there -- a direct
@@ -275,8 +257,8 @@ __device__ __forceinline__ void mma_block(float4v (&acc)[TT], const half8 (&A)[T
 // row tile (the K split) chosen for about kWaveTarget waves in the grid, at most kMaxWaves per
 // workgroup (1024 measured 3-9% faster than 2048-16384 over the Qwen3-4B projections at 3-8 tokens:
 // fewer waves per tile, less cross-wave reduction).
-constexpr int64_t kWaveTarget = NEKO_TUNE_MM_WAVE_TARGET;
-constexpr int kMaxWaves = NEKO_TUNE_MM_MAXW;
+constexpr int64_t kWaveTarget = 1024;
+constexpr int kMaxWaves = 16;
 constexpr int kGroup = 4;  // 32-wide blocks per group: one 8-byte load of a row's 4 block scales
 
 // Bytes of one row's 32-wide block; a group's bytes of one row; 16-byte pieces per lane per group.
@@ -478,13 +460,7 @@ __global__ __launch_bounds__(64 * max_waves(FMT, TT)) void mm_tile_kernel(MmArgs
 // c ^ ((row / 2) % 8), so the 16 rows one ds_read_b128 pass serves fall on distinct bank groups.
 // A stage's loads are issued before the previous stage's MFMAs and waited for (vmcnt) before the
 // barrier that publishes them.
-#ifndef NEKO_TUNE_MM_GEMM3
-#define NEKO_TUNE_MM_GEMM3 1
-#endif
-constexpr bool kGemm3 = NEKO_TUNE_MM_GEMM3;
-#ifndef NEKO_TUNE_MM_G3_GM
-#define NEKO_TUNE_MM_G3_GM 8
-#endif
+constexpr int kG3GroupM = 8;  // token tiles per group of the XCD-contiguous tile walk
 constexpr int kG3BM = 256, kG3BN = 256, kG3Threads = 512;
 
 struct Gemm3Lds {
@@ -507,7 +483,7 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3_kernel(MmArgs a, int t
     uint32_t b = blockIdx.x;
     const uint32_t nb = gridDim.x;
     if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
-    constexpr int GM = NEKO_TUNE_MM_G3_GM;
+    constexpr int GM = kG3GroupM;
     const int group = static_cast<int>(b) / (GM * tiles_n);
     const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
     const int in_group = static_cast<int>(b) - group * GM * tiles_n;
@@ -597,10 +573,6 @@ int launch_gemm3(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn) 
 // v_cvt_scalef32_pk_f16_fp4; exact f16 values), sums each 32-wide block with two MFMAs from zero and
 // adds it into the accumulators scaled by the block's f32 scale (one fma per output per block), as the
 // register-staged kernel does.
-#ifndef NEKO_TUNE_MM_GEMM3Q
-#define NEKO_TUNE_MM_GEMM3Q 1
-#endif
-constexpr bool kGemm3q = NEKO_TUNE_MM_GEMM3Q;
 
 template <int FMT>
 struct Gemm3qLds {
@@ -665,7 +637,7 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3q_kernel(MmArgs a, int 
     uint32_t b = blockIdx.x;
     const uint32_t nb = gridDim.x;
     if (nb % 8 == 0) b = (b % 8) * (nb / 8) + b / 8;
-    constexpr int GM = NEKO_TUNE_MM_G3_GM;
+    constexpr int GM = kG3GroupM;
     const int group = static_cast<int>(b) / (GM * tiles_n);
     const int first_m = group * GM, gm = min(GM, tiles_m - first_m);
     const int in_group = static_cast<int>(b) - group * GM * tiles_n;
@@ -724,9 +696,8 @@ __global__ __launch_bounds__(kG3Threads, 2) void mm_gemm3q_kernel(MmArgs a, int 
                 const int r = wn * 64 + j * 32 + l32;
                 g3q_read_b<FMT>(L.b[buf], bb, r, h, B[j]);
                 const half2v s2 = __builtin_bit_cast(half2v, L.s[buf][r]);
-                // FP8 codes decode to value / 2^8; FP4 always goes through the hardware conversion
-                // here (exact values), whatever the other kernels' decode knob says.
-                sc[j] = static_cast<float>(s2[bb]) * (FMT == 1 ? 256.0f : 1.0f);
+                // FP8 codes decode to value / 2^8; FP4 through the hardware conversion (exact values).
+                sc[j] = static_cast<float>(s2[bb]) * block_scale_factor<FMT>();
             }
 #pragma unroll
             for (int i = 0; i < TM; i++) {
@@ -774,33 +745,13 @@ int launch_gemm3q(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn)
 // that mm_splitk_reduce adds in order. (Adding them in the kernel, by the last workgroup of each row
 // group to arrive, measured several times slower: the device-scope fences that publish the partials
 // write back / invalidate an XCD's whole L2.)
-#ifndef NEKO_TUNE_MM_TILE2
-#define NEKO_TUNE_MM_TILE2 1
-#endif
-#ifndef NEKO_TUNE_MM_T2_LDS
-#define NEKO_TUNE_MM_T2_LDS 65536
-#endif
-#ifndef NEKO_TUNE_MM_T2_MIN_F16
-#define NEKO_TUNE_MM_T2_MIN_F16 16
-#endif
-#ifndef NEKO_TUNE_MM_T2_MIN_FP8
-#define NEKO_TUNE_MM_T2_MIN_FP8 12
-#endif
-#ifndef NEKO_TUNE_MM_T2_MIN_FP4
-#define NEKO_TUNE_MM_T2_MIN_FP4 4
-#endif
-#ifndef NEKO_TUNE_MM_T2_MAX_T
-#define NEKO_TUNE_MM_T2_MAX_T 48
-#endif
-#ifndef NEKO_TUNE_MM_T2_FILL
-#define NEKO_TUNE_MM_T2_FILL 4
-#endif
-constexpr bool kTile2 = NEKO_TUNE_MM_TILE2;
 constexpr int kT2Waves = 4;
-constexpr int kT2Lds = NEKO_TUNE_MM_T2_LDS;  // LDS per workgroup (two per CU at 64 KB)
-constexpr int64_t kT2MaxT = NEKO_TUNE_MM_T2_MAX_T;  // exclusive; at most 65 (four 16-token tiles)
+constexpr int kT2Lds = 65536;  // LDS per workgroup (two per CU at 64 KB)
+constexpr int64_t kT2MaxT = 48;  // exclusive; at most 65 (four 16-token tiles)
 static_assert(kT2MaxT <= 65, "the shared-activation kernel holds at most 64 tokens");
-constexpr int kT2Fill = NEKO_TUNE_MM_T2_FILL; // K slices until the grid holds this many workgroups per CU
+constexpr int kT2Fill = 4;  // K slices until the grid holds this many workgroups per CU
+// Token counts above which each format takes this kernel (below: the per-wave tile kernel).
+constexpr int64_t kT2MinF16 = 16, kT2MinFp8 = 12, kT2MinFp4 = 4;
 
 
 // Halves per staged token row for nb blocks: 32 nb plus 8 of padding (16-byte bank groups differ
@@ -1042,17 +993,11 @@ __device__ __forceinline__ float block_dot(const uint4v (&q)[FMT == 0 ? 4 : FMT 
     return d;
 }
 
-#ifndef NEKO_TUNE_MM_GEMV_MAX_T
-#define NEKO_TUNE_MM_GEMV_MAX_T 2
-#endif
-#ifndef NEKO_TUNE_MM_GEMV_WAVE_TARGET
-#define NEKO_TUNE_MM_GEMV_WAVE_TARGET 8192
-#endif
 // Largest T taking the GEMV path: 2 (measured on the Qwen3-4B projections: at 3 and 4 tokens the
 // MFMA tile kernels take 14% less time over the four projections, at 2 the GEMV 11% less).
-constexpr int64_t kGemvMaxT = NEKO_TUNE_MM_GEMV_MAX_T;
+constexpr int64_t kGemvMaxT = 2;
 static_assert(kGemvMaxT >= 1 && kGemvMaxT <= 4, "the GEMV holds 1, 2 or 4 tokens per pass");
-constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
+constexpr int64_t kGemvWaveTarget = 8192;
 // f32 activations (the reference's own type, as its ComputeBackend passes them) take the GEMV below
 // the two-plane split's threshold, and at any T its grid holds where the split cannot run (the
 // allocation-free entry): the MFMA kernels read f16 activations, and the GEMV's NT-token passes beat
@@ -1060,10 +1005,7 @@ constexpr int64_t kGemvWaveTarget = NEKO_TUNE_MM_GEMV_WAVE_TARGET;
 constexpr int64_t kGemv32MaxT = 65535;
 constexpr int kGemvRows = 4;    // weight rows per wave: 16 lanes each
 constexpr int kGemvWaves = 8;   // waves per workgroup: (8 / kw) row groups x kw slices of K
-#ifndef NEKO_TUNE_MM_GEMV_BATCH
-#define NEKO_TUNE_MM_GEMV_BATCH 2
-#endif
-constexpr int kGemvBatch = NEKO_TUNE_MM_GEMV_BATCH;  // 32-wide blocks per lane whose weights are requested together
+constexpr int kGemvBatch = 2;  // 32-wide blocks per lane whose weights are requested together
 
 // Grid: x = workgroups of 4 * 8 / kw weight rows, y = chunks of NT tokens. Wave w works on row
 // group w / kw and K slice w % kw (a.blocks_per_wave blocks). Dynamic LDS: the chunk's activations as TX [NT][xrow], rows padded as above (FP4: each 32-block
@@ -1191,48 +1133,20 @@ __host__ __device__ constexpr size_t gemv_lds_bytes(int K, int nt, int x_bytes =
 // codes decoded once to exact f16 values -- in double-buffered LDS; the next step's global loads are
 // in flight during this step's MFMAs. LDS bytes per MFMA fall as the wave tile grows (both operand
 // fragments are reused across the other dimension), which is what bounds a 64 x 64 wave tile.
-#ifndef NEKO_TUNE_MM_GEMM_MIN_T
-#define NEKO_TUNE_MM_GEMM_MIN_T 48
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_MIN_T_F16
-#define NEKO_TUNE_MM_GEMM_MIN_T_F16 33
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_MF
-#define NEKO_TUNE_MM_GEMM_MF 4
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_NF
-#define NEKO_TUNE_MM_GEMM_NF 4
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_WM
-#define NEKO_TUNE_MM_GEMM_WM 2
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_WN
-#define NEKO_TUNE_MM_GEMM_WN 2
-#endif
 // Smallest T taking the GEMM path: from 33 tokens for F16 rows, 48 for FP8 / FP4 (measured on the
 // Qwen3-4B projections: below these the shared-activation kernel's three token tiles are faster).
-constexpr int64_t kGemmMinT = NEKO_TUNE_MM_GEMM_MIN_T;
-constexpr int64_t kGemmMinTF16 = NEKO_TUNE_MM_GEMM_MIN_T_F16;
-constexpr int kGemmMF = NEKO_TUNE_MM_GEMM_MF, kGemmNF = NEKO_TUNE_MM_GEMM_NF;  // 16 x 16 fragments per wave
-constexpr int kGemmWM = NEKO_TUNE_MM_GEMM_WM, kGemmWN = NEKO_TUNE_MM_GEMM_WN;  // waves per workgroup
+constexpr int64_t kGemmMinT = 48;
+constexpr int64_t kGemmMinTF16 = 33;
+constexpr int kGemmMF = 4, kGemmNF = 4;  // 16-wide fragments per wave (two 32 x 32 MFMA tiles each way)
+constexpr int kGemmWM = 2, kGemmWN = 2;  // waves per workgroup
 constexpr int kGemmThreads = 64 * kGemmWM * kGemmWN;
 constexpr int kGemmBM = 16 * kGemmMF * kGemmWM, kGemmBN = 16 * kGemmNF * kGemmWN, kGemmBK = 32;
-#ifndef NEKO_TUNE_MM_GEMM_ROW
-#define NEKO_TUNE_MM_GEMM_ROW 40
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_SWZ
-#define NEKO_TUNE_MM_GEMM_SWZ 0
-#endif
-constexpr int kGemmRow = NEKO_TUNE_MM_GEMM_ROW;  // halves per LDS row (>= 32)
-constexpr int kGemmSwz = NEKO_TUNE_MM_GEMM_SWZ;  // XOR of the 16-byte chunk index with row bits
+constexpr int kGemmRow = 40;  // halves per LDS row: 32 plus 8 of padding (no bank conflicts)
 static_assert(kGemmBN == kGemmThreads / 2, "the weight-tile load split: two threads per weight row");
 static_assert((kGemmBM * 4) % kGemmThreads == 0, "activation pieces per thread");
 
 // Half offset of 16-byte chunk c (0..3) of row r in a staged tile.
-__device__ __forceinline__ int gemm_off(int r, int c) {
-    const int x = kGemmSwz == 0 ? 0 : kGemmSwz == 1 ? (r & 3) : kGemmSwz == 2 ? ((r >> 1) & 3) : ((r >> 2) & 3);
-    return r * kGemmRow + 8 * (c ^ x);
-}
+__device__ __forceinline__ int gemm_off(int r, int c) { return r * kGemmRow + 8 * c; }
 
 struct GemmLds {
     half_t a[2][kGemmBM * kGemmRow];
@@ -1333,23 +1247,12 @@ __device__ __forceinline__ void gemm_store(GemmLds& L, int buf, const GemmRegs<F
     }
 }
 
-// The wave's (16 MF) x (16 NF) accumulator tile, held as 16 x 16 MFMA tiles (v_mfma_f32_16x16x32_f16:
-// lane (n16, g) holds C[4g + e][n16]) or, with kGemm32, as 32 x 32 tiles (v_mfma_f32_32x32x16_f16:
-// lane (l32, h) holds C[8 (v / 4) + 4 h + v % 4][l32] in register v). Measured on MI355X, independent
+// The wave's (16 MF) x (16 NF) accumulator tile as 32 x 32 tiles (v_mfma_f32_32x32x16_f16: lane
+// (l32, h) holds C[8 (v / 4) + 4 h + v % 4][l32] in register v). Measured on MI355X, independent
 // 32 x 32 x 16 MFMAs sustain ~98% of the dense fp16 peak at one wave per SIMD; 16 x 16 x 32 ones need
 // 16 chains per wave at many waves per SIMD to pass ~55%.
-#ifndef NEKO_TUNE_MM_GEMM_M32
-#define NEKO_TUNE_MM_GEMM_M32 1
-#endif
-constexpr bool kGemm32 = NEKO_TUNE_MM_GEMM_M32;
-static_assert(!kGemm32 || (kGemmMF % 2 == 0 && kGemmNF % 2 == 0), "32 x 32 tiles need even fragment counts");
-
-template <bool M32>
+static_assert(kGemmMF % 2 == 0 && kGemmNF % 2 == 0, "32 x 32 tiles need even fragment counts");
 struct GemmAcc {
-    float4v v[kGemmMF][kGemmNF];
-};
-template <>
-struct GemmAcc<true> {
     float16v v[kGemmMF / 2][kGemmNF / 2];
 };
 
@@ -1357,7 +1260,7 @@ struct GemmAcc<true> {
 // block's k range in two halves of 16, lane (l32, h) supplying 16-byte chunk 2 q + h of its row to
 // MFMA q -- the same chunks on both operands.
 template <int FMT>
-__device__ __forceinline__ void gemm_step(GemmAcc<true>& acc, const GemmLds& L, int buf, int wm, int wn, int lane) {
+__device__ __forceinline__ void gemm_step(GemmAcc& acc, const GemmLds& L, int buf, int wm, int wn, int lane) {
     constexpr int MF = kGemmMF / 2, NF = kGemmNF / 2;
     const int l32 = lane & 31, h = lane >> 5;
     half8 B[NF][2];
@@ -1391,36 +1294,6 @@ __device__ __forceinline__ void gemm_step(GemmAcc<true>& acc, const GemmLds& L, 
     }
 }
 
-// One 32-wide step of the wave's (16 MF) x (16 NF) tile from LDS buffer buf, 16 x 16 MFMA tiles.
-template <int FMT>
-__device__ __forceinline__ void gemm_step(GemmAcc<false>& acc_t, const GemmLds& L, int buf, int wm, int wn, int lane) {
-    float4v (&acc)[kGemmMF][kGemmNF] = acc_t.v;
-    const int n16 = lane & 15, g = lane >> 4;
-    constexpr int MF = kGemmMF, NF = kGemmNF;
-    half8 B[NF];
-    float sc[NF];
-#pragma unroll
-    for (int j = 0; j < NF; j++) {
-        B[j] = *reinterpret_cast<const half8*>(&L.b[buf][gemm_off(wn * 16 * NF + j * 16 + n16, g)]);
-        sc[j] = FMT == 0 ? 1.0f : L.s[buf][wn * 16 * NF + j * 16 + n16];
-    }
-#pragma unroll
-    for (int i = 0; i < MF; i++) {
-        const half8 A = *reinterpret_cast<const half8*>(&L.a[buf][gemm_off(wm * 16 * MF + i * 16 + n16, g)]);
-#pragma unroll
-        for (int j = 0; j < NF; j++) {
-            if constexpr (FMT == 0) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[i][j], 0, 0, 0);
-            } else {
-                const float4v blk =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[i][j][e] = __builtin_fmaf(sc[j], blk[e], acc[i][j][e]);
-            }
-        }
-    }
-}
-
 // Grid: one workgroup per BM x BN output tile (1-D, remapped: each XCD -- the hardware deals
 // workgroups round-robin over the 8 -- takes a contiguous range, walked in groups of 8 token tiles
 // so that concurrent workgroups share activation and weight tiles in that XCD's L2).
@@ -1433,7 +1306,6 @@ __global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int 
     constexpr int MF = kGemmMF, NF = kGemmNF;
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & 63, wave = tid >> 6, wm = wave % kGemmWM, wn = wave / kGemmWM;
-    const int n16 = lane & 15, g = lane >> 4;
 
     uint32_t b = blockIdx.x;
     const uint32_t nb = gridDim.x;
@@ -1447,7 +1319,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int 
     const int64_t m0 = static_cast<int64_t>(first_m + in_group % gm) * kGemmBM;
     const int64_t n0 = static_cast<int64_t>(in_group / gm) * kGemmBN;
 
-    GemmAcc<kGemm32> acc = {};
+    GemmAcc acc = {};
 
     // Two register sets alternate: each step's global pieces are requested two steps before they are
     // written to LDS (requests past the last step re-read it: in bounds, never stored), so the loads
@@ -1479,27 +1351,16 @@ __global__ __launch_bounds__(kGemmThreads, 2) void mm_gemm_kernel(MmArgs a, int 
         if (partial) partial[(static_cast<int64_t>(slice) * a.T + t) * a.N + n] = v;
         else epilogue<TY>(a, t, n, v);
     };
-    if constexpr (kGemm32) {
-        // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
-        const int l32 = lane & 31, h = lane >> 5;
+    // Lane (l32, h) holds C[token 8 (e / 4) + 4 h + e % 4][row l32] of each 32 x 32 tile.
+    const int l32 = lane & 31, h = lane >> 5;
 #pragma unroll
-        for (int j = 0; j < NF / 2; j++)
+    for (int j = 0; j < NF / 2; j++)
 #pragma unroll
-            for (int i = 0; i < MF / 2; i++)
+        for (int i = 0; i < MF / 2; i++)
 #pragma unroll
-                for (int e = 0; e < 16; e++)
-                    put(m0 + wm * 16 * MF + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3), n0 + wn * 16 * NF + j * 32 + l32,
-                        acc.v[i][j][e]);
-    } else {
-        // Lane (n16, g) holds C[token 4g + e][row n16] of each 16 x 16 tile.
-#pragma unroll
-        for (int j = 0; j < NF; j++)
-#pragma unroll
-            for (int i = 0; i < MF; i++)
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    put(m0 + wm * 16 * MF + i * 16 + 4 * g + e, n0 + wn * 16 * NF + j * 16 + n16, acc.v[i][j][e]);
-    }
+            for (int e = 0; e < 16; e++)
+                put(m0 + wm * 16 * MF + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3), n0 + wn * 16 * NF + j * 32 + l32,
+                    acc.v[i][j][e]);
 }
 
 // The sum over slices of partial[slice][t][n .. n + width), added in slice order. Eight slices'
@@ -1557,23 +1418,9 @@ __global__ __launch_bounds__(256) void mm_splitk_reduce4(MmArgs a, const float* 
 // tokens: measured 10-20% faster than 128 x 128 there, and slightly slower for F16, which keeps
 // 128 x 128. (256 x 256 tiles need 128 accumulators per lane besides the staging registers and
 // spill at two waves per SIMD.) Needs K % 64 == 0; other K take the 32-wide kernel above.
-#ifndef NEKO_TUNE_MM_GEMM_V2
-#define NEKO_TUNE_MM_GEMM_V2 1
-#endif
-#ifndef NEKO_TUNE_MM_G2_ROW
-#define NEKO_TUNE_MM_G2_ROW 72
-#endif
-#ifndef NEKO_TUNE_MM_GEMM_BIG
-#define NEKO_TUNE_MM_GEMM_BIG 1
-#endif
-constexpr bool kGemmV2 = NEKO_TUNE_MM_GEMM_V2;
-constexpr bool kGemmBig = NEKO_TUNE_MM_GEMM_BIG;  // FP8 / FP4 take the 256-token tiles when their grid fills the GPU
-constexpr int kG2Row = NEKO_TUNE_MM_G2_ROW;     // halves per staged row (>= 64, a multiple of 8)
+constexpr int kG2Row = 72;  // halves per staged row: 64 plus 8 of padding
 constexpr int kG2BK = 64;
-#ifndef NEKO_TUNE_MM_G2_DEPTH
-#define NEKO_TUNE_MM_G2_DEPTH 2
-#endif
-constexpr int kG2Depth = NEKO_TUNE_MM_G2_DEPTH;  // F16: stages of global prefetch in registers (1 or 2)
+constexpr int kG2Depth = 2;  // F16: stages of global prefetch in registers (the scaled formats: 1)
 
 template <int BM_, int BN_, int WGM_, int WGN_>
 struct G2Cfg {
@@ -2112,9 +1959,6 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
                 int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int x_dtype, int y_dtype,
                 const Fixed& fixed, const char* what);
 
-#ifndef NEKO_TUNE_MM_F32_SPLIT_MIN_T
-#define NEKO_TUNE_MM_F32_SPLIT_MIN_T 9
-#endif
 // From this many tokens, f32 activations go through the MFMA kernels as two f16 planes. Measured on
 // the Qwen3-4B projections: at 3-8 tokens the f32 GEMV is faster in every format but one case (F16
 // down at 6 tokens, 5% slower; FP4 gate/up at 5-8 tokens 30-31 us against 36-38, FP4 down 23-25
@@ -2123,11 +1967,8 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
 // Weights of at most kF32SmallNK elements keep the GEMV through 16 tokens: at 10-16 it measured
 // 1.1-2.2x faster than the planes for the Qwen3-4B q/k/v [6144, 2560] and o [2560, 4096] and the
 // Qwen3-0.6B projections (the planes' four launches dominate there).
-constexpr int64_t kF32SplitMinT = NEKO_TUNE_MM_F32_SPLIT_MIN_T;
-#ifndef NEKO_TUNE_MM_F32_SPLIT_MIN_T_SMALL
-#define NEKO_TUNE_MM_F32_SPLIT_MIN_T_SMALL 17
-#endif
-constexpr int64_t kF32SplitMinTSmall = NEKO_TUNE_MM_F32_SPLIT_MIN_T_SMALL;
+constexpr int64_t kF32SplitMinT = 9;
+constexpr int64_t kF32SplitMinTSmall = 17;
 constexpr int64_t kF32SmallNK = int64_t{1} << 24;
 
 // f32 activations (16-byte aligned rows, K % 32 == 0) as two f16 planes: both through the f16 paths
@@ -2238,12 +2079,12 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
         }
     }
     if (fast && T >= (fmt == NEKO_FMT_F16 ? kGemmMinTF16 : kGemmMinT)) {
-        const bool v2 = kGemmV2 && K % kG2BK == 0;
+        const bool v2 = K % kG2BK == 0;
         // F16: 256 x 256 tiles with direct-to-LDS loads when they give every CU at least two (with
         // fewer, the partial last round of one-per-CU workgroups cost more than the wider tiles save:
         // measured on the 2560-row projections at T = 8192, 320 tiles).
         const int64_t g3_m = (T + kG3BM - 1) / kG3BM, g3_n = (N + kG3BN - 1) / kG3BN;
-        if (v2 && kGemm3 && fmt == NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
+        if (v2 && fmt == NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
             NEKO_REQUIRE(ctx, g3_m * g3_n <= 0x7fffffff, "%s: too many output tiles", what);
             const dim3 grid(static_cast<uint32_t>(g3_m * g3_n));
             const int tm = static_cast<int>(g3_m), tn = static_cast<int>(g3_n);
@@ -2252,7 +2093,7 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
             if (rc) return rc;
             return after_launch(ctx, what);
         }
-        if (v2 && kGemm3q && fmt != NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
+        if (v2 && fmt != NEKO_FMT_F16 && g3_m * g3_n >= 2 * static_cast<int64_t>(ctx->cu_count)) {
             NEKO_REQUIRE(ctx, g3_m * g3_n <= 0x7fffffff, "%s: too many output tiles", what);
             const dim3 grid(static_cast<uint32_t>(g3_m * g3_n));
             const int tm = static_cast<int>(g3_m), tn = static_cast<int>(g3_n);
@@ -2265,7 +2106,7 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
         // FP8 / FP4: 256-token x 128-row tiles (one workgroup per CU) when they alone give every CU a
         // workgroup.
         const int64_t big_m = (T + G2Big::BM - 1) / G2Big::BM, big_n = (N + G2Big::BN - 1) / G2Big::BN;
-        if (v2 && kGemmBig && fmt != NEKO_FMT_F16 && big_m * big_n >= ctx->cu_count) {
+        if (v2 && fmt != NEKO_FMT_F16 && big_m * big_n >= ctx->cu_count) {
             NEKO_REQUIRE(ctx, big_m * big_n <= 0x7fffffff, "%s: too many output tiles", what);
             if (int rc = launch_gemm2_fmt<G2Big>(ctx, fmt, y_dtype, dim3(static_cast<uint32_t>(big_m * big_n)), a,
                                                  static_cast<int>(big_m), static_cast<int>(big_n), 1, nullptr))
@@ -2304,9 +2145,8 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
     // The shared-activation kernel where it measured faster than the per-wave kernel (whose single
     // launch needs no reduction of K slices): FP4 above 4 tokens, FP8 above 12, F16 above 16 (and
     // below 33, where F16 takes the GEMM).
-    const bool tile2 = kTile2 && T < kT2MaxT &&
-                       ((fmt == NEKO_FMT_FP4 && T > NEKO_TUNE_MM_T2_MIN_FP4) || (fmt == NEKO_FMT_FP8 && T > NEKO_TUNE_MM_T2_MIN_FP8) ||
-                        (fmt == NEKO_FMT_F16 && T > NEKO_TUNE_MM_T2_MIN_F16));
+    const bool tile2 = T < kT2MaxT && ((fmt == NEKO_FMT_FP4 && T > kT2MinFp4) || (fmt == NEKO_FMT_FP8 && T > kT2MinFp8) ||
+                                       (fmt == NEKO_FMT_F16 && T > kT2MinF16));
     if (fast && tile2) {
         const int tt = static_cast<int>((T + 15) / 16);  // 1..4: one chunk of 16 tt tokens
         const int rows = static_cast<int>(T);           // token rows staged (the kernel's `rows`)

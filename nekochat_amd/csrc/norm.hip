@@ -25,54 +25,6 @@
 
 #include "internal.h"
 
-// Build-time tuning knobs (measured defaults): how a persistent wave overlaps its next row's loads
-// (0: not at all, 1: a second row buffer loaded before the current row is reduced, 2: rolling -- each
-// output chunk's registers are refilled with the next row's chunk right after its store), and
-// whether the grid is capped at the resident workgroup count (persistent) or covers every row.
-#ifndef NEKO_TUNE_NORM_PF
-#define NEKO_TUNE_NORM_PF 1
-#endif
-#ifndef NEKO_TUNE_NORM_FULLGRID
-#define NEKO_TUNE_NORM_FULLGRID 0
-#endif
-// 1: size a persistent grid so every wave gets the same number of rows (ceil(rows / resident
-// waves) each), instead of filling every resident slot and leaving a partial last round.
-#ifndef NEKO_TUNE_NORM_BALANCE
-#define NEKO_TUNE_NORM_BALANCE 0
-#endif
-// RMSNorm / LayerNorm take the one-row-per-wave grid from this many rows per resident persistent
-// wave on.
-#ifndef NEKO_TUNE_NORM_ROW_RATIO
-#define NEKO_TUNE_NORM_ROW_RATIO 3
-#endif
-// Where the one-wave-per-row kernel keeps the norm weights: 0 in every lane's registers, 1 in one
-// LDS copy per workgroup (frees CH * 8 VGPRs per lane for occupancy). Per norm kind.
-#ifndef NEKO_TUNE_NORM_WLDS_RMS
-#define NEKO_TUNE_NORM_WLDS_RMS 0
-#endif
-#ifndef NEKO_TUNE_NORM_WLDS_LAYER
-#define NEKO_TUNE_NORM_WLDS_LAYER 0
-#endif
-#ifndef NEKO_TUNE_NORM_WLDS_GATED
-#define NEKO_TUNE_NORM_WLDS_GATED 1
-#endif
-// Gated norm: 1 keeps y * silu(z) in float registers between the sum and the store, 0 evaluates it
-// again at the store (fewer registers, twice the silu work); and its prefetch mode (as NORM_PF: the
-// gated rows already hold two operands, and more resident waves beat a second row buffer).
-#ifndef NEKO_TUNE_GATED_KEEP
-#define NEKO_TUNE_GATED_KEEP 1
-#endif
-#ifndef NEKO_TUNE_GATED_PF
-#define NEKO_TUNE_GATED_PF 0
-#endif
-// Residual add + RMSNorm: weights in LDS (1) or registers (0), and its prefetch mode.
-#ifndef NEKO_TUNE_NORM_WLDS_ADD
-#define NEKO_TUNE_NORM_WLDS_ADD 1
-#endif
-#ifndef NEKO_TUNE_ADD_PF
-#define NEKO_TUNE_ADD_PF 1
-#endif
-
 namespace neko_hip {
 namespace {
 
@@ -96,48 +48,31 @@ struct NormArgs {
     float eps;
 };
 
-// Mamba2 output gate, granite_model.cpp:21: v / (1 + exp(-v)) in float. Evaluation (knob): 0 libm
-// expf and IEEE division, 1 silu_fast, 2 silu_lite (device.h). The gated norm streams two operands
-// per output and is VALU-limited on MI355X with the longer forms; silu_lite's relative error (< 1.3e-6
-// for |v| <= 20) stays far below the fp16 output's half ulp (4.9e-4).
-#ifndef NEKO_TUNE_GATED_SILU
-#define NEKO_TUNE_GATED_SILU 2
-#endif
-__device__ __forceinline__ float silu_ref(float v) {
-    if constexpr (NEKO_TUNE_GATED_SILU == 0) return v / (1.0f + expf(-v));
-    else if constexpr (NEKO_TUNE_GATED_SILU == 1) return silu_fast(v);
-    else return silu_lite(v);
-}
+// Mamba2 output gate, granite_model.cpp:21: v / (1 + exp(-v)) in float, from silu_lite (device.h):
+// the gated norm streams two operands per output and was VALU-limited on MI355X with the longer
+// forms; silu_lite's relative error (< 1.3e-6 for |v| <= 20) stays far below the fp16 output's half
+// ulp (4.9e-4).
+__device__ __forceinline__ float silu_ref(float v) { return silu_lite(v); }
 
-constexpr bool weights_in_lds(Norm k) {
-    return k == Norm::Rms     ? NEKO_TUNE_NORM_WLDS_RMS
-           : k == Norm::Layer ? NEKO_TUNE_NORM_WLDS_LAYER
-           : k == Norm::Gated ? NEKO_TUNE_NORM_WLDS_GATED
-                              : NEKO_TUNE_NORM_WLDS_ADD;
-}
-constexpr int prefetch_mode(Norm k) {
-    return k == Norm::Gated ? NEKO_TUNE_GATED_PF : k == Norm::AddRms ? NEKO_TUNE_ADD_PF : NEKO_TUNE_NORM_PF;
-}
+// Norm weights in one LDS copy per workgroup (gated and residual norms: frees registers for resident
+// waves) or in every lane's registers (RMSNorm, LayerNorm persistent kernels).
+constexpr bool weights_in_lds(Norm k) { return k == Norm::Gated || k == Norm::AddRms; }
 
-// Output stores: non-temporal (1) or plain (0), for the plain norms, the gated norm and the residual
-// add + RMSNorm (measured at [8192, 2560]: non-temporal 17.1 vs 17.9 us for the RMSNorm, plain 29.7 vs
-// 31.3 us for the residual add + RMSNorm, which stores two rows per row).
-#ifndef NEKO_TUNE_NORM_NT_STORE
-#define NEKO_TUNE_NORM_NT_STORE 1
-#endif
-#ifndef NEKO_TUNE_GATED_NT_STORE
-#define NEKO_TUNE_GATED_NT_STORE 0
-#endif
-#ifndef NEKO_TUNE_ADD_NT_STORE
-#define NEKO_TUNE_ADD_NT_STORE 0
-#endif
-// PLAIN: the one-row-per-wave kernel, whose plain loads and stores measured faster than the
-// non-temporal ones there.
+// Overlap of a persistent wave's next row: a second row buffer loaded before the current row is
+// reduced (RMSNorm, LayerNorm, residual add + RMSNorm), or none (the gated norm, whose rows hold two
+// operands: three times the resident waves beat a second buffer).
+constexpr bool prefetches(Norm k) { return k != Norm::Gated; }
+
+// RMSNorm / LayerNorm take the one-row-per-wave grid from this many rows per resident persistent wave.
+constexpr int64_t kRowRatio = 3;
+
+// Output stores: non-temporal for the plain norms, plain for the gated norm and the residual add +
+// RMSNorm (measured at [8192, 2560]: non-temporal 17.1 vs 17.9 us for the persistent RMSNorm, plain
+// 29.7 vs 31.3 us for the residual add + RMSNorm, which stores two rows per row). PLAIN: the
+// one-row-per-wave kernel, whose plain loads and stores measured faster than non-temporal ones there.
 template <Norm K, bool PLAIN = false, typename V>
 __device__ __forceinline__ void store_out(V* p, V v) {
-    constexpr bool nt = K == Norm::Gated    ? NEKO_TUNE_GATED_NT_STORE
-                        : K == Norm::AddRms ? NEKO_TUNE_ADD_NT_STORE
-                                            : NEKO_TUNE_NORM_NT_STORE;
+    constexpr bool nt = K == Norm::Rms || K == Norm::Layer;
     if constexpr (!PLAIN && nt) store_nt(p, v);
     else *p = v;
 }
@@ -174,13 +109,10 @@ struct RowRegs {
     V z[CH];
 };
 
-// Row loads: non-temporal (1) or plain (0).
-#ifndef NEKO_TUNE_NORM_NT_LOAD
-#define NEKO_TUNE_NORM_NT_LOAD 1
-#endif
+// Row loads: non-temporal, plain in the one-row-per-wave kernel (PLAIN).
 template <bool PLAIN = false, typename V>
 __device__ __forceinline__ V load_row_chunk(const V* p) {
-    if constexpr (!PLAIN && NEKO_TUNE_NORM_NT_LOAD) return load_nt(p);
+    if constexpr (!PLAIN) return load_nt(p);
     else return *p;
 }
 
@@ -271,12 +203,13 @@ struct Weights<K, T, CH, NT, true> {
 };
 
 // The row in float. Plain norms convert from the loaded halves on every use (cheaper than holding a
-// float copy in registers); the gated norm evaluates y * silu(z) once and keeps it. Lanes past the
-// row end hold zeros, which add nothing to the sums.
+// float copy in registers); the gated norm evaluates y * silu(z) once and keeps it (evaluating it again
+// at the store doubles the silu work). Lanes past the row end hold zeros, which add nothing to the
+// sums.
 template <Norm K, typename T, int CH>
 struct RowVals {
     static constexpr int N = Chunk16<T>::N;
-    static constexpr bool kKeep = K == Norm::Gated && NEKO_TUNE_GATED_KEEP;
+    static constexpr bool kKeep = K == Norm::Gated;
     float f[kKeep ? CH : 1][kKeep ? N : 1];
     const RowRegs<K, T, CH>* rr;
 
@@ -291,7 +224,6 @@ struct RowVals {
     }
     __device__ __forceinline__ float operator()(int k, int e) const {
         if constexpr (kKeep) return f[k][e];
-        else if constexpr (K == Norm::Gated) return to_f32(rr->x[k][e]) * silu_ref(to_f32(rr->z[k][e]));
         else return to_f32(rr->x[k][e]);
     }
 };
@@ -377,7 +309,7 @@ __device__ __forceinline__ void store_row(T* y, const F& f, float scale, float m
 // multiple of groups, or gives each wave at most one row). With WL the dynamic LDS holds the
 // groups * C weights (then C betas for LayerNorm). ROW: the grid covers every row, one per wave,
 // with plain loads and stores and no prefetch registers (the form for many rows per resident wave).
-template <Norm K, typename T, int CH, bool WL, bool ROW = false, int PF = ROW ? 0 : prefetch_mode(K)>
+template <Norm K, typename T, int CH, bool WL, bool ROW = false, bool PF = !ROW && prefetches(K)>
 __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     constexpr int N = Chunk16<T>::N;
     const int lane = threadIdx.x & 63;
@@ -409,7 +341,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
     load_row<K, T, CH, kWave, ROW>(cur, p0, lane, nch);
     for (; r < a.rows; r += nw) {
         const bool more = r + nw < a.rows;
-        if (PF == 1 && more) load_row<K, T, CH, kWave, ROW>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
+        if (PF && more) load_row<K, T, CH, kWave, ROW>(nxt, row_ptrs<K, T>(a, r + nw), lane, nch);
         add_residual(cur);
         RowVals<K, T, CH> f;
         f.init(cur);
@@ -423,30 +355,11 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(NormArgs a) {
             const double ss = wave_sum_f64(sum_squares<CH, N>(f));
             scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
         }
-        if constexpr (PF == 2) {
-            // Rolling: store chunk k, then load chunk k of the next row into the registers it used.
-            typedef typename Chunk16<T>::V V;
-            const RowPtrs<K, T> pc = row_ptrs<K, T>(a, r);
-            const RowPtrs<K, T> pn = row_ptrs<K, T>(a, more ? r + nw : r);
-#pragma unroll
-            for (int k = 0; k < CH; k++) {
-                const int j = k * kWave + lane;
-                if (j >= nch) continue;
-                store_out<K, ROW>(reinterpret_cast<V*>(pc.y + j * N), out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
-                if constexpr (K == Norm::AddRms)
-                    store_out<K, ROW>(reinterpret_cast<V*>(const_cast<T*>(pc.x) + j * N), cur.x[k]);
-                if (more) {
-                    cur.x[k] = load_row_chunk<ROW>(reinterpret_cast<const V*>(pn.x + j * N));
-                    if constexpr (has_z(K)) cur.z[k] = load_row_chunk<ROW>(reinterpret_cast<const V*>(pn.z + j * N));
-                }
-            }
-        } else {
-            const RowPtrs<K, T> pc = row_ptrs<K, T>(a, r);
-            store_row<K, T, CH, kWave, ROW>(pc.y, f, scale, mean_f, wt, lane, nch);
-            store_residual<K, T, CH, kWave, ROW>(cur, pc, lane, nch);
-            if (PF == 1 && more) cur = nxt;
-            else if (more) load_row<K, T, CH, kWave, ROW>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
-        }
+        const RowPtrs<K, T> pc = row_ptrs<K, T>(a, r);
+        store_row<K, T, CH, kWave, ROW>(pc.y, f, scale, mean_f, wt, lane, nch);
+        store_residual<K, T, CH, kWave, ROW>(cur, pc, lane, nch);
+        if (PF && more) cur = nxt;
+        else if (more) load_row<K, T, CH, kWave, ROW>(cur, row_ptrs<K, T>(a, r + nw), lane, nch);
     }
 }
 
@@ -768,13 +681,13 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         }
     }
     int64_t blocks;
-    if (W == 1 && has_row_form(kind) && !wl && !NEKO_TUNE_NORM_FULLGRID) {
+    if (W == 1 && has_row_form(kind) && !wl) {
         // Many rows per resident wave: one row per wave over the whole grid, which the dispatcher keeps
         // full, instead of persistent waves (measured at 2560 and 1536 halves: 16384 and 32768 rows
         // 7-12% faster, 8192 rows of 2560 -- 2.7 per resident wave -- 5% slower).
         const int64_t resident = static_cast<int64_t>(ctx->cu_count > 0 ? ctx->cu_count : 256) * 4 *
                                  resident_blocks_per_cu(reinterpret_cast<const void*>(k), 256, 0);
-        if (a.rows >= NEKO_TUNE_NORM_ROW_RATIO * resident) {
+        if (a.rows >= kRowRatio * resident) {
             NormKernel kr = nullptr;
             switch (kind) {
                 case Norm::Rms: kr = pick<Norm::Rms>(dtype, W, CH, wl, true); break;
@@ -794,11 +707,7 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         // Persistent waves: as many workgroups as stay resident together. A wave that handles several
         // rows must see one group index, so the wave count is then a multiple of groups.
         const int64_t need = (a.rows + 3) / 4;
-        blocks = NEKO_TUNE_NORM_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need, wl ? lds : 0);
-        if (NEKO_TUNE_NORM_BALANCE && blocks < need) {
-            const int64_t per = (a.rows + 4 * blocks - 1) / (4 * blocks);  // rows per wave
-            blocks = ((a.rows + per - 1) / per + 3) / 4;
-        }
+        blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need, wl ? lds : 0);
         if (blocks < need) {
             const int64_t m = a.groups / gcd64(a.groups, 4);
             blocks = blocks / m * m;

@@ -40,7 +40,7 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
     QkKernel k = nullptr;
     bool with_kv = false;
     // Widest per-lane vector whose lane count per head is a power of two and whose loads stay aligned.
-    const int vmax = static_cast<int>(16 / esz) < NEKO_TUNE_QK_MAXV ? static_cast<int>(16 / esz) : NEKO_TUNE_QK_MAXV;
+    const int vmax = static_cast<int>(16 / esz);
     for (int V = vmax; V >= 1 && !k; V /= 2) {
         if (half % V) continue;
         const int L = half / V;
@@ -61,7 +61,7 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
         // A wave takes at most kQkMaxTokensPerWave rows (the roll kernel holds one position per lane),
         // so larger row counts go in several launches.
         const int64_t need = (a.rows + 3) / 4;
-        int64_t blocks = NEKO_TUNE_QK_FULLGRID ? need : persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
+        int64_t blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
         const int64_t chunk = std::min<int64_t>(a.rows, 4 * blocks * kQkMaxTokensPerWave);
         if (blocks < need) {
             const int64_t per = (chunk + 4 * blocks - 1) / (4 * blocks);

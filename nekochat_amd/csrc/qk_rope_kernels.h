@@ -17,28 +17,6 @@
 
 #include "internal.h"
 
-// Build-time tuning knobs (measured defaults): persistent grid vs one token per wave, and the widest
-// per-lane vector (elements) a head half is split into.
-#ifndef NEKO_TUNE_QK_FULLGRID
-#define NEKO_TUNE_QK_FULLGRID 0
-#endif
-#ifndef NEKO_TUNE_QK_RSQ
-#define NEKO_TUNE_QK_RSQ 1
-#endif
-#ifndef NEKO_TUNE_QK_MAXV
-#define NEKO_TUNE_QK_MAXV 8
-#endif
-// Waves per SIMD the rolling kernel is compiled for (caps its VGPRs at 512 / waves) when a token's
-// data registers leave room for it; tokens that hold more take 3.
-#ifndef NEKO_TUNE_QK_WAVES
-#define NEKO_TUNE_QK_WAVES 4
-#endif
-// 1: a wave loads its first token's cos/sin row before that token's row data (waiting for the
-// position first); 0: after it (measured 0.8 us faster at the Qwen3-4B prefill shape).
-#ifndef NEKO_TUNE_QK_CS_FIRST
-#define NEKO_TUNE_QK_CS_FIRST 0
-#endif
-
 namespace neko_hip {
 
 struct QkArgs {
@@ -112,31 +90,20 @@ __device__ __forceinline__ void store_f16_buf(BufRes r, uint32_t off, const type
 
 // The head's norm scale float(1 / sqrt(ss / hd + eps)) (cpu_ops.cpp:508 with C = hd). ss / hd is
 // the exact product with 1/hd when hd is a power of two (every Qwen3 head size; the host passes it);
-// the reciprocal square root comes from rsqrt_to_float (device.h) or, with the knob off, the
-// libm-style expression.
+// the reciprocal square root comes from rsqrt_to_float (device.h).
 __device__ __forceinline__ float head_scale(const QkArgs& a, double ss) {
     const double m = a.inv_hd != 0.0 ? ss * a.inv_hd : ss / a.hd;
-    if constexpr (NEKO_TUNE_QK_RSQ) return rsqrt_to_float(m + static_cast<double>(a.eps));
-    else return static_cast<float>(1.0 / sqrt(m + static_cast<double>(a.eps)));
+    return rsqrt_to_float(m + static_cast<double>(a.eps));
 }
 
-// Head stores: non-temporal (knob 1) or plain (0).
-#ifndef NEKO_TUNE_QK_NT_STORE
-#define NEKO_TUNE_QK_NT_STORE 0
-#endif
+// Head loads non-temporal, stores plain (measured).
 template <typename VT>
 __device__ __forceinline__ void qk_store(VT* p, VT v) {
-    if constexpr (NEKO_TUNE_QK_NT_STORE) store_nt(p, v);
-    else *p = v;
+    *p = v;
 }
-// Head loads: non-temporal (knob 1) or plain (0).
-#ifndef NEKO_TUNE_QK_NT_LOAD
-#define NEKO_TUNE_QK_NT_LOAD 1
-#endif
 template <typename VT>
 __device__ __forceinline__ VT qk_load(const VT* p) {
-    if constexpr (NEKO_TUNE_QK_NT_LOAD) return load_nt(p);
-    else return *p;
+    return load_nt(p);
 }
 
 __device__ __forceinline__ bool row_position(const QkArgs& a, int64_t t, int64_t& pos) {
@@ -263,11 +230,11 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
 // unconditionally -- together these keep the compiler's memory-counter waits at "this pass's data"
 // rather than "everything outstanding". A token whose position lies outside the table is written
 // back unchanged (and not stored to the caches).
-// Waves per SIMD: the knob's 4 where the token's data registers leave room -- at most 40 of them
-// (32 with the KV store, whose cache addressing needs more), found to compile without spills -- else 3.
+// Waves per SIMD: 4 where the token's data registers leave room -- at most 40 of them (32 with the KV
+// store, whose cache addressing needs more), found to compile without spills -- else 3.
 template <typename T, int V, int U, bool KV>
 constexpr int qk_waves() {
-    return 2 * U * V * static_cast<int>(sizeof(T)) <= (KV ? 128 : 160) ? NEKO_TUNE_QK_WAVES : 3;
+    return 2 * U * V * static_cast<int>(sizeof(T)) <= (KV ? 128 : 160) ? 4 : 3;
 }
 
 // Tokens one wave of qk_rope_roll_kernel may take (one position per lane).
@@ -319,8 +286,8 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     if (norm) wv = buf_load16<false, float4v>(buf_res(a.wqk, 2 * HD * 4u), lane * 16u);
     VT A[U], B[U];
     auto load_pass = [&](const BufRes& r, int u) __attribute__((always_inline)) {
-        A[u] = buf_load16v<NEKO_TUNE_QK_NT_LOAD, VT>(r, off(u));
-        B[u] = buf_load16v<NEKO_TUNE_QK_NT_LOAD, VT>(r, off(u) + half * sizeof(T));
+        A[u] = buf_load16v<true, VT>(r, off(u));
+        B[u] = buf_load16v<true, VT>(r, off(u) + half * sizeof(T));
     };
     // Token k's position (wave-uniform) and whether it indexes the table.
     auto pos_of = [&](int k) __attribute__((always_inline)) -> int64_t {
@@ -385,8 +352,7 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
                         ss = __builtin_fma(static_cast<double>(fb[e]), static_cast<double>(fb[e]), ss);
                     }
                     ss = group_sum_f64<L>(ss);
-                    const float r = NEKO_TUNE_QK_RSQ ? rsqrt_to_float(ss * (1.0 / HD) + static_cast<double>(a.eps))
-                                                     : head_scale(a, ss);
+                    const float r = rsqrt_to_float(ss * (1.0 / HD) + static_cast<double>(a.eps));
                     const float* w = wl + (head < a.n_q ? 0 : HD) + i0;
 #pragma unroll
                     for (int e = 0; e < V; e++) {
@@ -418,8 +384,8 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
                 }
             }
             // q and k heads back in place (v heads and lanes past the last head fall outside `st`).
-            buf_store16v<NEKO_TUNE_QK_NT_STORE>(st, off(u), oa);
-            buf_store16v<NEKO_TUNE_QK_NT_STORE>(st, off(u) + half * sizeof(T), ob);
+            buf_store16v<false>(st, off(u), oa);
+            buf_store16v<false>(st, off(u) + half * sizeof(T), ob);
             if constexpr (KV) {
                 // Rotated k heads to the k cache row, untouched v heads to the v cache row; each
                 // resource's range drops the other heads' stores (their offsets wrap past it).
@@ -434,12 +400,11 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
         }
     };
 
-    // The first token's cos/sin row goes out before its row data when the knob asks for it (the load
-    // then waits for the position, but its staging does not wait for the row data: the memory counter
-    // completes in order).
+    // The first token's row data goes out first, then the weight copy and that token's cos/sin row
+    // (loading the cos/sin row first waits for the position before any row load is issued: measured
+    // 0.8 us slower at the Qwen3-4B prefill shape).
     {
         float2v r[PL];
-        if constexpr (NEKO_TUNE_QK_CS_FIRST) cs_load(pos_of(0), r);
         const BufRes ld = buf_res(row_of(t0), load_bytes);
 #pragma unroll
         for (int u = 0; u < U; u++) load_pass(ld, u);
@@ -448,7 +413,7 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
             for (int i = 256 + lane * 4; i < 2 * HD; i += 256)
                 *reinterpret_cast<float4v*>(&wsh[wave][i]) = *reinterpret_cast<const float4v*>(a.wqk + i);
         }
-        if constexpr (!NEKO_TUNE_QK_CS_FIRST) cs_load(pos_of(0), r);
+        cs_load(pos_of(0), r);
         cs_store(0, r);
     }
     // Token k with a next token: its passes, the refills, and the next cos/sin row staged in the other

@@ -106,3 +106,19 @@ def test_host_codec_argument_errors():
     assert L.neko_quantize_rows(1, 1, 32, None, None, 1, None) == _lib.NEKO_ERR_INVALID
     assert L.neko_rope_table(1e4, 3, 4, None) == _lib.NEKO_ERR_INVALID
     assert L.neko_quant_row_bytes(9, 32) == 0
+
+
+def test_kernel_sources_carry_no_build_time_variants():
+    """Every kernel source compiles one way: no NEKO_TUNE_* build-time switches whose other values no
+    build compiles or tests (measured alternatives are recorded as measurements, not kept as code)."""
+    import glob
+    import re
+
+    found = []
+    for path in sorted(glob.glob(os.path.join(ROOT, "nekochat_amd", "csrc", "*"))):
+        if not path.endswith((".hip", ".h", ".cpp", "Makefile")):
+            continue
+        for i, line in enumerate(open(path), 1):
+            if re.search(r"\bNEKO_TUNE_\w+", line):
+                found.append(f"{os.path.basename(path)}:{i}: {line.strip()}")
+    assert not found, "\n".join(found)
