@@ -137,7 +137,9 @@ class FloorLib:
                             ("neko_floor_inplace_rows", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_int,
                                                          c.c_int, c.c_void_p]),
                             ("neko_floor_rows_up", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_int,
-                                                    c.c_int, c.c_int, c.c_void_p])):
+                                                    c.c_int, c.c_int, c.c_void_p]),
+                            ("neko_floor_gather", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_void_p,
+                                                   c.c_int64, c.c_int64, c.c_int, c.c_void_p])):
             getattr(lib, name).argtypes = args_
             getattr(lib, name).restype = c.c_int
             self.bound.add(name)

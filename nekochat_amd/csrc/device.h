@@ -131,20 +131,6 @@ __device__ __forceinline__ float silu_lite(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// silu(g) = g / (1 + exp(-g)) with exp(-g) = v_exp_f32(g * -log2(e)) (the argument rounded once, no
-// split) and the quotient from v_rcp_f32 plus one Newton correction, fma(fma(-q, d, g), r, q). The
-// exponent argument is clamped at 126 so d stays finite for the correction; special values as in
-// silu_fast.
-__device__ __forceinline__ float silu_newton(float gate) {
-    const float e = __builtin_amdgcn_exp2f(fminf(gate * -1.44269504088896341f, 126.0f));
-    const float d = 1.0f + e;
-    const float r = __builtin_amdgcn_rcpf(d);
-    const float q0 = gate * r;
-    float q = __builtin_fmaf(__builtin_fmaf(-q0, d, gate), r, q0);
-    if (gate == __builtin_inff() || gate == 0.0f) q = gate;
-    return q;
-}
-
 // Two weight codes, one in the low byte of each 16-bit half of p, -> the f16 bit patterns whose
 // values are the codes' values / 2^8 (FP8 E4M3: (c & 0x7F) << 7 with the sign moved to bit 15) or
 // / 2^14 (FP4 E2M1: (c & 7) << 9, sign to bit 15; the high nibble of each byte is ignored). Exact:
@@ -217,7 +203,16 @@ __device__ __forceinline__ void unrolled(F&& f) {
 // ---------------------------------------------------------------- DPP cross-lane moves
 // dpp_ctrl encodings (GCN3+/CDNA): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
 // row_mirror = 0x140, row_half_mirror = 0x141, row_ror:8 = 0x128.
-enum : int { kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowMirror = 0x140, kDppRowHalfMirror = 0x141 };
+// quad_perm [0,2,0,2] = 0x88 and [1,3,1,3] = 0xDD: lanes 0 / 2 and 1 / 3 of each quad, even lanes of a
+// quad taking the first and odd lanes the second.
+enum : int {
+    kDppQuadXor1 = 0xB1,
+    kDppQuadXor2 = 0x4E,
+    kDppQuadPairLo = 0x88,
+    kDppQuadPairHi = 0xDD,
+    kDppRowMirror = 0x140,
+    kDppRowHalfMirror = 0x141
+};
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {

@@ -11,6 +11,8 @@
 // f16 output without wpe, the same rounding done by a packed f16 multiply, see fp8_pair_bits). This
 // keeps the reference's 0x7F / 0xFF = +-480 (not NaN) and -0 codes. With wpe the position row is
 // added in f32 first, then rounded once, as the reference does.
+#include <type_traits>
+
 #include "internal.h"
 
 namespace neko_hip {
@@ -59,43 +61,12 @@ __device__ __forceinline__ uint32_t word_of(const R& r, int w) {
     else return static_cast<uint32_t>(r[w]);
 }
 
-// Launch-shape knobs (compile-time; defaults are the fastest measured on MI355X for a 16384-token
-// gather of 2048-wide rows). NT_STORE 1 writes the output with non-temporal stores (no faster).
-#ifndef NEKO_TUNE_EMBED_NT_STORE
-#define NEKO_TUNE_EMBED_NT_STORE 0
-#endif
-
-// Tokens per wavefront, per table format (F16, FP8, FP4): more tokens put more rows' loads in
-// flight per wave, at the cost of registers (occupancy) for the decoding formats.
-#ifndef NEKO_TUNE_EMBED_TPW_F16
-#define NEKO_TUNE_EMBED_TPW_F16 4
-#endif
-#ifndef NEKO_TUNE_EMBED_TPW_FP8
-#define NEKO_TUNE_EMBED_TPW_FP8 2
-#endif
-#ifndef NEKO_TUNE_EMBED_TPW_FP4
-#define NEKO_TUNE_EMBED_TPW_FP4 2
-#endif
-// PACKED 1 decodes FP8/FP4 in packed f16 when the output is f16 and no position table is added.
-#ifndef NEKO_TUNE_EMBED_PACKED
-#define NEKO_TUNE_EMBED_PACKED 1
-#endif
-// 16-byte output chunks per lane per token in flight, per format.
-#ifndef NEKO_TUNE_EMBED_B_F16
-#define NEKO_TUNE_EMBED_B_F16 4
-#endif
-#ifndef NEKO_TUNE_EMBED_B_FP8
-#define NEKO_TUNE_EMBED_B_FP8 4
-#endif
-#ifndef NEKO_TUNE_EMBED_B_FP4
-#define NEKO_TUNE_EMBED_B_FP4 4
-#endif
-__host__ __device__ constexpr int chunks_in_flight(int fmt) {
-    return fmt == 0 ? NEKO_TUNE_EMBED_B_F16 : fmt == 1 ? NEKO_TUNE_EMBED_B_FP8 : NEKO_TUNE_EMBED_B_FP4;
-}
-__host__ __device__ constexpr int tokens_per_wave(int fmt) {
-    return fmt == 0 ? NEKO_TUNE_EMBED_TPW_F16 : fmt == 1 ? NEKO_TUNE_EMBED_TPW_FP8 : NEKO_TUNE_EMBED_TPW_FP4;
-}
+// Launch shape (the fastest measured on MI355X for a 16384-token gather of 2048-wide rows): tokens
+// per wavefront, per table format (F16, FP8, FP4) -- more tokens put more rows' loads in flight per
+// wave, at the cost of registers (occupancy) for the decoding formats -- and 16-byte output chunks
+// per lane per token in flight.
+__host__ __device__ constexpr int chunks_in_flight(int) { return 4; }
+__host__ __device__ constexpr int tokens_per_wave(int fmt) { return fmt == 1 ? 2 : 4; }
 
 // Vector path. FMT: 0 F16, 1 FP8, 2 FP4. The output row is cut into chunks of EPC = 16 bytes of
 // output elements (8 halves or 4 floats); lane l takes chunks l, l + 64, ..., so every store
@@ -104,6 +75,11 @@ __host__ __device__ constexpr int tokens_per_wave(int fmt) {
 // block that hold its elements (FP4: elements j < 16 sit in the low nibbles of bytes j, elements
 // 16 + j in the high nibbles). Requires C % 32 == 0 for FP8/FP4, C % EPC == 0 for F16, and
 // 16-byte aligned output rows (plus 2 * EPC-byte aligned table rows and wpe rows).
+// FP4 with f16 output: the four lanes of a quad hold the four chunks of one 32-weight block (chunk c
+// of lane l has c % 4 == l % 4), whose 16 code bytes each chunk needs half of: each lane loads one
+// dword of the block and takes the two it decodes from its quad by DPP, so the row's code bytes are
+// loaded once (measured for a 16384-token Zipf gather of 2048-wide rows: 16.8 us against 19.7 for
+// 8-byte loads per chunk, which fetch every byte twice).
 // Each wave owns tokens_per_wave(FMT) consecutive tokens: their ids come in one load, then every
 // row's chunk loads are issued before any is decoded.
 template <int FMT, typename TO, bool WPE>
@@ -113,9 +89,13 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     constexpr int B = chunks_in_flight(FMT);   // chunks per lane per token in flight
     typedef typename VecOf<TO, EPC>::V VO;
     typedef typename VecOf<half_t, EPC>::V VH;
-    constexpr bool kPacked = FMT != 0 && EPC == 8 && !WPE && NEKO_TUNE_EMBED_PACKED;
-    // Raw chunk bytes: F16 2*EPC bytes, FP8/FP4 EPC bytes.
+    // FP8 / FP4 decoded in packed f16 when the output is f16 and no position table is added.
+    constexpr bool kPacked = FMT != 0 && EPC == 8 && !WPE;
+    // Raw chunk bytes: F16 2*EPC bytes, FP8/FP4 EPC bytes (FP4 with f16 output: one dword of the block,
+    // the quad's shared load).
+    constexpr bool kQuad = FMT == 2 && EPC == 8;
     typedef typename VecOf<uint32_t, (FMT == 0 ? 2 * EPC : EPC) / 4>::V Raw;
+    typedef typename std::conditional<kQuad, uint32_t, Raw>::type Load;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * TPW;
@@ -134,7 +114,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     const int64_t soff = FMT == 1 ? a.C : a.C / 2;  // scales follow the codes
 
     for (int c0 = 0; c0 < nch; c0 += B * kWave) {
-        Raw raw[TPW][B];
+        Load raw[TPW][B];
         half_t sc[TPW][B];
         VH pw[TPW][B];
 #pragma unroll
@@ -153,7 +133,8 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
                     sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * (e0 >> 5));
                 } else {
                     const int blk = e0 >> 5, j0 = e0 & 15;
-                    raw[k][b] = *reinterpret_cast<const Raw*>(row + 16 * blk + j0);
+                    if constexpr (kQuad) raw[k][b] = *reinterpret_cast<const uint32_t*>(row + 16 * blk + 4 * (lane & 3));
+                    else raw[k][b] = *reinterpret_cast<const Raw*>(row + 16 * blk + j0);
                     sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * blk);
                 }
                 if constexpr (WPE) pw[k][b] = *reinterpret_cast<const VH*>(a.wpe + (a.pos0 + t0 + k) * a.C + e0);
@@ -166,7 +147,17 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 #pragma unroll
             for (int b = 0; b < B; b++) {
                 const int c = c0 + b * kWave + lane;
-                if (c >= nch) continue;
+                if (c >= nch) continue;  // whole quads: nch is a multiple of 4 for FP8 / FP4
+                // The chunk's code bytes: FP4 quad loads give lane q of a quad the block's bytes 0-7
+                // (q = 0, 2) or 8-15 (q = 1, 3), the dwords of quad lanes 2 (q % 2) and 2 (q % 2) + 1.
+                Raw rw;
+                if constexpr (kQuad) {
+                    const int d = static_cast<int>(raw[k][b]);
+                    rw[0] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, d, kDppQuadPairLo, 0xF, 0xF, false));
+                    rw[1] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, d, kDppQuadPairHi, 0xF, 0xF, false));
+                } else {
+                    rw = raw[k][b];
+                }
                 VO o;
                 if constexpr (kPacked) {
                     const half2v s2 = {sc[k][b], sc[k][b]};
@@ -175,7 +166,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
                     uint4v ob;
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const uint32_t word = word_of(raw[k][b], i >> 1) >> shift;
+                        const uint32_t word = word_of(rw, i >> 1) >> shift;
                         const uint32_t p = __builtin_amdgcn_perm(0u, word, (i & 1) ? 0x0C030C02u : 0x0C010C00u);
                         const uint32_t bits = FMT == 1 ? fp8_pair_bits(p) : fp4_pair_bits(p);
                         ob[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, bits) * k2 * s2);
@@ -184,14 +175,14 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
                 } else {
                     float v[EPC];
                     if constexpr (FMT == 0) {
-                        const VH h = __builtin_bit_cast(VH, raw[k][b]);
+                        const VH h = __builtin_bit_cast(VH, rw);
 #pragma unroll
                         for (int e = 0; e < EPC; e++) v[e] = static_cast<float>(h[e]);
                     } else if constexpr (FMT == 1) {
                         const float sf = static_cast<float>(sc[k][b]) * 256.0f;
 #pragma unroll
                         for (int w = 0; w < EPC / 4; w++) {
-                            const uint32_t word = word_of(raw[k][b], w);
+                            const uint32_t word = word_of(rw, w);
                             float f0, f1, f2, f3;
                             fp8_pair(word, f0, f1);
                             fp8_pair(word >> 16, f2, f3);
@@ -205,7 +196,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
                         const float sf = static_cast<float>(sc[k][b]) * 16384.0f;
 #pragma unroll
                         for (int w = 0; w < EPC / 4; w++) {
-                            const uint32_t word = word_of(raw[k][b], w) >> shift;
+                            const uint32_t word = word_of(rw, w) >> shift;
 #pragma unroll
                             for (int q = 0; q < 4; q++) v[4 * w + q] = fp4_code(word >> (8 * q)) * sf;
                         }
@@ -217,9 +208,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 #pragma unroll
                     for (int e = 0; e < EPC; e++) o[e] = from_f32<TO>(v[e]);
                 }
-                VO* dst = reinterpret_cast<VO*>(out + c * EPC);
-                if (NEKO_TUNE_EMBED_NT_STORE) store_nt(dst, o);
-                else *dst = o;
+                *reinterpret_cast<VO*>(out + c * EPC) = o;  // plain stores (non-temporal ones were no faster)
             }
         }
     }

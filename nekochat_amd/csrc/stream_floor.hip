@@ -5,7 +5,8 @@
 // write n), a two-input stream (read 2n, write n: SwiGLU's byte counts), the same with SwiGLU's row
 // layout (both inputs halves of one row), an in-place read-and-write-back of the first part of each
 // row (the q/k RoPE's layout; flat, and in that kernel's per-wave token order), rows moved in the
-// one-round row kernels' shape (every row of a wave loaded before any store), and a read-only sweep.
+// one-round row kernels' shape (every row of a wave loaded before any store), the embedding gather's
+// pattern (table rows read through token ids, contiguous output rows written), and a read-only sweep.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -146,6 +147,39 @@ __global__ __launch_bounds__(256) void rows_up_kernel(const u32x4* src, int64_t 
         u32x4* p = dst + row * ds + lane;
 #pragma unroll
         for (int j = 0; j < CPL; j++) __builtin_nontemporal_store(v[r][j] ^ key, p + 64 * j);
+    }
+}
+
+// The embedding gather's byte pattern without its decode: wave w takes tokens TPW w .. TPW w + TPW - 1
+// (their ids in one load), reads each token's table row (row_chunks 16-byte chunks, lane l chunks l,
+// l + 64, ...) and writes out_chunks 16-byte chunks of output per token (lane l chunks l, l + 64, ...:
+// 1 KB of contiguous output per store instruction), every output chunk the xor of the lane's row
+// chunks with `key`. row_chunks <= 256, out_chunks <= 256.
+template <int TPW>
+__global__ __launch_bounds__(256) void gather_kernel(const int32_t* ids, int64_t T, const u32x4* table, int64_t row_stride,
+                                                     int row_chunks, u32x4* out, int64_t out_stride, int out_chunks,
+                                                     uint32_t key) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * TPW;
+    if (t0 >= T) return;
+    const int32_t my_id = lane < TPW && t0 + lane < T ? ids[t0 + lane] : 0;
+    u32x4 acc[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; k++) {
+        const int64_t id = __builtin_amdgcn_readlane(my_id, k);
+        const u32x4* row = table + id * row_stride;
+        acc[k] = u32x4{key, key, key, key};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (64 * j + lane < row_chunks) acc[k] ^= __builtin_nontemporal_load(row + 64 * j + lane);
+    }
+#pragma unroll
+    for (int k = 0; k < TPW; k++) {
+        if (t0 + k >= T) break;
+        u32x4* o = out + (t0 + k) * out_stride;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (64 * j + lane < out_chunks) o[64 * j + lane] = acc[k] ^ u32x4{static_cast<uint32_t>(j), 0u, 0u, 0u};
     }
 }
 
@@ -294,6 +328,28 @@ int neko_floor_rows_up(const void* src, int64_t s_stride, void* dst, int64_t d_s
     }
     NEKO_ROWS_UP(1, 5) NEKO_ROWS_UP(2, 5) NEKO_ROWS_UP(3, 5) NEKO_ROWS_UP(1, 10) NEKO_ROWS_UP(2, 10) NEKO_ROWS_UP(3, 10)
 #undef NEKO_ROWS_UP
+    return hipGetLastError();
+}
+
+// The gather's bytes: for t < T, reads table row ids[t] (row_bytes of it; rows row_stride bytes apart)
+// and writes out_bytes at out + t * out_stride; ids must index the table (the caller checks), sizes
+// multiples of 16 bytes up to 4 KB, tpw (tokens per wave) 1, 2 or 4.
+int neko_floor_gather(const int32_t* ids, int64_t T, const void* table, int64_t row_stride, int64_t row_bytes, void* out,
+                      int64_t out_stride, int64_t out_bytes, int tpw, void* stream) {
+    if (!ok16(table) || !ok16(out) || row_stride % 16 || out_stride % 16 || row_bytes % 16 || out_bytes % 16 ||
+        row_bytes <= 0 || row_bytes > 4096 || out_bytes <= 0 || out_bytes > 4096 || row_stride < row_bytes ||
+        out_stride < out_bytes || T <= 0 || (tpw != 1 && tpw != 2 && tpw != 4))
+        return hipErrorInvalidValue;
+    const int64_t blocks = (T + 4 * tpw - 1) / (4 * tpw);
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>(blocks)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* tp = static_cast<const u32x4*>(table);
+    auto* op = static_cast<u32x4*>(out);
+    const int rc = static_cast<int>(row_bytes / 16), oc = static_cast<int>(out_bytes / 16);
+    if (tpw == 1) hipLaunchKernelGGL((gather_kernel<1>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u);
+    else if (tpw == 2) hipLaunchKernelGGL((gather_kernel<2>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u);
+    else hipLaunchKernelGGL((gather_kernel<4>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u);
     return hipGetLastError();
 }
 
