@@ -176,6 +176,13 @@ int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const vo
                    int64_t C, int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t wpe_rows, int64_t pos0,
                    void* out, int64_t out_stride, int out_dtype);
 
+/* Granite's gather (granite_model.cpp:298-301): as neko_hip_embed without a position table, each
+ * dequantised value then multiplied by `scale` in f32 (the model's embedding_multiplier: one f32
+ * rounding, as the reference's x[c] *= embeddingMult), f16 output one RNE rounding of that. */
+int neko_hip_embed_scaled(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const void* table, int64_t row_bytes,
+                          int fmt, int64_t C, int64_t row_base, int64_t rows, float scale, void* out, int64_t out_stride,
+                          int out_dtype);
+
 /* Load-time quantiser on the device (quantizeMatrix, quant.cpp:255-279, portable branch): rows x cols
  * weights (src_dtype f32, or f16 widened exactly; row stride src_stride elements, device memory)
  * encoded into device rows of neko_quant_row_bytes(*fmt_used, cols) bytes, bit-identical to

@@ -56,6 +56,7 @@ SIGNATURES = {
     "neko_hip_swiglu": (_i32, [_p, _p, _i64, _p, _i64, _i64, _i64, _i32]),
     "neko_hip_gelu_tanh": (_i32, [_p, _p, _p, _i64, _i32]),
     "neko_hip_embed": (_i32, [_p, _p, _i64, _p, _i64, _i32, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32]),
+    "neko_hip_embed_scaled": (_i32, [_p, _p, _i64, _p, _i64, _i32, _i64, _i64, _i64, _f32, _p, _i64, _i32]),
     "neko_quant_row_bytes": (_sz, [_i32, _i64]),
     "neko_quantize_rows": (_i32, [_i32, _i64, _i64, _p, _p, _i32, ctypes.POINTER(_i32)]),
     "neko_rope_table": (_i32, [ctypes.c_double, _i32, _i64, _p]),

@@ -6,8 +6,9 @@
 //
 // Per-kernel parameter blocks (PA = params[0..3], PB = params[4..7]; floats travel as raw bits, see
 // floatBits), activations f32, exactly as the reference's shaders take them:
-//   Embed      PA (T, C, pos0, flags{1: + f16 wpe, 2: FP8 table, 4: FP4 table})
-//              PB (rowBase, rows, rowWords = rowBytes / 4)   bindings tokens, table, wpe, x
+//   Embed      PA (T, C, pos0, flags{1: + f16 wpe, 2: FP8 table, 4: FP4 table, 8: x *= PB[3]})
+//              PB (rowBase, rows, rowWords = rowBytes / 4, multiplier bits for flag 8: Granite's
+//              embedding_multiplier, granite_model.cpp:298-301)       bindings tokens, table, wpe, x
 //   LayerNorm  PA (C, eps, rowOffset, flags{1: RMSNorm})     bindings x, y, gamma, beta; dispatch (rows, 1)
 //   Rope       PA (qkvStride, nHead, headDim, pos0)
 //              PB (eps, flags{1: per-head RMSNorm})           bindings qkv, wn[2 hd], cs; dispatch (nHead + nKv, T)

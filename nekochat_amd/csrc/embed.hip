@@ -30,7 +30,12 @@ struct EmbedArgs {
     int64_t pos0;
     void* out;
     int64_t out_stride;
+    float scale;  // the rows' f32 multiplier (Granite's embedding_multiplier; 1 for plain gathers)
 };
+
+// What the gather adds to the dequantised row: nothing, GPT-2's position row (added in f32), or a
+// multiplier (granite_model.cpp:298-301: x[c] *= embeddingMult, one f32 rounding).
+enum class Extra : int { None = 0, Wpe = 1, Scale = 2 };
 
 __device__ __forceinline__ float half_bits_to_f32(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(bits16)));
@@ -82,15 +87,16 @@ __host__ __device__ constexpr int tokens_per_wave(int fmt) { return fmt == 1 ? 2
 // 8-byte loads per chunk, which fetch every byte twice).
 // Each wave owns tokens_per_wave(FMT) consecutive tokens: their ids come in one load, then every
 // row's chunk loads are issued before any is decoded.
-template <int FMT, typename TO, bool WPE>
+template <int FMT, typename TO, Extra X>
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+    constexpr bool WPE = X == Extra::Wpe;
     constexpr int EPC = 16 / sizeof(TO);  // output elements per chunk
     constexpr int TPW = tokens_per_wave(FMT);  // tokens per wave, all in flight together
     constexpr int B = chunks_in_flight(FMT);   // chunks per lane per token in flight
     typedef typename VecOf<TO, EPC>::V VO;
     typedef typename VecOf<half_t, EPC>::V VH;
-    // FP8 / FP4 decoded in packed f16 when the output is f16 and no position table is added.
-    constexpr bool kPacked = FMT != 0 && EPC == 8 && !WPE;
+    // FP8 / FP4 decoded in packed f16 when the output is f16 and nothing is added or multiplied.
+    constexpr bool kPacked = FMT != 0 && EPC == 8 && X == Extra::None;
     // Raw chunk bytes: F16 2*EPC bytes, FP8/FP4 EPC bytes (FP4 with f16 output: one dword of the block,
     // the quad's shared load).
     constexpr bool kQuad = FMT == 2 && EPC == 8;
@@ -205,6 +211,10 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 #pragma unroll
                         for (int e = 0; e < EPC; e++) v[e] = v[e] + static_cast<float>(pw[k][b][e]);
                     }
+                    if constexpr (X == Extra::Scale) {
+#pragma unroll
+                        for (int e = 0; e < EPC; e++) v[e] = v[e] * a.scale;
+                    }
 #pragma unroll
                     for (int e = 0; e < EPC; e++) o[e] = from_f32<TO>(v[e]);
                 }
@@ -216,7 +226,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 
 // Any layout: one thread per element, byte addressing (the embed.comp scheme).
 template <typename TO>
-__global__ __launch_bounds__(256) void embed_generic(EmbedArgs a, int fmt, int use_wpe) {
+__global__ __launch_bounds__(256) void embed_generic(EmbedArgs a, int fmt, int use_wpe, int use_scale) {
     const int64_t t = blockIdx.y;
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= a.C) return;
@@ -240,35 +250,33 @@ __global__ __launch_bounds__(256) void embed_generic(EmbedArgs a, int fmt, int u
         }
     }
     if (use_wpe) v = v + static_cast<float>(a.wpe[(a.pos0 + t) * a.C + c]);
+    if (use_scale) v = v * a.scale;
     static_cast<TO*>(a.out)[t * a.out_stride + c] = from_f32<TO>(v);
 }
 
 typedef void (*EmbedKernel)(EmbedArgs);
 
 template <int FMT, typename TO>
-EmbedKernel pick_wpe(bool wpe) {
-    return wpe ? embed_kernel<FMT, TO, true> : embed_kernel<FMT, TO, false>;
+EmbedKernel pick_extra(Extra x) {
+    return x == Extra::Wpe     ? embed_kernel<FMT, TO, Extra::Wpe>
+           : x == Extra::Scale ? embed_kernel<FMT, TO, Extra::Scale>
+                               : embed_kernel<FMT, TO, Extra::None>;
 }
 
 template <typename TO>
-EmbedKernel pick_fmt(int fmt, bool wpe) {
+EmbedKernel pick_fmt(int fmt, Extra x) {
     switch (fmt) {
-        case 0: return pick_wpe<0, TO>(wpe);
-        case 1: return pick_wpe<1, TO>(wpe);
-        case 2: return pick_wpe<2, TO>(wpe);
+        case 0: return pick_extra<0, TO>(x);
+        case 1: return pick_extra<1, TO>(x);
+        case 2: return pick_extra<2, TO>(x);
     }
     return nullptr;
 }
 
-}  // namespace
-}  // namespace neko_hip
-
-using namespace neko_hip;
-
-extern "C" int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const void* table, int64_t row_bytes,
-                              int fmt, int64_t C, int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t wpe_rows,
-                              int64_t pos0, void* out, int64_t out_stride, int out_dtype) {
-    const char* what = "neko_hip_embed";
+// Argument checks, then the vector kernel or (any layout) the per-element one.
+int launch_embed(neko_hip_ctx* ctx, const char* what, const int32_t* tokens, int64_t T, const void* table, int64_t row_bytes,
+                 int fmt, int64_t C, int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t wpe_rows, int64_t pos0,
+                 float scale, bool scaled, void* out, int64_t out_stride, int out_dtype) {
     NEKO_ENTER(ctx);
     NEKO_REQUIRE(ctx, valid_dtype(out_dtype), "%s: bad dtype %d", what, out_dtype);
     NEKO_REQUIRE(ctx, fmt == NEKO_FMT_F16 || fmt == NEKO_FMT_FP8 || fmt == NEKO_FMT_FP4, "%s: bad format %d", what, fmt);
@@ -284,9 +292,10 @@ extern "C" int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t 
         NEKO_REQUIRE(ctx, pos0 >= 0 && pos0 + T <= wpe_rows, "%s: positions [%lld, %lld) outside the %lld-row wpe table",
                      what, (long long)pos0, (long long)(pos0 + T), (long long)wpe_rows);
     }
+    const Extra extra = wpe ? Extra::Wpe : scaled ? Extra::Scale : Extra::None;
     const size_t osz = dtype_size(out_dtype);
     EmbedArgs a{tokens, T, static_cast<const uint8_t*>(table), row_bytes, static_cast<int>(C), row_base, rows,
-                reinterpret_cast<const half_t*>(wpe), pos0, out, out_stride};
+                reinterpret_cast<const half_t*>(wpe), pos0, out, out_stride, scale};
     // Chunks of 16 output bytes: EPC elements; loads of 2*EPC (F16) or EPC (FP8/FP4) table bytes.
     const int64_t epc = static_cast<int64_t>(16 / osz);
     const int64_t chunk_in = fmt == NEKO_FMT_F16 ? 2 * epc : epc;
@@ -296,7 +305,7 @@ extern "C" int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t 
     if (vec) {
         const int64_t per_block = 4 * tokens_per_wave(fmt);
         NEKO_REQUIRE(ctx, T <= 0x7fffffffLL * per_block, "%s: too many tokens", what);
-        EmbedKernel k = out_dtype == NEKO_DT_F16 ? pick_fmt<half_t>(fmt, wpe != nullptr) : pick_fmt<float>(fmt, wpe != nullptr);
+        EmbedKernel k = out_dtype == NEKO_DT_F16 ? pick_fmt<half_t>(fmt, extra) : pick_fmt<float>(fmt, extra);
         hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>((T + per_block - 1) / per_block)), dim3(256), 0, ctx->stream, a);
         return after_launch(ctx, what);
     }
@@ -307,13 +316,33 @@ extern "C" int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t 
         s.T = T - t0 < 65535 ? T - t0 : 65535;
         s.pos0 = pos0 + t0;
         s.out = static_cast<char*>(out) + t0 * out_stride * static_cast<int64_t>(osz);
+        const int w = wpe ? 1 : 0, sc = scaled ? 1 : 0;
         if (out_dtype == NEKO_DT_F16)
             hipLaunchKernelGGL(embed_generic<half_t>, dim3(gx, static_cast<uint32_t>(s.T)), dim3(256), 0, ctx->stream, s, fmt,
-                               wpe ? 1 : 0);
+                               w, sc);
         else
             hipLaunchKernelGGL(embed_generic<float>, dim3(gx, static_cast<uint32_t>(s.T)), dim3(256), 0, ctx->stream, s, fmt,
-                               wpe ? 1 : 0);
+                               w, sc);
         if (int rc = after_launch(ctx, what)) return rc;
     }
     return NEKO_OK;
+}
+
+}  // namespace
+}  // namespace neko_hip
+
+using namespace neko_hip;
+
+extern "C" int neko_hip_embed(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const void* table, int64_t row_bytes,
+                              int fmt, int64_t C, int64_t row_base, int64_t rows, const uint16_t* wpe, int64_t wpe_rows,
+                              int64_t pos0, void* out, int64_t out_stride, int out_dtype) {
+    return launch_embed(ctx, "neko_hip_embed", tokens, T, table, row_bytes, fmt, C, row_base, rows, wpe, wpe_rows, pos0,
+                        1.0f, false, out, out_stride, out_dtype);
+}
+
+extern "C" int neko_hip_embed_scaled(neko_hip_ctx* ctx, const int32_t* tokens, int64_t T, const void* table,
+                                     int64_t row_bytes, int fmt, int64_t C, int64_t row_base, int64_t rows, float scale,
+                                     void* out, int64_t out_stride, int out_dtype) {
+    return launch_embed(ctx, "neko_hip_embed_scaled", tokens, T, table, row_bytes, fmt, C, row_base, rows, nullptr, 0, 0,
+                        scale, true, out, out_stride, out_dtype);
 }

@@ -147,6 +147,13 @@ private:
         void* tokens = need(b, 0, mul(T, 4), "Embed");
         void* table = need(b, 1, mul(rows, rowBytes), "Embed");
         void* out = need(b, 3, mul(T, C, 4), "Embed");
+        if (flags & 8) {
+            // Granite's embedding multiplier (granite_model.cpp:298-301), its bits in PB[3].
+            if (flags & 1) fail("HIP Embed: a position table and a multiplier are not combined");
+            check(neko_hip_embed_scaled(ctx_, static_cast<const int32_t*>(tokens), T, table, rowBytes, fmt, C, rowBase,
+                                        rows, bitsFloat(pb[3]), out, C, NEKO_DT_F32));
+            return;
+        }
         const uint16_t* wpe = nullptr;
         int64_t wpeRows = 0;
         if (flags & 1) {

@@ -321,10 +321,12 @@ def gelu(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 
 def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base: int = 0, rows: int | None = None,
           wpe: torch.Tensor | None = None, pos0: int = 0, out: torch.Tensor | None = None,
-          out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+          out_dtype: torch.dtype = torch.float16, scale: float | None = None) -> torch.Tensor:
     """Embedding gather with fused dequantisation (embed.comp, QMatrix::dequantizeRow).
-    table: uint8 [rows, row_bytes] in format fmt; tokens: int32 [T]; wpe: float16 [P, C] or None.
-    Tokens outside [row_base, row_base + rows) leave their out row untouched."""
+    table: uint8 [rows, row_bytes] in format fmt; tokens: int32 [T]; wpe: float16 [P, C] or None;
+    scale: Granite's embedding multiplier, applied in f32 to every dequantised value
+    (granite_model.cpp:298-301; not combined with wpe). Tokens outside [row_base, row_base + rows)
+    leave their out row untouched."""
     if not tokens.is_cuda:
         raise NekoError("tokens must be a GPU tensor")
     _on(table, "table", tokens.device)
@@ -349,6 +351,12 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, fmt: int, C: int, row_base:
             raise NekoError("wpe must be a contiguous float16 [P, C] table")
         wpe_ptr, wpe_rows = wpe.data_ptr(), wpe.shape[0]
     ctx = _ctx_for(tokens)
+    if scale is not None:
+        if wpe is not None:
+            raise NekoError("embed: a position table and a multiplier are not combined")
+        _issue(ctx, lib.neko_hip_embed_scaled, ctx.handle, tokens.data_ptr(), T, table.data_ptr(), table.shape[1],
+               int(fmt), int(C), int(row_base), n_rows, float(scale), out.data_ptr(), os_, _dtype_code(out))
+        return out
     _issue(ctx, lib.neko_hip_embed, ctx.handle, tokens.data_ptr(), T, table.data_ptr(), table.shape[1], int(fmt), int(C),
            int(row_base), n_rows, wpe_ptr, wpe_rows, int(pos0), out.data_ptr(), os_,
            _dtype_code(out))

@@ -191,6 +191,30 @@ struct Harness {
         }
     }
 
+    void scaledEmbed() {  // granite_model.cpp:298-301 through Embed flag 8 (the multiplier's bits in PB[3])
+        for (int fmt : {ORACLE_FMT_F16, ORACLE_FMT_FP8, ORACLE_FMT_FP4}) {
+            const int EV = 10, EC = 64, ET = 3;
+            const float mult = 12.0f;  // Granite-4.0's embedding_multiplier
+            auto table = rnd(size_t(EV * EC));
+            const size_t rb = oracle_quant_row_bytes(fmt, EC);
+            std::vector<uint8_t> q(rb * EV);
+            oracle_quantize_rows(fmt, EV, EC, table.data(), q.data());
+            int32_t toks[ET] = {3, 7, 9};
+            std::vector<float> ref(size_t(ET * EC));
+            for (int t = 0; t < ET; t++) {
+                oracle_dequantize_row(fmt, EC, q.data() + rb * size_t(toks[t]), ref.data() + t * EC);
+                for (int c = 0; c < EC; c++) ref[size_t(t * EC + c)] *= mult;  // x[c] *= embeddingMult
+            }
+            Buffer* out = be.create(ref.size() * 4, nullptr, true);
+            const int32_t ff = fmt == ORACLE_FMT_FP8 ? 2 : fmt == ORACLE_FMT_FP4 ? 4 : 0;
+            be.begin();
+            run(Kernel::Embed, {be.create(sizeof toks, toks), be.create(q.size(), q.data()), nullptr, out},
+                {ET, EC, 0, ff | 8, 0, EV, fmt == ORACLE_FMT_F16 ? EC / 2 : int(rb / 4), floatBits(mult)}, 1, ET);
+            be.submitAndWait();
+            closeOrFail(read(out, ref.size()), ref, 0.0f, "embed scaled", true);
+        }
+    }
+
     void gatedNorm() {  // granite_model.cpp:278-287 through the GatedRmsNorm extension
         const int T = 3, D = 128, groups = 2, zStride = 200;
         auto y = rnd(size_t(T * D)), z = rnd(size_t(T * zStride)), w = rnd(size_t(D));
@@ -353,6 +377,7 @@ extern "C" int backend_selftest(char* err, int err_bytes) {
         h.rope();
         h.siluMul();
         h.quantEmbed();
+        h.scaledEmbed();
         h.gatedNorm();
         h.kvStore();
         h.addRmsNorm();

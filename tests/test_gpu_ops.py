@@ -589,6 +589,31 @@ def test_embed_every_code_and_scale(dev, fmt):
     assert np.array_equal(got32.cpu().numpy().view(np.uint32), want32.view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt", [ops.FMT_F16, ops.FMT_FP8, ops.FMT_FP4])
+def test_embed_scaled_granite(dev, fmt):
+    """Granite's gather (granite_model.cpp:298-301): every dequantised value times the model's
+    embedding_multiplier in f32 -- one IEEE f32 multiply of the exact value -- and f16 output one RNE
+    rounding of that. Pinned by the closed form: the oracle's exact f32 gather times the multiplier in
+    numpy float32, then numpy's RNE to f16. Multipliers: Granite-4.0's 12, 0.3 (rounds), 2^-20
+    (exact), 70000 (f16 overflow to inf), on every code of every format and 3000 random tokens over
+    Granite's 1536-wide rows."""
+    _case(f"embed scaled fmt={fmt}")
+    C, V = 1536, 1000
+    x = wl.normal_f16((V, C), 0.0, 0.02, 36, "cpu").float().numpy()
+    x[0, :256] = np.linspace(-6.0, 6.0, 256, dtype=np.float32) * 0.02  # every magnitude class in one row
+    table, used = ops.quantize_rows(fmt, x)
+    assert used == fmt
+    ids = np.concatenate([np.zeros(4, np.int32), wl.uniform_ids(2996, V, 37)])
+    tt, it = torch.from_numpy(table).to(dev), torch.from_numpy(ids).to(dev)
+    base = O.embed(ids, table, fmt, C, out_f16=False)
+    for mult in (12.0, 0.3, 2.0 ** -20, 70000.0):
+        want32 = base * np.float32(mult)
+        got32 = ops.embed(it, tt, fmt, C, out_dtype=torch.float32, scale=mult).cpu().numpy()
+        assert np.array_equal(got32.view(np.uint32), want32.view(np.uint32)), f"f32 out, multiplier {mult}"
+        got16 = ops.embed(it, tt, fmt, C, scale=mult)
+        assert np.array_equal(to_bits(got16), want32.astype(np.float16).view(np.uint16)), f"f16 out, multiplier {mult}"
+
+
 def test_embed_gpt2_wpe(dev):
     """GPT-2 wte + wpe (f32 add, then one f16 rounding) at the configured shape: bit-exact."""
     cfg = wl.GPT2_CHAIN

@@ -41,9 +41,10 @@ using namespace neko::gpu;
 // What the reference's model code has in scope at its dispatch sites (qwen3_model.cpp:280-294,
 // granite_model.h:31-40).
 struct Layer { Buffer *wqkv, *bqkv, *norm, *ln2; };
-struct Config { float eps; int mGroups; };
+struct Config { float eps; int mGroups; float embeddingMult; };
 void dispatches(ComputeBackend& be, Layer L, Config cfg_, Buffer* xn, Buffer* qkv, Buffer* y, Buffer* proj, Buffer* x,
-                Buffer* d, int C, int QW, int T, int DI, int P, float eps) {
+                Buffer* d, int C, int QW, int T, int DI, int P, float eps, Buffer* tokens, Buffer* table, int flags,
+                int rows, int rowWords) {
     auto run = [&](Kernel k, Buffer* a, Buffer* b, Buffer* c, Buffer* e, std::initializer_list<int32_t> p, uint32_t gx,
                    uint32_t gy) {
         Buffer* binds[4] = {a, b, c, e};
@@ -53,7 +54,7 @@ void dispatches(ComputeBackend& be, Layer L, Config cfg_, Buffer* xn, Buffer* qk
         be.dispatch(k, binds, params, gx, gy);
     };
     (void)xn; (void)qkv; (void)y; (void)proj; (void)x; (void)d; (void)C; (void)QW; (void)T; (void)DI; (void)P;
-    (void)eps; (void)L; (void)cfg_;
+    (void)eps; (void)L; (void)cfg_; (void)tokens; (void)table; (void)flags; (void)rows; (void)rowWords;
 """
 
 
