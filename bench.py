@@ -786,10 +786,14 @@ def all_configs(args):
 
     # Qwen3-4B prefill (the headline layer)
     if want("qwen3_4b_prefill"):
-        cfg, per_op, _, layer = gpu_bench(argparse.Namespace(only=None, copy_mib=0, steps=args.steps,
-                                                             warmup=args.warmup, no_flush=False))
+        cfg, per_op, _, layer, floors = gpu_bench(argparse.Namespace(only=None, copy_mib=0, steps=args.steps,
+                                                                     warmup=args.warmup, no_flush=False, no_floors=False))
+        for op, d in per_op.items():
+            b = floors["best"][op]
+            d.update({"floor_us": b["us"], "floor_kind": b["kind"], "over_floor": round(d["us"] / b["us"] - 1, 4)})
         out["qwen3_4b_prefill"] = {"workload": "Qwen3-4B prefill layer (headline)", "ops": per_op,
-                                   "layer_step_us": round(statistics.median(layer) * 1e3, 3)}
+                                   "layer_step_us": round(statistics.median(layer) * 1e3, 3),
+                                   "layer_floor_us": floors["layer_step_us"]}
 
     # The headline layer's four ops on f32 activations, the type the reference's ComputeBackend (and so
     # the C++ adapter) passes: twice the activation bytes, the same kernels instantiated for f32.
@@ -966,6 +970,12 @@ def all_configs(args):
                 calls9[name].table = tab9
                 bytes9[name] = wl.bytes_matmul(c9.T, K, N, tab9.shape[1])
                 flops9[name] = 2 * c9.T * N * K
+                if fmt == ops.FMT_F16:  # the library's product exactly: f16 output
+                    ours16 = torch.empty((c9.T, N), dtype=torch.float16, device=dev)
+                    calls9[f"{name}_out16"] = ops.prepare(ops.matmul, x9, tab9, fmt, K, out=ours16)[0]
+                    calls9[f"{name}_out16"].keep = (tab9, ours16)
+                    bytes9[f"{name}_out16"] = wl.bytes_matmul(c9.T, K, N, tab9.shape[1], y_bytes=2)
+                    flops9[f"{name}_out16"] = flops9[name]
             del wsrc
         run("qwen3_4b_prefill_matmul", calls9, bytes9,
             "Qwen3-4B prefill, T=8192: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
@@ -974,7 +984,7 @@ def all_configs(args):
                               HipTimer(torch.cuda.current_stream().cuda_stream))
         for n, v in lib_ops.items():
             tf = flops9[n] / (v["us"] * 1e-6) / 1e12
-            out["qwen3_4b_prefill_matmul"]["ops"][n].update(
+            out["qwen3_4b_prefill_matmul"]["ops"][f"{n}_out16"].update(
                 {"library_us": v["us"], "library_TFLOPs": round(tf, 1), "library": "torch.matmul f16 x f16 -> f16 (hipBLASLt)"})
         del calls9, lib9
 

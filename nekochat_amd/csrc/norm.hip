@@ -386,8 +386,12 @@ struct RoundWeights {
 
 template <Norm K, typename T, int CH, int R>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void norm_round_kernel(NormArgs a) {
-    static_assert(K == Norm::Rms || K == Norm::Layer, "plain norms only");
+    static_assert(K != Norm::Gated, "plain norms and the residual add + RMSNorm");
     constexpr int N = Chunk16<T>::N;
+    constexpr bool kAdd = K == Norm::AddRms;
+    // Stores: non-temporal for the plain norms; plain for the residual add + RMSNorm, which writes two
+    // rows per row (measured at [8192, 2560]: 28.9 us plain, 30.8 non-temporal).
+    constexpr bool kNt = !kAdd;
     typedef typename Chunk16<T>::V V;
     extern __shared__ float4v rlds[];
     const int lane = threadIdx.x & 63;
@@ -395,7 +399,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void n
     const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nch = a.C / N;
     const uint32_t row_bytes = static_cast<uint32_t>(a.C) * sizeof(T);
-    V x[R][CH];
+    V x[R][CH], z[kAdd ? R : 1][kAdd ? CH : 1];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const int64_t row = w + r * nw;
@@ -403,6 +407,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void n
         const BufRes res = buf_res(static_cast<const T*>(a.x) + (in ? row : 0) * a.xs, in ? row_bytes : 0u);
 #pragma unroll
         for (int k = 0; k < CH; k++) x[r][k] = buf_load16<true, V>(res, static_cast<uint32_t>(k * kWave + lane) * 16u);
+        if constexpr (kAdd) {
+            const BufRes rz = buf_res(static_cast<const T*>(a.z) + (in ? row : 0) * a.zs, in ? row_bytes : 0u);
+#pragma unroll
+            for (int k = 0; k < CH; k++) z[r][k] = buf_load16<true, V>(rz, static_cast<uint32_t>(k * kWave + lane) * 16u);
+        }
     }
     {
         const int nq = nch * (N / 4);
@@ -421,7 +430,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void n
         if (row >= a.rows) break;  // wave-uniform
         auto f = [&](int k, int e) __attribute__((always_inline)) -> float { return to_f32(x[r][k][e]); };
         float scale, mean_f = 0.0f;
-        if constexpr (K == Norm::Layer) {
+        if constexpr (kAdd) {
+            // The residual x + delta, rounded once to T (cpu_ops.cpp:123), is what the norm reads; its
+            // squares are summed as each value is formed.
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < CH; k++)
+#pragma unroll
+                for (int e = 0; e < N; e++) {
+                    x[r][k][e] = from_f32<T>(to_f32(x[r][k][e]) + to_f32(z[r][k][e]));
+                    const double d = static_cast<double>(to_f32(x[r][k][e]));
+                    ss = __builtin_fma(d, d, ss);
+                }
+            ss = wave_sum_f64(ss);
+            scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
+        } else if constexpr (K == Norm::Layer) {
             const double mean = wave_sum_f64(sum_values<CH, N>(f)) / a.C;
             const double var = wave_sum_f64(sum_centered<CH, N, kWave>(f, mean, lane, nch)) / a.C;
             scale = static_cast<float>(1.0 / sqrt(var + static_cast<double>(a.eps)));
@@ -431,9 +454,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void n
             scale = static_cast<float>(1.0 / sqrt(ss / a.C + static_cast<double>(a.eps)));
         }
         const BufRes res = buf_res(static_cast<T*>(a.y) + row * a.ys, row_bytes);
+        const BufRes rx = buf_res(static_cast<const T*>(a.x) + row * a.xs, kAdd ? row_bytes : 0u);
 #pragma unroll
-        for (int k = 0; k < CH; k++)
-            buf_store16<true>(res, static_cast<uint32_t>(k * kWave + lane) * 16u, out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
+        for (int k = 0; k < CH; k++) {
+            const uint32_t off = static_cast<uint32_t>(k * kWave + lane) * 16u;
+            if constexpr (kAdd) buf_store16<kNt>(rx, off, x[r][k]);  // the residual back over x
+            buf_store16<kNt>(res, off, out_chunk<K, T, CH>(f, k, scale, mean_f, wt));
+        }
     }
 }
 
@@ -570,10 +597,12 @@ constexpr bool has_row_form(Norm k) { return k == Norm::Rms || k == Norm::Layer;
 
 // The one-round kernel for R rows of CH chunks per lane, instantiated where it compiles within 128
 // VGPRs (four waves per SIMD) without spills: RMSNorm while a wave's rows take at most 60 data
-// registers (CH * R <= 15 16-byte chunks), LayerNorm -- whose two passes keep the row's values widened
-// to double between them -- up to 4 chunks.
-constexpr int round_max_chunks(Norm k) { return k == Norm::Layer ? 4 : 15; }
-constexpr int kRoundMaxRows = 4;
+// registers (CH * R <= 15 16-byte chunks), the residual add + RMSNorm (two operand rows) up to 10,
+// LayerNorm -- whose two passes keep the row's values widened to double between them -- up to 4.
+constexpr int round_max_chunks(Norm k) { return k == Norm::Layer ? 4 : k == Norm::AddRms ? 10 : 15; }
+// Up to three rows per wave: four (16384 rows of 1536 halves) measured 3% slower than one row per wave
+// over the whole grid.
+constexpr int kRoundMaxRows = 3;
 
 template <Norm K, typename T, int CH>
 NormKernel pick_round_r(int R) {
@@ -582,7 +611,6 @@ NormKernel pick_round_r(int R) {
         case 1: if constexpr (CH <= M) return norm_round_kernel<K, T, CH, 1>; break;
         case 2: if constexpr (2 * CH <= M) return norm_round_kernel<K, T, CH, 2>; break;
         case 3: if constexpr (3 * CH <= M) return norm_round_kernel<K, T, CH, 3>; break;
-        case 4: if constexpr (4 * CH <= M) return norm_round_kernel<K, T, CH, 4>; break;
     }
     return nullptr;
 }
@@ -657,8 +685,8 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         case Norm::AddRms: k = pick<Norm::AddRms>(dtype, W, CH, wl); break;
     }
     if (!k) return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: no kernel for C=%d", what, a.C);
-    if (W == 1 && (kind == Norm::Rms || kind == Norm::Layer) && a.groups == 1) {
-        // Up to four rows per wave in one round of four waves per SIMD: R = the rows per wave that
+    if (W == 1 && kind != Norm::Gated && a.groups == 1) {
+        // Up to three rows per wave in one round of four waves per SIMD: R = the rows per wave that
         // round needs (measured at 2560 halves: 4096 rows R = 1 9.3 us against 11.0 for the
         // one-row-per-wave grid, 8192 rows R = 2 15.0 against 17.1 persistent, 12288 rows R = 3 22.8
         // against 23.3; at 8192 rows R = 1 over the whole grid at eight waves per SIMD took 16.9).
@@ -668,8 +696,14 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
         if (R <= kRoundMaxRows) {
             const bool h = dtype == NEKO_DT_F16;
             const int r = static_cast<int>(R);
-            kr = kind == Norm::Rms ? (h ? pick_round<Norm::Rms, half_t>(CH, r) : pick_round<Norm::Rms, float>(CH, r))
-                                   : (h ? pick_round<Norm::Layer, half_t>(CH, r) : pick_round<Norm::Layer, float>(CH, r));
+            switch (kind) {
+                case Norm::Rms: kr = h ? pick_round<Norm::Rms, half_t>(CH, r) : pick_round<Norm::Rms, float>(CH, r); break;
+                case Norm::Layer: kr = h ? pick_round<Norm::Layer, half_t>(CH, r) : pick_round<Norm::Layer, float>(CH, r); break;
+                case Norm::AddRms:
+                    kr = h ? pick_round<Norm::AddRms, half_t>(CH, r) : pick_round<Norm::AddRms, float>(CH, r);
+                    break;
+                default: break;
+            }
         }
         if (kr) {
             const size_t rl = static_cast<size_t>(a.C) * sizeof(float) * (kind == Norm::Layer ? 2 : 1);

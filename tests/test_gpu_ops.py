@@ -34,11 +34,11 @@ def _w(n, stream, dev, mean=1.0, std=0.05):
 @pytest.mark.parametrize("T,C,eps", [
     (64, 1024, 1e-6),      # Qwen3-0.6B decode (one round, one row per wave)
     (8192, 2560, 1e-6),    # Qwen3-4B prefill (one round, two rows per wave)
-    (16384, 1536, 1e-5),   # Granite pre-norm (one round, four rows per wave)
+    (16384, 1536, 1e-5),   # Granite pre-norm (one row per wave over the whole grid)
     (12288, 2560, 1e-6),   # one round, three rows per wave
     (4096, 2560, 1e-6),    # one round, one row of five chunks per lane
     (8191, 2000, 1e-6),    # two rows per wave, the last wave one short; 250 chunks: lanes past the row end
-    (32768, 2560, 1e-6),   # one row per wave over the whole grid (more than one round's four rows per wave)
+    (32768, 2560, 1e-6),   # one row per wave over the whole grid (more than one round's three rows per wave)
     (3, 96, 1e-6),         # reference self-test width
     (5, 4104, 1e-6),       # four waves per row
     (7, 100, 1e-6),        # width not a multiple of 8: fallback kernel
@@ -410,11 +410,14 @@ def test_store_kv(dev, dtype, width, k_off, v_off):
 # ------------------------------------------------------------------ residual add + RMSNorm
 
 @pytest.mark.parametrize("T,C,dtype", [
-    (8192, 2560, torch.float16),   # Qwen3-4B prefill
-    (64, 1024, torch.float16),
+    (8192, 2560, torch.float16),   # Qwen3-4B prefill (one round, two rows per wave)
+    (64, 1024, torch.float16),     # one round, one row per wave
+    (8191, 2000, torch.float16),   # one round, two rows per wave, the last wave one short; lanes past the row end
+    (12288, 2560, torch.float16),  # three rows of five chunks: more than the one-round budget, persistent waves
     (7, 100, torch.float16),       # odd width: generic kernel
     (3, 20000, torch.float16),     # four waves per row
     (33, 1536, torch.float32),
+    (8192, 1024, torch.float32),   # f32, one round, two rows per wave
 ])
 def test_add_rmsnorm(dev, T, C, dtype):
     _case(f"add + rmsnorm {T}x{C} {dtype}")
