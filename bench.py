@@ -715,6 +715,13 @@ def all_configs(args):
     dev = torch.device("cuda:0")
     flush = torch.ones(256 << 20, dtype=torch.float32, device=dev)
     out = {}
+    if args.copy_mib:  # one plain device copy of known size: calibrates rocprof byte counters
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        flush.sum()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     labels = ("gpt2_small_chain", "qwen3_0.6b_decode", "qwen3_4b_prefill", "qwen3_4b_prefill_f32", "quant_gather_qwen3_1.7b",
               "qwen3_4b_fused",
