@@ -139,7 +139,7 @@ class FloorLib:
                             ("neko_floor_rows_up", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_int,
                                                     c.c_int, c.c_int, c.c_void_p]),
                             ("neko_floor_gather", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_void_p,
-                                                   c.c_int64, c.c_int64, c.c_int, c.c_void_p])):
+                                                   c.c_int64, c.c_int64, c.c_int, c.c_int, c.c_void_p])):
             getattr(lib, name).argtypes = args_
             getattr(lib, name).restype = c.c_int
             self.bound.add(name)
@@ -181,20 +181,14 @@ class FloorLib:
 
 
 def headline_floors(cfg, inp, dev, fl):
-    """Floor candidates for each headline op over the op's own byte pattern: the floor kernels (copies
-    in the op's layout) and the runtime's device-to-device copies (hipMemcpyAsync, hipMemcpy2DAsync,
-    torch's copy_). Returns (calls, bytes, {op: [candidate names]}, {op: {candidate: call}} for the
+    """Floor candidates for each headline op over the op's own byte pattern and data (the op's input
+    tensors as the sources): the floor kernels (copies in the op's layout) and the runtime's
+    device-to-device copies (hipMemcpyAsync, hipMemcpy2DAsync, torch's copy_). Returns (calls, bytes, {op: [candidate names]}, {op: {candidate: call}} for the
     layer-floor step, whose two RMSNorm floors use separate buffers so neither finds the other's bytes
     in a cache)."""
     import torch
 
     from nekochat_amd import workloads as wl
-
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(12345)
-
-    def rand_bytes(n):
-        return torch.randint(-2 ** 31, 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device=dev, generator=gen)
 
     calls, nbytes, groups, layer = {}, {}, {}, {}
     half = cfg.T * cfg.C * 2  # one [T, C] fp16 row set
@@ -203,7 +197,10 @@ def headline_floors(cfg, inp, dev, fl):
     r_up = -(-cfg.T // (16 * torch.cuda.get_device_properties(dev).multi_processor_count))
     row_b = cfg.C * 2
     for op in ("rmsnorm_in", "rmsnorm_post"):
-        src, dst = rand_bytes(half), rand_bytes(half)
+        # The op's own input rows as the source, as for the other ops' floors below: uniformly random
+        # bits move measurably slower than f16 activations (and constant data faster).
+        src = inp["x" if op == "rmsnorm_in" else "x_post"]
+        dst = torch.empty_like(src)
         cand = {
             "copy_i1_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 1, 1, 1),
             "copy_i4_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 4, 1, 1),
@@ -245,13 +242,13 @@ def headline_floors(cfg, inp, dev, fl):
     h = inp["h"]
     gout = torch.empty((cfg.T, cfg.I), dtype=torch.float16, device=dev)
     tot = 3 * gi // 2 // 16 * 16
-    s1, d1 = rand_bytes(tot), rand_bytes(tot)
+    d1 = torch.empty(tot, dtype=torch.uint8, device=dev)
     cand = {
         "rows2_ntpl": fl.rows2(h.data_ptr(), 2 * gi // cfg.T, gout.data_ptr(), gi // cfg.T, cfg.T, gi // cfg.T, 1, 0),
         "copy2_ntpl": fl.copy2(h.data_ptr(), h.data_ptr() + gi, gout.data_ptr(), gi, 1, 0),
-        "hipMemcpyAsync_same_total": fl.memcpy(d1.data_ptr(), s1.data_ptr(), tot),
+        "hipMemcpyAsync_same_total": fl.memcpy(d1.data_ptr(), h.data_ptr(), tot),
     }
-    layer["swiglu"] = dict(cand, _keep=(gout, s1, d1))
+    layer["swiglu"] = dict(cand, _keep=(gout, d1))
     groups["swiglu"] = []
     for k, v in cand.items():
         calls[f"swiglu:{k}"], nbytes[f"swiglu:{k}"] = v, 3 * gi if not k.startswith("hip") else 2 * tot
@@ -833,7 +830,8 @@ def all_configs(args):
         calls4, bytes4 = {}, {}
         unique = int(np.unique(ids4).size)
         # The floor of each gather's byte pattern: the same table rows read through the same ids, the
-        # same 4 KB output rows written, nothing decoded (1, 2 or 4 tokens per wave; the fastest counts).
+        # same 4 KB output rows written, nothing decoded (1, 2 or 4 tokens per wave, non-temporal or plain
+        # row loads -- plain ones let repeated ids hit in L2, as the op's do; the fastest counts).
         fl4 = FloorLib(torch.cuda.current_stream().cuda_stream)
         fo4 = torch.empty_like(o4)
         floor_names = {}
@@ -846,11 +844,12 @@ def all_configs(args):
             rb = tab.shape[1]
             floor_names[name] = []
             for tpw in (1, 2, 4):
-                fname = f"floor_{name}_tpw{tpw}"
-                calls4[fname] = fl4.gather(ids4_t.data_ptr(), c4.T, tab_t.data_ptr(), rb, rb, fo4.data_ptr(), c4.C * 2,
-                                           c4.C * 2, tpw)
-                bytes4[fname] = bytes4[name]
-                floor_names[name].append(fname)
+                for ntl in (1, 0):
+                    fname = f"floor_{name}_tpw{tpw}_{'nt' if ntl else 'pl'}"
+                    calls4[fname] = fl4.gather(ids4_t.data_ptr(), c4.T, tab_t.data_ptr(), rb, rb, fo4.data_ptr(),
+                                               c4.C * 2, c4.C * 2, tpw, ntl)
+                    bytes4[fname] = bytes4[name]
+                    floor_names[name].append(fname)
         del src
         run("quant_gather_qwen3_1.7b", calls4, bytes4,
             f"Qwen3-1.7B tied table 151936x2048, 16384 Zipf(1.1) ids ({unique} unique rows): mostly cache-served")
@@ -966,10 +965,11 @@ def all_configs(args):
             wsrc = wl.normal_f16((N, K), 0.0, 0.02, 91, dev).float()
             x9 = wl.normal_f16((c9.T, K), 0.0, 1.0, 92, dev)
             y9 = torch.empty((c9.T, N), dtype=torch.float32, device=dev)
-            # The vendor library on the same F16 product (torch.matmul -> hipBLASLt; f16 output):
-            # a reference point for the MFMA kernel, not part of the path.
+            # The vendor library on the same F16 product (torch -> hipBLASLt), with f16 output and with
+            # f32 output (this path's own): a reference point for the MFMA kernel, not part of the path.
             w16, y16 = wsrc.half(), torch.empty((c9.T, N), dtype=torch.float16, device=dev)
-            lib9[f"{pname}_f16"] = (lambda x=x9, w=w16, y=y16: torch.matmul(x, w.t(), out=y))
+            lib9[f"{pname}_f16_out16"] = (lambda x=x9, w=w16, y=y16: torch.matmul(x, w.t(), out=y))
+            lib9[f"{pname}_f16"] = (lambda x=x9, w=w16: torch.mm(x, w.t(), out_dtype=torch.float32))
             for fmt, fname in ((ops.FMT_F16, "f16"), (ops.FMT_FP8, "fp8"), (ops.FMT_FP4, "fp4")):
                 tab9, _ = ops.quantize(wsrc, fmt)
                 name = f"{pname}_{fname}"
@@ -991,8 +991,11 @@ def all_configs(args):
                               HipTimer(torch.cuda.current_stream().cuda_stream))
         for n, v in lib_ops.items():
             tf = flops9[n] / (v["us"] * 1e-6) / 1e12
-            out["qwen3_4b_prefill_matmul"]["ops"][f"{n}_out16"].update(
-                {"library_us": v["us"], "library_TFLOPs": round(tf, 1), "library": "torch.matmul f16 x f16 -> f16 (hipBLASLt)"})
+            kind = "f16" if n.endswith("_out16") else "f32"
+            out["qwen3_4b_prefill_matmul"]["ops"][n].update(
+                {"library_us": v["us"], "library_TFLOPs": round(tf, 1),
+                 "library": f"torch f16 x f16 -> {kind} (hipBLASLt)",
+                 "vs_library": round(v["us"] / out["qwen3_4b_prefill_matmul"]["ops"][n]["us"], 4)})
         del calls9, lib9
 
     if not args.no_cpu:
@@ -1106,6 +1109,15 @@ def stream_floor(args, flush, time_ops):
     calls["qk_norm_rope_op"] = ops.prepare(ops.qk_norm_rope, qk_in["qkv"], cfg.n_q, cfg.n_kv, cfg.hd, qk_in["cs"], cfg.eps,
                                            wqk=qk_in["wqk"], positions=qk_in["positions"])[0]
     nbytes["qk_norm_rope_op"] = wl.bytes_qk_rope(cfg.T, cfg.n_q, cfg.n_kv, cfg.hd)
+    # The RMSNorm's bytes copied from its own input rows (f16 activations) instead of random bits.
+    x_own = qk_in["x"]
+    x_dst = torch.empty_like(x_own)
+    for items, ntl, nts in ((1, 1, 1), (4, 0, 0)):
+        name = f"copy_rmsnorm_i{items}_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}_owndata"
+        calls[name], nbytes[name] = fl.copy(x_own.data_ptr(), x_dst.data_ptr(), half, items, ntl, nts), 2 * half
+    calls["rows_up_rmsnorm_r2_owndata"] = fl.rows_up(x_own.data_ptr(), cfg.C * 2, x_dst.data_ptr(), cfg.C * 2, cfg.T, 2,
+                                                     cfg.C * 2 // 1024, 0)
+    nbytes["rows_up_rmsnorm_r2_owndata"] = 2 * half
     waves = 16 * torch.cuda.get_device_properties(dev).multi_processor_count
     for ntl, nts in ((1, 0), (0, 0)):
         name = f"inplace_qk_rows_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"

@@ -154,8 +154,9 @@ __global__ __launch_bounds__(256) void rows_up_kernel(const u32x4* src, int64_t 
 // (their ids in one load), reads each token's table row (row_chunks 16-byte chunks, lane l chunks l,
 // l + 64, ...) and writes out_chunks 16-byte chunks of output per token (lane l chunks l, l + 64, ...:
 // 1 KB of contiguous output per store instruction), every output chunk the xor of the lane's row
-// chunks with `key`. row_chunks <= 256, out_chunks <= 256.
-template <int TPW>
+// chunks with `key`. row_chunks <= 256, out_chunks <= 256. NTL: non-temporal row loads (plain ones keep
+// the rows that repeated ids read again in L2).
+template <int TPW, bool NTL>
 __global__ __launch_bounds__(256) void gather_kernel(const int32_t* ids, int64_t T, const u32x4* table, int64_t row_stride,
                                                      int row_chunks, u32x4* out, int64_t out_stride, int out_chunks,
                                                      uint32_t key) {
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t* ids, int64_t
         acc[k] = u32x4{key, key, key, key};
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            if (64 * j + lane < row_chunks) acc[k] ^= __builtin_nontemporal_load(row + 64 * j + lane);
+            if (64 * j + lane < row_chunks) acc[k] ^= NTL ? __builtin_nontemporal_load(row + 64 * j + lane) : row[64 * j + lane];
     }
 #pragma unroll
     for (int k = 0; k < TPW; k++) {
@@ -333,9 +334,9 @@ int neko_floor_rows_up(const void* src, int64_t s_stride, void* dst, int64_t d_s
 
 // The gather's bytes: for t < T, reads table row ids[t] (row_bytes of it; rows row_stride bytes apart)
 // and writes out_bytes at out + t * out_stride; ids must index the table (the caller checks), sizes
-// multiples of 16 bytes up to 4 KB, tpw (tokens per wave) 1, 2 or 4.
+// multiples of 16 bytes up to 4 KB, tpw (tokens per wave) 1, 2 or 4, ntl: non-temporal row loads.
 int neko_floor_gather(const int32_t* ids, int64_t T, const void* table, int64_t row_stride, int64_t row_bytes, void* out,
-                      int64_t out_stride, int64_t out_bytes, int tpw, void* stream) {
+                      int64_t out_stride, int64_t out_bytes, int tpw, int ntl, void* stream) {
     if (!ok16(table) || !ok16(out) || row_stride % 16 || out_stride % 16 || row_bytes % 16 || out_bytes % 16 ||
         row_bytes <= 0 || row_bytes > 4096 || out_bytes <= 0 || out_bytes > 4096 || row_stride < row_bytes ||
         out_stride < out_bytes || T <= 0 || (tpw != 1 && tpw != 2 && tpw != 4))
@@ -347,9 +348,15 @@ int neko_floor_gather(const int32_t* ids, int64_t T, const void* table, int64_t 
     const auto* tp = static_cast<const u32x4*>(table);
     auto* op = static_cast<u32x4*>(out);
     const int rc = static_cast<int>(row_bytes / 16), oc = static_cast<int>(out_bytes / 16);
-    if (tpw == 1) hipLaunchKernelGGL((gather_kernel<1>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u);
-    else if (tpw == 2) hipLaunchKernelGGL((gather_kernel<2>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u);
-    else hipLaunchKernelGGL((gather_kernel<4>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u);
+#define NEKO_FLOOR_GATHER(TPW, NTL) \
+    hipLaunchKernelGGL((gather_kernel<TPW, NTL>), g, b, 0, st, ids, T, tp, row_stride / 16, rc, op, out_stride / 16, oc, 0u)
+    if (tpw == 1 && ntl) NEKO_FLOOR_GATHER(1, true);
+    else if (tpw == 1) NEKO_FLOOR_GATHER(1, false);
+    else if (tpw == 2 && ntl) NEKO_FLOOR_GATHER(2, true);
+    else if (tpw == 2) NEKO_FLOOR_GATHER(2, false);
+    else if (ntl) NEKO_FLOOR_GATHER(4, true);
+    else NEKO_FLOOR_GATHER(4, false);
+#undef NEKO_FLOOR_GATHER
     return hipGetLastError();
 }
 
