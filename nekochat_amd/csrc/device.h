@@ -74,6 +74,16 @@ __device__ __forceinline__ V buf_load16(BufRes r, uint32_t off) {
     static_assert(sizeof(V) == 16, "16-byte vector");
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, NT ? 2 : 0));
 }
+// 4, 8 or 16 bytes at byte offset `off` (plain cache policy).
+template <typename V>
+__device__ __forceinline__ V buf_load(BufRes r, uint32_t off) {
+    if constexpr (sizeof(V) == 16) return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    else if constexpr (sizeof(V) == 8) return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    else {
+        static_assert(sizeof(V) == 4, "4, 8 or 16 bytes");
+        return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    }
+}
 template <bool NT, typename V>
 __device__ __forceinline__ void buf_store16(BufRes r, uint32_t off, V v) {
     static_assert(sizeof(V) == 16, "16-byte vector");

@@ -66,12 +66,11 @@ __device__ __forceinline__ uint32_t word_of(const R& r, int w) {
     else return static_cast<uint32_t>(r[w]);
 }
 
-// Launch shape (the fastest measured on MI355X for a 16384-token gather of 2048-wide rows): tokens
-// per wavefront, per table format (F16, FP8, FP4) -- more tokens put more rows' loads in flight per
-// wave, at the cost of registers (occupancy) for the decoding formats -- and 16-byte output chunks
-// per lane per token in flight.
+// Launch shape (the fastest measured on MI355X for a 16384-token gather of 2048-wide rows): four
+// tokens per wavefront for every format (two: F16 20.8, FP8 18.5, FP4 17.5 us against 19.0 / 17.5 /
+// 15.4 with four) and four 16-byte output chunks per lane per token in flight.
 __host__ __device__ constexpr int chunks_in_flight(int) { return 4; }
-__host__ __device__ constexpr int tokens_per_wave(int fmt) { return fmt == 1 ? 2 : 4; }
+__host__ __device__ constexpr int tokens_per_wave(int) { return 4; }
 
 // Vector path. FMT: 0 F16, 1 FP8, 2 FP4. The output row is cut into chunks of EPC = 16 bytes of
 // output elements (8 halves or 4 floats); lane l takes chunks l, l + 64, ..., so every store
@@ -86,10 +85,18 @@ __host__ __device__ constexpr int tokens_per_wave(int fmt) { return fmt == 1 ? 2
 // loaded once (measured for a 16384-token Zipf gather of 2048-wide rows: 16.8 us against 19.7 for
 // 8-byte loads per chunk, which fetch every byte twice).
 // Each wave owns tokens_per_wave(FMT) consecutive tokens: their ids come in one load, then every
-// row's chunk loads are issued before any is decoded.
+// row's chunk loads are issued before any is decoded. Two ways to move the bytes, chosen per format
+// by measurement (16384 Zipf tokens of 2048-wide rows, f16 out, side by side):
+// - F16 and FP8: plain loads and stores per chunk (a chunk past the row's end skips both), FP8's block
+//   scale loaded per chunk: 19.0 / 17.5 us, on the floors of their patterns (19.0 / 17.2); the form
+//   below took 20.3 / 19.2.
+// - FP4: every load and store through range-checked buffer resources (device.h), so nothing is under a
+//   branch and the compiler's memory-counter waits stay per token, and one dword of block scales per
+//   lane and step shared by ds_bpermute: 15.4 us, under its floor (16.1); the form above took 16.5.
 template <int FMT, typename TO, Extra X>
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     constexpr bool WPE = X == Extra::Wpe;
+    constexpr bool kRes = FMT == 2;
     constexpr int EPC = 16 / sizeof(TO);  // output elements per chunk
     constexpr int TPW = tokens_per_wave(FMT);  // tokens per wave, all in flight together
     constexpr int B = chunks_in_flight(FMT);   // chunks per lane per token in flight
@@ -108,52 +115,94 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     if (t0 >= a.T) return;
     // The wave's token ids in one load (lane i holds token t0 + i), then broadcast as scalars.
     const int32_t my_id = lane < TPW && t0 + lane < a.T ? a.tokens[t0 + lane] : 0;
+    // Each token's row: a pointer, and for kRes a resource over it (empty for a token outside this table
+    // chunk; loads past a resource return zeros with no memory access, stores past it are dropped).
     const uint8_t* rowp[TPW];
+    BufRes rowr[TPW], wper[TPW];
     bool live[TPW];
+    const uint32_t rbytes = static_cast<uint32_t>(a.row_bytes);
 #pragma unroll
     for (int k = 0; k < TPW; k++) {
         const int64_t r = static_cast<int64_t>(__builtin_amdgcn_readlane(my_id, k)) - a.row_base;
         live[k] = t0 + k < a.T && r >= 0 && r < a.rows;  // other tokens belong to another table chunk
         rowp[k] = a.table + (live[k] ? r : 0) * a.row_bytes;
+        if constexpr (kRes) {
+            rowr[k] = buf_res(rowp[k], live[k] ? rbytes : 0u);
+            if constexpr (WPE)
+                wper[k] = buf_res(a.wpe + (live[k] ? a.pos0 + t0 + k : 0) * a.C, live[k] ? static_cast<uint32_t>(a.C) * 2u : 0u);
+        }
     }
     const int nch = a.C / EPC;
     const int64_t soff = FMT == 1 ? a.C : a.C / 2;  // scales follow the codes
+    // kRes block scales: a step of B * 64 chunks spans (B * 64) / CPB blocks (at most 64 halves: 32
+    // dwords); lane l loads dword l % 32 of them and each lane takes its chunk's scale from the lane
+    // holding it (ds_bpermute).
+    constexpr int CPB = 32 / EPC;  // chunks per 32-wide block
+    static_assert(B * kWave / CPB <= 64, "one dword of scales per lane covers a step");
 
     for (int c0 = 0; c0 < nch; c0 += B * kWave) {
         Load raw[TPW][B];
         half_t sc[TPW][B];
+        uint32_t scw[TPW];
         VH pw[TPW][B];
+        const uint32_t blk0 = static_cast<uint32_t>(c0 / CPB);  // the step's first block (c0: a multiple of B * 64)
 #pragma unroll
         for (int k = 0; k < TPW; k++) {
-            if (!live[k]) continue;
-            const uint8_t* row = rowp[k];
+            if constexpr (kRes) {
+                scw[k] = buf_load<uint32_t>(rowr[k], static_cast<uint32_t>(soff) + 2 * blk0 + 4 * (lane & 31));
 #pragma unroll
-            for (int b = 0; b < B; b++) {
-                const int c = c0 + b * kWave + lane;
-                if (c >= nch) continue;
-                const int e0 = c * EPC;
-                if constexpr (FMT == 0) {
-                    raw[k][b] = *reinterpret_cast<const Raw*>(row + 2 * e0);
-                } else if constexpr (FMT == 1) {
-                    raw[k][b] = *reinterpret_cast<const Raw*>(row + e0);
-                    sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * (e0 >> 5));
-                } else {
-                    const int blk = e0 >> 5, j0 = e0 & 15;
-                    if constexpr (kQuad) raw[k][b] = *reinterpret_cast<const uint32_t*>(row + 16 * blk + 4 * (lane & 3));
-                    else raw[k][b] = *reinterpret_cast<const Raw*>(row + 16 * blk + j0);
-                    sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * blk);
+                for (int b = 0; b < B; b++) {
+                    // Chunks past the row's last one load whatever the row holds there, or zeros past
+                    // its end; they are not stored.
+                    const uint32_t e0 = static_cast<uint32_t>((c0 + b * kWave + lane) * EPC);
+                    const uint32_t blk = e0 >> 5, j0 = e0 & 15;
+                    if constexpr (kQuad) raw[k][b] = buf_load<uint32_t>(rowr[k], 16 * blk + 4 * (lane & 3));
+                    else raw[k][b] = buf_load<Raw>(rowr[k], 16 * blk + j0);
+                    if constexpr (WPE) pw[k][b] = buf_load<VH>(wper[k], 2 * e0);
                 }
-                if constexpr (WPE) pw[k][b] = *reinterpret_cast<const VH*>(a.wpe + (a.pos0 + t0 + k) * a.C + e0);
+            } else {
+                if (!live[k]) continue;
+                const uint8_t* row = rowp[k];
+#pragma unroll
+                for (int b = 0; b < B; b++) {
+                    const int c = c0 + b * kWave + lane;
+                    if (c >= nch) continue;
+                    const int e0 = c * EPC;
+                    if constexpr (FMT == 0) {
+                        raw[k][b] = *reinterpret_cast<const Raw*>(row + 2 * e0);
+                    } else {
+                        raw[k][b] = *reinterpret_cast<const Raw*>(row + e0);
+                        sc[k][b] = *reinterpret_cast<const half_t*>(row + soff + 2 * (e0 >> 5));
+                    }
+                    if constexpr (WPE) pw[k][b] = *reinterpret_cast<const VH*>(a.wpe + (a.pos0 + t0 + k) * a.C + e0);
+                }
             }
         }
 #pragma unroll
         for (int k = 0; k < TPW; k++) {
-            if (!live[k]) continue;
+            if constexpr (!kRes) {
+                if (!live[k]) continue;
+            }
             TO* out = static_cast<TO*>(a.out) + (t0 + k) * a.out_stride;
+            const BufRes outr = buf_res(out, kRes && live[k] ? static_cast<uint32_t>(a.C * sizeof(TO)) : 0u);
+            // kRes: each chunk's block scale from the lane that loaded it (all lanes active here).
+            half_t scs[B];
+            if constexpr (kRes) {
+#pragma unroll
+                for (int b = 0; b < B; b++) {
+                    const int rb = (b * kWave + lane) / CPB;  // block relative to blk0
+                    const half2v s2 = __builtin_bit_cast(
+                        half2v, __builtin_amdgcn_ds_bpermute(4 * (rb >> 1), static_cast<int>(scw[k])));
+                    scs[b] = s2[rb & 1];
+                }
+            }
 #pragma unroll
             for (int b = 0; b < B; b++) {
                 const int c = c0 + b * kWave + lane;
-                if (c >= nch) continue;  // whole quads: nch is a multiple of 4 for FP8 / FP4
+                if constexpr (!kRes) {
+                    if (c >= nch) continue;
+                    if constexpr (FMT != 0) scs[b] = sc[k][b];
+                }
                 // The chunk's code bytes: FP4 quad loads give lane q of a quad the block's bytes 0-7
                 // (q = 0, 2) or 8-15 (q = 1, 3), the dwords of quad lanes 2 (q % 2) and 2 (q % 2) + 1.
                 Raw rw;
@@ -166,7 +215,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
                 }
                 VO o;
                 if constexpr (kPacked) {
-                    const half2v s2 = {sc[k][b], sc[k][b]};
+                    const half2v s2 = {scs[b], scs[b]};
                     const half2v k2 = FMT == 1 ? half2v{256.0f16, 256.0f16} : half2v{16384.0f16, 16384.0f16};
                     const int shift = FMT == 2 && ((c * EPC) & 16) ? 4 : 0;
                     uint4v ob;
@@ -185,7 +234,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 #pragma unroll
                         for (int e = 0; e < EPC; e++) v[e] = static_cast<float>(h[e]);
                     } else if constexpr (FMT == 1) {
-                        const float sf = static_cast<float>(sc[k][b]) * 256.0f;
+                        const float sf = static_cast<float>(scs[b]) * 256.0f;
 #pragma unroll
                         for (int w = 0; w < EPC / 4; w++) {
                             const uint32_t word = word_of(rw, w);
@@ -199,7 +248,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
                         }
                     } else {
                         const int shift = ((c * EPC) & 16) ? 4 : 0;  // high nibbles for elements 16..31 of the block
-                        const float sf = static_cast<float>(sc[k][b]) * 16384.0f;
+                        const float sf = static_cast<float>(scs[b]) * 16384.0f;
 #pragma unroll
                         for (int w = 0; w < EPC / 4; w++) {
                             const uint32_t word = word_of(rw, w) >> shift;
@@ -218,7 +267,9 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 #pragma unroll
                     for (int e = 0; e < EPC; e++) o[e] = from_f32<TO>(v[e]);
                 }
-                *reinterpret_cast<VO*>(out + c * EPC) = o;  // plain stores (non-temporal ones were no faster)
+                // plain stores (non-temporal ones were no faster)
+                if constexpr (kRes) buf_store16<false>(outr, static_cast<uint32_t>(c) * 16u, o);
+                else *reinterpret_cast<VO*>(out + c * EPC) = o;
             }
         }
     }

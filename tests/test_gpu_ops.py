@@ -617,6 +617,24 @@ def test_embed_scaled_granite(dev, fmt):
         assert np.array_equal(to_bits(got16), want32.astype(np.float16).view(np.uint16)), f"f16 out, multiplier {mult}"
 
 
+@pytest.mark.parametrize("fmt", [ops.FMT_FP8, ops.FMT_FP4])
+@pytest.mark.parametrize("C", [96, 2080, 4096, 5152])
+def test_embed_widths(dev, fmt, C):
+    """Row widths around the kernel's steps of 256 output chunks, whose block scales one load per lane
+    brings in: a few blocks (96), one step and a few chunks more with an odd block count (2080: 65
+    blocks), two whole steps (4096), and an odd count past two steps (5152: 161 blocks). The table's last
+    row is among the ids (its scale area ends the buffer). Bit-exact, f16 and f32 out."""
+    _case(f"embed widths fmt={fmt} C={C}")
+    V, T = 40, 130
+    table = _table(fmt, V, C, 41)
+    ids = wl.uniform_ids(T, V, 42)
+    ids[:2] = [V - 1, 0]
+    tt, it = torch.from_numpy(table).to(dev), torch.from_numpy(ids).to(dev)
+    assert np.array_equal(to_bits(ops.embed(it, tt, fmt, C)), O.embed(ids, table, fmt, C))
+    got32 = ops.embed(it, tt, fmt, C, out_dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(got32.view(np.uint32), O.embed(ids, table, fmt, C, out_f16=False).view(np.uint32))
+
+
 def test_embed_gpt2_wpe(dev):
     """GPT-2 wte + wpe (f32 add, then one f16 rounding) at the configured shape: bit-exact."""
     cfg = wl.GPT2_CHAIN
