@@ -983,19 +983,33 @@ def all_configs(args):
                     calls9[f"{name}_out16"].keep = (tab9, ours16)
                     bytes9[f"{name}_out16"] = wl.bytes_matmul(c9.T, K, N, tab9.shape[1], y_bytes=2)
                     flops9[f"{name}_out16"] = flops9[name]
+                    # The same product on this library's own MFMA kernels (the context's hipBLASLt
+                    # dispatch switched off around the call).
+                    ctx9 = ops.context(dev.index or 0)
+                    run_lib = calls9[name]
+
+                    def own(run=run_lib, c=ctx9):
+                        c.set_matmul_library(False)
+                        try:
+                            run()
+                        finally:
+                            c.set_matmul_library(True)
+                    calls9[f"{name}_own"], bytes9[f"{name}_own"], flops9[f"{name}_own"] = own, bytes9[name], flops9[name]
             del wsrc
         run("qwen3_4b_prefill_matmul", calls9, bytes9,
             "Qwen3-4B prefill, T=8192: q/k/v [6144,2560], o [2560,4096], gate/up [19456,2560], down [2560,9728] "
             "weight matmuls in F16 / FP8 / FP4 rows, f16 activations, f32 outputs", flops9)
         lib_ops, _ = time_ops(lib9, bytes9, list(lib9), args.steps, args.warmup, flush,
                               HipTimer(torch.cuda.current_stream().cuda_stream))
+        ops9 = out["qwen3_4b_prefill_matmul"]["ops"]
         for n, v in lib_ops.items():
             tf = flops9[n] / (v["us"] * 1e-6) / 1e12
             kind = "f16" if n.endswith("_out16") else "f32"
-            out["qwen3_4b_prefill_matmul"]["ops"][n].update(
-                {"library_us": v["us"], "library_TFLOPs": round(tf, 1),
-                 "library": f"torch f16 x f16 -> {kind} (hipBLASLt)",
-                 "vs_library": round(v["us"] / out["qwen3_4b_prefill_matmul"]["ops"][n]["us"], 4)})
+            for m in (n, f"{n}_own"):  # the op as shipped, and on the own kernels
+                if m in ops9:
+                    ops9[m].update({"library_us": v["us"], "library_TFLOPs": round(tf, 1),
+                                    "library": f"torch f16 x f16 -> {kind} (hipBLASLt)",
+                                    "vs_library": round(v["us"] / ops9[m]["us"], 4)})
         del calls9, lib9
 
     if not args.no_cpu:

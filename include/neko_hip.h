@@ -224,8 +224,18 @@ int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t 
                     int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags,
                     int x_dtype, int y_dtype);
 
+/* F16 weight rows with f16 activations from 2048 tokens, without NEKO_MM_GELU and without a bias
+ * added to an accumulated y (16-byte aligned y rows): neko_hip_matmul runs the product on hipBLASLt (the vendor GEMM library; measured faster than this library's own MFMA
+ * kernels at prefill sizes), which draws up to 64 MiB of the context's workspace. enable = 0 keeps
+ * every product of this context on the library's own kernels (enable = 1, the default, allows it).
+ * No counterpart in the reference (its matmul is its own). */
+int neko_hip_set_matmul_library(neko_hip_ctx* ctx, int enable);
+
 /* neko_hip_matmul without any allocation: the same kernels, the same split of K and bit-identical
- * results, but the memory neko_hip_matmul takes from the context's workspace -- split-K partial sums,
+ * results (except for the F16 products neko_hip_matmul hands to hipBLASLt, which this entry point runs
+ * on the library's own kernels, as neko_hip_matmul does with neko_hip_set_matmul_library(ctx, 0): the
+ * same f32 sums in another order, within the same bound), but the memory neko_hip_matmul takes from
+ * the context's workspace -- split-K partial sums,
  * and for f32 activations from 9 tokens (17 for weights of at most 2^24 elements) the two f16 planes
  * and their sums -- comes from a fixed 32 MiB array in device memory (one per GPU, held from the
  * library's first use on that GPU until the process ends). No counterpart in the reference: this is

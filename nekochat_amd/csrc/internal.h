@@ -13,6 +13,10 @@
 #include "../../include/neko_hip.h"
 #include "device.h"
 
+namespace neko_hip {
+struct LtState;  // hipBLASLt handle and per-shape plans (matmul_lib.hip)
+}
+
 struct neko_hip_ctx {
     int device = -1;
     hipStream_t stream = nullptr;  // null = the device's null stream
@@ -28,6 +32,8 @@ struct neko_hip_ctx {
     std::vector<void*> retired;  // outgrown workspaces, kept until destroy (captured graphs may use them)
     hipEvent_t switch_event = nullptr;  // orders a newly routed stream after the previous one
     void* scratch = nullptr;  // device address of the matmul's fixed split-K scratch on this device
+    neko_hip::LtState* lt = nullptr;  // created by the first matmul that takes hipBLASLt
+    bool use_library = true;          // neko_hip_set_matmul_library
 };
 
 namespace neko_hip {
@@ -53,6 +59,13 @@ int workspace(neko_hip_ctx* ctx, size_t bytes, void** out, int slot = 0);
 // Looks up (once per device, with that device current) and records in ctx the device address of
 // the fixed scratch array that neko_hip_matmul_noalloc uses (matmul.hip).
 int matmul_scratch_setup(neko_hip_ctx* ctx);
+// The plain F16 weight matmul (f16 activations) on hipBLASLt: *done = true when the library ran it;
+// false (NEKO_OK) when it has no algorithm for the shape, or the library could not be initialised --
+// the caller then runs its own kernels.
+int lt_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, int64_t K, const void* w, int64_t row_bytes,
+              int64_t N, const float* bias, void* y, int64_t y_stride, int flags, int y_dtype, bool* done);
+// Frees ctx's hipBLASLt handle and plans (neko_hip_destroy, after its stream has drained).
+void lt_release(neko_hip_ctx* ctx);
 // Gives up ctx's claim on its device's scratch array (taken by its first neko_hip_matmul_noalloc
 // call), once its stream has drained.
 void matmul_scratch_release(const neko_hip_ctx* ctx);

@@ -1968,6 +1968,9 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
 // 1.1-2.2x faster than the planes for the Qwen3-4B q/k/v [6144, 2560] and o [2560, 4096] and the
 // Qwen3-0.6B projections (the planes' four launches dominate there).
 constexpr int64_t kF32SplitMinT = 9;
+// From this many tokens the plain F16 product (f16 activations) goes to hipBLASLt (matmul_lib.hip):
+// measured faster than the own GEMM kernels on every Qwen3-4B projection at 8192 tokens.
+constexpr int64_t kLibMinT = 2048;
 constexpr int64_t kF32SplitMinTSmall = 17;
 constexpr int64_t kF32SmallNK = int64_t{1} << 24;
 
@@ -2077,6 +2080,17 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
             case NEKO_FMT_FP8: return launch_gemv_nt<1>(ctx, a, y_dtype, grid, kw, gemv_nt, fast32);
             default: return launch_gemv_nt<2>(ctx, a, y_dtype, grid, kw, gemv_nt, fast32);
         }
+    }
+    // The plain F16 product at prefill sizes: hipBLASLt where the context allows it. The GELU epilogue
+    // (the library has none of the reference's form), a bias added to an accumulated y (the library
+    // adds y before the bias, the reference y + (dot + bias)) and the allocation-free entry point (the
+    // library allocates) stay on the own kernels.
+    if (fast && fmt == NEKO_FMT_F16 && T >= kLibMinT && ctx->use_library && !fixed.p && (flags & kGelu) == 0 &&
+        !(bias && (flags & kAccumulate)) && aligned(y, 16) &&
+        (y_stride * static_cast<int64_t>(dtype_size(y_dtype))) % 16 == 0) {
+        bool done = false;
+        if (int rc = lt_matmul(ctx, x, x_stride, T, K, w, row_bytes, N, bias, y, y_stride, flags, y_dtype, &done)) return rc;
+        if (done) return NEKO_OK;
     }
     if (fast && T >= (fmt == NEKO_FMT_F16 ? kGemmMinTF16 : kGemmMinT)) {
         const bool v2 = K % kG2BK == 0;

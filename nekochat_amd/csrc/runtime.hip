@@ -154,6 +154,7 @@ int neko_hip_destroy(neko_hip_ctx* ctx) {
     int rc = enter(ctx);
     if (rc == NEKO_OK) rc = check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     matmul_scratch_release(ctx);
+    lt_release(ctx);
     for (void* p : ctx->allocs) (void)hipFree(p);
     for (void* p : ctx->workspace)
         if (p) (void)hipFree(p);
@@ -172,6 +173,12 @@ int neko_hip_device_name(neko_hip_ctx* ctx, char* buf, size_t buf_bytes) {
 }
 
 size_t neko_hip_max_buffer_bytes(const neko_hip_ctx* ctx) { return ctx ? ctx->max_alloc : 0; }
+
+int neko_hip_set_matmul_library(neko_hip_ctx* ctx, int enable) {
+    NEKO_REQUIRE(ctx, ctx, "neko_hip_set_matmul_library: null context");
+    ctx->use_library = enable != 0;
+    return NEKO_OK;
+}
 
 int neko_hip_set_stream(neko_hip_ctx* ctx, void* hip_stream) {
     NEKO_ENTER(ctx);

@@ -51,6 +51,11 @@ class Context:
     def synchronize(self) -> None:
         self.check(lib.neko_hip_synchronize(self.handle))
 
+    def set_matmul_library(self, enable: bool) -> None:
+        """Whether this context's plain F16 prefill matmuls may run on hipBLASLt (default True) or
+        stay on the library's own kernels."""
+        self.check(lib.neko_hip_set_matmul_library(self.handle, 1 if enable else 0))
+
     def device_name(self) -> str:
         buf = ctypes.create_string_buffer(256)
         self.check(lib.neko_hip_device_name(self.handle, buf, 256))

@@ -282,6 +282,55 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
         assert np.abs(y - want).max() <= float(((2 * K + 65) * U * mag).max())
 
 
+@pytest.mark.parametrize("T,K,N", [
+    (2048, 1024, 16384),  # 256 x 256 tiles on the own kernels
+    (4096, 1024, 4096),   # 128 x 128 tiles on the own kernels
+    (2048, 2560, 2560),   # an o-projection-shaped product
+])
+def test_matmul_f16_prefill_library_and_own(dev, T, K, N):
+    """Plain F16 products from 2048 tokens run on hipBLASLt by default and on the library's own MFMA
+    kernels with the context's switch off (neko_hip_set_matmul_library): both bit-identical to the exact
+    result on integer-valued data -- f32 output with bias, f16 output (one rounding of the exact value)
+    and accumulation into y -- and both within the f32 summation bound on random data."""
+    ctx = ops.context(dev.index or 0)
+    rng = np.random.default_rng(900 + T + N)
+    tab, w = M.integer_table(ops.FMT_F16, N, K, rng)
+    x = rng.integers(-4, 5, (T, K)).astype(np.float32)
+    bias = rng.integers(-50, 51, N).astype(np.float32)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T + bias
+    assert np.abs(exact).max() < 2 ** 24
+    e32 = exact.astype(np.float32)
+    xd, td, bd = (torch.from_numpy(v).to(dev) for v in (x.astype(np.float16), tab, bias))
+    y0 = rng.integers(-1000, 1001, (T, N)).astype(np.float32)
+    wr = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    tr, _ = ops.quantize_rows(ops.FMT_F16, wr)
+    xr = rng.standard_normal((T, K)).astype(np.float16)
+    br = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    ex_r, mag = M.exact_and_bound(xr.astype(np.float32), M.dequant(ops.FMT_F16, tr, K), br)
+    for lib in (True, False):
+        _case(f"matmul F16 prefill {'hipBLASLt' if lib else 'own kernels'} T={T} K={K} N={N}")
+        ctx.set_matmul_library(lib)
+        try:
+            got = ops.matmul(xd, td, ops.FMT_F16, K, bias=bd).cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), e32.view(np.uint32))
+            got16 = ops.matmul(xd, td, ops.FMT_F16, K, bias=bd, out_dtype=torch.float16).cpu().numpy()
+            assert np.array_equal(got16.view(np.uint16), O.f32_to_f16(e32))
+            # accumulated without a bias (the library's), and with one (y + (dot + bias), own kernels)
+            acc = torch.from_numpy(y0).to(dev)
+            ops.matmul(xd, td, ops.FMT_F16, K, out=acc, flags=ops.MM_ACCUMULATE)
+            want = (y0.astype(np.float64) + (exact - bias)).astype(np.float32)
+            assert np.array_equal(acc.cpu().numpy().view(np.uint32), want.view(np.uint32))
+            acc = torch.from_numpy(y0 + 0.25).to(dev)
+            ops.matmul(xd, td, ops.FMT_F16, K, bias=bd, out=acc, flags=ops.MM_ACCUMULATE)
+            want = ((y0 + 0.25).astype(np.float64) + exact).astype(np.float32)
+            assert np.array_equal(acc.cpu().numpy().view(np.uint32), want.view(np.uint32))
+            yr = ops.matmul(torch.from_numpy(xr).to(dev), torch.from_numpy(tr).to(dev), ops.FMT_F16, K,
+                            bias=torch.from_numpy(br).to(dev)).cpu().numpy()
+            _bound_check(yr, ex_r, mag, K, f"F16 {'hipBLASLt' if lib else 'own'} T={T} K={K} N={N}")
+        finally:
+            ctx.set_matmul_library(True)
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 9, 16, 17, 33])
 def test_matmul_f32_activations_integer_bitexact(dev, fmt, T):
