@@ -2083,13 +2083,19 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
     }
     // The plain F16 product at prefill sizes: hipBLASLt where the context allows it. The GELU epilogue
     // (the library has none of the reference's form), a bias added to an accumulated y (the library
-    // adds y before the bias, the reference y + (dot + bias)) and the allocation-free entry point (the
-    // library allocates) stay on the own kernels.
+    // adds y before the bias, the reference y + (dot + bias)), the allocation-free entry point (the
+    // library allocates) and calls on a stream under graph capture (the library's stream-K kernels
+    // clear their flags with a memset, which a captured graph does not replay reliably) stay on the own
+    // kernels.
     if (fast && fmt == NEKO_FMT_F16 && T >= kLibMinT && ctx->use_library && !fixed.p && (flags & kGelu) == 0 &&
         !(bias && (flags & kAccumulate)) && aligned(y, 16) &&
         (y_stride * static_cast<int64_t>(dtype_size(y_dtype))) % 16 == 0) {
+        bool cap = false;
+        if (int rc = capturing(ctx, ctx->stream, &cap)) return rc;
         bool done = false;
-        if (int rc = lt_matmul(ctx, x, x_stride, T, K, w, row_bytes, N, bias, y, y_stride, flags, y_dtype, &done)) return rc;
+        if (!cap)
+            if (int rc = lt_matmul(ctx, x, x_stride, T, K, w, row_bytes, N, bias, y, y_stride, flags, y_dtype, &done))
+                return rc;
         if (done) return NEKO_OK;
     }
     if (fast && T >= (fmt == NEKO_FMT_F16 ? kGemmMinTF16 : kGemmMinT)) {

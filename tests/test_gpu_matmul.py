@@ -115,6 +115,32 @@ def test_matmul_split_k_graph_replays(dev):
         assert torch.equal(out_g.view(torch.int32), eager.view(torch.int32)), f"replay {i}"
 
 
+def test_matmul_f16_prefill_graph_replays(dev):
+    """An F16 product at prefill size captured in a HIP graph runs on the own kernels (the hipBLASLt
+    path is not taken under capture: its stream-K kernels clear their flags with a memset), and each of
+    three replays on fresh integer-valued inputs, with eager work and synchronisations between them,
+    equals the uncaptured call (hipBLASLt) bit for bit: every partial sum is exact."""
+    _case("matmul F16 prefill graph capture + 3 replays")
+    rng = np.random.default_rng(951)
+    fmt, T, K, N = ops.FMT_F16, 2048, 1024, 4096
+    tab, _ = M.integer_table(fmt, N, K, rng)
+    td = torch.from_numpy(tab).to(dev)
+    xd = torch.from_numpy(rng.integers(-4, 5, (T, K)).astype(np.float32)).to(dev).half()
+    out_g = torch.zeros((T, N), dtype=torch.float32, device=dev)
+    ops.matmul(xd, td, fmt, K, out=out_g)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.matmul(xd, td, fmt, K, out=out_g)
+    for i in range(3):
+        xd.copy_(torch.from_numpy(rng.integers(-4, 5, (T, K)).astype(np.float32)).half())
+        g.replay()
+        torch.cuda.synchronize()
+        eager = ops.matmul(xd, td, fmt, K)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g.view(torch.int32), eager.view(torch.int32)), f"replay {i}"
+
+
 def test_matmul_workspace_growth_refused_under_capture(dev):
     """A fresh context has no workspace: a split-K call captured into a graph would have to allocate
     it, and fails with NEKO_ERR_INVALID instead (naming the way out) without breaking the capture."""
