@@ -240,6 +240,9 @@ constexpr int qk_waves() {
 // Tokens one wave of qk_rope_roll_kernel may take (one position per lane).
 constexpr int kQkMaxTokensPerWave = 64;
 
+// What the kernel's scalar load of its first position reads when the call has no positions array.
+static __device__ const int32_t kQkNoPosition = 0;
+
 template <typename T, int L, int V, int U, bool KV>
 __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_kernel(QkArgs a) {
     constexpr int HPW = kWave / L;  // heads per wave pass
@@ -282,6 +285,11 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     // row -- none of them waits for another.
     int32_t posv = 0;
     if (a.positions) posv = a.positions[t0 + static_cast<int64_t>(lane < ntok ? lane : ntok - 1) * nw];
+    // The first token's position once more, through the scalar cache (a uniform address in the constant
+    // address space: s_load, issued here and waited for only after the row loads below): the first
+    // cos/sin row waits on it, and a scalar load returns well before the vector load above.
+    const int32_t* const pfirst = a.positions ? a.positions + t0 : &kQkNoPosition;
+    const int32_t pos32 = ((const __attribute__((address_space(4))) int32_t*)pfirst)[0];  // (a C cast: address spaces)
     float4v wv{};
     if (norm) wv = buf_load16<false, float4v>(buf_res(a.wqk, 2 * HD * 4u), lane * 16u);
     VT A[U], B[U];
@@ -402,18 +410,20 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
 
     // The first token's row data goes out first, then the weight copy and that token's cos/sin row
     // (loading the cos/sin row first waits for the position before any row load is issued: measured
-    // 0.8 us slower at the Qwen3-4B prefill shape).
+    // 0.8 us slower at the Qwen3-4B prefill shape), whose position comes from the scalar load above.
     {
         float2v r[PL];
         const BufRes ld = buf_res(row_of(t0), load_bytes);
 #pragma unroll
         for (int u = 0; u < U; u++) load_pass(ld, u);
+        __builtin_amdgcn_sched_barrier(0);  // every row load issued before the wait for the position
+        const int64_t pos_first = a.positions ? static_cast<int64_t>(pos32) : a.pos0 + t0;
         if (norm) {
             *reinterpret_cast<float4v*>(&wsh[wave][lane * 4]) = wv;
             for (int i = 256 + lane * 4; i < 2 * HD; i += 256)
                 *reinterpret_cast<float4v*>(&wsh[wave][i]) = *reinterpret_cast<const float4v*>(a.wqk + i);
         }
-        cs_load(pos_of(0), r);
+        cs_load(pos_first, r);
         cs_store(0, r);
     }
     // Token k with a next token: its passes, the refills, and the next cos/sin row staged in the other
