@@ -1969,8 +1969,9 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
 // Qwen3-0.6B projections (the planes' four launches dominate there).
 constexpr int64_t kF32SplitMinT = 9;
 // From this many tokens the plain F16 product (f16 activations) goes to hipBLASLt (matmul_lib.hip):
-// measured faster than the own GEMM kernels on every Qwen3-4B projection at 8192 tokens.
-constexpr int64_t kLibMinT = 2048;
+// measured faster than the own GEMM kernels on every Qwen3-4B projection from 512 tokens (12-40%); at
+// 64-256 tokens the own kernels win for the 2560-row projections (down by up to 43%).
+constexpr int64_t kLibMinT = 512;
 constexpr int64_t kF32SplitMinTSmall = 17;
 constexpr int64_t kF32SmallNK = int64_t{1} << 24;
 

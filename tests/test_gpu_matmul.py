@@ -312,9 +312,10 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
     (2048, 1024, 16384),  # 256 x 256 tiles on the own kernels
     (4096, 1024, 4096),   # 128 x 128 tiles on the own kernels
     (2048, 2560, 2560),   # an o-projection-shaped product
+    (512, 9728, 2560),    # the down projection at the library's threshold
 ])
 def test_matmul_f16_prefill_library_and_own(dev, T, K, N):
-    """Plain F16 products from 2048 tokens run on hipBLASLt by default and on the library's own MFMA
+    """Plain F16 products from 512 tokens run on hipBLASLt by default and on the library's own MFMA
     kernels with the context's switch off (neko_hip_set_matmul_library): both bit-identical to the exact
     result on integer-valued data -- f32 output with bias, f16 output (one rounding of the exact value)
     and accumulation into y -- and both within the f32 summation bound on random data."""
