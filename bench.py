@@ -139,7 +139,15 @@ class FloorLib:
                             ("neko_floor_rows_up", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_int,
                                                     c.c_int, c.c_int, c.c_void_p]),
                             ("neko_floor_gather", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_void_p,
-                                                   c.c_int64, c.c_int64, c.c_int, c.c_int, c.c_void_p])):
+                                                   c.c_int64, c.c_int64, c.c_int, c.c_int, c.c_void_p]),
+                            ("neko_floor_add2", [c.c_void_p, c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_int, c.c_int,
+                                                 c.c_void_p]),
+                            ("neko_floor_split2", [c.c_void_p, c.c_int64, c.c_int64, c.c_void_p, c.c_void_p, c.c_int64,
+                                                   c.c_int64, c.c_void_p]),
+                            ("neko_floor_inplace_kv", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int64, c.c_void_p,
+                                                       c.c_void_p, c.c_int64, c.c_void_p]),
+                            ("neko_floor_gate", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_void_p, c.c_int64,
+                                                 c.c_int64, c.c_int64, c.c_void_p])):
             getattr(lib, name).argtypes = args_
             getattr(lib, name).restype = c.c_int
             self.bound.add(name)
@@ -731,13 +739,19 @@ def all_configs(args):
     def want(label):
         return args.workload is None or args.workload == label
 
-    def run(label, calls, op_bytes, workload, op_flops=None):
+    def run(label, calls, op_bytes, workload, op_flops=None, floors=None):
+        """Times `calls` round-robin; floors: {op: [names of floor candidates among calls]} -- each op
+        then carries the fastest as floor_us / floor_kind / over_floor."""
         progress(f"timing {label}")
         timer = HipTimer(torch.cuda.current_stream().cuda_stream)
         per_op, _ = time_ops(calls, op_bytes, list(calls), args.steps, args.warmup, flush, timer)
         for n, f in (op_flops or {}).items():  # MFMA-bound ops: their roofline is the dense f16 peak
             tf = f / (per_op[n]["us"] * 1e-6) / 1e12
             per_op[n].update({"flops": f, "TFLOPs": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+        for n, cands in (floors or {}).items():
+            best = min(cands, key=lambda f: per_op[f]["us"])
+            per_op[n].update({"floor_us": per_op[best]["us"], "floor_kind": best,
+                              "over_floor": round(per_op[n]["us"] / per_op[best]["us"] - 1, 4)})
         out[label] = {"workload": workload, "ops": per_op}
         torch.cuda.synchronize()
 
@@ -876,19 +890,46 @@ def all_configs(args):
         kc6 = torch.empty((c6.T, kw6), dtype=torch.float16, device=dev)
         vc6 = torch.empty_like(kc6)
         qoff = c6.n_q * c6.hd
-        run("qwen3_4b_fused", {
+        calls6 = {
             "add_rmsnorm": ops.prepare(ops.add_rms_norm, x6, d6, w6, c6.eps, out=xn6)[0],
             "qk_norm_rope_kv": ops.prepare(ops.qk_norm_rope_kv, qkv6, c6.n_q, c6.n_kv, c6.hd, cs6, c6.eps, kc6, vc6,
                                            wqk=wqk6, positions=pos6)[0],
             "qk_norm_rope": ops.prepare(ops.qk_norm_rope, qkv6, c6.n_q, c6.n_kv, c6.hd, cs6, c6.eps, wqk=wqk6,
                                         positions=pos6)[0],
             "store_kv": ops.prepare(ops.store_kv, qkv6, qoff, qoff + kw6, kw6, kc6, vc6, positions=pos6)[0],
-        }, {"add_rmsnorm": wl.bytes_add_rmsnorm(c6.T, c6.C),
-            "qk_norm_rope_kv": wl.bytes_qk_rope_kv(c6.T, c6.n_q, c6.n_kv, c6.hd),
-            "qk_norm_rope": wl.bytes_qk_rope(c6.T, c6.n_q, c6.n_kv, c6.hd),
-            "store_kv": wl.bytes_store_kv(c6.T, kw6)},
+        }
+        bytes6 = {"add_rmsnorm": wl.bytes_add_rmsnorm(c6.T, c6.C),
+                  "qk_norm_rope_kv": wl.bytes_qk_rope_kv(c6.T, c6.n_q, c6.n_kv, c6.hd),
+                  "qk_norm_rope": wl.bytes_qk_rope(c6.T, c6.n_q, c6.n_kv, c6.hd),
+                  "store_kv": wl.bytes_store_kv(c6.T, kw6)}
+        # Floors of each op's byte pattern, over copies of its inputs: the residual add's two rows in and
+        # two out (x in place), the q/k rows rewritten in place (with the KV store: k copied out as well,
+        # v copied to its cache row), the k and v parts of each row split into the two caches.
+        fl6 = FloorLib(torch.cuda.current_stream().cuda_stream)
+        xf, df, cf = x6.clone(), d6.clone(), torch.empty_like(x6)
+        qf, qf2, kf, vf = qkv6.clone(), qkv6.clone(), torch.empty_like(kc6), torch.empty_like(vc6)
+        rs6, qk_w6, kvb = c6.qkv_stride * 2, (c6.n_q + c6.n_kv) * c6.hd * 2, kw6 * 2
+        waves6 = 16 * torch.cuda.get_device_properties(dev).multi_processor_count
+        floors6 = {"add_rmsnorm": [], "qk_norm_rope_kv": [], "qk_norm_rope": [], "store_kv": []}
+        for items in (1, 4):
+            for ntl, nts in ((1, 1), (0, 0)):
+                name = f"floor_add2_i{items}_{'ntnt' if ntl else 'plpl'}"
+                calls6[name] = fl6.add2(xf.data_ptr(), df.data_ptr(), cf.data_ptr(), c6.T * c6.C * 2, items, ntl, nts)
+                floors6["add_rmsnorm"].append(name)
+        calls6["floor_inplace_kv"] = fl6.inplace_kv(qf.data_ptr(), rs6, c6.T, qk_w6, kvb, kf.data_ptr(), vf.data_ptr(), kvb)
+        floors6["qk_norm_rope_kv"].append("floor_inplace_kv")
+        calls6["floor_inplace_plpl"] = fl6.inplace(qf2.data_ptr(), rs6, c6.T, qk_w6, 0, 0)
+        calls6["floor_inplace_rows_ntpl"] = fl6.inplace_rows(qf2.data_ptr(), rs6, c6.T, qk_w6, waves6, 1, 0)
+        floors6["qk_norm_rope"] += ["floor_inplace_plpl", "floor_inplace_rows_ntpl"]
+        calls6["floor_split2"] = fl6.split2(qf2.data_ptr() + qoff * 2, rs6, kvb, kf.data_ptr(), vf.data_ptr(), kvb, c6.T)
+        floors6["store_kv"].append("floor_split2")
+        for fl_names in floors6.values():
+            for f in fl_names:
+                bytes6[f] = bytes6[next(k for k, v in floors6.items() if f in v)]
+        run("qwen3_4b_fused", calls6, bytes6,
             "Qwen3-4B fused neighbours: residual add + RMSNorm [8192,2560]; q/k RoPE + KV store of an 8192-token "
-            "sequence, beside the unfused q/k RoPE and KV store")
+            "sequence, beside the unfused q/k RoPE and KV store", floors=floors6)
+        del xf, df, cf, qf, qf2, kf, vf
 
     # Load-time quantiser: the 151936 x 2048 tied table in f32 (1.24 GB) encoded on the device into each
     # weight format; bytes = the f32 rows read + the encoded rows written.
@@ -917,13 +958,32 @@ def all_configs(args):
         og = torch.empty_like(ya)
         h5 = wl.normal_f16((c5.T, 2 * c5.I), 0.0, 1.0, 56, dev)
         o5 = torch.empty((c5.T, c5.I), dtype=torch.float16, device=dev)
-        run("granite_4.0h_norms", {
+        calls5 = {
             "rmsnorm": ops.prepare(ops.rms_norm, x5, w5, c5.eps, out=y5)[0],
             "gated_rmsnorm": ops.prepare(ops.gated_rms_norm, ya, za, wg, c5.groups, c5.eps, out=og)[0],
             "swiglu": ops.prepare(ops.silu_mul, h5, out=o5)[0],
-        }, {"rmsnorm": wl.bytes_rmsnorm(c5.T, c5.C), "gated_rmsnorm": wl.bytes_gated(c5.T, c5.D),
-            "swiglu": wl.bytes_swiglu(c5.T, c5.I)},
-            "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096")
+        }
+        bytes5 = {"rmsnorm": wl.bytes_rmsnorm(c5.T, c5.C), "gated_rmsnorm": wl.bytes_gated(c5.T, c5.D),
+                  "swiglu": wl.bytes_swiglu(c5.T, c5.I)}
+        # Floors of each op's byte pattern, reading the op's own inputs: copies of the RMSNorm's rows, the
+        # gated norm's y and z rows into one output row, SwiGLU's two halves of each row into one.
+        fl5 = FloorLib(torch.cuda.current_stream().cuda_stream)
+        y5f, og5f, o5f = torch.empty_like(y5), torch.empty_like(og), torch.empty_like(o5)
+        floors5 = {"rmsnorm": [], "gated_rmsnorm": ["floor_gate"], "swiglu": ["floor_rows2_ntpl"]}
+        for items in (1, 4):
+            for ntl, nts in ((1, 1), (0, 0)):
+                name = f"floor_copy_i{items}_{'ntnt' if ntl else 'plpl'}"
+                calls5[name] = fl5.copy(x5.data_ptr(), y5f.data_ptr(), c5.T * c5.C * 2, items, ntl, nts)
+                floors5["rmsnorm"].append(name)
+                bytes5[name] = bytes5["rmsnorm"]
+        calls5["floor_gate"] = fl5.gate(ya.data_ptr(), c5.D * 2, za.data_ptr(), c5.D * 2, og5f.data_ptr(), c5.D * 2,
+                                        c5.D * 2, c5.T)
+        bytes5["floor_gate"] = bytes5["gated_rmsnorm"]
+        calls5["floor_rows2_ntpl"] = fl5.rows2(h5.data_ptr(), 2 * c5.I * 2, o5f.data_ptr(), c5.I * 2, c5.T, c5.I * 2, 1, 0)
+        bytes5["floor_rows2_ntpl"] = bytes5["swiglu"]
+        run("granite_4.0h_norms", calls5, bytes5,
+            "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096", floors=floors5)
+        del y5f, og5f, o5f
 
     # Qwen3-4B decode step (T = 1): the four weight matmuls in each weight format, f16 activations,
     # f32 outputs; bytes = the weight rows once + activations + outputs.

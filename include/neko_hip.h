@@ -224,7 +224,7 @@ int neko_hip_matmul(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t 
                     int64_t row_bytes, int fmt, int64_t N, const float* bias, void* y, int64_t y_stride, int flags,
                     int x_dtype, int y_dtype);
 
-/* F16 weight rows with f16 activations from 512 tokens, without NEKO_MM_GELU and without a bias
+/* F16 weight rows with f16 activations from 512 tokens (64 for 16384 rows or more), without NEKO_MM_GELU and without a bias
  * added to an accumulated y (16-byte aligned y rows), on a stream not under graph capture:
  * neko_hip_matmul runs the product on hipBLASLt (the vendor GEMM library; measured faster than this library's own MFMA
  * kernels at prefill sizes), which draws up to 64 MiB of the context's workspace. enable = 0 keeps

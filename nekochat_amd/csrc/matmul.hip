@@ -1970,8 +1970,11 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
 constexpr int64_t kF32SplitMinT = 9;
 // From this many tokens the plain F16 product (f16 activations) goes to hipBLASLt (matmul_lib.hip):
 // measured faster than the own GEMM kernels on every Qwen3-4B projection from 512 tokens (12-40%); at
-// 64-256 tokens the own kernels win for the 2560-row projections (down by up to 43%).
+// 64-256 tokens only for the widest (gate/up, 19456 rows: 17-31%), while the own kernels win for the
+// 2560-row projections (down by up to 43%) -- hence from kLibMinTWide tokens for kLibWideN rows.
 constexpr int64_t kLibMinT = 512;
+constexpr int64_t kLibMinTWide = 64;
+constexpr int64_t kLibWideN = 16384;
 constexpr int64_t kF32SplitMinTSmall = 17;
 constexpr int64_t kF32SmallNK = int64_t{1} << 24;
 
@@ -2088,7 +2091,7 @@ int matmul_impl(neko_hip_ctx* ctx, const void* x, int64_t x_stride, int64_t T, i
     // library allocates) and calls on a stream under graph capture (the library's stream-K kernels
     // clear their flags with a memset, which a captured graph does not replay reliably) stay on the own
     // kernels.
-    if (fast && fmt == NEKO_FMT_F16 && T >= kLibMinT && ctx->use_library && !fixed.p && (flags & kGelu) == 0 &&
+    if (fast && fmt == NEKO_FMT_F16 && (T >= kLibMinT || (T >= kLibMinTWide && N >= kLibWideN)) && ctx->use_library && !fixed.p && (flags & kGelu) == 0 &&
         !(bias && (flags & kAccumulate)) && aligned(y, 16) &&
         (y_stride * static_cast<int64_t>(dtype_size(y_dtype))) % 16 == 0) {
         bool cap = false;

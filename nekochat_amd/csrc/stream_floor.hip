@@ -6,7 +6,9 @@
 // layout (both inputs halves of one row), an in-place read-and-write-back of the first part of each
 // row (the q/k RoPE's layout; flat, and in that kernel's per-wave token order), rows moved in the
 // one-round row kernels' shape (every row of a wave loaded before any store), the embedding gather's
-// pattern (table rows read through token ids, contiguous output rows written), and a read-only sweep.
+// pattern (table rows read through token ids, contiguous output rows written), the residual add +
+// RMSNorm's, the KV store's, the fused q/k RoPE + KV store's and the gated norm's byte patterns, and a
+// read-only sweep.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -184,6 +186,74 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t* ids, int64_t
     }
 }
 
+// The residual add + RMSNorm's bytes: two streams in (a, b), two out (a rewritten in place, c): chunk
+// i = (block * ITEMS + k) * 256 + thread as in copy_kernel.
+template <int ITEMS, bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void add2_kernel(u32x4* a, const u32x4* __restrict__ b, u32x4* __restrict__ c, int64_t n,
+                                                   uint32_t key) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * ITEMS * 256 + threadIdx.x;
+    u32x4 va[ITEMS], vb[ITEMS];
+#pragma unroll
+    for (int k = 0; k < ITEMS; k++) {
+        const int64_t i = base + k * 256;
+        if (i < n) {
+            va[k] = ld<NTL>(a + i);
+            vb[k] = ld<NTL>(b + i);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < ITEMS; k++) {
+        const int64_t i = base + k * 256;
+        if (i < n) {
+            st<NTS>(a + i, va[k] ^ vb[k]);
+            st<NTS>(c + i, va[k] ^ key);
+        }
+    }
+}
+
+// One workgroup per row (all three below): `row`-th rows of the buffers, 16-byte chunks j.
+// The KV store's bytes: the k and v parts of each qkv row (2 * cw chunks, contiguous) read, the first
+// cw chunks written to dst1's row, the next cw to dst2's.
+__global__ __launch_bounds__(256) void split2_kernel(const u32x4* __restrict__ src, int64_t ss, int cw, u32x4* __restrict__ d1,
+                                                     u32x4* __restrict__ d2, int64_t ds) {
+    const int64_t row = blockIdx.x;
+    for (int j = threadIdx.x; j < 2 * cw; j += 256) {
+        const u32x4 v = ld<true>(src + row * ss + j);
+        if (j < cw) d1[row * ds + j] = v;
+        else d2[row * ds + j - cw] = v;
+    }
+}
+
+// The q/k RoPE fused with the KV store: the first cq chunks of each row rewritten in place, the last
+// ck of those also written to kd's row, and the cv chunks after them (v) copied to vd's row.
+__global__ __launch_bounds__(256) void inplace_kv_kernel(u32x4* buf, int64_t stride, int cq, int ck, int cv,
+                                                         u32x4* __restrict__ kd, u32x4* __restrict__ vd, int64_t ds,
+                                                         uint32_t key) {
+    const int64_t row = blockIdx.x;
+    u32x4* r = buf + row * stride;
+    for (int j = threadIdx.x; j < cq + cv; j += 256) {
+        const u32x4 v = ld<true>(r + j);
+        if (j < cq) {
+            const u32x4 w = v ^ key;
+            r[j] = w;
+            if (j >= cq - ck) kd[row * ds + j - (cq - ck)] = w;
+        } else {
+            vd[row * ds + j - cq] = v;
+        }
+    }
+}
+
+// The gated norm's bytes: a y row and a z row (each its own buffer and stride) read, an output row
+// written (o may be y: in place).
+__global__ __launch_bounds__(256) void gate_kernel(const u32x4* y, int64_t ys, const u32x4* __restrict__ z, int64_t zs,
+                                                   u32x4* o, int64_t os, int cw) {
+    const int64_t row = blockIdx.x;
+    for (int j = threadIdx.x; j < cw; j += 256) {
+        const u32x4 a = ld<true>(y + row * ys + j), b = ld<true>(z + row * zs + j);
+        o[row * os + j] = a ^ b;
+    }
+}
+
 bool ok16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <int ITEMS>
@@ -357,6 +427,70 @@ int neko_floor_gather(const int32_t* ids, int64_t T, const void* table, int64_t 
     else if (ntl) NEKO_FLOOR_GATHER(4, true);
     else NEKO_FLOOR_GATHER(4, false);
 #undef NEKO_FLOOR_GATHER
+    return hipGetLastError();
+}
+
+// a[i] = a[i] ^ b[i], c[i] = a[i] ^ key over `bytes` of each (a in place; 1 or 4 chunks per lane).
+int neko_floor_add2(void* a, const void* b, void* c, size_t bytes, int items, int nt_load, int nt_store, void* stream) {
+    if (!ok16(a) || !ok16(b) || !ok16(c) || bytes % 16 || (items != 1 && items != 4)) return hipErrorInvalidValue;
+    const int64_t n = static_cast<int64_t>(bytes / 16);
+    const int64_t blocks = (n + 256 * items - 1) / (256 * items);
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>(blocks)), bl(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    u32x4* pa = static_cast<u32x4*>(a);
+    const u32x4* pb = static_cast<const u32x4*>(b);
+    u32x4* pc = static_cast<u32x4*>(c);
+#define NEKO_FLOOR_ADD2(I, L, S) hipLaunchKernelGGL((add2_kernel<I, L, S>), g, bl, 0, st, pa, pb, pc, n, 0u)
+    if (items == 1 && nt_load && nt_store) NEKO_FLOOR_ADD2(1, true, true);
+    else if (items == 1 && nt_load) NEKO_FLOOR_ADD2(1, true, false);
+    else if (items == 1) NEKO_FLOOR_ADD2(1, false, false);
+    else if (nt_load && nt_store) NEKO_FLOOR_ADD2(4, true, true);
+    else if (nt_load) NEKO_FLOOR_ADD2(4, true, false);
+    else NEKO_FLOOR_ADD2(4, false, false);
+#undef NEKO_FLOOR_ADD2
+    return hipGetLastError();
+}
+
+// For each of `rows` rows: 2 * width bytes at src + row * s_stride, the first width to dst1 + row *
+// d_stride, the next width to dst2 + row * d_stride (strides in bytes, everything 16-byte aligned).
+int neko_floor_split2(const void* src, int64_t s_stride, int64_t width, void* dst1, void* dst2, int64_t d_stride,
+                      int64_t rows, void* stream) {
+    if (!ok16(src) || !ok16(dst1) || !ok16(dst2) || s_stride % 16 || d_stride % 16 || width % 16 || width <= 0 ||
+        rows <= 0 || rows > 0x7fffffff || s_stride < 2 * width || d_stride < width || width / 16 > (1 << 20))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(split2_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4*>(src), s_stride / 16, static_cast<int>(width / 16), static_cast<u32x4*>(dst1),
+                       static_cast<u32x4*>(dst2), d_stride / 16);
+    return hipGetLastError();
+}
+
+// For each of `rows` rows of buf (stride bytes apart): its first qk_bytes rewritten in place, the last
+// kv_bytes of those also written to kdst + row * d_stride, and the kv_bytes after them copied to vdst +
+// row * d_stride.
+int neko_floor_inplace_kv(void* buf, int64_t stride, int64_t rows, int64_t qk_bytes, int64_t kv_bytes, void* kdst,
+                          void* vdst, int64_t d_stride, void* stream) {
+    if (!ok16(buf) || !ok16(kdst) || !ok16(vdst) || stride % 16 || qk_bytes % 16 || kv_bytes % 16 || d_stride % 16 ||
+        kv_bytes <= 0 || qk_bytes < kv_bytes || stride < qk_bytes + kv_bytes || d_stride < kv_bytes || rows <= 0 ||
+        rows > 0x7fffffff || qk_bytes / 16 > (1 << 20))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(inplace_kv_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<u32x4*>(buf), stride / 16, static_cast<int>(qk_bytes / 16), static_cast<int>(kv_bytes / 16),
+                       static_cast<int>(kv_bytes / 16), static_cast<u32x4*>(kdst), static_cast<u32x4*>(vdst), d_stride / 16, 0u);
+    return hipGetLastError();
+}
+
+// For each of `rows` rows: width bytes of y and of z read (y_stride / z_stride bytes apart), width
+// bytes written at out + row * out_stride (out may be y).
+int neko_floor_gate(const void* y, int64_t y_stride, const void* z, int64_t z_stride, void* out, int64_t out_stride,
+                    int64_t width, int64_t rows, void* stream) {
+    if (!ok16(y) || !ok16(z) || !ok16(out) || y_stride % 16 || z_stride % 16 || out_stride % 16 || width % 16 ||
+        width <= 0 || y_stride < width || z_stride < width || out_stride < width || rows <= 0 || rows > 0x7fffffff ||
+        width / 16 > (1 << 20))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gate_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const u32x4*>(y), y_stride / 16, static_cast<const u32x4*>(z), z_stride / 16,
+                       static_cast<u32x4*>(out), out_stride / 16, static_cast<int>(width / 16));
     return hipGetLastError();
 }
 

@@ -313,6 +313,7 @@ def test_matmul_random_within_bound(dev, fmt, T, K, N):
     (4096, 1024, 4096),   # 128 x 128 tiles on the own kernels
     (2048, 2560, 2560),   # an o-projection-shaped product
     (512, 9728, 2560),    # the down projection at the library's threshold
+    (64, 2560, 19456),    # gate/up-wide rows: the library from 64 tokens
 ])
 def test_matmul_f16_prefill_library_and_own(dev, T, K, N):
     """Plain F16 products from 512 tokens run on hipBLASLt by default and on the library's own MFMA
