@@ -5,10 +5,11 @@
 // Fast path: one 64-wide wavefront per row, persistent. A grid of as many 256-thread workgroups as
 // stay resident walks the rows. RMSNorm / LayerNorm waves keep their norm weights in registers for
 // all of their rows and issue the 16-byte non-temporal loads of the next row before they reduce the
-// current one, so HBM is read once, written once, and always has loads in flight. The gated norm,
-// which holds two operands per row, reads its weights from one LDS copy per workgroup and runs
-// without the second row buffer, trading per-wave prefetch for three times the resident waves; the
-// residual add + RMSNorm streams x and delta, writes the sum back over x and the norm to xn.
+// current one, so HBM is read once, written once, and always has loads in flight. The f16 gated
+// norm, which holds two operands per row, spreads each row over 2-8 waves of one workgroup (two
+// 16-byte chunks per lane and operand) where its rows split so, else runs persistent with its weights
+// in one LDS copy per workgroup and no second row buffer (three times the resident waves instead);
+// the residual add + RMSNorm streams x and delta, writes the sum back over x and the norm to xn.
 // With many rows per resident wave (3 or more), RMSNorm and LayerNorm instead cover every row with
 // its own wave over the whole grid, which the dispatcher keeps full (plain loads and stores, no
 // prefetch): a persistent grid's partial last rounds then cost more than its prefetch saves.
@@ -464,30 +465,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void n
     }
 }
 
-// Four wavefronts per row for rows wider than one wave's registers; partial sums meet in LDS.
-template <Norm K, typename T, int CH>
-__global__ __launch_bounds__(256) void norm_wide_kernel(NormArgs a) {
+// WPR wavefronts per row (one row per workgroup), CH chunks per lane: rows wider than one wave's
+// registers (four waves, non-temporal loads), and the f16 gated norm wherever its rows split evenly
+// into two chunks per lane over 2-8 waves (PLAIN loads): at [16384, 3072] three waves per row take
+// 47.9 us against 51.6 for the persistent one-wave kernel (every output bit-identical), at eight
+// waves per SIMD and without a second row buffer -- the waves of the other rows are the overlap.
+// (Plain loads beat non-temporal ones there by 0.7 us, plain stores non-temporal ones by 4 us; two
+// waves of three chunks took 50.5, six of one 52.9, one wave of six over the whole grid 51.0.) The
+// partial sums meet in LDS.
+template <Norm K, typename T, int CH, int WPR = 4, bool PLAIN = false>
+__global__ __launch_bounds__(WPR * kWave) void norm_wide_kernel(NormArgs a) {
     constexpr int N = Chunk16<T>::N;
-    constexpr int NT = 4 * kWave;
+    constexpr int NT = WPR * kWave;
     const int64_t r = blockIdx.x;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int nch = a.C / N;
     const RowPtrs<K, T> p = row_ptrs<K, T>(a, r);
     RowRegs<K, T, CH> rr;
-    load_row<K, T, CH, NT>(rr, p, tid, nch);
+    load_row<K, T, CH, NT, PLAIN>(rr, p, tid, nch);
     add_residual(rr);
     Weights<K, T, CH, NT, false> wt;
     wt.init(p.w, p.b, tid, nch);
     RowVals<K, T, CH> f;
     f.init(rr);
 
-    __shared__ double part[2][4];
+    __shared__ double part[2][WPR];
     auto block_total = [&](double v, int slot) -> double {
         v = wave_sum_f64(v);
         if ((tid & 63) == 0) part[slot][wave] = v;
         __syncthreads();
-        return (part[slot][0] + part[slot][1]) + (part[slot][2] + part[slot][3]);
+        if constexpr (WPR == 4) return (part[slot][0] + part[slot][1]) + (part[slot][2] + part[slot][3]);
+        double s = part[slot][0];
+#pragma unroll
+        for (int i = 1; i < WPR; i++) s += part[slot][i];
+        return s;
     };
     float scale, mean_f = 0.0f;
     if constexpr (K == Norm::Layer) {
@@ -591,6 +603,20 @@ NormKernel pick_wide(int CH) {
     return nullptr;
 }
 
+// The f16 gated norm over WPR waves per row, two chunks per lane (plain loads).
+NormKernel pick_gated_split(int WPR) {
+    switch (WPR) {
+        case 2: return norm_wide_kernel<Norm::Gated, half_t, 2, 2, true>;
+        case 3: return norm_wide_kernel<Norm::Gated, half_t, 2, 3, true>;
+        case 4: return norm_wide_kernel<Norm::Gated, half_t, 2, 4, true>;
+        case 5: return norm_wide_kernel<Norm::Gated, half_t, 2, 5, true>;
+        case 6: return norm_wide_kernel<Norm::Gated, half_t, 2, 6, true>;
+        case 7: return norm_wide_kernel<Norm::Gated, half_t, 2, 7, true>;
+        case 8: return norm_wide_kernel<Norm::Gated, half_t, 2, 8, true>;
+    }
+    return nullptr;
+}
+
 // The one-row-per-wave form exists for the plain norms (RMSNorm, LayerNorm) with weights in
 // registers; the gated and residual norms measured no gain from it.
 constexpr bool has_row_form(Norm k) { return k == Norm::Rms || k == Norm::Layer; }
@@ -677,6 +703,18 @@ int launch_norm(neko_hip_ctx* ctx, Norm kind, const NormArgs& a, int dtype, cons
     // Weights staged in LDS: groups * C floats (+ C betas), when they fit and the kind asks for it.
     const size_t lds = (static_cast<size_t>(a.groups) * a.C + (kind == Norm::Layer ? a.C : 0)) * sizeof(float);
     const bool wl = W == 1 && weights_in_lds(kind) && lds <= kMaxWeightLds && (kind != Norm::Layer || aligned(a.b, 16));
+    // The f16 gated norm whose rows split into two chunks per lane over 2-8 waves: one row per
+    // workgroup of that many waves.
+    if (kind == Norm::Gated && vec && dtype == NEKO_DT_F16 && a.C / N % (2 * kWave) == 0) {
+        const int wpr = a.C / N / (2 * kWave);
+        if (wpr >= 2 && wpr <= 8) {
+            if (a.rows > 0x7fffffff)
+                return fail(ctx, NEKO_ERR_UNSUPPORTED, "%s: %lld rows exceed one launch", what, (long long)a.rows);
+            hipLaunchKernelGGL(pick_gated_split(wpr), dim3(static_cast<uint32_t>(a.rows)), dim3(wpr * kWave), 0, ctx->stream,
+                               a);
+            return after_launch(ctx, what);
+        }
+    }
     NormKernel k = nullptr;
     switch (kind) {
         case Norm::Rms: k = pick<Norm::Rms>(dtype, W, CH, wl); break;

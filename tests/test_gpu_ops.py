@@ -149,7 +149,9 @@ def test_layernorm_f32(dev):
 
 # ------------------------------------------------------------------ gated RMSNorm
 
-@pytest.mark.parametrize("T,D,groups,zpad", [(16384, 3072, 1, 0), (64, 3072, 1, 640), (37, 1024, 4, 8), (5, 300, 3, 0)])
+@pytest.mark.parametrize("T,D,groups,zpad", [(16384, 3072, 1, 0), (64, 3072, 1, 640), (37, 1024, 4, 8), (5, 300, 3, 0),
+                                               (256, 6144, 2, 0), (300, 2048, 1, 24), (40, 8192, 1, 0),
+                                               (24, 9216, 1, 0)])
 def test_gated_rmsnorm_f16(dev, T, D, groups, zpad):
     _case(f"gated rmsnorm T={T} D={D} groups={groups} zpad={zpad}")
     y = _f16((T, D), 15, dev)
@@ -171,13 +173,18 @@ def test_gated_rmsnorm_inplace(dev):
     assert_f16_close(to_bits(y), want, what="gated in place")
 
 
-def test_gated_rmsnorm_every_gate(dev):
-    """Every f16 gate value, one per element (subnormals, +-65504, +-inf and NaNs, which fill rows 31
-    and 63), under random y: within 2 ulp of the oracle, NaN exactly where the oracle has NaN."""
-    _case("gated rmsnorm every gate value")
-    D = 1024
-    z = torch.from_numpy(np.arange(65536, dtype=np.uint16).view(np.float16).reshape(64, D).copy()).to(dev)
-    y = _f16((64, D), 57, dev)
+@pytest.mark.parametrize("D", [1024, 3072])
+def test_gated_rmsnorm_every_gate(dev, D):
+    """Every f16 gate value, one per element (subnormals, +-65504, +-inf and NaNs, in bit-pattern
+    order), under random y: within 2 ulp of the oracle, NaN exactly where the oracle has NaN. D = 1024
+    runs the one-wave kernel, D = 3072 (the Granite width) three waves per row; the last of its 22 rows
+    is padded with zero gates."""
+    _case(f"gated rmsnorm every gate value D={D}")
+    rows = -(-65536 // D)
+    codes = np.zeros(rows * D, dtype=np.uint16)
+    codes[:65536] = np.arange(65536, dtype=np.uint16)
+    z = torch.from_numpy(codes.view(np.float16).reshape(rows, D).copy()).to(dev)
+    y = _f16((rows, D), 57, dev)
     w = _w(D, 58, dev)
     out = ops.gated_rms_norm(y, z, w, 1, 1e-5)
     want = O.gated_rmsnorm_f16(to_bits(y), to_bits(z), w.cpu().numpy(), 1, 1e-5)
