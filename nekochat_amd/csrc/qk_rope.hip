@@ -39,6 +39,7 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
     const int nqk = a.n_q + a.n_kv;
     QkKernel k = nullptr;
     bool with_kv = false;
+    int split = 1;  // work items per token (the roll kernel's S)
     // Widest per-lane vector whose lane count per head is a power of two and whose loads stay aligned.
     const int vmax = static_cast<int>(16 / esz);
     for (int V = vmax; V >= 1 && !k; V /= 2) {
@@ -49,23 +50,27 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
         if (!aligned(a.qkv, vb) || (a.stride * esz) % vb || (half * esz) % vb) continue;
         if (!aligned(a.cs, 8)) break;
         if (kv && aligned(a.k_cache, 2 * V) && aligned(a.v_cache, 2 * V)) {
-            k = dtype == NEKO_DT_F16 ? pick_qk_f16(L, V, nqk + a.n_kv, true) : pick_qk_f32(L, V, nqk + a.n_kv, true);
+            k = dtype == NEKO_DT_F16 ? pick_qk_f16(L, V, nqk + a.n_kv, true, &split)
+                                     : pick_qk_f32(L, V, nqk + a.n_kv, true, &split);
             with_kv = k != nullptr;
         }
-        if (!k) k = dtype == NEKO_DT_F16 ? pick_qk_f16(L, V, nqk, false) : pick_qk_f32(L, V, nqk, false);
+        if (!k) k = dtype == NEKO_DT_F16 ? pick_qk_f16(L, V, nqk, false, &split) : pick_qk_f32(L, V, nqk, false, &split);
     }
     if (!with_kv) a.k_cache = a.v_cache = nullptr;
     if (k) {
         // Persistent waves: as many workgroups as stay resident together, trimmed so that every wave
-        // gets the same number of rows (ceil(rows / resident waves)) and no partial last round is left.
-        // A wave takes at most kQkMaxTokensPerWave rows (the roll kernel holds one position per lane),
-        // so larger row counts go in several launches.
-        const int64_t need = (a.rows + 3) / 4;
+        // gets the same number of work items (ceil(items / resident waves)) and no partial last round
+        // is left; a token is `split` items, and the wave count (4 x blocks) stays a multiple of it.
+        // A wave takes at most kQkMaxTokensPerWave items (the roll kernel holds one position per
+        // lane), so larger row counts go in several launches.
+        NEKO_REQUIRE(ctx, split == 1 || split == 2, "%s: bad split %d", what, split);  // 4 x blocks is even
+        const int64_t need = (a.rows * split + 3) / 4;
         int64_t blocks = persistent_grid(ctx, reinterpret_cast<const void*>(k), 256, need);
-        const int64_t chunk = std::min<int64_t>(a.rows, 4 * blocks * kQkMaxTokensPerWave);
+        const int64_t chunk = std::min<int64_t>(a.rows, 4 * blocks * kQkMaxTokensPerWave / split);
         if (blocks < need) {
-            const int64_t per = (chunk + 4 * blocks - 1) / (4 * blocks);
-            blocks = ((chunk + per - 1) / per + 3) / 4;
+            const int64_t items = chunk * split;
+            const int64_t per = (items + 4 * blocks - 1) / (4 * blocks);
+            blocks = ((items + per - 1) / per + 3) / 4;
         }
         for (int64_t r0 = 0; r0 < a.rows; r0 += chunk) {
             QkArgs s = a;
@@ -73,7 +78,7 @@ int qk_launch(neko_hip_ctx* ctx, const char* what, QkArgs a, int dtype, bool kv,
             s.qkv = static_cast<char*>(a.qkv) + r0 * a.stride * static_cast<int64_t>(esz);
             if (a.positions) s.positions = a.positions + r0;
             else s.pos0 = a.pos0 + r0;
-            const int64_t b = std::min<int64_t>(blocks, (s.rows + 3) / 4);
+            const int64_t b = std::min<int64_t>(blocks, (s.rows * split + 3) / 4);
             hipLaunchKernelGGL(k, dim3(static_cast<uint32_t>(b)), dim3(256), 0, ctx->stream, s);
             if (int rc = after_launch(ctx, what)) return rc;
         }

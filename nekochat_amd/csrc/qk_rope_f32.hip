@@ -4,8 +4,8 @@
 
 namespace neko_hip {
 
-QkKernel pick_qk_f32(int L, int V, int nh, bool kv) {
-    return kv ? pick_lv<float, true>(L, V, nh) : pick_lv<float, false>(L, V, nh);
+QkKernel pick_qk_f32(int L, int V, int nh, bool kv, int* split) {
+    return kv ? pick_lv<float, true>(L, V, nh, split) : pick_lv<float, false>(L, V, nh, split);
 }
 
 }  // namespace neko_hip

@@ -219,7 +219,12 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
 // the token being computed, with one token's worth of data registers, and because every load is
 // issued after the stores it follows, waiting for it never waits on later stores.
 // Wave w takes tokens w, w + nw, ... (nw waves in the grid; at most 64 each, which the host
-// guarantees). Everything a token needs besides its row is fetched ahead of it: the positions of all
+// guarantees). With S > 1 a token is S work items of U passes each (item i: token i / S, passes
+// (i % S) * U ...), and wave w takes items w, w + nw, ... -- all of one part, as nw is a multiple of
+// S (the host's grid): the fused KV store at six or eight passes runs as two items of three or four,
+// which halves a wave's data registers and serial passes (8192 tokens of 32 + 8 + 8 heads x 128:
+// 5 waves per SIMD instead of 3, 38.0-39.2 us against 39.2-39.4 on the same buffers, bit-identical).
+// Everything a token needs besides its row is fetched ahead of it: the positions of all
 // of the wave's tokens in one vector load at the start (lane k holds token k's), and the cos/sin row
 // of the next token, loaded with one coalesced load spread over the lanes (8 bytes each at hd 128)
 // and staged in the wave's own LDS double buffer, from which every pass reads its (c, s) pairs. The
@@ -243,7 +248,7 @@ constexpr int kQkMaxTokensPerWave = 64;
 // What the kernel's scalar load of its first position reads when the call has no positions array.
 static __device__ const int32_t kQkNoPosition = 0;
 
-template <typename T, int L, int V, int U, bool KV>
+template <typename T, int L, int V, int U, bool KV, int S = 1>
 __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_kernel(QkArgs a) {
     constexpr int HPW = kWave / L;  // heads per wave pass
     constexpr int HD = 2 * L * V;   // the head size (a power of two): offsets and 1/HD are constants
@@ -256,9 +261,13 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, kept in SGPRs
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-    if (t0 >= a.rows) return;  // wave-uniform
-    const int ntok = static_cast<int>((a.rows - 1 - t0) / nw) + 1;
+    const int64_t item0 = static_cast<int64_t>(blockIdx.x) * 4 + wave;  // first work item: (token, part)
+    const int64_t items = S == 1 ? a.rows : a.rows * S;
+    if (item0 >= items) return;  // wave-uniform
+    const int ntok = static_cast<int>((items - 1 - item0) / nw) + 1;
+    const int part = S == 1 ? 0 : static_cast<int>(item0 % S);  // the same for all of a wave's items (nw % S == 0)
+    const int64_t t0 = S == 1 ? item0 : item0 / S;  // its first token; the next ones follow tnw apart
+    const int64_t tnw = S == 1 ? nw : nw / S;
     const int hl = lane % L;
     const int hs = lane / L;
     constexpr int half = HD / 2;
@@ -267,14 +276,17 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     const int nh = KV ? nqk + a.n_kv : nqk;  // with the KV store, the v heads ride along as extra passes
     const int64_t kvw = static_cast<int64_t>(a.n_kv) * HD;
     // Byte extents: the heads a wave loads (v included with the KV store) and the ones it writes back.
-    const uint32_t load_bytes = static_cast<uint32_t>(nh) * HD * sizeof(T);
-    const uint32_t store_bytes = static_cast<uint32_t>(nqk) * HD * sizeof(T);
+    const int hb = part * U * HPW;  // this part's first head
+    const int hl_end = S == 1 || nh < hb + U * HPW ? nh : hb + U * HPW;
+    const int hs_end = S == 1 || nqk < hb + U * HPW ? nqk : hb + U * HPW;
+    const uint32_t load_bytes = static_cast<uint32_t>(hl_end > hb ? hl_end - hb : 0) * HD * sizeof(T);
+    const uint32_t store_bytes = static_cast<uint32_t>(hs_end > hb ? hs_end - hb : 0) * HD * sizeof(T);
     const uint32_t cache_bytes = static_cast<uint32_t>(kvw) * 2u;
     const bool norm = a.wqk != nullptr;
     float* const cb = &csl[wave][0][0];
     const float* const wl = &wsh[wave][0];
     auto row_of = [&](int64_t t) __attribute__((always_inline)) -> const T* {
-        return static_cast<const T*>(a.qkv) + t * a.stride;
+        return static_cast<const T*>(a.qkv) + t * a.stride + static_cast<int64_t>(hb) * HD;
     };
     // Byte offsets of this lane's vector of pass u in a row (first half; the partner is half later).
     auto off = [&](int u) __attribute__((always_inline)) -> uint32_t {
@@ -284,7 +296,7 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     // Issued first: the wave's positions (lane k: token k's), its weight copy, then the first token's
     // row -- none of them waits for another.
     int32_t posv = 0;
-    if (a.positions) posv = a.positions[t0 + static_cast<int64_t>(lane < ntok ? lane : ntok - 1) * nw];
+    if (a.positions) posv = a.positions[t0 + static_cast<int64_t>(lane < ntok ? lane : ntok - 1) * tnw];
     // The first token's position once more, through the scalar cache (a uniform address in the constant
     // address space: s_load, issued here and waited for only after the row loads below): the first
     // cos/sin row waits on it, and a scalar load returns well before the vector load above.
@@ -299,7 +311,7 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     };
     // Token k's position (wave-uniform) and whether it indexes the table.
     auto pos_of = [&](int k) __attribute__((always_inline)) -> int64_t {
-        return a.positions ? static_cast<int64_t>(__builtin_amdgcn_readlane(posv, k)) : a.pos0 + t0 + k * nw;
+        return a.positions ? static_cast<int64_t>(__builtin_amdgcn_readlane(posv, k)) : a.pos0 + t0 + k * tnw;
     };
     auto in_table = [&](int64_t p) __attribute__((always_inline)) -> bool { return p >= 0 && p < a.n_pos; };
     // Pairs lane, lane + 64, ... of the row at `pos` (row 0 for a position outside the table): loaded
@@ -323,12 +335,12 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     // Normalises, rotates and stores every pass of token k (cos/sin from LDS buffer `buf`); with
     // `more`, refills each pass's registers with token k + 1's right after its stores.
     auto step = [&](int k, int buf, bool more) __attribute__((always_inline)) {
-        const int64_t t = t0 + k * nw;
+        const int64_t t = t0 + k * tnw;
         const int64_t pos = pos_of(k);
         const bool valid = in_table(pos);
         const float* cr = cb + buf * HD + 2 * i0;  // this lane's V (cos, sin) pairs
         const BufRes st = buf_res(row_of(t), store_bytes);
-        const BufRes ld = buf_res(row_of(more ? t + nw : t), load_bytes);
+        const BufRes ld = buf_res(row_of(more ? t + tnw : t), load_bytes);
         // The cache rows of this token's position (only written with the KV store, and only for a
         // position inside the table: otherwise the resources are empty and every store drops).
         const int64_t cpos = valid ? pos : 0;
@@ -337,7 +349,7 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
         const BufRes vc = buf_res(KV ? static_cast<const void*>(a.v_cache + cpos * kvw) : a.qkv, cbytes);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int head = u * HPW + hs;
+            const int head = hb + u * HPW + hs;  // absolute head index
             VT oa = A[u], ob = B[u];
             if (valid) {
                 float fa[V], fb[V];
@@ -523,8 +535,16 @@ QkKernel pick_fit(bool fit) {
     else return fit ? qk_rope_roll_kernel<T, L, V, U, false> : qk_rope_batch_kernel<T, L, V, U>;
 }
 
+// *split = the work items per token (1, or 2 for the fused KV store at six or eight passes).
 template <typename T, int L, int V, bool KV>
-QkKernel pick_u(int passes) {
+QkKernel pick_u(int passes, int* split) {
+    *split = 1;
+    if constexpr (KV) {
+        if (passes == 6 || passes == 8) {
+            *split = 2;
+            return passes == 6 ? qk_rope_roll_kernel<T, L, V, 3, true, 2> : qk_rope_roll_kernel<T, L, V, 4, true, 2>;
+        }
+    }
     switch (passes) {
         case 1: return pick_fit<T, L, V, 1, KV>(true);
         case 2: return pick_fit<T, L, V, 2, KV>(true);
@@ -539,35 +559,36 @@ QkKernel pick_u(int passes) {
 }
 
 template <typename T, int V, bool KV>
-QkKernel pick_l(int L, int nh) {
+QkKernel pick_l(int L, int nh, int* split) {
     const int passes = (nh + kWave / L - 1) / (kWave / L);
     switch (L) {
-        case 2: return pick_u<T, 2, V, KV>(passes);
-        case 4: return pick_u<T, 4, V, KV>(passes);
-        case 8: return pick_u<T, 8, V, KV>(passes);
-        case 16: return pick_u<T, 16, V, KV>(passes);
-        case 32: return pick_u<T, 32, V, KV>(passes);
+        case 2: return pick_u<T, 2, V, KV>(passes, split);
+        case 4: return pick_u<T, 4, V, KV>(passes, split);
+        case 8: return pick_u<T, 8, V, KV>(passes, split);
+        case 16: return pick_u<T, 16, V, KV>(passes, split);
+        case 32: return pick_u<T, 32, V, KV>(passes, split);
         case 64:
-            if constexpr (2 * 64 * V <= 512) return pick_u<T, 64, V, KV>(passes);  // head sizes up to 512
+            if constexpr (2 * 64 * V <= 512) return pick_u<T, 64, V, KV>(passes, split);  // head sizes up to 512
             return nullptr;
     }
     return nullptr;
 }
 
 template <typename T, bool KV>
-QkKernel pick_lv(int L, int V, int nh) {
+QkKernel pick_lv(int L, int V, int nh, int* split) {
+    *split = 1;
     // The fused KV store exists for 16-byte lane vectors only (every power-of-two head size); other
     // shapes take the unfused pair.
     if constexpr (KV) {
-        return V == Chunk16<T>::N ? pick_l<T, Chunk16<T>::N, true>(L, nh) : nullptr;
+        return V == Chunk16<T>::N ? pick_l<T, Chunk16<T>::N, true>(L, nh, split) : nullptr;
     } else {
         // Lane vectors are at most 16 bytes (the launcher's limit): 8 halves or 4 floats.
         switch (V) {
-            case 1: return pick_l<T, 1, false>(L, nh);
-            case 2: return pick_l<T, 2, false>(L, nh);
-            case 4: return pick_l<T, 4, false>(L, nh);
+            case 1: return pick_l<T, 1, false>(L, nh, split);
+            case 2: return pick_l<T, 2, false>(L, nh, split);
+            case 4: return pick_l<T, 4, false>(L, nh, split);
             case 8:
-                if constexpr (sizeof(T) == 2) return pick_l<T, 8, false>(L, nh);
+                if constexpr (sizeof(T) == 2) return pick_l<T, 8, false>(L, nh, split);
                 return nullptr;
         }
         return nullptr;
@@ -575,8 +596,9 @@ QkKernel pick_lv(int L, int V, int nh) {
 }
 
 // Kernel pickers per activation type (qk_rope_f16.hip, qk_rope_f32.hip): the kernel for a head
-// split into L lanes of V elements and nh heads per row, with or without the fused KV store.
-QkKernel pick_qk_f16(int L, int V, int nh, bool kv);
-QkKernel pick_qk_f32(int L, int V, int nh, bool kv);
+// split into L lanes of V elements and nh heads per row, with or without the fused KV store, and in
+// *split the work items it makes of each token (the roll kernel's S).
+QkKernel pick_qk_f16(int L, int V, int nh, bool kv, int* split);
+QkKernel pick_qk_f32(int L, int V, int nh, bool kv, int* split);
 
 }  // namespace neko_hip

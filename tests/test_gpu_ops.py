@@ -369,6 +369,9 @@ def test_qk_rope_kv_prefill(dev):
     (3, 1, 96, torch.float16),     # no fused kernel for this head size: rope then store
     (64, 8, 128, torch.float16),   # 80 heads > 8 passes: rope then store
     (8, 2, 128, torch.float32),
+    (32, 8, 128, torch.float16),   # Qwen3-4B heads: 6 passes, each token two work items of 3
+    (40, 12, 128, torch.float16),  # 8 passes: two items of 4
+    (16, 8, 128, torch.float32),   # f32, 4 heads per pass: 8 passes, two items of 4
 ])
 def test_qk_rope_kv_shapes(dev, n_q, n_kv, hd, dtype):
     _case(f"qk rope + kv n_q={n_q} n_kv={n_kv} hd={hd} {dtype}")
@@ -378,9 +381,22 @@ def test_qk_rope_kv_shapes(dev, n_q, n_kv, hd, dtype):
     _kv_case(dev, 37, n_q, n_kv, hd, 512, pos, dtype=dtype)
 
 
-def test_qk_rope_kv_pos0(dev):
-    _case("qk rope + kv store, pos0 form")
-    _kv_case(dev, 9, 4, 2, 128, 16, None, pos0=5)  # rows 7 and 8 fall outside the 16-row table
+@pytest.mark.parametrize("n_q,n_kv", [(4, 2), (32, 8)])
+def test_qk_rope_kv_pos0(dev, n_q, n_kv):
+    _case(f"qk rope + kv store, pos0 form, heads {n_q}+{n_kv}")
+    _kv_case(dev, 13, n_q, n_kv, 128, 16, None, pos0=5)  # rows 11 and 12 fall outside the 16-row table
+
+
+def test_qk_rope_kv_rows_beyond_one_launch(dev):
+    """The fused KV store over two work items per token (64 + 16 + 16 heads x 64: six passes) on more
+    rows than one launch takes (at most 64 items per wave: 163,840 rows at the 1280 workgroups that
+    stay resident), so the op runs in two launches; distinct positions, some outside the table."""
+    _case("qk rope + kv store, 166000 rows (two launches)")
+    T, n_q, n_kv, hd = 166000, 64, 16, 64
+    rng = np.random.default_rng(63)
+    pos = rng.permutation(T).astype(np.int32)
+    pos[rng.integers(0, T, 40)] = -3
+    _kv_case(dev, T, n_q, n_kv, hd, T, pos, stream=64)
 
 
 @pytest.mark.parametrize("dtype,width,k_off,v_off", [
