@@ -147,7 +147,11 @@ class FloorLib:
                             ("neko_floor_inplace_kv", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int64, c.c_void_p,
                                                        c.c_void_p, c.c_int64, c.c_void_p]),
                             ("neko_floor_gate", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_void_p, c.c_int64,
-                                                 c.c_int64, c.c_int64, c.c_void_p])):
+                                                 c.c_int64, c.c_int64, c.c_void_p]),
+                            ("neko_floor_copy_x", [c.c_void_p, c.c_void_p, c.c_size_t, c.c_int, c.c_int, c.c_int, c.c_void_p]),
+                            ("neko_floor_rows2_x", [c.c_void_p, c.c_int64, c.c_void_p, c.c_int64, c.c_int64, c.c_int64,
+                                                    c.c_int, c.c_void_p]),
+                            ("neko_floor_inplace_x", [c.c_void_p, c.c_int64, c.c_int64, c.c_int64, c.c_int, c.c_void_p])):
             getattr(lib, name).argtypes = args_
             getattr(lib, name).restype = c.c_int
             self.bound.add(name)
@@ -214,6 +218,8 @@ def headline_floors(cfg, inp, dev, fl):
             "copy_i4_ntnt": fl.copy(src.data_ptr(), dst.data_ptr(), half, 4, 1, 1),
             "copy_i1_plpl": fl.copy(src.data_ptr(), dst.data_ptr(), half, 1, 0, 0),
             "copy_i4_plpl": fl.copy(src.data_ptr(), dst.data_ptr(), half, 4, 0, 0),
+            "copy_i1_plpl_x128": fl.copy_x(src.data_ptr(), dst.data_ptr(), half, 0, 0, 128),
+            "copy_i1_ntnt_x128": fl.copy_x(src.data_ptr(), dst.data_ptr(), half, 1, 1, 128),
             "hipMemcpyAsync": fl.memcpy(dst.data_ptr(), src.data_ptr(), half),
             "torch_copy_": (lambda d=dst, s=src: d.copy_(s)),
         }
@@ -237,6 +243,8 @@ def headline_floors(cfg, inp, dev, fl):
     cand = {
         "inplace_rows_ntpl": fl.inplace_rows(qf.data_ptr(), rs, cfg.T, qk_w, waves, 1, 0),
         "inplace_plpl": fl.inplace(qf.data_ptr(), rs, cfg.T, qk_w, 0, 0),
+        "inplace_plpl_x64": fl.inplace_x(qf.data_ptr(), rs, cfg.T, qk_w, 64),
+        "inplace_plpl_x128": fl.inplace_x(qf.data_ptr(), rs, cfg.T, qk_w, 128),
         "hipMemcpy2DAsync": fl.memcpy2d(qf2.data_ptr(), rs, qf.data_ptr(), rs, qk_w, cfg.T),
     }
     layer["qk_norm_rope"] = dict(cand, _keep=(qf, qf2))
@@ -253,6 +261,7 @@ def headline_floors(cfg, inp, dev, fl):
     d1 = torch.empty(tot, dtype=torch.uint8, device=dev)
     cand = {
         "rows2_ntpl": fl.rows2(h.data_ptr(), 2 * gi // cfg.T, gout.data_ptr(), gi // cfg.T, cfg.T, gi // cfg.T, 1, 0),
+        "rows2_ntpl_x128": fl.rows2_x(h.data_ptr(), 2 * gi // cfg.T, gout.data_ptr(), gi // cfg.T, cfg.T, gi // cfg.T, 128),
         "copy2_ntpl": fl.copy2(h.data_ptr(), h.data_ptr() + gi, gout.data_ptr(), gi, 1, 0),
         "hipMemcpyAsync_same_total": fl.memcpy(d1.data_ptr(), h.data_ptr(), tot),
     }
@@ -919,8 +928,9 @@ def all_configs(args):
         calls6["floor_inplace_kv"] = fl6.inplace_kv(qf.data_ptr(), rs6, c6.T, qk_w6, kvb, kf.data_ptr(), vf.data_ptr(), kvb)
         floors6["qk_norm_rope_kv"].append("floor_inplace_kv")
         calls6["floor_inplace_plpl"] = fl6.inplace(qf2.data_ptr(), rs6, c6.T, qk_w6, 0, 0)
+        calls6["floor_inplace_plpl_x64"] = fl6.inplace_x(qf2.data_ptr(), rs6, c6.T, qk_w6, 64)
         calls6["floor_inplace_rows_ntpl"] = fl6.inplace_rows(qf2.data_ptr(), rs6, c6.T, qk_w6, waves6, 1, 0)
-        floors6["qk_norm_rope"] += ["floor_inplace_plpl", "floor_inplace_rows_ntpl"]
+        floors6["qk_norm_rope"] += ["floor_inplace_plpl", "floor_inplace_rows_ntpl", "floor_inplace_plpl_x64"]
         calls6["floor_split2"] = fl6.split2(qf2.data_ptr() + qoff * 2, rs6, kvb, kf.data_ptr(), vf.data_ptr(), kvb, c6.T)
         floors6["store_kv"].append("floor_split2")
         for fl_names in floors6.values():
@@ -976,11 +986,16 @@ def all_configs(args):
                 calls5[name] = fl5.copy(x5.data_ptr(), y5f.data_ptr(), c5.T * c5.C * 2, items, ntl, nts)
                 floors5["rmsnorm"].append(name)
                 bytes5[name] = bytes5["rmsnorm"]
+        calls5["floor_copy_i1_plpl_x128"] = fl5.copy_x(x5.data_ptr(), y5f.data_ptr(), c5.T * c5.C * 2, 0, 0, 128)
+        floors5["rmsnorm"].append("floor_copy_i1_plpl_x128")
+        bytes5["floor_copy_i1_plpl_x128"] = bytes5["rmsnorm"]
         calls5["floor_gate"] = fl5.gate(ya.data_ptr(), c5.D * 2, za.data_ptr(), c5.D * 2, og5f.data_ptr(), c5.D * 2,
                                         c5.D * 2, c5.T)
         bytes5["floor_gate"] = bytes5["gated_rmsnorm"]
         calls5["floor_rows2_ntpl"] = fl5.rows2(h5.data_ptr(), 2 * c5.I * 2, o5f.data_ptr(), c5.I * 2, c5.T, c5.I * 2, 1, 0)
-        bytes5["floor_rows2_ntpl"] = bytes5["swiglu"]
+        calls5["floor_rows2_ntpl_x128"] = fl5.rows2_x(h5.data_ptr(), 2 * c5.I * 2, o5f.data_ptr(), c5.I * 2, c5.T, c5.I * 2, 128)
+        floors5["swiglu"].append("floor_rows2_ntpl_x128")
+        bytes5["floor_rows2_ntpl"] = bytes5["floor_rows2_ntpl_x128"] = bytes5["swiglu"]
         run("granite_4.0h_norms", calls5, bytes5,
             "Granite-4.0-H: 16384 tokens, RMSNorm 1536, gated RMSNorm y*silu(z) 3072, SwiGLU I=4096", floors=floors5)
         del y5f, og5f, o5f

@@ -8,9 +8,13 @@
 // one-round row kernels' shape (every row of a wave loaded before any store), the embedding gather's
 // pattern (table rows read through token ids, contiguous output rows written), the residual add +
 // RMSNorm's, the KV store's, the fused q/k RoPE + KV store's and the gated norm's byte patterns, and a
-// read-only sweep.
+// read-only sweep. The flat copies, SwiGLU's layout and the flat in-place rewrite also come with their
+// workgroups' data in runs of X per XCD (xcd_block, device.h), the order the SwiGLU and q/k RoPE
+// kernels use.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "device.h"
 
 namespace {
 
@@ -31,9 +35,16 @@ __global__ void empty_kernel() {}
 
 // Chunk i = (block * ITEMS + k) * 256 + thread: each load instruction of a wave covers 1 KB of
 // contiguous bytes; all ITEMS loads are issued before the first store.
-template <int ITEMS, bool NTL, bool NTS>
+// Data block of workgroup b of G: b itself (X = 0) or in runs of X per XCD.
+template <int X>
+__device__ __forceinline__ uint32_t data_block(uint32_t b, uint32_t G) {
+    if constexpr (X == 0) return b;
+    else return neko_hip::xcd_block<X>(b, G);
+}
+
+template <int ITEMS, bool NTL, bool NTS, int X = 0>
 __global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * ITEMS + threadIdx.x;
+    const int64_t base = static_cast<int64_t>(data_block<X>(blockIdx.x, gridDim.x)) * 256 * ITEMS + threadIdx.x;
     u32x4 v[ITEMS];
 #pragma unroll
     for (int k = 0; k < ITEMS; k++) {
@@ -71,10 +82,10 @@ __global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ src
 
 // SwiGLU's layout without its arithmetic: rows of h hold two halves of `cpr` chunks; out[r][c] =
 // h[r][c] ^ h[r][cpr + c], the flattened (row, chunk) index split with a division by cpr.
-template <bool NTL, bool NTS>
+template <bool NTL, bool NTS, int X = 0>
 __global__ __launch_bounds__(256) void rows2_kernel(const u32x4* __restrict__ h, int64_t hs, u32x4* __restrict__ out,
                                                     int64_t os, uint32_t cpr, uint32_t items) {
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t idx = data_block<X>(blockIdx.x, gridDim.x) * 256u + threadIdx.x;
     if (idx >= items) return;
     const uint32_t row = idx / cpr, col = idx - row * cpr;
     const u32x4* hp = h + row * hs + col;
@@ -84,9 +95,9 @@ __global__ __launch_bounds__(256) void rows2_kernel(const u32x4* __restrict__ h,
 // The q/k RoPE's layout without its arithmetic: the first `cpr` chunks of each row (stride `stride`
 // chunks) are read and written back in place, xored with `key` (0 at run time, unknown to the
 // compiler, so every store is kept).
-template <bool NTL, bool NTS>
+template <bool NTL, bool NTS, int X = 0>
 __global__ __launch_bounds__(256) void inplace_kernel(u32x4* buf, int64_t stride, uint32_t cpr, uint32_t items, uint32_t key) {
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t idx = data_block<X>(blockIdx.x, gridDim.x) * 256u + threadIdx.x;
     if (idx >= items) return;
     const uint32_t row = idx / cpr, col = idx - row * cpr;
     u32x4* p = buf + row * stride + col;
@@ -491,6 +502,70 @@ int neko_floor_gate(const void* y, int64_t y_stride, const void* z, int64_t z_st
     hipLaunchKernelGGL(gate_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const u32x4*>(y), y_stride / 16, static_cast<const u32x4*>(z), z_stride / 16,
                        static_cast<u32x4*>(out), out_stride / 16, static_cast<int>(width / 16));
+    return hipGetLastError();
+}
+
+// The XCD-ordered forms, runs of `run` workgroups (64, 128 or 256) per XCD: neko_floor_copy with one
+// chunk per lane, neko_floor_rows2 and neko_floor_inplace, same arguments otherwise.
+int neko_floor_copy_x(const void* src, void* dst, size_t bytes, int nt_load, int nt_store, int run, void* stream) {
+    if (!ok16(src) || !ok16(dst) || bytes % 16) return hipErrorInvalidValue;
+    const int64_t n = static_cast<int64_t>(bytes / 16), blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff || nt_load != nt_store) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>(blocks)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* s = static_cast<const u32x4*>(src);
+    auto* d = static_cast<u32x4*>(dst);
+    const bool nt = nt_load != 0;
+    switch (run * 2 + (nt ? 1 : 0)) {
+        case 128: hipLaunchKernelGGL((copy_kernel<1, false, false, 64>), g, b, 0, st, s, d, n); break;
+        case 129: hipLaunchKernelGGL((copy_kernel<1, true, true, 64>), g, b, 0, st, s, d, n); break;
+        case 256: hipLaunchKernelGGL((copy_kernel<1, false, false, 128>), g, b, 0, st, s, d, n); break;
+        case 257: hipLaunchKernelGGL((copy_kernel<1, true, true, 128>), g, b, 0, st, s, d, n); break;
+        case 512: hipLaunchKernelGGL((copy_kernel<1, false, false, 256>), g, b, 0, st, s, d, n); break;
+        case 513: hipLaunchKernelGGL((copy_kernel<1, true, true, 256>), g, b, 0, st, s, d, n); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// SwiGLU's layout, non-temporal loads and plain stores (its own cache policy), XCD-ordered.
+int neko_floor_rows2_x(const void* h, int64_t h_stride, void* out, int64_t out_stride, int64_t rows, int64_t half, int run,
+                       void* stream) {
+    if (!ok16(h) || !ok16(out) || half % 16 || h_stride % 16 || out_stride % 16 || half <= 0 || rows <= 0)
+        return hipErrorInvalidValue;
+    const int64_t cpr = half / 16, items = rows * cpr;
+    if (items >= (int64_t(1) << 32) - 256) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>((items + 255) / 256)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto* hp = static_cast<const u32x4*>(h);
+    auto* op = static_cast<u32x4*>(out);
+    const int64_t hs = h_stride / 16, os = out_stride / 16;
+    const uint32_t c = static_cast<uint32_t>(cpr), n = static_cast<uint32_t>(items);
+    switch (run) {
+        case 64: hipLaunchKernelGGL((rows2_kernel<true, false, 64>), g, b, 0, st, hp, hs, op, os, c, n); break;
+        case 128: hipLaunchKernelGGL((rows2_kernel<true, false, 128>), g, b, 0, st, hp, hs, op, os, c, n); break;
+        case 256: hipLaunchKernelGGL((rows2_kernel<true, false, 256>), g, b, 0, st, hp, hs, op, os, c, n); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// The flat in-place rewrite, plain loads and stores, XCD-ordered.
+int neko_floor_inplace_x(void* buf, int64_t stride, int64_t rows, int64_t width, int run, void* stream) {
+    if (!ok16(buf) || width % 16 || stride % 16 || width <= 0 || rows <= 0 || stride < width) return hipErrorInvalidValue;
+    const int64_t cpr = width / 16, items = rows * cpr;
+    if (items >= (int64_t(1) << 32) - 256) return hipErrorInvalidValue;
+    const dim3 g(static_cast<uint32_t>((items + 255) / 256)), b(256);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    auto* p = static_cast<u32x4*>(buf);
+    const int64_t s = stride / 16;
+    const uint32_t c = static_cast<uint32_t>(cpr), n = static_cast<uint32_t>(items);
+    switch (run) {
+        case 64: hipLaunchKernelGGL((inplace_kernel<false, false, 64>), g, b, 0, st, p, s, c, n, 0u); break;
+        case 128: hipLaunchKernelGGL((inplace_kernel<false, false, 128>), g, b, 0, st, p, s, c, n, 0u); break;
+        case 256: hipLaunchKernelGGL((inplace_kernel<false, false, 256>), g, b, 0, st, p, s, c, n, 0u); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
