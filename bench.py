@@ -1146,6 +1146,12 @@ def stream_floor(args, flush, time_ops):
                 name = f"copy_{label}_i{items}_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
                 calls[name] = fl.copy(a_ptr, d_ptr, each, items, ntl, nts)
                 nbytes[name] = 2 * each
+        # one chunk per lane with the workgroups' data in runs of 64 / 128 / 256 per XCD
+        for run_ in (64, 128, 256):
+            for nt in (1, 0):
+                name = f"copy_{label}_i1_{'ntnt' if nt else 'plpl'}_x{run_}"
+                calls[name] = fl.copy_x(a_ptr, d_ptr, each, nt, nt, run_)
+                nbytes[name] = 2 * each
         # the runtime's copy of the same bytes, and torch's copy_ (which calls it)
         calls[f"hipMemcpyAsync_{label}"], nbytes[f"hipMemcpyAsync_{label}"] = fl.memcpy(d_ptr, a_ptr, each), 2 * each
         sv, dv = src[:each // 4], dst[:each // 4]
@@ -1166,6 +1172,10 @@ def stream_floor(args, flush, time_ops):
     for ntl, nts in ((1, 0), (1, 1), (0, 0)):
         name = f"rows2_swiglu_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
         calls[name] = fl.rows2(a_ptr, 2 * gi // cfg.T, d_ptr, gi // cfg.T, cfg.T, gi // cfg.T, ntl, nts)
+        nbytes[name] = 3 * gi
+    for run_ in (64, 128, 256):  # SwiGLU's layout and cache policy in XCD order
+        name = f"rows2_swiglu_ntpl_x{run_}"
+        calls[name] = fl.rows2_x(a_ptr, 2 * gi // cfg.T, d_ptr, gi // cfg.T, cfg.T, gi // cfg.T, run_)
         nbytes[name] = 3 * gi
     # The same SwiGLU-layout stream over constant input (every output line zero): how much cheaper
     # uniform data is, the reason the sources above are random.
@@ -1190,6 +1200,10 @@ def stream_floor(args, flush, time_ops):
     for ntl, nts in ((0, 0), (1, 0), (1, 1), (0, 1)):
         name = f"inplace_qk_{'nt' if ntl else 'pl'}{'nt' if nts else 'pl'}"
         calls[name] = fl.inplace(d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, ntl, nts)
+        nbytes[name] = 2 * cfg.T * qk_w
+    for run_ in (64, 128, 256):
+        name = f"inplace_qk_plpl_x{run_}"
+        calls[name] = fl.inplace_x(d_ptr, cfg.qkv_stride * 2, cfg.T, qk_w, run_)
         nbytes[name] = 2 * cfg.T * qk_w
     # The op itself on the headline's inputs, and the same rewrite of its own qkv buffer in the q/k
     # kernel's schedule: whole rows per wave, wave w taking rows w, w + nw, ..., at the kernel's
