@@ -537,7 +537,9 @@ QkKernel pick_fit(bool fit) {
     else return fit ? qk_rope_roll_kernel<T, L, V, U, false> : qk_rope_batch_kernel<T, L, V, U>;
 }
 
-// *split = the work items per token (1, or 2 for the fused KV store at six or eight passes).
+// *split = the work items per token: 2 for the fused KV store at six or eight passes, and for 16-byte
+// lane vectors at an even pass count from 10 to 16 (f32 rows of 32 + 8 heads x 128: ten passes, two
+// rolling items of five instead of the batch kernel); else 1.
 template <typename T, int L, int V, bool KV>
 QkKernel pick_u(int passes, int* split) {
     *split = 1;
@@ -545,6 +547,17 @@ QkKernel pick_u(int passes, int* split) {
         if (passes == 6 || passes == 8) {
             *split = 2;
             return passes == 6 ? qk_rope_roll_kernel<T, L, V, 3, true, 2> : qk_rope_roll_kernel<T, L, V, 4, true, 2>;
+        }
+    }
+    if constexpr (V == Chunk16<T>::N) {
+        if (passes >= 10 && passes <= 16 && passes % 2 == 0) {
+            *split = 2;
+            switch (passes / 2) {
+                case 5: return qk_rope_roll_kernel<T, L, V, 5, KV, 2>;
+                case 6: return qk_rope_roll_kernel<T, L, V, 6, KV, 2>;
+                case 7: return qk_rope_roll_kernel<T, L, V, 7, KV, 2>;
+                case 8: return qk_rope_roll_kernel<T, L, V, 8, KV, 2>;
+            }
         }
     }
     switch (passes) {

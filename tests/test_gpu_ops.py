@@ -251,6 +251,9 @@ def test_qk_rope_prefill(dev):
     (4, 2, 256, True, torch.float16),
     (2, 1, 64, True, torch.float32),
     (8, 2, 128, True, torch.float32),
+    (32, 8, 128, True, torch.float32),   # Qwen3-4B heads in f32: ten passes, two rolling items of five
+    (64, 16, 128, True, torch.float16),  # ten passes in f16
+    (64, 8, 128, True, torch.float16),   # nine passes: the batch kernel
 ])
 def test_qk_rope_shapes(dev, n_q, n_kv, hd, norm, dtype):
     _case(f"qk rope n_q={n_q} n_kv={n_kv} hd={hd} norm={norm} {dtype}")
@@ -367,7 +370,9 @@ def test_qk_rope_kv_prefill(dev):
     (16, 8, 128, torch.float16),   # Qwen3-0.6B decode
     (2, 1, 64, torch.float16),
     (3, 1, 96, torch.float16),     # no fused kernel for this head size: rope then store
-    (64, 8, 128, torch.float16),   # 80 heads > 8 passes: rope then store
+    (64, 8, 128, torch.float16),   # 80 heads: ten passes, two items of five
+    (64, 12, 128, torch.float16),  # 88 heads: eleven passes, no fused kernel: rope then store
+    (32, 8, 128, torch.float32),   # f32, 4 heads per pass: 12 passes, two items of six
     (8, 2, 128, torch.float32),
     (32, 8, 128, torch.float16),   # Qwen3-4B heads: 6 passes, each token two work items of 3
     (40, 12, 128, torch.float16),  # 8 passes: two items of 4
