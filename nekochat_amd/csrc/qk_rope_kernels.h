@@ -223,7 +223,11 @@ __device__ __forceinline__ void rotate_token(const TokenRegs<T, V, U>& tr, const
 // (i % S) * U ...), and wave w takes items w, w + nw, ... -- all of one part, as nw is a multiple of
 // S (the host's grid): the fused KV store at six or eight passes runs as two items of three or four,
 // which halves a wave's data registers and serial passes (8192 tokens of 32 + 8 + 8 heads x 128:
-// 5 waves per SIMD instead of 3, 38.0-39.2 us against 39.2-39.4 on the same buffers, bit-identical).
+// 5 waves per SIMD instead of 3, 38.0-39.2 us against 39.2-39.4 on the same buffers, bit-identical),
+// and a token of 10-16 passes (an even count) as two items of half of them, which the one-token roll
+// cannot hold (f32 rows of 32 + 8 heads x 128, ten passes: 51.5 us against 59.2 on the batch kernel).
+// Wave w's first item is taken from workgroup xcd_block<64>(w / 4) rather than w / 4, so that the
+// workgroups of each XCD take runs of consecutive rows.
 // Everything a token needs besides its row is fetched ahead of it: the positions of all
 // of the wave's tokens in one vector load at the start (lane k holds token k's), and the cos/sin row
 // of the next token, loaded with one coalesced load spread over the lanes (8 bytes each at hd 128)
