@@ -744,7 +744,10 @@ int launch_gemm3q(neko_hip_ctx* ctx, dim3 grid, const MmArgs& a, int tm, int tn)
 // in mm_tile_kernel. K is split over the grid's z: with several slices the waves write f32 partials
 // that mm_splitk_reduce adds in order. (Adding them in the kernel, by the last workgroup of each row
 // group to arrive, measured several times slower: the device-scope fences that publish the partials
-// write back / invalidate an XCD's whole L2.)
+// write back / invalidate an XCD's whole L2. Without fences -- partials stored and re-read as
+// device-scope relaxed atomics, which go past the XCD's L2, and a device-scope arrival counter --
+// it was still slower on every Qwen3-4B projection at 16 and 24 tokens: FP8 down 16.7 -> 22.0 us,
+// FP4 o 11.1 -> 14.0, against the launch it saves.)
 constexpr int kT2Waves = 4;
 constexpr int kT2Lds = 65536;  // LDS per workgroup (two per CU at 64 KB)
 constexpr int64_t kT2MaxT = 48;  // exclusive; at most 65 (four 16-token tiles)
