@@ -311,6 +311,12 @@ __device__ __forceinline__ typename BRaw<FMT>::T read_b(const uint8_t* tile, int
 
 // One group: request the next group's activations, write this group's weights to the wave's LDS
 // tile, request the weights two groups ahead into the same registers, then the group's MFMAs.
+// (hipcc keeps `sc` in the old scale registers and copies the new scales into them at the loop's
+// back edge, a copy that waits for every load in flight -- vmcnt(0) -- once per two groups, here and
+// in t2_step. Passing the scales through the LDS tile instead, and giving each loop a single exit,
+// removed every such wait and left the Qwen3-4B projections at 4, 16 and 24 tokens unchanged in
+// total (-0.9% to +0.4%; +3 to +9% for gate/up, -2 to -9% for the others): the waits are not what
+// bounds these kernels.)
 template <int FMT, int TT>
 __device__ __forceinline__ void mm_step(float4v (&acc)[TT], MmStage<FMT>& st, const half8 (&A)[kGroup][TT],
                                         half8 (&A_next)[kGroup][TT], const uint8_t* const (&prow)[pieces(FMT)],
