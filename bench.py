@@ -36,6 +36,10 @@ sys.path.insert(0, ROOT)
 METRIC = ("achieved HBM GB/s (% of 8 TB/s) per fused op; µs/layer non-GEMM ops, Qwen3-4B")
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+VALU_F32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector FMA
+# qwen3_4b_attention: (op, tokens, first position, first token of the CPU sample)
+ATTENTION_CASES = (("decode_4k", 1, 4095, 0), ("decode_32k", 1, 32767, 0), ("prefill_2k", 2048, 0, 2032),
+                   ("prefill_8k", 8192, 0, 8188))
 OPS = ("rmsnorm_in", "qk_norm_rope", "rmsnorm_post", "swiglu")
 DOMINANT = "swiglu"
 
@@ -57,7 +61,7 @@ def parse():
                         "quant_gather_qwen3_1.7b, qwen3_4b_fused, quantize_qwen3_1.7b_table, granite_4.0h_norms, "
                         "qwen3_4b_decode_matmul, qwen3_4b_decode4_matmul, qwen3_4b_decode16_matmul, qwen3_4b_decode24_matmul, "
                         "qwen3_4b_decode_matmul_f32, qwen3_4b_decode16_matmul_f32, "
-                        "qwen3_4b_prefill_matmul, stream_floor)")
+                        "qwen3_4b_prefill_matmul, qwen3_4b_attention, stream_floor)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     return p.parse_args()
@@ -627,6 +631,28 @@ def add_cpu_jobs(leg, want):
         leg.add("qwen3_4b_fused", "qk_norm_rope", qk_kv(True, False), c.T / n, s)
         leg.add("qwen3_4b_fused", "store_kv", qk_kv(False, True), c.T / n, s + ": storeKv")
 
+    def attention_jobs():  # qwen3_4b_attention
+        c = wl.QWEN3_PREFILL
+        H, KV, hd = c.n_q, c.n_kv, c.hd
+
+        def make(T, pos0, t0):  # the workload's tokens t0 .. T-1 (positions pos0 + t0 ..) through cpu::attention
+            def mk():
+                n = T - t0
+                q = _f32((n, H * hd), 0.0, 1.0, 101)
+                kc = _f32((pos0 + T, KV * hd), 0.0, 1.0, 102).astype(np.float16).view(np.uint16)
+                vc = _f32((pos0 + T, KV * hd), 0.0, 1.0, 103).astype(np.float16).view(np.uint16)
+                o = np.empty((n, H * hd), np.float32)
+                return (lambda: R.ref_attention(P(q), H * hd, P(kc), P(vc), P(o), n, H, KV, hd, pos0 + t0)), None
+            return mk
+
+        for name, T, pos0, t0 in ATTENTION_CASES:
+            pairs = T * pos0 + T * (T + 1) // 2  # (token, key) pairs of the whole call
+            sample = sum(pos0 + t + 1 for t in range(t0, T))
+            what = (f"the last {T - t0} of {T} tokens (median of {leg.reps}), scaled by (token, key) pairs to all {T}"
+                    if t0 else f"all {T} token(s) (median of {leg.reps})")
+            leg.add("qwen3_4b_attention", name, make(T, pos0, t0), pairs / sample,
+                    f"{what} through cpu::attention on a one-thread pool; {core}")
+
     def quantize_jobs():  # quantize_qwen3_1.7b_table
         c, n = wl.QUANT_GATHER, 512
 
@@ -713,6 +739,7 @@ def add_cpu_jobs(leg, want):
             ("qwen3_4b_decode16_matmul_f32",
              lambda: matmul_jobs("qwen3_4b_decode16_matmul_f32", wl.QWEN3_DECODE16_MATMUL)),
             ("qwen3_4b_prefill_matmul", prefill_matmul_jobs),
+            ("qwen3_4b_attention", attention_jobs),
     ):
         if want(label):
             jobs()
@@ -741,7 +768,7 @@ def all_configs(args):
               "qwen3_4b_fused",
               "quantize_qwen3_1.7b_table", "granite_4.0h_norms", "qwen3_4b_decode_matmul", "qwen3_4b_decode4_matmul",
               "qwen3_4b_decode16_matmul", "qwen3_4b_decode24_matmul", "qwen3_4b_decode_matmul_f32",
-              "qwen3_4b_decode16_matmul_f32", "qwen3_4b_prefill_matmul", "stream_floor")
+              "qwen3_4b_decode16_matmul_f32", "qwen3_4b_prefill_matmul", "qwen3_4b_attention", "stream_floor")
     if args.workload is not None and args.workload not in labels:
         raise SystemExit(f"bench.py: unknown workload {args.workload!r}; one of {', '.join(labels)}")
 
@@ -940,6 +967,33 @@ def all_configs(args):
             "Qwen3-4B fused neighbours: residual add + RMSNorm [8192,2560]; q/k RoPE + KV store of an 8192-token "
             "sequence, beside the unfused q/k RoPE and KV store", floors=floors6)
         del xf, df, cf, qf, qf2, kf, vf
+
+    # Qwen3-4B attention over the f16 KV cache (the reference's Attention kernel; cpu::attention), f32 q
+    # and out as the adapter passes them: one decode token over 4096 and 32768 cached positions (bytes =
+    # the k and v rows once + q + out: HBM-bound) and prefills of 2048 and 8192 tokens from position 0
+    # (flops = 4 hd per (head, token, key): the q.k and p.v products).
+    if want("qwen3_4b_attention"):
+        c10 = wl.QWEN3_PREFILL
+        H10, KV10, hd10 = c10.n_q, c10.n_kv, c10.hd
+        kw10 = KV10 * hd10
+        calls10, bytes10, flops10 = {}, {}, {}
+        for name, T, pos0, _ in ATTENTION_CASES:
+            q10 = wl.normal_f16((T, H10 * hd10), 0.0, 1.0, 101, dev).float()
+            kc10 = wl.normal_f16((pos0 + T, kw10), 0.0, 1.0, 102, dev)
+            vc10 = wl.normal_f16((pos0 + T, kw10), 0.0, 1.0, 103, dev)
+            o10 = torch.empty_like(q10)
+            calls10[name] = ops.prepare(ops.attention, q10, kc10, vc10, H10, KV10, hd10, pos0, out=o10)[0]
+            calls10[name].keep = (q10, kc10, vc10, o10)
+            bytes10[name] = (pos0 + T) * kw10 * 2 * 2 + 2 * T * H10 * hd10 * 4
+            flops10[name] = 4 * hd10 * H10 * (T * pos0 + T * (T + 1) // 2)
+        run("qwen3_4b_attention", calls10, bytes10,
+            "Qwen3-4B attention (32 q / 8 kv heads x 128) over an f16 KV cache, f32 q and out: decode of one token "
+            "over 4096 / 32768 cached positions, prefill of 2048 / 8192 tokens from position 0")
+        for name, f in flops10.items():  # the kernel's products run on the f32 vector units
+            op = out["qwen3_4b_attention"]["ops"][name]
+            tf = f / (op["us"] * 1e-6) / 1e12
+            op.update({"flops": f, "TFLOPs": round(tf, 2), "valu_f32_frac": round(tf / VALU_F32_PEAK_TFLOPS, 4)})
+        del calls10
 
     # Load-time quantiser: the 151936 x 2048 tied table in f32 (1.24 GB) encoded on the device into each
     # weight format; bytes = the f32 rows read + the encoded rows written.

@@ -137,6 +137,20 @@ int neko_hip_store_kv(neko_hip_ctx* ctx, const void* qkv, int64_t row_stride, in
                       int64_t width, int64_t pos0, const int32_t* positions, uint16_t* k_cache, uint16_t* v_cache,
                       int64_t cache_rows, int dtype);
 
+/* Causal grouped-query attention over the f16 KV caches (cpu::attention, cpu_ops.cpp:544-575; the GPU
+ * kernel Attention, attention.comp, dispatched by qwen3_model.cpp:317 and gpt2_model.cpp:255): for
+ * token t = 0 .. T-1 at position pos0 + t and query head h < n_head,
+ *   out[t*out_stride + h*hd + d] = sum_j w_j v_j[d] / sum_j w_j,  w_j = exp(scale * q . k_j - max),
+ * over cache rows j = 0 .. pos0 + t, where q = q[t*q_stride + h*hd ..] (dtype) and k_j / v_j are the hd
+ * halves of k_cache / v_cache at j*n_kv*hd + (h / (n_head / n_kv))*hd (the reference's cache layout:
+ * rows of n_kv*hd halves, holding positions 0 .. pos0 + T - 1). n_head a multiple of n_kv; hd even,
+ * 2..256; the reference's scale is 1/sqrt(hd); caches 4-byte aligned. out may not overlap q or the
+ * caches. f32 sums in another order than the reference's CPU loop (whose order its own shader does not
+ * follow either): within 1e-6 relative of it at the tested shapes. */
+int neko_hip_attention(neko_hip_ctx* ctx, const void* q, int64_t q_stride, const uint16_t* k_cache, const uint16_t* v_cache,
+                       void* out, int64_t out_stride, int64_t T, int n_head, int n_kv, int hd, int64_t pos0, float scale,
+                       int dtype);
+
 /* ---------------------------------------------------------------- residual */
 
 /* Residual add + RMSNorm: x[t] = x[t] + delta[t] (float add, rounded once to the activation type,

@@ -49,6 +49,7 @@ SIGNATURES = {
     "neko_hip_qk_norm_rope_kv": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p, _i64,
                                         _i32]),
     "neko_hip_store_kv": (_i32, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i32]),
+    "neko_hip_attention": (_i32, [_p, _p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i64, _f32, _i32]),
     "neko_hip_add_rmsnorm": (_i32, [_p, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _f32, _i32]),
     "neko_hip_matmul": (_i32, [_p, _p, _i64, _i64, _i64, _p, _i64, _i32, _i64, _p, _p, _i64, _i32, _i32, _i32]),
     "neko_hip_set_matmul_library": (_i32, [_p, _i32]),

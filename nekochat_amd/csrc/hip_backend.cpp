@@ -87,12 +87,13 @@ public:
             case Kernel::Gelu: gelu(bindings, pa); return;
             case Kernel::KvStore: kvStore(bindings, pa, pb); return;
             case Kernel::AddRmsNorm: addRmsNorm(bindings, pa, gx); return;
+            case Kernel::Attention: attention(bindings, pa, pb); return;
             case Kernel::Matmul: matmul(bindings, pa, pb, gx, NEKO_FMT_F16); return;
             case Kernel::MatmulQ8: matmul(bindings, pa, pb, gx, NEKO_FMT_FP8); return;
             case Kernel::MatmulQ4: matmul(bindings, pa, pb, gx, NEKO_FMT_FP4); return;
             default: break;
         }
-        fail(std::string("HIP backend: kernel ") + kernelName(k) + " is not implemented (attention)");
+        fail(std::string("HIP backend: unknown kernel ") + kernelName(k));
     }
 
 private:
@@ -249,6 +250,26 @@ private:
         auto* kc = static_cast<uint16_t*>(need(b, 1, mul(pos0 + T, W, 2), "KvStore"));
         auto* vc = static_cast<uint16_t*>(need(b, 2, mul(pos0 + T, W, 2), "KvStore"));
         check(neko_hip_store_kv(ctx_, qkv, stride, kOff, vOff, T, W, pos0, nullptr, kc, vc, pos0 + T, NEKO_DT_F32));
+    }
+
+    // attention.comp: PA (T, qStride, nHead, pos0), PB (headDim, scale bits, kvWidth); bindings qkv
+    // (f32 rows of qStride, head h of token t at t*qStride + h*hd), the k and v caches (f16 rows of
+    // kvWidth, positions 0 .. pos0 + T - 1), out (f32 [T][nHead*hd]); dispatch (nHead, T).
+    void attention(Buffer* const b[4], const int32_t* pa, const int32_t* pb) {
+        const int64_t T = pa[0], qs = pa[1], H = pa[2], pos0 = pa[3], hd = pb[0], kvw = pb[2];
+        const float scale = bitsFloat(pb[1]);
+        positive(T, "Attention");
+        positive(qs, "Attention");
+        positive(pos0, "Attention");
+        if (T == 0) return;
+        if (H <= 0 || hd <= 0 || kvw <= 0 || kvw % hd || H % (kvw / hd))
+            fail("HIP Attention: nHead must be a multiple of kvWidth / headDim");
+        void* q = need(b, 0, mul(add(mul(T - 1, qs), mul(H, hd)), 4), "Attention");
+        auto* kc = static_cast<const uint16_t*>(need(b, 1, mul(pos0 + T, kvw, 2), "Attention"));
+        auto* vc = static_cast<const uint16_t*>(need(b, 2, mul(pos0 + T, kvw, 2), "Attention"));
+        void* out = need(b, 3, mul(mul(T, H), hd, 4), "Attention");
+        check(neko_hip_attention(ctx_, q, qs, kc, vc, out, H * hd, T, static_cast<int>(H), static_cast<int>(kvw / hd),
+                                 static_cast<int>(hd), pos0, scale, NEKO_DT_F32));
     }
 
     // Residual add + RMSNorm: PA (C, eps); bindings x (in/out), delta, xn, w; dispatch (rows, 1).

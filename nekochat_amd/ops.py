@@ -283,6 +283,28 @@ def store_kv(qkv: torch.Tensor, k_off: int, v_off: int, width: int, k_cache: tor
            int(pos0), pos_ptr, k_cache.data_ptr(), v_cache.data_ptr(), cache_rows, _dtype_code(qkv))
 
 
+def attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int, n_kv: int, hd: int,
+              pos0: int = 0, scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """cpu::attention (cpu_ops.cpp:544-575): causal grouped-query attention of the q rows (token t at
+    position pos0 + t; head h at columns [h*hd, +hd)) over float16 caches [>= pos0 + T, n_kv*hd]
+    holding positions 0 .. pos0 + T - 1. scale defaults to the reference's 1/sqrt(hd). Returns
+    [T, n_head*hd] in q's dtype."""
+    T, width, qs = _rows(q, "q")
+    if n_kv <= 0 or n_head % n_kv:
+        raise NekoError("n_head must be a positive multiple of n_kv")
+    if width < n_head * hd:
+        raise NekoError(f"q rows hold {width} values, fewer than {n_head} heads x {hd}")
+    _cache(k_cache, pos0 + T, n_kv * hd, "k_cache", q.device)
+    _cache(v_cache, pos0 + T, n_kv * hd, "v_cache", q.device)
+    out = _out_like(q, T, n_head * hd, out, "out")
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    ctx = _ctx_for(q)
+    _issue(ctx, lib.neko_hip_attention, ctx.handle, q.data_ptr(), qs, k_cache.data_ptr(), v_cache.data_ptr(),
+           out.data_ptr(), out.stride(0), T, int(n_head), int(n_kv), int(hd), int(pos0), float(scale), _dtype_code(q))
+    return out
+
+
 def add_rms_norm(x: torch.Tensor, delta: torch.Tensor, w: torch.Tensor, eps: float,
                  out: torch.Tensor | None = None) -> torch.Tensor:
     """Residual add + RMSNorm: x += delta (float add, rounded to x's dtype, in place) -- the

@@ -175,6 +175,53 @@ void oracle_store_kv(const float* k, const float* v, int64_t src_stride, uint16_
     }
 }
 
+/* Causal grouped-query attention (cpu_ops.cpp:544-575): for token t (position pos0 + t) and head h,
+ * over cache rows j = 0 .. pos0 + t: s_j = (sum over d, in d order, of q[d] * k_j[d]) * scale, scale =
+ * 1 / sqrtf(hd); mx = the largest s_j; e_j = expf(s_j - mx), summed in j order; acc[d] = sum over j, in j
+ * order, of e_j * v_j[d]; out[d] = acc[d] * (1 / sum). k_j / v_j: kv head h / (n_head / n_kv) of cache
+ * row j (rows of n_kv * hd halves); out rows are n_head * hd floats. */
+void oracle_attention(const float* q, int64_t q_stride, const uint16_t* kc, const uint16_t* vc, float* out, int64_t T,
+                      int n_head, int n_kv, int hd, int64_t pos0) {
+    const int64_t kvw = (int64_t)n_kv * hd;
+    const int group = n_head / n_kv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* scores = malloc(sizeof(float) * (size_t)(pos0 + T));
+    float* acc = malloc(sizeof(float) * (size_t)hd);
+    if (!scores || !acc) abort();
+    for (int64_t t = 0; t < T; t++) {
+        for (int h = 0; h < n_head; h++) {
+            const int64_t L = pos0 + t + 1;
+            const float* qh = q + t * q_stride + (int64_t)h * hd;
+            const int64_t off = (int64_t)(h / group) * hd;
+            float mx = -INFINITY;
+            for (int64_t j = 0; j < L; j++) {
+                const uint16_t* kr = kc + j * kvw + off;
+                float s = 0.0f;
+                for (int d = 0; d < hd; d++) s += qh[d] * oracle_f16_to_f32(kr[d]);
+                s = s * scale;
+                scores[j] = s;
+                mx = mx < s ? s : mx; /* std::max(mx, s) */
+            }
+            float sum = 0.0f;
+            for (int64_t j = 0; j < L; j++) {
+                const float e = expf(scores[j] - mx);
+                scores[j] = e;
+                sum += e;
+            }
+            for (int d = 0; d < hd; d++) acc[d] = 0.0f;
+            for (int64_t j = 0; j < L; j++) {
+                const uint16_t* vr = vc + j * kvw + off;
+                for (int d = 0; d < hd; d++) acc[d] += scores[j] * oracle_f16_to_f32(vr[d]);
+            }
+            const float inv = 1.0f / sum;
+            float* o = out + t * (int64_t)n_head * hd + (int64_t)h * hd;
+            for (int d = 0; d < hd; d++) o[d] = acc[d] * inv;
+        }
+    }
+    free(scores);
+    free(acc);
+}
+
 /* Residual add then RMSNorm: the matmul epilogue with kAccumulate adds the product into the residual
  * row, dst = dst + v in float (cpu_ops.cpp:123), and the next op norms that row (qwen3_model.cpp:264,
  * cpu_ops.cpp:502-511). Here v is the delta row d. */

@@ -64,6 +64,9 @@ void oracle_rope_table(double theta, int hd, int n_pos, float* cs);
  * into cache rows pos0 + t. */
 void oracle_store_kv(const float* k, const float* v, int64_t src_stride, uint16_t* kc, uint16_t* vc, int width,
                      int64_t T, int64_t pos0);
+/* Causal grouped-query attention over f16 caches (cpu_ops.cpp:544-575); out rows of n_head*hd floats. */
+void oracle_attention(const float* q, int64_t q_stride, const uint16_t* kc, const uint16_t* vc, float* out, int64_t T,
+                      int n_head, int n_kv, int hd, int64_t pos0);
 /* Residual add (matmul kAccumulate epilogue, cpu_ops.cpp:123: x = x + d in float), then RMSNorm of
  * the updated rows into xn (qwen3_model.cpp:264, cpu_ops.cpp:502-511). x is updated in place. */
 void oracle_add_rmsnorm(float* x, const float* d, float* xn, const float* w, int rows, int C, float eps);

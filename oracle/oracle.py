@@ -95,6 +95,7 @@ _ORACLE_SIGS = {
     "oracle_qk_norm_rope_kv_f32": (None, [_p, _i64, _i64, _i32, _i32, _i32, _i64, _p, _p, _p, _i64, _f32, _p, _p]),
     "oracle_add_rmsnorm_f16": (None, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _f32]),
     "oracle_matmul": (None, [_i32, _p, _i64, _i32, _p, _i64, _i64, _p, _p, _i32]),
+    "oracle_attention": (None, [_p, _i64, _p, _p, _p, _i64, _i32, _i32, _i32, _i64]),
 }
 
 _REF_SIGS = {
@@ -127,6 +128,7 @@ _REF_SIGS = {
     "ref_qmatrix_gather": (None, [_p, _p, _i32, _p, _p]),
     "ref_qmatrix_free": (None, [_p]),
     "ref_qmatrix_matmul": (None, [_p, _p, _i32, _p, _p, _i32]),
+    "ref_attention": (None, [_p, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32]),
 }
 
 _oracle = None
@@ -232,6 +234,20 @@ def store_kv(qkv, k_off, v_off, width, cache_rows, positions=None, pos0=0):
     lib().oracle_store_kv_rows(_ptr(src), int(f16), stride, k_off, v_off, width, rows, pos0, _ptr(pos), cache_rows,
                                _ptr(kc), _ptr(vc))
     return kc, vc
+
+
+def attention(q, kc, vc, n_head, n_kv, hd, pos0, use_ref=False):
+    """cpu::attention's meaning: q float32 [T, q_stride], caches uint16 (f16 bits) [>= pos0 + T, n_kv*hd];
+    returns float32 [T, n_head*hd]. use_ref: the compiled reference instead of the restatement."""
+    q = _c32(q)
+    kc, vc = _c16(kc), _c16(vc)
+    T, qs = q.shape
+    out = np.empty((T, n_head * hd), np.float32)
+    if use_ref:
+        ref().ref_attention(_ptr(q), qs, _ptr(kc), _ptr(vc), _ptr(out), T, n_head, n_kv, hd, pos0)
+    else:
+        lib().oracle_attention(_ptr(q), qs, _ptr(kc), _ptr(vc), _ptr(out), T, n_head, n_kv, hd, pos0)
+    return out
 
 
 def add_rmsnorm_f16(x, d, w, eps):

@@ -139,6 +139,13 @@ void ref_store_kv(const float* k, const float* v, int src_stride, uint16_t* kc, 
     cpu::storeKv(k, v, src_stride, kc, vc, width, T, pos0);
 }
 
+// Causal grouped-query attention: the compiled cpu::attention on a one-thread pool.
+void ref_attention(const float* q, int q_stride, const uint16_t* kc, const uint16_t* vc, float* out, int T, int n_head,
+                   int n_kv, int hd, int pos0) {
+    static ThreadPool pool(1);
+    cpu::attention(pool, q, q_stride, kc, vc, out, T, n_head, n_kv, hd, pos0);
+}
+
 // Residual add + RMSNorm with f16 I/O, entirely through compiled reference code: the add is the
 // matmulF16 kAccumulate epilogue (cpu_ops.cpp:123) with an identity weight matrix, so each output
 // row is y = y + (sum of 1 * d[n] and exact zeros) = y + d (finite d); then cpu::rmsNorm of the

@@ -1,9 +1,8 @@
-// Port of the reference's GPU backend self-test (gpu/compute.cpp:32-290) for the kernels the HIP
-// backend implements, driven through neko::gpu::ComputeBackend::dispatch with the reference's own
-// parameter blocks. The CPU side is the oracle (oracle/neko_oracle.c), standing where the reference
-// calls its cpu:: ops. Same inputs scheme (std::mt19937(1234), uniform(-1, 1), f16-rounded weights),
-// same shapes and the reference's tolerance test |gpu - cpu| <= tol * (1 + |cpu|); the gather cases
-// additionally require bit equality.
+// Port of the reference's GPU backend self-test (gpu/compute.cpp:32-290), every case, driven through
+// neko::gpu::ComputeBackend::dispatch with the reference's own parameter blocks. The CPU side is the
+// oracle (oracle/neko_oracle.c), standing where the reference calls its cpu:: ops. Same inputs scheme
+// (std::mt19937(1234), uniform(-1, 1), f16-rounded weights), same shapes and the reference's tolerance
+// test |gpu - cpu| <= tol * (1 + |cpu|); the gather cases additionally require bit equality.
 //
 // Built into tests/cpp/_build/libbackend_selftest.so and called from tests/test_gpu_backend.py.
 #include <cmath>
@@ -331,14 +330,36 @@ struct Harness {
         }
     }
 
-    void unsupported() {  // attention is outside the HIP backend and must throw, not run
+    void attention() {  // compute.cpp:262-283: kv_store + grouped-query attention, pos0 > 1024
+        const int H = 4, KV = 2, hd = 64, T = 3, pos0 = 1030, ctx = pos0 + T;
+        const int stride = (H + 2 * KV) * hd, kvW = KV * hd, kOff = H * hd, vOff = (H + KV) * hd;
+        auto qkv = rnd(size_t(T * stride));
+        auto kf = rnd(size_t(ctx * kvW)), vf = rnd(size_t(ctx * kvW));
+        auto kc = halves(kf), vc = halves(vf);
+        std::vector<uint16_t> kcRef = kc, vcRef = vc;
+        std::vector<float> ref(size_t(T * H * hd));
+        oracle_store_kv(qkv.data() + kOff, qkv.data() + vOff, stride, kcRef.data(), vcRef.data(), kvW, T, pos0);
+        oracle_attention(qkv.data(), stride, kcRef.data(), vcRef.data(), ref.data(), T, H, KV, hd, pos0);
+        Buffer* bq = be.create(qkv.size() * 4, qkv.data());
+        Buffer* bk = be.create(kc.size() * 2, kc.data());
+        Buffer* bv = be.create(vc.size() * 2, vc.data());
+        Buffer* bo = be.create(ref.size() * 4, nullptr, true);
+        be.begin();
+        run(Kernel::KvStore, {bq, bk, bv}, {T, kvW, pos0, 0, stride, kOff, vOff}, uint32_t((kvW / 2 + 63) / 64), T);
+        run(Kernel::Attention, {bq, bk, bv, bo}, {T, stride, H, pos0, hd, floatBits(1.0f / std::sqrt(float(hd))), kvW},
+            H, T);
+        be.submitAndWait();
+        closeOrFail(read(bo, ref.size()), ref, 2e-3f, "attention", false);
+    }
+
+    void unknownKernel() {  // a kernel id past the enum throws, not runs
         Buffer* b = be.create(64);
         try {
-            run(Kernel::Attention, {b, b, b, b}, {4, 4, 1, 0}, 4, 1);
+            run(Kernel::Count, {b, b, b, b}, {4, 4, 1, 0}, 4, 1);
         } catch (const NekoError&) {
             return;
         }
-        throw Failure{"Attention dispatch did not throw"};
+        throw Failure{"dispatch of an unknown kernel did not throw"};
     }
 
     void outOfRange() {  // a dispatch reading past a buffer throws instead of faulting
@@ -382,7 +403,8 @@ extern "C" int backend_selftest(char* err, int err_bytes) {
         h.kvStore();
         h.addRmsNorm();
         h.matmul();
-        h.unsupported();
+        h.attention();
+        h.unknownKernel();
         h.outOfRange();
         std::snprintf(err, size_t(err_bytes), "ok on %s (%s)", be->deviceName().c_str(), be->name());
         return 0;

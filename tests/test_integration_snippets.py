@@ -38,13 +38,13 @@ CPP_PRELUDE = r"""
 #include <initializer_list>
 #include "compute.h"
 using namespace neko::gpu;
-// What the reference's model code has in scope at its dispatch sites (qwen3_model.cpp:280-294,
+// What the reference's model code has in scope at its dispatch sites (qwen3_model.cpp:280-317,
 // granite_model.h:31-40).
-struct Layer { Buffer *wqkv, *bqkv, *norm, *ln2; };
+struct Layer { Buffer *wqkv, *bqkv, *norm, *ln2, *kCache, *vCache; };
 struct Config { float eps; int mGroups; float embeddingMult; };
 void dispatches(ComputeBackend& be, Layer L, Config cfg_, Buffer* xn, Buffer* qkv, Buffer* y, Buffer* proj, Buffer* x,
                 Buffer* d, int C, int QW, int T, int DI, int P, float eps, Buffer* tokens, Buffer* table, int flags,
-                int rows, int rowWords) {
+                int rows, int rowWords, Buffer* gQkv_, Buffer* gAtt_, int H, int pos0, int hd, int32_t scale, int KW) {
     auto run = [&](Kernel k, Buffer* a, Buffer* b, Buffer* c, Buffer* e, std::initializer_list<int32_t> p, uint32_t gx,
                    uint32_t gy) {
         Buffer* binds[4] = {a, b, c, e};
@@ -55,6 +55,7 @@ void dispatches(ComputeBackend& be, Layer L, Config cfg_, Buffer* xn, Buffer* qk
     };
     (void)xn; (void)qkv; (void)y; (void)proj; (void)x; (void)d; (void)C; (void)QW; (void)T; (void)DI; (void)P;
     (void)eps; (void)L; (void)cfg_; (void)tokens; (void)table; (void)flags; (void)rows; (void)rowWords;
+    (void)gQkv_; (void)gAtt_; (void)H; (void)pos0; (void)hd; (void)scale; (void)KW;
 """
 
 

@@ -627,3 +627,77 @@ def test_matmul_float_within_summation_bound(fmt):
     dropped = np.abs(O.matmul(fmt, x2, tab, K).astype(np.float64) - exact)
     assert (dropped > (K + 1) * 2.0 ** -24 * mag)[np.abs(x[:, 100:101] * wd[None, :, 100]) > 1e-3 * mag].all()
 
+
+
+ATTN_SHAPES = [(3, 4, 2, 64, 1030), (1, 32, 8, 128, 300), (5, 12, 12, 64, 7), (2, 6, 2, 96, 40), (4, 3, 1, 256, 20),
+               (3, 4, 2, 6, 9)]
+
+
+def _attn_inputs(T, H, KV, hd, pos0, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((T, (H + 2 * KV) * hd)).astype(np.float32)
+    kc = rng.standard_normal((pos0 + T, KV * hd)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((pos0 + T, KV * hd)).astype(np.float16).view(np.uint16)
+    return q, kc, vc
+
+
+@needs_ref
+@pytest.mark.parametrize("T,H,KV,hd,pos0", ATTN_SHAPES)
+def test_ref_attention_bitexact(T, H, KV, hd, pos0):
+    """The restatement is the compiled cpu::attention bit for bit (the same summation orders)."""
+    q, kc, vc = _attn_inputs(T, H, KV, hd, pos0, T * 7 + hd)
+    got = O.attention(q, kc, vc, H, KV, hd, pos0)
+    want = O.attention(q, kc, vc, H, KV, hd, pos0, use_ref=True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _attn_f64(q, kc, vc, H, KV, hd, pos0, kv_of=None, scale=None, extra=0):
+    """Textbook causal softmax attention in float64: head h reads kv head kv_of(h) of rows 0 .. pos0 + t
+    (+ extra), scores scaled by 1/sqrt(hd)."""
+    kv_of = kv_of or (lambda h: h // (H // KV))
+    scale = 1.0 / np.sqrt(hd) if scale is None else scale
+    k = kc.view(np.float16).astype(np.float64)
+    v = vc.view(np.float16).astype(np.float64)
+    T = q.shape[0]
+    out = np.empty((T, H * hd))
+    for t in range(T):
+        L = min(pos0 + t + 1 + extra, k.shape[0])
+        for h in range(H):
+            g = kv_of(h)
+            s = k[:L, g * hd:(g + 1) * hd] @ q[t, h * hd:(h + 1) * hd].astype(np.float64) * scale
+            p = np.exp(s - s.max())
+            out[t, h * hd:(h + 1) * hd] = (p / p.sum()) @ v[:L, g * hd:(g + 1) * hd]
+    return out
+
+
+@pytest.mark.parametrize("T,H,KV,hd,pos0", ATTN_SHAPES)
+def test_attention_float64_softmax(T, H, KV, hd, pos0):
+    """Within 1e-5 of a float64 softmax attention with the grouped-query head mapping h -> h / (H / KV);
+    a wrong mapping (h % KV), a missing scale or one key too many each miss it by far."""
+    q, kc, vc = _attn_inputs(T, H, KV, hd, pos0, T * 5 + hd)
+    got = O.attention(q, kc, vc, H, KV, hd, pos0).astype(np.float64)
+    rel = lambda a: np.abs(got - a) / (1.0 + np.abs(a))  # noqa: E731
+    assert rel(_attn_f64(q, kc, vc, H, KV, hd, pos0)).max() <= 1e-5
+    if KV > 1 and H // KV > 1:
+        assert rel(_attn_f64(q, kc, vc, H, KV, hd, pos0, kv_of=lambda h: h % KV)).max() > 1e-2
+    assert rel(_attn_f64(q, kc, vc, H, KV, hd, pos0, scale=1.0)).max() > 1e-2
+    if T > 1:  # one more key than the causal range (the last token has no later row)
+        assert rel(_attn_f64(q, kc, vc, H, KV, hd, pos0, extra=1)).max() > 1e-3
+
+
+def test_attention_closed_forms():
+    """Position 0 sees one key: out = v_0 bit for bit. Equal keys weight every row alike: out = the
+    f32 mean of the v rows, within a few ulp."""
+    q, kc, vc = _attn_inputs(1, 4, 2, 64, 0, 31)
+    out = O.attention(q, kc, vc, 4, 2, 64, 0)
+    v0 = vc[0].view(np.float16).astype(np.float32)
+    assert np.array_equal(out[0], np.concatenate([v0[:64], v0[:64], v0[64:], v0[64:]]))
+    T, pos0 = 2, 50
+    q, kc, vc = _attn_inputs(T, 4, 2, 64, pos0, 32)
+    kc[:] = kc[0]
+    out = O.attention(q, kc, vc, 4, 2, 64, pos0)
+    v = vc.view(np.float16).astype(np.float64)
+    for t in range(T):
+        m = v[: pos0 + t + 1].mean(0)
+        want = np.concatenate([m[:64], m[:64], m[64:], m[64:]])
+        assert np.abs(out[t] - want).max() <= 1e-6
