@@ -24,10 +24,11 @@
 namespace neko_hip {
 namespace {
 
-constexpr int kAttnHeads = 4;              // query heads per work item, at most
+constexpr int kAttnHeads = 4;              // query heads per work item, at most (HB = 4 or 1)
 constexpr int kAttnWaves = 4;              // waves per work item (its steps interleaved)
 constexpr int64_t kAttnTargetWaves = 4096;  // keys split until a launch holds about this many waves
 constexpr int64_t kAttnMaxSplits = 1024;    // the merge kernel's LDS weights
+constexpr int64_t kAttnOneHeadBytes = int64_t{32} << 20;  // K + V bytes up to which items take one head
 
 struct AttnArgs {
     const void* q;
@@ -42,7 +43,7 @@ struct AttnArgs {
     int n_head;
     int n_kv;
     int group;    // n_head / n_kv
-    int hblocks;  // ceil(group / kAttnHeads)
+    int hblocks;  // ceil(group / HB): the head blocks per kv head
     int hd;
     float scale;
     int splits;          // key splits per (token, kv head, head block)
@@ -125,18 +126,18 @@ __device__ __forceinline__ float* part_ml(const AttnArgs& a, int64_t th, int spl
 // rows j0 + KR u + r, u = 0 .. KU - 1 -- so each load instruction reads KR whole head rows of K or V
 // (16 lanes per 256-byte row of a 128-dimension head) and each lane keeps its chunk of the q rows in
 // registers. HDP: the head size rounded up to 64, 128 or 256 (DC = HDP / 8 chunks); a step is KR x 8
-// keys (64 / 32 / 16): eight K and eight V loads per lane, all issued at the step's start (sixteen of
-// each held the kernel at one wave per SIMD). NW waves per workgroup share one work item, its steps
+// keys (64 / 32 / 16): eight K and eight V loads per lane, issued before the previous step's
+// arithmetic. NW waves per workgroup share one work item, its steps
 // dealt round robin; their states merge through LDS at the end.
-template <typename TQ, int HDP, bool AL, int NW>
+template <typename TQ, int HDP, bool AL, int NW, int HB, bool PF>
 __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
     constexpr int DC = HDP / 8;
     constexpr int KR = 64 / DC;
     constexpr int KU = 8;
     constexpr int STEP = KR * KU;
-    __shared__ float ssh[NW][kAttnHeads][STEP];  // the step's scores by key, then its weights by (r, u)
-    __shared__ float msh[NW][kAttnHeads], lsh[NW][kAttnHeads];
-    __shared__ __align__(16) float ash[NW][kAttnHeads][HDP];
+    __shared__ float ssh[NW][HB][STEP];  // the step's scores by key, then its weights by (r, u)
+    __shared__ float msh[NW][HB], lsh[NW][HB];
+    __shared__ __align__(16) float ash[NW][HB][HDP];
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int c = lane % DC, r = lane / DC;
@@ -149,8 +150,8 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
     rest /= a.splits;
     const int hb = static_cast<int>(rest % a.hblocks);
     const int g = static_cast<int>(rest / a.hblocks);
-    const int h0 = g * a.group + hb * kAttnHeads;
-    const int nh = min(kAttnHeads, a.group - hb * kAttnHeads);
+    const int h0 = g * a.group + hb * HB;
+    const int nh = min(HB, a.group - hb * HB);
     const int hd = a.hd;
     const int64_t L = a.pos0 + t + 1;
     const int64_t k0 = static_cast<int64_t>(split) * a.split_keys;
@@ -158,17 +159,17 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
 
     // This lane's chunk of each q row, f32.
     const TQ* qrow = static_cast<const TQ*>(a.q) + t * a.qs + static_cast<int64_t>(h0) * hd;
-    float qv[kAttnHeads][8];
+    float qv[HB][8];
 #pragma unroll
-    for (int i = 0; i < kAttnHeads; i++)
+    for (int i = 0; i < HB; i++)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int d = 8 * c + e;
             qv[i][e] = i < nh && d < hd ? to_f32(qrow[static_cast<int64_t>(i) * hd + d]) : 0.0f;
         }
-    float m[kAttnHeads], l[kAttnHeads], acc[kAttnHeads][8];
+    float m[HB], l[HB], acc[HB][8];
 #pragma unroll
-    for (int i = 0; i < kAttnHeads; i++) {
+    for (int i = 0; i < HB; i++) {
         m[i] = -INFINITY;
         l[i] = 0.0f;
 #pragma unroll
@@ -178,30 +179,22 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
     const uint16_t* vbase = a.vc + static_cast<int64_t>(g) * hd;
     float(*sw)[STEP] = ssh[wave];
 
-    for (int64_t j0 = k0 + static_cast<int64_t>(wave) * STEP; j0 < k1; j0 += NW * STEP) {
-        // Every load of the step first: K and V rows j0 + KR u + r (past k1: row k1 - 1, not counted).
-        uint32_t kr[KU][4], vr[KU][4];
+    // The K and V rows of the step at j0 (rows j0 + KR u + r; past k1: row k1 - 1, not counted). Nothing
+    // here uses the loaded registers, so the loads stay in flight.
+    auto load_step = [&](int64_t j0, uint32_t(&kr)[KU][4], uint32_t(&vr)[KU][4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < KU; u++) {
-            const int64_t jj = min(j0 + KR * u + r, k1 - 1);
-            load8<AL>(kbase + jj * a.kvw, 8 * c, hd, kr[u]);
-        }
+        for (int u = 0; u < KU; u++) load8<AL>(kbase + min(j0 + KR * u + r, k1 - 1) * a.kvw, 8 * c, hd, kr[u]);
 #pragma unroll
-        for (int u = 0; u < KU; u++) {
-            const int64_t jj = min(j0 + KR * u + r, k1 - 1);
-            load8<AL>(vbase + jj * a.kvw, 8 * c, hd, vr[u]);
-            if (j0 + KR * u + r >= k1) {  // weight 0; its row is not read as its own (0 x inf would be NaN)
-#pragma unroll
-                for (int e = 0; e < 4; e++) vr[u][e] = 0u;
-            }
-        }
+        for (int u = 0; u < KU; u++) load8<AL>(vbase + min(j0 + KR * u + r, k1 - 1) * a.kvw, 8 * c, hd, vr[u]);
+    };
+    auto step = [&](int64_t j0, const uint32_t(&kr)[KU][4], const uint32_t(&vr)[KU][4]) __attribute__((always_inline)) {
         // Scores: each lane's 8-dimension partial dot, summed over the DC lanes of its key row.
 #pragma unroll
         for (int u = 0; u < KU; u++) {
             const int key = KR * u + r;
             const bool valid = j0 + key < k1;
 #pragma unroll
-            for (int i = 0; i < kAttnHeads; i++) {
+            for (int i = 0; i < HB; i++) {
                 if (i >= nh) break;
                 float p = 0.0f;
 #pragma unroll
@@ -213,7 +206,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
         wave_sync_lds();
         // Streaming softmax per head, lane = key; the weights go back to LDS by (r, u).
 #pragma unroll
-        for (int i = 0; i < kAttnHeads; i++) {
+        for (int i = 0; i < HB; i++) {
             if (i >= nh) break;
             const float s = lane < STEP ? sw[i][lane] : -INFINITY;
             const float mn = fmaxf(m[i], wave_max_f32(s));  // finite: the step holds a valid key
@@ -227,24 +220,55 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
             if (lane < STEP) sw[i][(lane % KR) * KU + lane / KR] = p;
         }
         wave_sync_lds();
-        // Weighted v rows: this lane's keys KR u + r, chunk c.
+        // Weighted v rows: this lane's keys KR u + r, chunk c (a key past k1 adds nothing: its row is
+        // another key's, and 0 x inf would be NaN).
 #pragma unroll
-        for (int i = 0; i < kAttnHeads; i++) {
-            if (i >= nh) break;
+        for (int u = 0; u < KU; u++) {
+            const bool valid = j0 + KR * u + r < k1;
+            float vf[8];
 #pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const float w = sw[i][r * KU + u];  // 0 for keys past k1
+            for (int e = 0; e < 8; e++) vf[e] = valid ? half_at(vr[u], e) : 0.0f;
 #pragma unroll
-                for (int e = 0; e < 8; e++) acc[i][e] = __builtin_fmaf(w, half_at(vr[u], e), acc[i][e]);
+            for (int i = 0; i < HB; i++) {
+                if (i >= nh) break;
+                const float w = sw[i][r * KU + u];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[i][e] = __builtin_fmaf(w, vf[e], acc[i][e]);
             }
         }
         wave_sync_lds();  // the next step rewrites sw
+    };
+    // Steps j0, j0 + NW STEP, ...; with PF (waves of several steps) the next step's loads are issued
+    // before each step's arithmetic, in two register sets that alternate (no copy of registers a load
+    // is still filling; the last prefetch re-reads row k1 - 1). Without PF each step loads, then
+    // computes, in half the registers.
+    const int64_t stride = static_cast<int64_t>(NW) * STEP;
+    int64_t j0 = k0 + static_cast<int64_t>(wave) * STEP;
+    if constexpr (!PF) {
+        for (; j0 < k1; j0 += stride) {
+            uint32_t ka[KU][4], va[KU][4];
+            load_step(j0, ka, va);
+            step(j0, ka, va);
+        }
+    } else if (j0 < k1) {
+        uint32_t ka[KU][4], va[KU][4], kb[KU][4], vb[KU][4];
+        load_step(j0, ka, va);
+        for (;;) {
+            load_step(j0 + stride, kb, vb);
+            step(j0, ka, va);
+            j0 += stride;
+            if (j0 >= k1) break;
+            load_step(j0 + stride, ka, va);
+            step(j0, kb, vb);
+            j0 += stride;
+            if (j0 >= k1) break;
+        }
     }
 
     // The wave's accumulators: summed over its KR key residues (lanes DC apart), then through LDS the
     // waves merge -- wave i merging head i, in wave order.
 #pragma unroll
-    for (int i = 0; i < kAttnHeads; i++) {
+    for (int i = 0; i < HB; i++) {
         if (i >= nh) break;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -368,11 +392,24 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     }
 }
 
+template <typename TQ, int HDP, int HB>
+void launch_hb(neko_hip_ctx* ctx, const AttnArgs& a, dim3 grid, bool vec, bool pf) {
+    const dim3 block(64 * kAttnWaves);
+    if (!vec) hipLaunchKernelGGL((attn_kernel<TQ, HDP, false, kAttnWaves, HB, false>), grid, block, 0, ctx->stream, a);
+    else if (pf) hipLaunchKernelGGL((attn_kernel<TQ, HDP, true, kAttnWaves, HB, true>), grid, block, 0, ctx->stream, a);
+    else hipLaunchKernelGGL((attn_kernel<TQ, HDP, true, kAttnWaves, HB, false>), grid, block, 0, ctx->stream, a);
+}
+
 template <typename TQ, int HDP>
-int launch_hdp(neko_hip_ctx* ctx, const char* what, const AttnArgs& a, bool vec, int64_t items) {
-    const dim3 grid(static_cast<uint32_t>(items)), block(64 * kAttnWaves);
-    if (vec) hipLaunchKernelGGL((attn_kernel<TQ, HDP, true, kAttnWaves>), grid, block, 0, ctx->stream, a);
-    else hipLaunchKernelGGL((attn_kernel<TQ, HDP, false, kAttnWaves>), grid, block, 0, ctx->stream, a);
+int launch_hdp(neko_hip_ctx* ctx, const char* what, const AttnArgs& a, bool vec, int64_t items, bool one_head) {
+    const dim3 grid(static_cast<uint32_t>(items));
+    // The prefetching form where a wave has more than one step (measured: 4096-position decode, one
+    // step per wave, 12.7 us without and 15.5 with it; 32768 positions 56.3 -> 49.6 us, the 2048- and
+    // 8192-token prefills 6% faster).
+    const int step = 8 * (512 / HDP);
+    const bool pf = a.split_keys > static_cast<int64_t>(kAttnWaves) * step;
+    if (one_head) launch_hb<TQ, HDP, 1>(ctx, a, grid, vec, pf);
+    else launch_hb<TQ, HDP, kAttnHeads>(ctx, a, grid, vec, pf);
     if (int rc = after_launch(ctx, what)) return rc;
     if (a.splits == 1) return NEKO_OK;
     hipLaunchKernelGGL((attn_merge_kernel<TQ>), dim3(static_cast<uint32_t>(a.T * a.n_head)), dim3(256), 0, ctx->stream, a);
@@ -380,10 +417,10 @@ int launch_hdp(neko_hip_ctx* ctx, const char* what, const AttnArgs& a, bool vec,
 }
 
 template <typename TQ>
-int launch_typed(neko_hip_ctx* ctx, const char* what, const AttnArgs& a, bool vec, int64_t items) {
-    if (a.hd <= 64) return launch_hdp<TQ, 64>(ctx, what, a, vec, items);
-    if (a.hd <= 128) return launch_hdp<TQ, 128>(ctx, what, a, vec, items);
-    return launch_hdp<TQ, 256>(ctx, what, a, vec, items);
+int launch_typed(neko_hip_ctx* ctx, const char* what, const AttnArgs& a, bool vec, int64_t items, bool one_head) {
+    if (a.hd <= 64) return launch_hdp<TQ, 64>(ctx, what, a, vec, items, one_head);
+    if (a.hd <= 128) return launch_hdp<TQ, 128>(ctx, what, a, vec, items, one_head);
+    return launch_hdp<TQ, 256>(ctx, what, a, vec, items, one_head);
 }
 
 }  // namespace
@@ -428,7 +465,13 @@ extern "C" int neko_hip_attention(neko_hip_ctx* ctx, const void* q, int64_t q_st
     a.n_head = n_head;
     a.n_kv = n_kv;
     a.group = n_head / n_kv;
-    a.hblocks = (a.group + kAttnHeads - 1) / kAttnHeads;
+    // One query head per item where the K and V rows are few (their re-reads by the group's heads stay
+    // in L2) and the launch would otherwise be short of waves; else up to four heads share each load.
+    const int64_t kv_bytes = (pos0 + T) * static_cast<int64_t>(n_kv) * hd * 4;
+    const bool one_head = T * n_kv * ((a.group + kAttnHeads - 1) / kAttnHeads) * kAttnWaves < kAttnTargetWaves &&
+                          kv_bytes <= kAttnOneHeadBytes;
+    const int hb_size = one_head ? 1 : kAttnHeads;
+    a.hblocks = (a.group + hb_size - 1) / hb_size;
     a.hd = hd;
     a.scale = scale;
     // Split the keys when tokens x kv heads x head blocks leave the chip short of waves (each split at
@@ -453,6 +496,6 @@ extern "C" int neko_hip_attention(neko_hip_ctx* ctx, const void* q, int64_t q_st
         a.part = static_cast<float*>(ws);
     }
     const bool vec = hd % 8 == 0 && aligned(k_cache, 16) && aligned(v_cache, 16);
-    return dtype == NEKO_DT_F16 ? launch_typed<half_t>(ctx, what, a, vec, items)
-                                : launch_typed<float>(ctx, what, a, vec, items);
+    return dtype == NEKO_DT_F16 ? launch_typed<half_t>(ctx, what, a, vec, items, one_head)
+                                : launch_typed<float>(ctx, what, a, vec, items, one_head);
 }

@@ -7,9 +7,9 @@ in different orders -- so the bar is a tolerance, written below: |gpu - oracle| 
 with TOL = 2e-6 for f32 outputs (the reference's own self-test allows 2e-3), and f16 outputs within
 half an f16 ulp of the oracle's f32 result plus that bar. Shapes: the reference self-test case, the Qwen3-4B
 decode (one token over 4096 and 40000 cached positions: the keys split over many workgroups and
-merged; one kv head over 100000 positions: 391 splits)
-and a 256-token prefill, GPT-2 heads, head sizes 6 / 96 / 256 (the 4-byte and masked paths), groups
-of 3 and 8 query heads per kv head, strided q / out rows, f16 activations, and the argument checks.
+merged; one kv head over 100000 positions: 391 splits) and a 256-token prefill, GPT-2 heads, head
+sizes 6 / 96 / 256 (the per-half and masked loads), groups of 3 and 8 query heads per kv head, work
+items of one and of four query heads, strided q / out rows, f16 activations, and the argument checks.
 """
 import numpy as np
 import pytest
@@ -58,11 +58,14 @@ def _check_f32(got, want, what):
     (4, 32, 8, 128, 2000),  # four-sequence decode step
     (256, 32, 8, 128, 0),   # Qwen3-4B prefill of 256 tokens: one item per (token, kv head)
     (64, 12, 12, 64, 0),    # GPT-2 small: one query head per kv head
-    (8, 8, 2, 256, 100),    # head size 256
+    (8, 8, 2, 256, 100),    # head size 256, one query head per work item
+    (512, 8, 2, 256, 0),    # head size 256, four query heads per work item
     (5, 6, 2, 96, 70),      # head size 96: dimensions past hd masked
-    (3, 4, 2, 6, 9),        # head size 6: 4-byte key loads
+    (3, 4, 2, 6, 9),        # head size 6: per-half loads, one query head per work item
+    (512, 4, 2, 6, 0),      # head size 6, two query heads per work item
     (7, 12, 4, 64, 200),    # three query heads per kv head
-    (2, 16, 2, 128, 3000),  # eight query heads per kv head: two head blocks
+    (2, 16, 2, 128, 3000),  # eight query heads per kv head, one per work item
+    (1, 16, 2, 128, 40000),  # eight query heads per kv head: two blocks of four (41 MB of K and V)
     (1, 32, 8, 128, 40000),  # long context: 126 splits merged
     (1, 4, 1, 128, 100000),  # one kv head: 391 splits (the merge's threads each take several)
 ])
