@@ -103,6 +103,6 @@ def test_c_snippet_compiles(tmp_path):
     src = ("#include <stdio.h>\n#include <stdint.h>\n#include \"neko_hip.h\"\n"
            "void example(void* x, void* xn, const float* w, void* qkv, const int32_t* positions, const float* wqk,\n"
            "             const float* cs, void* h, void* g, uint16_t* k_cache, uint16_t* v_cache, void* delta,\n"
-           "             const uint8_t* w_gate_up, float* gu) {\n" + "\n".join(lines) + "\n}\n")
+           "             const uint8_t* w_gate_up, float* gu, void* att) {\n" + "\n".join(lines) + "\n}\n")
     _compile(tmp_path, "example.c", src, "gcc", ["-std=c11", "-Wall", "-Werror", "-Wno-unused-variable",
                                                  "-I", os.path.join(ROOT, "include")])
