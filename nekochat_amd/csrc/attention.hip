@@ -447,6 +447,8 @@ extern "C" int neko_hip_attention(neko_hip_ctx* ctx, const void* q, int64_t q_st
                  (long long)T, (long long)pos0);
     const size_t esz = dtype_size(dtype);
     const int64_t kvw = static_cast<int64_t>(n_kv) * hd;
+    NEKO_REQUIRE(ctx, pos0 + T <= (int64_t(1) << 62) / (kvw * 2), "%s: caches of %lld rows x %lld halves span more "
+                 "than 2^62 bytes", what, (long long)(pos0 + T), (long long)kvw);
     const size_t sq = rows_span(T, width, q_stride, esz), so = rows_span(T, width, out_stride, esz);
     const size_t sc = static_cast<size_t>((pos0 + T) * kvw) * 2;
     NEKO_REQUIRE(ctx, sq != 0 && so != 0, "%s: q / out rows span more than 2^62 bytes", what);
