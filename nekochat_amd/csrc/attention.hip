@@ -141,15 +141,17 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(AttnArgs a) {
     const int lane = static_cast<int>(threadIdx.x) & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int c = lane % DC, r = lane / DC;
-    const int64_t per_t = static_cast<int64_t>(a.n_kv) * a.hblocks * a.splits;
-    const int64_t item = blockIdx.x;
-    // The latest tokens (the most keys) first.
-    const int64_t t = a.T - 1 - item / per_t;
-    int64_t rest = item - (a.T - 1 - t) * per_t;
-    const int split = static_cast<int>(rest % a.splits);
-    rest /= a.splits;
-    const int hb = static_cast<int>(rest % a.hblocks);
-    const int g = static_cast<int>(rest / a.hblocks);
+    // Item index -> (token, kv head, head block, split), in 32 bits (the host keeps items below 2^31;
+    // 64-bit division is a loop on this target). The latest tokens (the most keys) first.
+    const uint32_t per_t = static_cast<uint32_t>(a.n_kv) * static_cast<uint32_t>(a.hblocks) * static_cast<uint32_t>(a.splits);
+    const uint32_t item = blockIdx.x;
+    const uint32_t tr = item / per_t;
+    const int64_t t = a.T - 1 - tr;
+    uint32_t rest = item - tr * per_t;
+    const int split = static_cast<int>(rest % static_cast<uint32_t>(a.splits));
+    rest /= static_cast<uint32_t>(a.splits);
+    const int hb = static_cast<int>(rest % static_cast<uint32_t>(a.hblocks));
+    const int g = static_cast<int>(rest / static_cast<uint32_t>(a.hblocks));
     const int h0 = g * a.group + hb * HB;
     const int nh = min(HB, a.group - hb * HB);
     const int hd = a.hd;
@@ -337,8 +339,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
     __shared__ float osh[8][256];
     const int tid = static_cast<int>(threadIdx.x), wave = tid >> 6;
     const int64_t th = blockIdx.x;
-    const int64_t t = th / a.n_head;
-    const int h = static_cast<int>(th - t * a.n_head);
+    const uint32_t tq = blockIdx.x / static_cast<uint32_t>(a.n_head);  // 32-bit: T * n_head < 2^31
+    const int64_t t = tq;
+    const int h = static_cast<int>(blockIdx.x - tq * static_cast<uint32_t>(a.n_head));
     const int hd = a.hd, S = a.splits;
     float ms[kPer], ls[kPer];
     float mx = -INFINITY;
