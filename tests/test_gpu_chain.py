@@ -5,8 +5,9 @@ Qwen3-4B prefill (qwen3_model.cpp:244-265) and a Granite-4.0-H Mamba layer (gran
 (neko_hip_matmul) with one-hot F16 weight rows -- row n holds a single 1.0 at column
 (m n + a) mod K -- so each output is exactly one input value whatever the summation order: the chain
 carries the GPU's own outputs forward through the real matmul kernels, and the oracle side of each
-product is an exact column selection. Attention and the Mamba scan are outside this path; their
-outputs are stood in for by the rotated q heads and by a slice of the in_proj row.
+product is an exact column selection. The Qwen3 layer runs the real attention over each sequence's
+caches (checked against the oracle at sampled tokens: within half an f16 ulp of its f32 result plus
+2e-6 relative); the Mamba scan is outside this path, stood in for by a slice of the in_proj row.
 
 Every op stage is compared with the oracle applied to the same input the GPU stage received (the
 previous GPU stage's output): norms, RoPE and SwiGLU to the fp16 parity bar, residual sums, V heads,
@@ -46,9 +47,9 @@ def _project(x, table, K, cols, what):
 
 
 def test_qwen3_prefill_layer_chain(dev):
-    """rmsNorm -> q/k/v projection -> per-head q/k norm + RoPE with the KV store -> (attention
-    stand-in) -> o projection -> residual add + rmsNorm -> gate/up projection -> SwiGLU -> down
-    projection accumulated into the residual; 4 sequences x 2048 tokens, hidden 2560."""
+    """rmsNorm -> q/k/v projection -> per-head q/k norm + RoPE with the KV store -> attention -> o
+    projection -> residual add + rmsNorm -> gate/up projection -> SwiGLU -> down projection
+    accumulated into the residual; 4 sequences x 2048 tokens, hidden 2560."""
     cfg = wl.QWEN3_PREFILL
     T, C, H, KV, hd, F, S = cfg.T, cfg.C, cfg.n_q, cfg.n_kv, cfg.hd, cfg.I, cfg.seq
     QW, QH, KVW = cfg.qkv_stride, cfg.n_q * cfg.hd, cfg.n_kv * cfg.hd
@@ -83,9 +84,26 @@ def test_qwen3_prefill_layer_chain(dev):
         assert_f16_close(to_bits(kc[s]), wk, what=f"qwen3 chain k cache seq {s}")
         assert np.array_equal(to_bits(vc[s]), wv), f"v cache seq {s}"
 
+    _case("qwen3 chain: attention over each sequence's caches")
+    att = torch.empty((T, QH), dtype=torch.float16, device=dev)
+    for s in range(T // S):
+        rows = slice(s * S, (s + 1) * S)
+        ops.attention(qkv[rows, :QH], kc[s], vc[s], H, KV, hd, 0, out=att[rows])
+    got_att = att.float().cpu().numpy()
+    rng = np.random.default_rng(9)
+    for s in range(T // S):
+        kb = to_bits(kc[s])
+        vb = to_bits(vc[s])
+        for t in sorted({0, 1, S - 1, *rng.integers(2, S - 1, 5).tolist()}):
+            qrow = got[s * S + t:s * S + t + 1, :QH].view(np.float16).astype(np.float32)
+            want = O.attention(qrow, kb[:t + 1], vb[:t + 1], H, KV, hd, t)[0]
+            half_ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float32) / 2
+            excess = np.abs(got_att[s * S + t] - want) - half_ulp - 2e-6 * (1.0 + np.abs(want))
+            assert (excess <= 0).all(), f"qwen3 chain attention seq {s} token {t}"
+
     _case("qwen3 chain: o projection + residual add + rmsnorm")
     w_o, c_o = _onehot(C, QH, 3, 11, dev)
-    delta = _project(qkv[:, :QH], w_o, QH, c_o, "o")  # the rotated q heads stand in for attention's output
+    delta = _project(att, w_o, QH, c_o, "o")
     x_in = to_bits(x).copy()
     xn2 = ops.add_rms_norm(x, delta, w_post, cfg.eps)
     want_x, want_xn = O.add_rmsnorm_f16(x_in, to_bits(delta), w_post.cpu().numpy(), cfg.eps)
